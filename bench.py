@@ -1,0 +1,155 @@
+"""Decode benchmark: Llama-3.1-8B-shaped Q4_K_M, batch 1, 4k context, one MI355X.
+
+A "step" is one greedy decode step (one token through every layer and the
+output head).  The KV cache is first filled by a 4096-token seeded prompt
+(run through the same decode path, token by token, as the reference's
+runPrompt does), then W untimed warm-up steps run, then exactly K timed steps
+(positions ~4.1k).  tok/s = K / decode wall time, the reference's definition
+(runtime/types.zig:220-223).  Weights are random N(0, 0.02) of the
+Llama-3.1-8B shape quantized by this package's own Q4_K_M mix; data is
+synthetic.
+
+Also reported, on the same JSON line:
+  hbm_fraction  -- (weight + KV bytes per token) x tok/s / 8 TB/s;
+  roofline      -- the dominant kernel (fused RMSNorm + gate/up + SwiGLU, Q4_K),
+                   timed with HIP events rotating over the 32 layers so its
+                   weights stream from HBM, against the 8 TB/s HBM peak;
+  cpu_baseline  -- the CPU oracle (a C restatement of the reference's CPU
+                   decode path, same threads policy: 1 + min(11, ncpu - 1))
+                   decoding the same model at the same context on host cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "ziggy-llm_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=4096)
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--model", default="llama8b", choices=["llama8b", "tinyllama", "qwen3"])
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-iters", type=int, default=64)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (batch-1 decode of this "
+              f"model does not shard profitably; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    from zhip import hip, synth
+
+    ctx_len = args.prompt + args.warmup + args.steps + 8
+    spec = {"llama8b": synth.llama8b_spec, "tinyllama": synth.tinyllama_spec,
+            "qwen3": synth.qwen3_8b_spec}[args.model](context=ctx_len)
+    t0 = time.time()
+    img = synth.build(spec, seed=args.seed)
+    log(f"built {spec.name} ({img.buf.nbytes / 1e9:.2f} GB) in {time.time() - t0:.1f}s")
+
+    ctx = hip.Context(0)
+    t0 = time.time()
+    sess = hip.Session(ctx, img, context=ctx_len)
+    log(f"session on {ctx.info.name.decode()} ({ctx.info.arch.decode()}, {ctx.info.compute_units} CUs) "
+        f"in {time.time() - t0:.1f}s")
+
+    prompt = synth.prompt_tokens(args.seed, args.prompt, spec.vocab)
+    t0 = time.time()
+    warm_tokens, wst = sess.generate(prompt, args.warmup)
+    log(f"prefill {args.prompt} tokens + {args.warmup} warm-up steps in {time.time() - t0:.1f}s")
+
+    toks, st = sess.generate(np.array([wst.next_token], np.uint32), args.steps)
+    wall_s = st.wall_ns / 1e9
+    tok_s = args.steps / wall_s
+    ms_per_step = 1000.0 * wall_s / args.steps
+    pos0 = args.prompt + args.warmup + 1
+    mean_pos = pos0 + (args.steps - 1) / 2.0
+    bytes_per_token = spec.weight_bytes_per_token() + spec.kv_bytes_per_token(int(round(mean_pos)))
+    hbm_frac = bytes_per_token * tok_s / (HBM_PEAK_GBS * 1e9)
+    log(f"decode: {tok_s:.1f} tok/s ({ms_per_step:.3f} ms/step, gpu events {st.gpu_elapsed_ns / 1e6 / args.steps:.3f}"
+        f" ms/step), {bytes_per_token / 1e9:.3f} GB/token -> {100 * hbm_frac:.1f}% of HBM peak")
+
+    kernels = {}
+    for name in ("qkv", "rope_kv", "attention", "o_proj", "gate_up", "down", "output"):
+        iters = args.kernel_iters if name != "output" else max(4, args.kernel_iters // 8)
+        ns, nb = sess.time_kernel(name, iters)
+        kernels[name] = {"avg_us": round(ns / 1e3, 2), "bytes": nb, "gbs": round(nb / ns, 1) if ns else None}
+        log(f"kernel {name}: {ns / 1e3:.2f} us, {nb / 1e6:.2f} MB -> {nb / max(ns, 1):.0f} GB/s")
+    dom = kernels["gate_up"]
+    roofline = {"bound": "hbm", "kernel": "gate_up (fused RMSNorm + Q4_K gate/up + SwiGLU)",
+                "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "bytes_per_launch": dom["bytes"], "avg_launch_us": dom["avg_us"]}
+    sess.close()
+    ctx.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import zo
+        ncpu = os.cpu_count() or 1
+        threads = 1 + min(11, ncpu - 1)
+        m = zo.Model(img.buf)
+        o = zo.Session(m, context=ctx_len, kv_f16=False, threads=threads)
+        o.fill_kv_pattern(pos0, seed=1)
+        tok = int(toks[0])
+        n, t_cpu = 0, 0.0
+        while t_cpu < args.cpu_seconds or n < 2:
+            t1 = time.perf_counter()
+            tok = o.step_greedy(tok)
+            t_cpu += time.perf_counter() - t1
+            n += 1
+            if n >= 64:
+                break
+        cpu = {"value": round(n / t_cpu, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"{n} greedy decode steps of the same {spec.name} model from position {pos0} "
+                         f"(KV cache filled with a fixed pattern; decode cost does not depend on its values), "
+                         f"C restatement of the reference CPU path, {threads} threads of {ncpu} host cores"}
+        log(f"cpu baseline: {cpu['value']} tok/s over {n} steps ({t_cpu:.1f}s)")
+
+    line = {
+        "metric": "decode tok/s + % of HBM roofline, Llama-3.1-8B-shaped Q4_K_M, batch 1, 4k ctx",
+        "value": round(tok_s, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{spec.name} Q4_K_M greedy decode, batch 1, positions {pos0}-{pos0 + args.steps - 1}"
+                               f" after a {args.prompt}-token prompt",
+                   "weights": "Q4_K (Q6_K attn_v, 16/32 ffn_down, output), random N(0,0.02)",
+                   "kv_cache": "binary16", "batch": 1, "context": pos0 + args.steps, "parallelism": "none"},
+        "hbm_fraction": round(hbm_frac, 4),
+        "bytes_per_token": bytes_per_token,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+        "tokens_head": [int(t) for t in toks[:8]],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,376 @@
+/*
+ * ziggy_hip.h -- C ABI of libziggy_hip, the MI355X (gfx950) decode backend for
+ * ziggy-llm.
+ *
+ * This is the HIP counterpart of the reference's Metal bridge
+ * (src/runtime/metal/bridge.h).  Conventions carried over unchanged so the
+ * Zig wrapper pattern of src/runtime/metal_backend.zig applies as-is:
+ *   - opaque context / buffer handles (bridge.h:9-10);
+ *   - every call returns an int status from the enum below (bridge.h:25-32)
+ *     and takes a trailing (char *error_message, size_t error_message_len)
+ *     pair that receives a NUL-terminated, truncated message
+ *     (bridge.m:95-101, metal_backend.zig:2027-2047);
+ *   - ops enqueue while a sequence is open and run synchronously otherwise
+ *     (bridge.m:350-384, 448-485);
+ *   - rows = output dimension, cols = reduction dimension; quant matrices are
+ *     raw GGUF rows, row-major, row_stride = cols / QK * block_bytes;
+ *   - the KV cache is [layer][pos][kv_dim] binary16 with
+ *     layer_base = layer * context_length * kv_dim (gpu/session.zig:382-383).
+ * Differences, each deliberate:
+ *   - buffers live in HBM (hipMalloc), not shared memory: reads and writes
+ *     are explicit copies;
+ *   - kernels come from the library's own gfx950 code object, not source
+ *     compiled at run time, so there is no shader-source argument;
+ *   - dense f32/f16 projections use GGUF's row-major rows (the Metal path
+ *     re-lays them column-major on the host, tensor_store.zig:208-225);
+ *   - status 6 (INVALID_ARGUMENT) reports shape/offset errors that the Zig
+ *     wrapper checks before calling Metal (metal_backend.zig:266-327).
+ * A context is not thread-safe; use one context per host thread.
+ */
+#ifndef ZIGGY_HIP_H
+#define ZIGGY_HIP_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ZiggyHipContext ZiggyHipContext;
+typedef struct ZiggyHipBuffer ZiggyHipBuffer;
+typedef struct ZiggyHipSession ZiggyHipSession;
+
+/* Replaces ZiggyMetalDeviceInfo (bridge.h:12-17). */
+typedef struct {
+    char name[128];
+    char arch[64];                 /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    uint64_t total_memory;         /* HBM bytes */
+    uint32_t compute_units;
+    uint32_t wavefront_size;
+    uint32_t clock_khz;
+    uint32_t l2_bytes;
+} ZiggyHipDeviceInfo;
+
+/* Replaces ZiggyMetalCommitStats (bridge.h:19-23). */
+typedef struct {
+    uint64_t cpu_wait_ns;
+    uint64_t gpu_elapsed_ns;
+    bool gpu_timestamps_valid;
+} ZiggyHipCommitStats;
+
+/* Status codes (bridge.h:25-32), plus INVALID_ARGUMENT. */
+enum {
+    ZIGGY_HIP_OK = 0,
+    ZIGGY_HIP_UNAVAILABLE = 1,
+    ZIGGY_HIP_INITIALIZATION_FAILED = 2,
+    ZIGGY_HIP_COMPILATION_FAILED = 3,
+    ZIGGY_HIP_BUFFER_FAILED = 4,
+    ZIGGY_HIP_EXECUTION_FAILED = 5,
+    ZIGGY_HIP_INVALID_ARGUMENT = 6,
+};
+
+/* GGUF tensor type ids accepted by the matvec family (model/loader.zig:119-153). */
+enum {
+    ZIGGY_HIP_TYPE_F32 = 0,
+    ZIGGY_HIP_TYPE_F16 = 1,
+    ZIGGY_HIP_TYPE_Q8_0 = 8,
+    ZIGGY_HIP_TYPE_Q3_K = 11,
+    ZIGGY_HIP_TYPE_Q4_K = 12,
+    ZIGGY_HIP_TYPE_Q6_K = 14,
+    ZIGGY_HIP_TYPE_IQ4_XS = 23,
+};
+
+/* ---- context (replaces ziggy_metal_create_context / destroy, bridge.h:34-42) ---- */
+int ziggy_hip_create_context(int device_index, ZiggyHipContext **out_ctx, ZiggyHipDeviceInfo *out_info,
+                             char *error_message, size_t error_message_len);
+void ziggy_hip_destroy_context(ZiggyHipContext *ctx);
+
+/* ---- buffers (replace bridge.h:44-77) ---- */
+int ziggy_hip_create_buffer(ZiggyHipContext *ctx, const void *bytes, size_t length, ZiggyHipBuffer **out_buffer,
+                            char *error_message, size_t error_message_len);
+int ziggy_hip_create_empty_buffer(ZiggyHipContext *ctx, size_t length, ZiggyHipBuffer **out_buffer,
+                                  char *error_message, size_t error_message_len);
+void ziggy_hip_destroy_buffer(ZiggyHipBuffer *buffer);
+size_t ziggy_hip_buffer_length(const ZiggyHipBuffer *buffer);
+int ziggy_hip_write_buffer(ZiggyHipBuffer *buffer, const void *bytes, size_t length, size_t offset,
+                           char *error_message, size_t error_message_len);
+int ziggy_hip_read_buffer(const ZiggyHipBuffer *buffer, void *out_bytes, size_t length, size_t offset,
+                          char *error_message, size_t error_message_len);
+/* replaces ziggy_metal_copy_buffer_region (bridge.h:396-405) */
+int ziggy_hip_copy_buffer_region(ZiggyHipContext *ctx, const ZiggyHipBuffer *src, size_t src_offset,
+                                 ZiggyHipBuffer *dst, size_t dst_offset, size_t length, char *error_message,
+                                 size_t error_message_len);
+
+/* ---- sequences (replace bridge.h:497-514) ---- */
+int ziggy_hip_begin_sequence(ZiggyHipContext *ctx, char *error_message, size_t error_message_len);
+int ziggy_hip_commit_sequence(ZiggyHipContext *ctx, char *error_message, size_t error_message_len);
+int ziggy_hip_commit_sequence_timed(ZiggyHipContext *ctx, ZiggyHipCommitStats *out_stats, char *error_message,
+                                    size_t error_message_len);
+
+/* ---- dequant-matvec (replaces the ziggy_metal_run_matvec_{f32,q4k,q6k,q8_0,q3k}_f32
+ * {,_to_dst,_add} family, bridge.h:79-292).  One typed entry point:
+ *   output[output_offset_bytes/4 + r] (=|+=) dot(row r of matrix, input[0..cols))
+ * matrix rows start at matrix_offset bytes; add != 0 selects the _add variant. ---- */
+int ziggy_hip_run_matvec(ZiggyHipContext *ctx, uint32_t tensor_type, const ZiggyHipBuffer *matrix,
+                         size_t matrix_offset, const ZiggyHipBuffer *input, ZiggyHipBuffer *output,
+                         size_t output_offset_bytes, uint32_t rows, uint32_t cols, int add, char *error_message,
+                         size_t error_message_len);
+/* Named per-type wrappers with the reference's exact shapes (bridge.h:113-292). */
+#define ZIGGY_HIP_DECLARE_MATVEC(sfx)                                                                              \
+    int ziggy_hip_run_matvec_##sfx##_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *matrix,                        \
+                                         const ZiggyHipBuffer *input, ZiggyHipBuffer *output, uint32_t rows,         \
+                                         uint32_t cols, char *error_message, size_t error_message_len);              \
+    int ziggy_hip_run_matvec_##sfx##_f32_to_dst(ZiggyHipContext *ctx, const ZiggyHipBuffer *matrix,                 \
+                                                const ZiggyHipBuffer *input, ZiggyHipBuffer *output,                 \
+                                                size_t output_offset_bytes, uint32_t rows, uint32_t cols,            \
+                                                char *error_message, size_t error_message_len);                      \
+    int ziggy_hip_run_matvec_##sfx##_add_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *matrix,                    \
+                                             const ZiggyHipBuffer *input, ZiggyHipBuffer *output, uint32_t rows,     \
+                                             uint32_t cols, char *error_message, size_t error_message_len);
+ZIGGY_HIP_DECLARE_MATVEC(q4k)
+ZIGGY_HIP_DECLARE_MATVEC(q6k)
+ZIGGY_HIP_DECLARE_MATVEC(q8_0)
+ZIGGY_HIP_DECLARE_MATVEC(q3k)
+ZIGGY_HIP_DECLARE_MATVEC(f16)
+ZIGGY_HIP_DECLARE_MATVEC(dense)
+
+/* Fused SwiGLU + down projection + residual (replaces
+ * ziggy_metal_run_matvec_q4k_silu_down_add_f32, bridge.h:372-382; any type):
+ *   output[r] += dot(row r, silu(gate) * up). */
+int ziggy_hip_run_matvec_silu_down_add(ZiggyHipContext *ctx, uint32_t tensor_type, const ZiggyHipBuffer *matrix,
+                                       const ZiggyHipBuffer *gate, const ZiggyHipBuffer *up,
+                                       ZiggyHipBuffer *output, uint32_t rows, uint32_t cols, char *error_message,
+                                       size_t error_message_len);
+int ziggy_hip_run_matvec_q4k_silu_down_add_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *matrix,
+                                               const ZiggyHipBuffer *gate, const ZiggyHipBuffer *up,
+                                               ZiggyHipBuffer *output, uint32_t rows, uint32_t cols,
+                                               char *error_message, size_t error_message_len);
+
+/* Fused matvec + greedy argmax (replaces ziggy_metal_run_matvec_q6k_argmax_f32,
+ * bridge.h:215-224).  output_state is 2 x u32: {ordered logit bits, token};
+ * initialise it to {0, 0xFFFFFFFF} (the reference's convention); ties resolve
+ * to the lowest token. */
+int ziggy_hip_run_matvec_argmax(ZiggyHipContext *ctx, uint32_t tensor_type, const ZiggyHipBuffer *matrix,
+                                const ZiggyHipBuffer *input, ZiggyHipBuffer *output_state, uint32_t rows,
+                                uint32_t cols, char *error_message, size_t error_message_len);
+int ziggy_hip_run_matvec_q6k_argmax_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *matrix,
+                                        const ZiggyHipBuffer *input, ZiggyHipBuffer *output_state, uint32_t rows,
+                                        uint32_t cols, char *error_message, size_t error_message_len);
+
+/* Bit-exact block decode of `rows` rows to f32 (debug/parity entry; the
+ * reference's counterpart is the CPU dequantizeRow, model/loader.zig:3428-3459). */
+int ziggy_hip_dequantize_rows(ZiggyHipContext *ctx, uint32_t tensor_type, const ZiggyHipBuffer *matrix,
+                              size_t matrix_offset, ZiggyHipBuffer *output, uint32_t rows, uint32_t cols,
+                              char *error_message, size_t error_message_len);
+
+/* ---- expert-indexed matvec (replace bridge.h:294-336, 701-757).  The expert id
+ * is entries[slot_idx].token_id of a ShortlistEntry{u32, f32} array; rows
+ * are offset by expert_id * rows_per_expert. ---- */
+int ziggy_hip_indexed_matvec(ZiggyHipContext *ctx, uint32_t tensor_type, const ZiggyHipBuffer *matrix,
+                             const ZiggyHipBuffer *input, ZiggyHipBuffer *output, uint32_t rows, uint32_t cols,
+                             const ZiggyHipBuffer *entries, uint32_t slot_idx, uint32_t rows_per_expert,
+                             int add_weighted, char *error_message, size_t error_message_len);
+int ziggy_hip_dual_indexed_matvec(ZiggyHipContext *ctx, uint32_t tensor_type, const ZiggyHipBuffer *matrix_a,
+                                  const ZiggyHipBuffer *matrix_b, const ZiggyHipBuffer *input,
+                                  ZiggyHipBuffer *output_a, ZiggyHipBuffer *output_b, uint32_t rows, uint32_t cols,
+                                  const ZiggyHipBuffer *entries, uint32_t slot_idx, uint32_t rows_per_expert,
+                                  char *error_message, size_t error_message_len);
+int ziggy_hip_indexed_matvec_iq4_xs_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *matrix,
+                                        const ZiggyHipBuffer *input, ZiggyHipBuffer *output, uint32_t rows,
+                                        uint32_t cols, const ZiggyHipBuffer *entries, uint32_t slot_idx,
+                                        uint32_t rows_per_expert, char *error_message, size_t error_message_len);
+int ziggy_hip_indexed_matvec_iq4_xs_add_weighted_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *matrix,
+                                                     const ZiggyHipBuffer *input, ZiggyHipBuffer *output,
+                                                     uint32_t rows, uint32_t cols, const ZiggyHipBuffer *entries,
+                                                     uint32_t slot_idx, uint32_t rows_per_expert,
+                                                     char *error_message, size_t error_message_len);
+int ziggy_hip_indexed_matvec_q3k_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *matrix,
+                                     const ZiggyHipBuffer *input, ZiggyHipBuffer *output, uint32_t rows,
+                                     uint32_t cols, const ZiggyHipBuffer *entries, uint32_t slot_idx,
+                                     uint32_t rows_per_expert, char *error_message, size_t error_message_len);
+int ziggy_hip_dual_indexed_matvec_q3k_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *matrix_a,
+                                          const ZiggyHipBuffer *matrix_b, const ZiggyHipBuffer *input,
+                                          ZiggyHipBuffer *output_a, ZiggyHipBuffer *output_b, uint32_t rows,
+                                          uint32_t cols, const ZiggyHipBuffer *entries, uint32_t slot_idx,
+                                          uint32_t rows_per_expert, char *error_message,
+                                          size_t error_message_len);
+int ziggy_hip_indexed_matvec_q3k_add_weighted_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *matrix,
+                                                  const ZiggyHipBuffer *input, ZiggyHipBuffer *output,
+                                                  uint32_t rows, uint32_t cols, const ZiggyHipBuffer *entries,
+                                                  uint32_t slot_idx, uint32_t rows_per_expert,
+                                                  char *error_message, size_t error_message_len);
+
+/* ---- elementwise / attention (replace bridge.h:407-620) ---- */
+int ziggy_hip_apply_rope_f32(ZiggyHipContext *ctx, ZiggyHipBuffer *vector, uint32_t head_count, uint32_t head_dim,
+                             uint32_t rope_dim, uint32_t position, float freq_base, uint32_t rope_style,
+                             char *error_message, size_t error_message_len);
+int ziggy_hip_apply_rope_at_offset_f32(ZiggyHipContext *ctx, ZiggyHipBuffer *vector, size_t vector_offset_bytes,
+                                       uint32_t head_count, uint32_t head_dim, uint32_t rope_dim, uint32_t position,
+                                       float freq_base, uint32_t rope_style, char *error_message,
+                                       size_t error_message_len);
+int ziggy_hip_apply_rope_to_dst_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *src, ZiggyHipBuffer *dst,
+                                    size_t dst_offset_bytes, uint32_t head_count, uint32_t head_dim,
+                                    uint32_t rope_dim, uint32_t position, float freq_base, uint32_t rope_style,
+                                    char *error_message, size_t error_message_len);
+int ziggy_hip_store_kv_half(ZiggyHipContext *ctx, const ZiggyHipBuffer *src, ZiggyHipBuffer *dst,
+                            size_t dst_offset_elements, uint32_t count, char *error_message,
+                            size_t error_message_len);
+/* GQA decode attention over the binary16 cache; split-K flash decoding with a
+ * merge pass (replaces ziggy_metal_attention_fused_f32, bridge.h:459-477).
+ * softcap must be 0 (softcapping belongs to Gemma, outside this path). */
+int ziggy_hip_attention_fused_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *q, const ZiggyHipBuffer *k_cache,
+                                  const ZiggyHipBuffer *v_cache, ZiggyHipBuffer *output, uint32_t head_count,
+                                  uint32_t head_count_kv, uint32_t head_dim, uint32_t kv_dim,
+                                  uint32_t context_length, uint32_t position, uint32_t layer_base,
+                                  uint32_t window_start, float scale, float softcap, char *error_message,
+                                  size_t error_message_len);
+int ziggy_hip_silu_mul_f32(ZiggyHipContext *ctx, ZiggyHipBuffer *gate, const ZiggyHipBuffer *up, uint32_t count,
+                           char *error_message, size_t error_message_len);
+int ziggy_hip_add_in_place_f32(ZiggyHipContext *ctx, ZiggyHipBuffer *dst, const ZiggyHipBuffer *src,
+                               uint32_t count, char *error_message, size_t error_message_len);
+int ziggy_hip_add_bias_f32(ZiggyHipContext *ctx, ZiggyHipBuffer *dst, const ZiggyHipBuffer *bias, uint32_t count,
+                           char *error_message, size_t error_message_len);
+int ziggy_hip_rms_norm_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *input, const ZiggyHipBuffer *weights,
+                           ZiggyHipBuffer *output, uint32_t count, float eps, float weight_offset,
+                           char *error_message, size_t error_message_len);
+int ziggy_hip_rms_norm_per_head_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *input,
+                                    const ZiggyHipBuffer *weights, ZiggyHipBuffer *output, uint32_t head_count,
+                                    uint32_t head_dim, float eps, float weight_offset, char *error_message,
+                                    size_t error_message_len);
+int ziggy_hip_argmax_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *input, ZiggyHipBuffer *output_token,
+                         uint32_t count, char *error_message, size_t error_message_len);
+/* Top-k (k <= 64) as ShortlistEntry{u32 id, f32 score}, descending, ties to the
+ * lower index (replaces ziggy_metal_topk_f32, bridge.h:568-576). */
+int ziggy_hip_topk_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *input, ZiggyHipBuffer *output_entries,
+                       uint32_t count, uint32_t top_k, char *error_message, size_t error_message_len);
+int ziggy_hip_normalize_topk_f32(ZiggyHipContext *ctx, ZiggyHipBuffer *entries, uint32_t top_k,
+                                 bool apply_softmax, bool normalize_weights, float scale, char *error_message,
+                                 size_t error_message_len);
+int ziggy_hip_weighted_sum_topk_f32(ZiggyHipContext *ctx, ZiggyHipBuffer *dst, const ZiggyHipBuffer *src,
+                                    const ZiggyHipBuffer *entries, uint32_t count, uint32_t slot_idx,
+                                    char *error_message, size_t error_message_len);
+int ziggy_hip_sigmoid_scale_add_f32(ZiggyHipContext *ctx, ZiggyHipBuffer *dst, const ZiggyHipBuffer *src,
+                                    const ZiggyHipBuffer *scalar, uint32_t count, char *error_message,
+                                    size_t error_message_len);
+
+/* ---- decode session (replaces the Zig gpu.Session, runtime/gpu/session.zig:27-651,
+ * which drives the entry points above one dispatch at a time).  The session
+ * uploads the weights once (DenseTensorStore.prewarm,
+ * runtime/gpu/metal/tensor_store.zig:112-144), owns the binary16 KV cache and
+ * runs one decode step as a single captured HIP graph of fused kernels. ---- */
+
+/* One tensor as the loader sees it (gpu/types.zig:22-27): raw GGUF bytes on the
+ * host, row length (dims[0]) and row count. */
+typedef struct {
+    const void *data;   /* NULL = absent */
+    uint64_t rows;
+    uint64_t cols;
+    uint32_t tensor_type;
+    uint32_t reserved;
+} ZiggyHipTensorDesc;
+
+/* Per-layer tensors (gpu/types.zig:48-67; the Gemma/Qwen3.5-only fields are omitted). */
+typedef struct {
+    ZiggyHipTensorDesc attn_norm, attn_q, attn_k, attn_v, attn_output;
+    ZiggyHipTensorDesc attn_q_bias, attn_k_bias, attn_v_bias, attn_q_norm, attn_k_norm;
+    ZiggyHipTensorDesc ffn_norm, ffn_gate, ffn_up, ffn_down;
+} ZiggyHipLayerDesc;
+
+/* Model hyperparameters (gpu/types.zig:69-112, subset on this path). */
+typedef struct {
+    uint32_t embedding_length, block_count, context_length, feed_forward_length;
+    uint32_t head_count, head_count_kv, head_dim, rope_dim;
+    uint32_t vocab_size, rope_style; /* 0 = interleaved pairs, 1 = NeoX halves */
+    float rms_norm_eps, rope_freq_base;
+} ZiggyHipModelDesc;
+
+typedef struct {
+    uint64_t steps;
+    uint64_t gpu_elapsed_ns;   /* HIP events around the decode steps */
+    uint64_t wall_ns;          /* host clock around the decode steps */
+    uint32_t next_token;       /* greedy token of the last step (not emitted) */
+    uint32_t reserved;
+} ZiggyHipGenerateStats;
+
+/* Kernels of one decode step, for ziggy_hip_session_time_kernel. */
+enum {
+    ZIGGY_HIP_KERNEL_QKV = 0,      /* fused RMSNorm + q/k/v projections */
+    ZIGGY_HIP_KERNEL_ROPE_KV = 1,  /* bias, QK-norm, RoPE, binary16 K/V store */
+    ZIGGY_HIP_KERNEL_ATTENTION = 2,/* split-K partials + merge */
+    ZIGGY_HIP_KERNEL_O_PROJ = 3,   /* output projection + residual */
+    ZIGGY_HIP_KERNEL_GATE_UP = 4,  /* fused RMSNorm + gate/up + SiLU(gate) * up */
+    ZIGGY_HIP_KERNEL_DOWN = 5,     /* down projection + residual */
+    ZIGGY_HIP_KERNEL_OUTPUT = 6,   /* fused RMSNorm + output head + argmax */
+};
+
+int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *model,
+                             const ZiggyHipTensorDesc *token_embd, const ZiggyHipTensorDesc *output_norm,
+                             const ZiggyHipTensorDesc *output, const ZiggyHipLayerDesc *layers,
+                             ZiggyHipSession **out_session, char *error_message, size_t error_message_len);
+void ziggy_hip_session_destroy(ZiggyHipSession *session);
+/* Clears the cache and the position (ReusableSession.reset, model/loader.zig:857-868). */
+int ziggy_hip_session_reset(ZiggyHipSession *session, char *error_message, size_t error_message_len);
+uint32_t ziggy_hip_session_position(const ZiggyHipSession *session);
+
+/* Per-layer contract of gpu.Session (session.zig:258-261, 339-513, 615-651): the
+ * host computes the embedding and drives the layers one call at a time. */
+int ziggy_hip_session_begin_token(ZiggyHipSession *session, const float *hidden, char *error_message,
+                                  size_t error_message_len);
+int ziggy_hip_session_run_attention_block(ZiggyHipSession *session, uint32_t layer_index, uint32_t position,
+                                          char *error_message, size_t error_message_len);
+int ziggy_hip_session_run_ffn_block(ZiggyHipSession *session, uint32_t layer_index, char *error_message,
+                                    size_t error_message_len);
+int ziggy_hip_session_run_output(ZiggyHipSession *session, float *logits, char *error_message,
+                                 size_t error_message_len);
+int ziggy_hip_session_run_output_argmax(ZiggyHipSession *session, uint32_t *out_token, char *error_message,
+                                        size_t error_message_len);
+int ziggy_hip_session_read_hidden(ZiggyHipSession *session, float *out, char *error_message,
+                                  size_t error_message_len);
+int ziggy_hip_session_write_hidden(ZiggyHipSession *session, const float *values, char *error_message,
+                                   size_t error_message_len);
+/* Reads back K and V of one cache row (binary16 widened to f32). */
+int ziggy_hip_session_read_kv(ZiggyHipSession *session, uint32_t layer, uint32_t position, float *k_out,
+                              float *v_out, char *error_message, size_t error_message_len);
+
+/* One whole greedy step (Session.stepGreedy, model/loader.zig:1080-1099) as one
+ * graph launch: embedding gather on the device, every layer, final norm,
+ * output projection fused with argmax.  Advances the position by one. */
+int ziggy_hip_session_step_greedy(ZiggyHipSession *session, uint32_t token, uint32_t *out_next,
+                                  char *error_message, size_t error_message_len);
+/* Session.stepNoOutput (model/loader.zig:1100-1109): a step without the output head. */
+int ziggy_hip_session_step_no_output(ZiggyHipSession *session, uint32_t token, char *error_message,
+                                     size_t error_message_len);
+/* Device-resident greedy generation (generateLoadedStreaming's greedy loop,
+ * model/loader.zig:2065-2279): the prompt is consumed token by token, then
+ * `steps` tokens are generated with every token fed back on the device;
+ * replays of one step graph are queued back to back.  out_tokens receives
+ * the generated ids.  EOS is not checked (the benchmark configurations
+ * disable it). */
+int ziggy_hip_session_generate(ZiggyHipSession *session, const uint32_t *prompt, uint32_t prompt_len,
+                               uint32_t steps, uint32_t *out_tokens, ZiggyHipGenerateStats *stats,
+                               char *error_message, size_t error_message_len);
+/* Logits of the most recent step that ran the output head (f32, vocab_size). */
+int ziggy_hip_session_read_logits(ZiggyHipSession *session, float *out, char *error_message,
+                                  size_t error_message_len);
+
+/* Times one kernel of the decode step (no counterpart in the reference; its
+ * Metal profiler times host-side encode, runtime/metal_profile.zig:80-315):
+ * `iterations` launches at the session's current position, rotating over the
+ * layers so successive launches read distinct weights from HBM; each launch
+ * is bracketed by its own HIP events on the session stream.  Reports the
+ * mean launch duration and the algorithmic bytes one launch streams
+ * (weights + binary16 KV; activations excluded).  Leaves the KV cache and
+ * position as they were, but overwrites the hidden state. */
+int ziggy_hip_session_time_kernel(ZiggyHipSession *session, uint32_t kernel, uint32_t iterations,
+                                  uint64_t *avg_ns, uint64_t *bytes_per_launch, char *error_message,
+                                  size_t error_message_len);
+
+/* Library build tag, for logs. */
+const char *ziggy_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,148 @@
+// zh_internal.h -- host-side internals of libziggy_hip: context, buffers,
+// status/error plumbing and the launcher interface between the C ABI and the
+// kernels.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "ziggy_hip.h"
+
+struct ZiggyHipContext {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool seq_open = false;
+    hipEvent_t seq_begin = nullptr, seq_end = nullptr;
+    ZiggyHipDeviceInfo info{};
+    // device scratch shared by the primitive ops (attention partials, argmax slot)
+    void *scratch = nullptr;
+    size_t scratch_len = 0;
+};
+
+struct ZiggyHipBuffer {
+    ZiggyHipContext *ctx = nullptr;
+    int device = 0;  // destroy needs only this, so a buffer may outlive its context
+    void *ptr = nullptr;
+    size_t len = 0;
+};
+
+namespace zh {
+
+inline void set_err(char *err, size_t len, const char *fmt, ...) {
+    if (!err || len == 0) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, len, fmt, ap);
+    va_end(ap);
+    err[len - 1] = 0;
+}
+
+inline int hip_fail(hipError_t e, const char *what, char *err, size_t len) {
+    set_err(err, len, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+    return ZIGGY_HIP_EXECUTION_FAILED;
+}
+
+#define ZH_TRY(call, what)                                          \
+    do {                                                            \
+        hipError_t _e = (call);                                     \
+        if (_e != hipSuccess) return zh::hip_fail(_e, what, err, err_len); \
+    } while (0)
+
+// Completes an op: synchronous unless a sequence is open (bridge.m:448-485).
+inline int finish_op(ZiggyHipContext *ctx, const char *what, char *err, size_t err_len) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, what, err, err_len);
+    if (!ctx->seq_open) {
+        e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return hip_fail(e, what, err, err_len);
+    }
+    return ZIGGY_HIP_OK;
+}
+
+inline bool buf_ok(const ZiggyHipBuffer *b, size_t need) { return b && b->ptr && b->len >= need; }
+
+// ---------------- kernel launchers (implemented in the .hip files) ----------------
+
+enum InMode : int { IN_PLAIN = 0, IN_NORM = 1, IN_SILU = 2 };
+enum OutMode : int { OUT_STORE = 0, OUT_ADD = 1, OUT_SWIGLU = 2, OUT_ARGMAX = 3, OUT_WADD = 4 };
+
+struct MvSeg {
+    const uint8_t *w;       // first row of the segment
+    uint64_t stride;        // bytes per row
+    float *y;               // output (STORE/ADD/SWIGLU/ARGMAX logits; may be null for ARGMAX)
+    const uint8_t *w2;      // SWIGLU: the "up" matrix (same format/shape as w)
+    int rows;
+    int fmt;
+    int wg_begin;           // first workgroup of this segment
+    int rows_per_wg;
+};
+
+struct MvParams {
+    MvSeg seg[4];
+    int nseg;
+    int cols;
+    int slots;              // cols / 64
+    int team;               // lanes per row team (power of two, <= 256)
+    int rows_per_team;
+    const float *x;         // PLAIN: input; NORM: hidden to normalise; SILU: gate
+    const float *x2;        // SILU: up
+    const float *norm_w;    // NORM: f32 weights
+    float eps;
+    unsigned long long *argmax_slot;  // ARGMAX: packed (ordered value << 32 | ~row)
+    const uint32_t *expert;           // indexed: entries (ShortlistEntry) + slot
+    int expert_slot;
+    int rows_per_expert;
+    int expert_limit;                 // expert ids >= this are ignored (no rows are read)
+    float weight_scale;               // WADD: y += scale * dot (scale from entries if expert set)
+    const int *gate_flag;             // optional device flag: kernel exits if *gate_flag == 0
+};
+
+// Builds the launch plan (team size, rows per team, workgroup ranges) and launches.
+hipError_t launch_matvec(const MvParams &p, int in_mode, int out_mode, hipStream_t s);
+void plan_matvec(MvParams &p, int target_wgs);
+
+hipError_t launch_dequant(int fmt, const uint8_t *w, uint64_t stride, float *out, int rows, int cols,
+                          hipStream_t s);
+
+// small ops (zh_ops.hip)
+hipError_t launch_rms_norm(const float *x, const float *w, float *out, int n, float eps, float off, hipStream_t s);
+hipError_t launch_rms_norm_per_head(const float *x, const float *w, float *out, int heads, int hd, float eps,
+                                    float off, hipStream_t s);
+hipError_t launch_rope(const float *src, float *dst, int heads, int hd, int rope_dim, int pos, float base,
+                       int style, hipStream_t s);
+hipError_t launch_store_kv_half(const float *src, __half *dst, int count, hipStream_t s);
+hipError_t launch_silu_mul(float *gate, const float *up, int n, hipStream_t s);
+hipError_t launch_add(float *dst, const float *src, int n, hipStream_t s);
+hipError_t launch_argmax(const float *x, int n, uint32_t *out_token, unsigned long long *tmp, hipStream_t s);
+hipError_t launch_topk(const float *x, int n, int k, void *entries, hipStream_t s);
+hipError_t launch_normalize_topk(void *entries, int k, int softmax, int normalize, float scale, hipStream_t s);
+hipError_t launch_weighted_sum_topk(float *dst, const float *src, const void *entries, int n, int slot,
+                                    hipStream_t s);
+hipError_t launch_sigmoid_scale_add(float *dst, const float *src, const float *scalar, int n, hipStream_t s);
+hipError_t launch_argmax_finalize(const unsigned long long *slot, uint32_t *state, hipStream_t s);
+hipError_t launch_fill_u64(unsigned long long *p, unsigned long long v, int n, hipStream_t s);
+
+// attention (zh_attn.hip)
+struct AttnParams {
+    const float *q;            // [head_count * head_dim]
+    const __half *k_cache;     // layer base applied: [ctx][kv_dim]
+    const __half *v_cache;
+    float *out;                // [head_count * head_dim]
+    float *part_o;             // [kv_heads][max_splits][group][head_dim]
+    float *part_ml;            // [kv_heads][max_splits][group][2]
+    int head_count, head_count_kv, head_dim, kv_dim;
+    int position;              // attend to [window_start, position]
+    const int *position_dev;   // if set, position is read from device memory (graph replay)
+    int window_start;
+    float scale;
+    int chunk;                 // positions per split
+    int max_splits;
+};
+hipError_t launch_attention(const AttnParams &p, hipStream_t s);
+size_t attention_scratch_floats(int head_count, int head_dim, int max_splits);
+
+}  // namespace zh

@@ -1,0 +1,316 @@
+// zh_matvec.hip -- batch-1 dequant-matvec kernels for gfx950.
+//
+// Design (bandwidth-bound, VALU co-limited for Q4_K):
+//   * A row is processed by a "team" of T lanes (T = next power of two of
+//     cols/64, at most 256); lane j owns weight slot j (64 weights) of every
+//     row the team visits, so its 64 activations are loaded (and normalised /
+//     SiLU-gated when fused) once per workgroup and stay in VGPRs.
+//   * Quant blocks are read in their native GGUF layout with 16-byte loads;
+//     scales are unpacked in registers (zh_quant.h).
+//   * Team partial sums are reduced with cross-lane shuffles; teams wider than
+//     a wavefront finish the reduction through LDS.
+//   * Epilogues: store, residual add, SwiGLU pair (silu(gate) * up from two
+//     matrices sharing the staged input), greedy argmax (packed 64-bit
+//     atomicMax, ties to the lowest row), expert-weighted add.
+//   * Input prologues: plain, fused RMSNorm (each workgroup recomputes the
+//     1/rms scale; rmsNorm order (scale * x) * w as model/loader.zig:3404-3426),
+//     fused SiLU(gate) * up (the silu_down path, matvec.metal:2229-2300).
+#include "zh_internal.h"
+#include "zh_quant.h"
+
+namespace zh {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float wave_sum(float v, int width) {
+    for (int o = width >> 1; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Reduces v over a team of T lanes; valid result in every lane of the team
+// for T <= 64, in lane 0 of the team for T > 64 (uses lds[4], two barriers).
+__device__ __forceinline__ float team_sum(float v, int T, float *lds) {
+    if (T <= 64) return wave_sum(v, T);
+    v = wave_sum(v, 64);
+    const int tid = threadIdx.x, wave = tid >> 6;
+    if ((tid & 63) == 0) lds[wave] = v;
+    __syncthreads();
+    const int per = T >> 6, first = (wave / per) * per;
+    float r = 0.f;
+    for (int i = 0; i < per; i++) r += lds[first + i];
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ uint32_t ordered_bits(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Workgroup-wide 1/sqrt(mean(x^2) + eps) (rmsNorm, model/loader.zig:3404-3426).
+__device__ float rms_scale(const float *__restrict__ x, int n, float eps, float *lds) {
+    float ss = 0.f;
+    for (int i = threadIdx.x * 4; i < n; i += kThreads * 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(x + i);
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+    }
+    ss = wave_sum(ss, 64);
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (lds[0] + lds[1]) + (lds[2] + lds[3]);
+    __syncthreads();
+    return 1.0f / sqrtf(tot / (float)n + eps);
+}
+
+template <int F, int IN>
+__device__ __forceinline__ void stage_x(XSlot &xs, int s, bool active, const MvParams &p, float nscale) {
+#pragma unroll
+    for (int w = 0; w < 4; w++) xs.sum[w] = 0.f;
+    if (!active) {
+#pragma unroll
+        for (int i = 0; i < 64; i++) xs.v[i] = 0.f;
+        return;
+    }
+    const int base = Geom<F>::x_base(s);
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const int o = base + w * Geom<F>::kXStride;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float4 a = *reinterpret_cast<const float4 *>(p.x + o + 4 * c);
+            float t[4] = {a.x, a.y, a.z, a.w};
+            if (IN == IN_NORM) {
+                const float4 nw = *reinterpret_cast<const float4 *>(p.norm_w + o + 4 * c);
+                const float ww[4] = {nw.x, nw.y, nw.z, nw.w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) t[k] = (nscale * t[k]) * ww[k];
+            } else if (IN == IN_SILU) {
+                const float4 u = *reinterpret_cast<const float4 *>(p.x2 + o + 4 * c);
+                const float uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) t[k] = (t[k] / (1.0f + expf(-t[k]))) * uu[k];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                xs.v[16 * w + 4 * c + k] = t[k];
+                xs.sum[w] += t[k];
+            }
+        }
+    }
+}
+
+template <int F, int IN, int OUT>
+__device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int wg_in_seg, float nscale, float *lds) {
+    const int tid = threadIdx.x, T = p.team, teams = kThreads / T;
+    const int team = tid / T, lane = tid % T;
+    const bool active = lane < p.slots;
+    XSlot xs;
+    stage_x<F, IN>(xs, lane, active, p, nscale);
+
+    const uint8_t *wbase = sg.w, *wbase2 = sg.w2;
+    float wscale = p.weight_scale;
+    bool skip = false;
+    if (p.expert) {
+        const uint32_t e = p.expert[2 * p.expert_slot];
+        skip = e >= (uint32_t)p.expert_limit;
+        const uint64_t off = (uint64_t)e * (uint64_t)p.rows_per_expert * sg.stride;
+        wbase += off;
+        if (wbase2) wbase2 += off;
+        wscale = __uint_as_float(p.expert[2 * p.expert_slot + 1]);
+    }
+    const int r_begin = wg_in_seg * sg.rows_per_wg;
+    const int r_end = min(r_begin + sg.rows_per_wg, sg.rows);
+    float best_v = -INFINITY;
+    int best_r = 0x7fffffff;
+    for (int it = 0; it < p.rows_per_team; ++it) {
+        const int r = r_begin + it * teams + team;
+        const bool valid = !skip && r < r_end;
+        float v = 0.f, v2 = 0.f;
+        if (valid && active) {
+            v = slot_dot<F>(wbase + (uint64_t)r * sg.stride, lane, xs);
+            if (OUT == OUT_SWIGLU) v2 = slot_dot<F>(wbase2 + (uint64_t)r * sg.stride, lane, xs);
+        }
+        v = team_sum(v, T, lds);
+        if (OUT == OUT_SWIGLU) v2 = team_sum(v2, T, lds);
+        if (valid && lane == 0) {
+            if (OUT == OUT_STORE) {
+                sg.y[r] = v;
+            } else if (OUT == OUT_ADD) {
+                sg.y[r] += v;
+            } else if (OUT == OUT_WADD) {
+                sg.y[r] = fmaf(v, wscale, sg.y[r]);
+            } else if (OUT == OUT_SWIGLU) {
+                sg.y[r] = (v / (1.0f + expf(-v))) * v2;  // siluInPlace then gate * up
+            } else if (OUT == OUT_ARGMAX) {
+                if (sg.y) sg.y[r] = v;
+                if (v > best_v || (v == best_v && r < best_r)) {
+                    best_v = v;
+                    best_r = r;
+                }
+            }
+        }
+    }
+    if (OUT == OUT_ARGMAX) {
+        __shared__ unsigned long long keys[kThreads];
+        unsigned long long key = 0ull;
+        if (lane == 0 && best_r != 0x7fffffff)
+            key = ((unsigned long long)ordered_bits(best_v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_r);
+        if (lane == 0) keys[team] = key;
+        __syncthreads();
+        if (tid == 0) {
+            unsigned long long k = keys[0];
+            for (int i = 1; i < teams; i++) k = keys[i] > k ? keys[i] : k;
+            if (k) atomicMax(p.argmax_slot, k);
+        }
+    }
+}
+
+template <int F1, int F2, int IN, int OUT>
+__global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
+    __shared__ float lds[8];
+    if (p.gate_flag && *p.gate_flag == 0) return;
+    const int wg = blockIdx.x;
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < 4; i++)
+        if (i < p.nseg && wg >= p.seg[i].wg_begin) si = i;
+    const MvSeg &sg = p.seg[si];
+    float nscale = 1.f;
+    if (IN == IN_NORM) nscale = rms_scale(p.x, p.cols, p.eps, lds);
+    if (F1 == F2 || sg.fmt == F1)
+        mv_body<F1, IN, OUT>(p, sg, wg - sg.wg_begin, nscale, lds);
+    else
+        mv_body<F2, IN, OUT>(p, sg, wg - sg.wg_begin, nscale, lds);
+}
+
+// ---------------- host-side planning and dispatch ----------------
+
+static int next_pow2(int v) {
+    int t = 1;
+    while (t < v) t <<= 1;
+    return t;
+}
+
+void plan_matvec(MvParams &p, int target_wgs) {
+    p.slots = p.cols / 64;
+    p.team = next_pow2(p.slots);
+    if (p.team > kThreads) p.team = kThreads;
+    const int teams = kThreads / p.team;
+    int total_rows = 0;
+    for (int i = 0; i < p.nseg; i++) total_rows += p.seg[i].rows;
+    int rpt = total_rows / (teams * (target_wgs > 0 ? target_wgs : 1024));
+    if (rpt < 1) rpt = 1;
+    if (rpt > 16) rpt = 16;
+    p.rows_per_team = rpt;
+    int wg = 0;
+    for (int i = 0; i < p.nseg; i++) {
+        p.seg[i].rows_per_wg = teams * rpt;
+        p.seg[i].wg_begin = wg;
+        wg += (p.seg[i].rows + teams * rpt - 1) / (teams * rpt);
+    }
+    for (int i = p.nseg; i < 4; i++) p.seg[i].wg_begin = 0x7fffffff;
+}
+
+static int total_wgs(const MvParams &p) {
+    int wg = 0;
+    for (int i = 0; i < p.nseg; i++) wg += (p.seg[i].rows + p.seg[i].rows_per_wg - 1) / p.seg[i].rows_per_wg;
+    return wg;
+}
+
+typedef void (*MvKernel)(MvParams);
+
+template <int F1, int F2> static MvKernel pick(int in, int out) {
+    if (in == IN_PLAIN && out == OUT_STORE) return mv_kernel<F1, F2, IN_PLAIN, OUT_STORE>;
+    if (in == IN_PLAIN && out == OUT_ADD) return mv_kernel<F1, F2, IN_PLAIN, OUT_ADD>;
+    if (in == IN_NORM && out == OUT_STORE) return mv_kernel<F1, F2, IN_NORM, OUT_STORE>;
+    if (in == IN_NORM && out == OUT_SWIGLU) return mv_kernel<F1, F2, IN_NORM, OUT_SWIGLU>;
+    if (in == IN_PLAIN && out == OUT_SWIGLU) return mv_kernel<F1, F2, IN_PLAIN, OUT_SWIGLU>;
+    if (in == IN_PLAIN && out == OUT_ARGMAX) return mv_kernel<F1, F2, IN_PLAIN, OUT_ARGMAX>;
+    if (in == IN_NORM && out == OUT_ARGMAX) return mv_kernel<F1, F2, IN_NORM, OUT_ARGMAX>;
+    if (in == IN_SILU && out == OUT_ADD) return mv_kernel<F1, F2, IN_SILU, OUT_ADD>;
+    if (in == IN_PLAIN && out == OUT_WADD) return mv_kernel<F1, F2, IN_PLAIN, OUT_WADD>;
+    return nullptr;
+}
+
+hipError_t launch_matvec(const MvParams &p, int in, int out, hipStream_t s) {
+    int f1 = p.seg[0].fmt, f2 = f1;
+    for (int i = 1; i < p.nseg; i++)
+        if (p.seg[i].fmt != f1) f2 = p.seg[i].fmt;
+    for (int i = 0; i < p.nseg; i++)
+        if (p.seg[i].fmt != f1 && p.seg[i].fmt != f2) return hipErrorInvalidValue;
+    MvKernel k = nullptr;
+    if (f1 == f2) {
+        switch (f1) {
+        case Q4_K: k = pick<Q4_K, Q4_K>(in, out); break;
+        case Q6_K: k = pick<Q6_K, Q6_K>(in, out); break;
+        case Q8_0: k = pick<Q8_0, Q8_0>(in, out); break;
+        case Q3_K: k = pick<Q3_K, Q3_K>(in, out); break;
+        case IQ4_XS: k = pick<IQ4_XS, IQ4_XS>(in, out); break;
+        case F16: k = pick<F16, F16>(in, out); break;
+        case F32: k = pick<F32, F32>(in, out); break;
+        default: break;
+        }
+    } else if (f1 == Q4_K && f2 == Q6_K && in == IN_NORM && out == OUT_STORE) {
+        k = mv_kernel<Q4_K, Q6_K, IN_NORM, OUT_STORE>;
+    } else if (f1 == Q6_K && f2 == Q4_K && in == IN_NORM && out == OUT_STORE) {
+        k = mv_kernel<Q6_K, Q4_K, IN_NORM, OUT_STORE>;
+    }
+    if (!k) return hipErrorInvalidValue;
+    const int grid = total_wgs(p);
+    if (grid <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), 0, s, p);
+    return hipGetLastError();
+}
+
+// ---------------- bit-exact dequant (one thread per block) ----------------
+
+template <int F>
+__global__ void dequant_kernel(const uint8_t *__restrict__ w, uint64_t stride, float *__restrict__ out, int rows,
+                               int cols) {
+    constexpr int V = Geom<F>::kValues, B = Geom<F>::kBytes;
+    const int blocks_per_row = cols / V;
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)rows * blocks_per_row) return;
+    const int r = (int)(i / blocks_per_row), b = (int)(i % blocks_per_row);
+    dequant_block<F>(w + (uint64_t)r * stride + (uint64_t)b * B, out + (uint64_t)r * cols + (uint64_t)b * V);
+}
+
+__global__ void dequant_dense_kernel(const uint8_t *__restrict__ w, uint64_t stride, float *__restrict__ out,
+                                     int rows, int cols, int is_f16) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)rows * cols) return;
+    const int r = (int)(i / cols), c = (int)(i % cols);
+    const uint8_t *row = w + (uint64_t)r * stride;
+    out[i] = is_f16 ? h2f(ld2(row + 2 * c)) : __uint_as_float(ld4(row + 4 * c));
+}
+
+hipError_t launch_dequant(int fmt, const uint8_t *w, uint64_t stride, float *out, int rows, int cols, hipStream_t s) {
+    auto go = [&](auto kern, int values) {
+        const long long n = (long long)rows * (cols / values);
+        const int grid = (int)((n + 255) / 256);
+        if (grid > 0) hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, s, w, stride, out, rows, cols);
+        return hipGetLastError();
+    };
+    switch (fmt) {
+    case Q4_K: return go(dequant_kernel<Q4_K>, 256);
+    case Q6_K: return go(dequant_kernel<Q6_K>, 256);
+    case Q8_0: return go(dequant_kernel<Q8_0>, 32);
+    case Q3_K: return go(dequant_kernel<Q3_K>, 256);
+    case IQ4_XS: return go(dequant_kernel<IQ4_XS>, 256);
+    case F16:
+    case F32: {
+        const long long n = (long long)rows * cols;
+        const int grid = (int)((n + 255) / 256);
+        if (grid > 0)
+            hipLaunchKernelGGL(dequant_dense_kernel, dim3(grid), dim3(256), 0, s, w, stride, out, rows, cols,
+                               fmt == F16 ? 1 : 0);
+        return hipGetLastError();
+    }
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace zh

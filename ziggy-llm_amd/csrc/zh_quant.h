@@ -1,0 +1,409 @@
+// zh_quant.h -- device-side GGUF block decoders for gfx950.
+//
+// Every format is processed in "slots" of 64 weights of one row.  A lane owns
+// one slot for every row it visits, so its 64 activation values stay in VGPRs
+// across rows.  The 64 values of a slot always come as 4 runs of 16
+// contiguous activations: run w starts at x_base(slot) + w * x_stride.
+//
+// Block layouts and value formulas follow the reference decoders:
+//   Q4_K  model/loader.zig:3647-3726, getScaleMinK4 :3814-3825
+//   Q6_K  model/loader.zig:3728-3812
+//   Q8_0  model/loader.zig:3589-3617
+//   Q3_K  model/quant_extra.zig:45-126, expandQ3KScales :248-279
+//   IQ4_XS model/quant_extra.zig:191-246, kvalues_iq4nl :8
+// The matvec dots factor the per-block scales out of the 16/32-value sums
+// (as the reference's own dotQ4KRow / dotQ6KRow do); unsigned-offset
+// encodings (Q6_K q+32, Q3_K q+4) are corrected with per-run activation sums.
+// The dequant_* functions reproduce the reference's exact binary32 operation
+// order (no contraction) and are bit-exact with the CPU decoder.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace zh {
+
+enum Fmt : int { F32 = 0, F16 = 1, Q8_0 = 8, Q3_K = 11, Q4_K = 12, Q6_K = 14, IQ4_XS = 23 };
+
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+__device__ __forceinline__ uint2 ld8(const uint8_t *p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+__device__ __forceinline__ uint32_t ld4(const uint8_t *p) {
+    uint32_t v;
+    __builtin_memcpy(&v, p, 4);
+    return v;
+}
+__device__ __forceinline__ uint32_t ld2(const uint8_t *p) {
+    uint16_t v;
+    __builtin_memcpy(&v, p, 2);
+    return v;
+}
+// binary16 bits -> f32 (exact, subnormals included)
+__device__ __forceinline__ float h2f(uint32_t bits) { return __half2float(__ushort_as_half((unsigned short)(bits & 0xFFFFu))); }
+// unsigned byte k of w as f32 (v_cvt_f32_ubyteK)
+__device__ __forceinline__ float ub(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xFFu); }
+__device__ __forceinline__ float sb(uint32_t w, int k) { return (float)(int8_t)((w >> (8 * k)) & 0xFFu); }
+__device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t width) {
+    return __builtin_amdgcn_ubfe(v, off, width);
+}
+// Hides the known bits of v from the optimiser so byte extracts of a masked
+// word select v_cvt_f32_ubyte{1,2,3} directly instead of v_bfe + ubyte0.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
+template <int F> struct Geom;
+template <> struct Geom<Q4_K> {
+    static constexpr int kValues = 256, kBytes = 144, kSlotsPerBlock = 4;
+    __device__ static int x_base(int s) { return (s >> 2) * 256 + (s & 3) * 64; }
+    static constexpr int kXStride = 16;
+};
+template <> struct Geom<Q6_K> {
+    static constexpr int kValues = 256, kBytes = 210, kSlotsPerBlock = 4;
+    __device__ static int x_base(int s) { return (s >> 2) * 256 + ((s >> 1) & 1) * 128 + (s & 1) * 16; }
+    static constexpr int kXStride = 32;
+};
+template <> struct Geom<Q3_K> {
+    static constexpr int kValues = 256, kBytes = 110, kSlotsPerBlock = 4;
+    __device__ static int x_base(int s) { return (s >> 2) * 256 + ((s >> 1) & 1) * 128 + (s & 1) * 16; }
+    static constexpr int kXStride = 32;
+};
+template <> struct Geom<IQ4_XS> {
+    static constexpr int kValues = 256, kBytes = 136, kSlotsPerBlock = 4;
+    __device__ static int x_base(int s) { return (s >> 2) * 256 + (s & 3) * 64; }
+    static constexpr int kXStride = 16;
+};
+template <> struct Geom<Q8_0> {
+    static constexpr int kValues = 32, kBytes = 34, kSlotsPerBlock = 1;  // a slot spans 2 blocks
+    __device__ static int x_base(int s) { return s * 64; }
+    static constexpr int kXStride = 16;
+};
+template <> struct Geom<F16> {
+    static constexpr int kValues = 1, kBytes = 2, kSlotsPerBlock = 1;
+    __device__ static int x_base(int s) { return s * 64; }
+    static constexpr int kXStride = 16;
+};
+template <> struct Geom<F32> {
+    static constexpr int kValues = 1, kBytes = 4, kSlotsPerBlock = 1;
+    __device__ static int x_base(int s) { return s * 64; }
+    static constexpr int kXStride = 16;
+};
+
+// The 64 activations a lane owns, plus per-run sums.
+struct XSlot {
+    float v[64];
+    float sum[4];
+};
+
+// ---------------- slot dots: dot(64 weights of slot s in `row`, xs) ----------------
+
+template <int F> __device__ __forceinline__ float slot_dot(const uint8_t *__restrict__ row, int s, const XSlot &xs);
+
+// Q4_K: slot = (block b, group g): 32 qs bytes -> sub-block 2g (low nibbles) and 2g+1 (high).
+template <> __device__ __forceinline__ float slot_dot<Q4_K>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+    const int g = s & 3;
+    const uint8_t *blk = row + (s >> 2) * 144;
+    const uint4 hd = ld16(blk);
+    const uint4 qa = ld16(blk + 16 + 32 * g);
+    const uint4 qb = ld16(blk + 32 + 32 * g);
+    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+    // getScaleMinK4 for j = 2g, 2g+1 with lane-uniform formulas
+    const bool lo = g < 2;
+    const uint32_t a_sc = lo ? hd.y : hd.w, a_m = lo ? hd.z : hd.w;
+    const uint32_t o0 = lo ? 16u * g : 16u * (g - 2), o1 = o0 + 8u;
+    const uint32_t wa = lo ? 6u : 4u, wb = lo ? 0u : 2u, om = lo ? 0u : 4u;
+    const uint32_t sc0 = bfe(a_sc, o0, wa) | (bfe(hd.y, o0 + 6, wb) << 4);
+    const uint32_t m0 = bfe(a_m, o0 + om, wa) | (bfe(hd.z, o0 + 6, wb) << 4);
+    const uint32_t sc1 = bfe(a_sc, o1, wa) | (bfe(hd.y, o1 + 6, wb) << 4);
+    const uint32_t m1 = bfe(a_m, o1 + om, wa) | (bfe(hd.z, o1 + 6, wb) << 4);
+    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    float dl = 0.f, dh = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        // high nibbles are converted in place as 16 * q (exact), undone by the 1/16 below
+        const uint32_t l4 = opaque(q[k] & 0x0F0F0F0Fu), h4 = opaque(q[k] & 0xF0F0F0F0u);
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            dl = fmaf(ub(l4, b), xs.v[4 * k + b], dl);
+            dh = fmaf(ub(h4, b), xs.v[32 + 4 * k + b], dh);
+        }
+    }
+    const float d1 = d * (float)sc0, mm1 = dmin * (float)m0, d2 = d * (float)sc1, mm2 = dmin * (float)m1;
+    float r = d1 * dl;
+    r = fmaf(-mm1, xs.sum[0] + xs.sum[1], r);
+    r = fmaf(d2, dh * 0.0625f, r);
+    r = fmaf(-mm2, xs.sum[2] + xs.sum[3], r);
+    return r;
+}
+
+// Q6_K: slot = (block b, half h, l0 in {0,16}): ql[64h+l0..], ql[64h+32+l0..], qh[32h+l0..].
+template <> __device__ __forceinline__ float slot_dot<Q6_K>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+    const uint8_t *blk = row + (s >> 2) * 210;
+    const int h = (s >> 1) & 1, l0 = (s & 1) * 16;
+    const uint4 qa = ld16(blk + 64 * h + l0);
+    const uint4 qb = ld16(blk + 64 * h + 32 + l0);
+    const uint4 qh = ld16(blk + 128 + 32 * h + l0);
+    const uint2 scw = ld8(blk + 192 + 8 * h);
+    const float d = h2f(ld2(blk + 208));
+    const int sb0 = s & 1;
+    const uint32_t a[4] = {qa.x, qa.y, qa.z, qa.w}, bq[4] = {qb.x, qb.y, qb.z, qb.w}, hh[4] = {qh.x, qh.y, qh.z, qh.w};
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t u0 = opaque((a[k] & 0x0F0F0F0Fu) | ((hh[k] & 0x03030303u) << 4));
+        const uint32_t u1 = opaque((bq[k] & 0x0F0F0F0Fu) | ((hh[k] & 0x0C0C0C0Cu) << 2));
+        const uint32_t u2 = opaque(((a[k] >> 4) & 0x0F0F0F0Fu) | (hh[k] & 0x30303030u));
+        const uint32_t u3 = opaque(((bq[k] >> 4) & 0x0F0F0F0Fu) | ((hh[k] >> 2) & 0x30303030u));
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            acc[0] = fmaf(ub(u0, b), xs.v[0 + 4 * k + b], acc[0]);
+            acc[1] = fmaf(ub(u1, b), xs.v[16 + 4 * k + b], acc[1]);
+            acc[2] = fmaf(ub(u2, b), xs.v[32 + 4 * k + b], acc[2]);
+            acc[3] = fmaf(ub(u3, b), xs.v[48 + 4 * k + b], acc[3]);
+        }
+    }
+    // sc[8h + l0/16 + 2w]: byte sb0 (+2) of scw.x (w = 0, 1) and scw.y (w = 2, 3)
+    const float s0 = d * sb(scw.x, sb0), s1 = d * sb(scw.x, sb0 + 2);
+    const float s2 = d * sb(scw.y, sb0), s3 = d * sb(scw.y, sb0 + 2);
+    float r = s0 * fmaf(-32.f, xs.sum[0], acc[0]);
+    r = fmaf(s1, fmaf(-32.f, xs.sum[1], acc[1]), r);
+    r = fmaf(s2, fmaf(-32.f, xs.sum[2], acc[2]), r);
+    r = fmaf(s3, fmaf(-32.f, xs.sum[3], acc[3]), r);
+    return r;
+}
+
+// Q8_0: slot = 2 consecutive 34-byte blocks (68 bytes, 4-byte aligned within a row).
+template <> __device__ __forceinline__ float slot_dot<Q8_0>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+    const uint8_t *p = row + 68 * s;
+    const uint4 a = ld16(p), b = ld16(p + 16), c = ld16(p + 32), e = ld16(p + 48);
+    const uint32_t f = ld4(p + 64);
+    const uint32_t w[17] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, e.x, e.y, e.z, e.w, f};
+    const float d0 = h2f(w[0]), d1 = h2f(w[8] >> 16);
+    // signed bytes read as unsigned q + 128 (xor 0x80); the 128 * sum(x) offset is removed below
+    uint32_t u[17];
+#pragma unroll
+    for (int k = 0; k < 17; k++) u[k] = opaque(w[k] ^ 0x80808080u);
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const int bi = 2 + i;  // block 0 quants start at byte 2
+        s0 = fmaf(ub(u[bi >> 2], bi & 3), xs.v[i], s0);
+        s1 = fmaf(ub(u[9 + (i >> 2)], i & 3), xs.v[32 + i], s1);
+    }
+    s0 = fmaf(-128.f, xs.sum[0] + xs.sum[1], s0);
+    s1 = fmaf(-128.f, xs.sum[2] + xs.sum[3], s1);
+    return fmaf(d1, s1, d0 * s0);
+}
+
+// Q3_K: slot = (block b, half h, 16-group sh): qs[32h+16sh..], hmask[16sh..], 4 shifts.
+template <> __device__ __forceinline__ float slot_dot<Q3_K>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+    const uint8_t *blk = row + (s >> 2) * 110;
+    const int h = (s >> 1) & 1, sh = s & 1;
+    const uint4 hm = ld16(blk + 16 * sh);
+    const uint4 qs = ld16(blk + 32 + 32 * h + 16 * sh);
+    const uint32_t r0 = ld4(blk + 96), r1 = ld4(blk + 100), r2 = ld4(blk + 104);
+    const float dall = h2f(ld2(blk + 108));
+    const uint32_t hmw[4] = {hm.x, hm.y, hm.z, hm.w}, qw[4] = {qs.x, qs.y, qs.z, qs.w};
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            // (q + 4) = low 2 bits | high-mask bit << 2, per byte
+            const uint32_t u =
+                opaque(((qw[k] >> (2 * j)) & 0x03030303u) | (((hmw[k] >> (4 * h + j)) & 0x01010101u) << 2));
+#pragma unroll
+            for (int b = 0; b < 4; b++) acc[j] = fmaf(ub(u, b), xs.v[16 * j + 4 * k + b], acc[j]);
+        }
+    }
+    float r = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        // scale index i = 8h + 2j + sh (expandQ3KScales)
+        const int i = 8 * h + 2 * j + sh, qd = i & 3, grp = i >> 2;
+        const uint32_t lowsrc = (grp & 1) ? r1 : r0;
+        const uint32_t low4 = bfe(lowsrc, 8 * qd + 4 * (grp >> 1), 4);
+        const uint32_t hi2 = bfe(r2, 8 * qd + 2 * grp, 2);
+        const float sc = (float)((int)(low4 | (hi2 << 4)) - 32);
+        r = fmaf(dall * sc, fmaf(-4.f, xs.sum[j], acc[j]), r);
+    }
+    return r;
+}
+
+__device__ __constant__ static const float kIq4nl[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
+                                                         1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
+
+// IQ4_XS: slot = (block b, sub-block pair k): sub-blocks 2k, 2k+1.
+template <> __device__ __forceinline__ float slot_dot<IQ4_XS>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+    const uint8_t *blk = row + (s >> 2) * 136;
+    const int k = s & 3;
+    const float d = h2f(ld2(blk));
+    const uint32_t sh = ld2(blk + 2), sl = blk[4 + k];
+    const uint4 q0 = ld16(blk + 8 + 32 * k), q1 = ld16(blk + 24 + 32 * k);
+    const uint32_t ls0 = (sl & 0xF) | (bfe(sh, 4 * k, 2) << 4), ls1 = (sl >> 4) | (bfe(sh, 4 * k + 2, 2) << 4);
+    const uint32_t w0[4] = {q0.x, q0.y, q0.z, q0.w}, w1[4] = {q1.x, q1.y, q1.z, q1.w};
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const uint32_t y0 = (w0[c] >> (8 * b)) & 0xFFu, y1 = (w1[c] >> (8 * b)) & 0xFFu;
+            a0 = fmaf(kIq4nl[y0 & 0xF], xs.v[4 * c + b], a0);
+            a0 = fmaf(kIq4nl[y0 >> 4], xs.v[16 + 4 * c + b], a0);
+            a1 = fmaf(kIq4nl[y1 & 0xF], xs.v[32 + 4 * c + b], a1);
+            a1 = fmaf(kIq4nl[y1 >> 4], xs.v[48 + 4 * c + b], a1);
+        }
+    }
+    return fmaf(d * (float)((int)ls1 - 32), a1, (d * (float)((int)ls0 - 32)) * a0);
+}
+
+template <> __device__ __forceinline__ float slot_dot<F16>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+    const uint8_t *p = row + 128 * s;
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        const uint4 v = ld16(p + 16 * c);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            acc = fmaf(h2f(w[k]), xs.v[8 * c + 2 * k], acc);
+            acc = fmaf(h2f(w[k] >> 16), xs.v[8 * c + 2 * k + 1], acc);
+        }
+    }
+    return acc;
+}
+
+template <> __device__ __forceinline__ float slot_dot<F32>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+    const uint8_t *p = row + 256 * s;
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; c++) {
+        const uint4 v = ld16(p + 16 * c);
+        acc = fmaf(__uint_as_float(v.x), xs.v[4 * c + 0], acc);
+        acc = fmaf(__uint_as_float(v.y), xs.v[4 * c + 1], acc);
+        acc = fmaf(__uint_as_float(v.z), xs.v[4 * c + 2], acc);
+        acc = fmaf(__uint_as_float(v.w), xs.v[4 * c + 3], acc);
+    }
+    return acc;
+}
+
+// ---------------- bit-exact block decode (reference operation order) ----------------
+
+#pragma clang fp contract(off)
+
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t *s, int &sc, int &m) {
+    if (j < 4) {
+        sc = s[j] & 63;
+        m = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+// Decodes the 256 (or 32 for Q8_0) values of one block into out[].
+template <int F> __device__ void dequant_block(const uint8_t *blk, float *out);
+
+template <> __device__ void dequant_block<Q4_K>(const uint8_t *blk, float *out) {
+    const float d = h2f(ld2(blk)), dmin = h2f(ld2(blk + 2));
+    const uint8_t *sc = blk + 4, *q = blk + 16;
+    for (int g = 0; g < 4; g++) {
+        int s0, m0, s1, m1;
+        scale_min_k4(2 * g, sc, s0, m0);
+        scale_min_k4(2 * g + 1, sc, s1, m1);
+        const float d1 = __fmul_rn(d, (float)s0), mm1 = __fmul_rn(dmin, (float)m0);
+        const float d2 = __fmul_rn(d, (float)s1), mm2 = __fmul_rn(dmin, (float)m1);
+        for (int l = 0; l < 32; l++) {
+            out[64 * g + l] = __fsub_rn(__fmul_rn(d1, (float)(q[l] & 0x0F)), mm1);
+            out[64 * g + 32 + l] = __fsub_rn(__fmul_rn(d2, (float)(q[l] >> 4)), mm2);
+        }
+        q += 32;
+    }
+}
+
+template <> __device__ void dequant_block<Q6_K>(const uint8_t *blk, float *out) {
+    const uint8_t *ql = blk, *qh = blk + 128, *sc = blk + 192;
+    const float d = h2f(ld2(blk + 208));
+    for (int half = 0; half < 2; half++) {
+        for (int l = 0; l < 32; l++) {
+            const int is = l / 16;
+            const int q1 = ((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+            const int q2 = ((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            const float a = d * (float)(int8_t)sc[is + 0], b = d * (float)(int8_t)sc[is + 2];
+            const float c = d * (float)(int8_t)sc[is + 4], e = d * (float)(int8_t)sc[is + 6];
+            out[l + 0] = a * (float)q1;
+            out[l + 32] = b * (float)q2;
+            out[l + 64] = c * (float)q3;
+            out[l + 96] = e * (float)q4;
+        }
+        out += 128;
+        ql += 64;
+        qh += 32;
+        sc += 8;
+    }
+}
+
+template <> __device__ void dequant_block<Q8_0>(const uint8_t *blk, float *out) {
+    const float d = h2f(ld2(blk));
+    for (int i = 0; i < 32; i++) out[i] = d * (float)(int8_t)blk[2 + i];
+}
+
+template <> __device__ void dequant_block<Q3_K>(const uint8_t *blk, float *out) {
+    const uint8_t *hm = blk, *qs = blk + 32, *raw = blk + 96;
+    const float dall = h2f(ld2(blk + 108));
+    int scv[16];
+    for (int i = 0; i < 16; i++) {
+        const int qd = i & 3, grp = i >> 2;
+        const int low4 = (raw[(grp & 1) * 4 + qd] >> (4 * (grp >> 1))) & 0xF;
+        const int hi2 = (raw[8 + qd] >> (2 * grp)) & 3;
+        scv[i] = (low4 | (hi2 << 4)) - 32;
+    }
+    int o = 0, si = 0;
+    uint8_t mask = 1;
+    for (int h = 0; h < 2; h++) {
+        int shift = 0;
+        for (int j = 0; j < 4; j++) {
+            for (int half16 = 0; half16 < 2; half16++) {
+                const float dl = dall * (float)scv[si++];
+                for (int l = 0; l < 16; l++) {
+                    const int idx = 32 * h + 16 * half16 + l;
+                    const int v = (int)((qs[idx] >> shift) & 3) - ((hm[16 * half16 + l] & mask) ? 0 : 4);
+                    out[o++] = dl * (float)v;
+                }
+            }
+            shift += 2;
+            mask = (uint8_t)(mask << 1);
+        }
+    }
+}
+
+template <> __device__ void dequant_block<IQ4_XS>(const uint8_t *blk, float *out) {
+    const float d = h2f(ld2(blk));
+    const uint32_t sh = ld2(blk + 2);
+    const uint8_t *qs = blk + 8;
+    for (int ib = 0; ib < 8; ib++) {
+        const int low = (blk[4 + ib / 2] >> (4 * (ib % 2))) & 0x0f;
+        const int high = (sh >> (2 * ib)) & 0x03;
+        const float dl = d * (float)((low | (high << 4)) - 32);
+        for (int j = 0; j < 16; j++) {
+            out[32 * ib + j] = dl * kIq4nl[qs[j] & 0x0f];
+            out[32 * ib + j + 16] = dl * kIq4nl[qs[j] >> 4];
+        }
+        qs += 16;
+    }
+}
+
+#pragma clang fp contract(on)
+
+}  // namespace zh

@@ -1,0 +1,688 @@
+// zh_session.cpp -- the HIP decode session: the MI355X counterpart of the Zig
+// gpu.Session (runtime/gpu/session.zig:27-651) plus a device-resident step.
+//
+// Weights are uploaded once into one HBM arena (raw GGUF bytes; f32 norm
+// vectors as-is), the binary16 KV cache is [layer][pos][kv_dim]
+// (session.zig:108-111, 382-383), and one decode step is:
+//   step_begin   token (host, prompt or previous argmax) -> embedding row
+//   per layer:   qkv       fused RMSNorm + q/k/v matvec (one launch, mixed formats)
+//                rope_kv   bias, QK-norm, RoPE, binary16 K/V store
+//                attention split-K partials + merge
+//                o_proj    matvec + residual add
+//                gate_up   fused RMSNorm + gate/up matvec + SiLU(gate) * up
+//                down      matvec + residual add
+//   output:      fused RMSNorm + output matvec + argmax (skipped on prompt steps)
+// The step is captured once into a HIP graph; position and token live in
+// device memory, so the same graph replays every step.
+#include <algorithm>
+#include <chrono>
+#include <new>
+#include <vector>
+
+#include "zh_internal.h"
+#include "zh_quant.h"
+#include "zh_step.h"
+
+using namespace zh;
+
+namespace {
+
+struct DT {
+    const uint8_t *p = nullptr;
+    uint64_t rows = 0, cols = 0, stride = 0;
+    int type = -1;
+    bool present = false;
+};
+
+struct LayerW {
+    DT attn_norm, q, k, v, o, q_bias, k_bias, v_bias, q_norm, k_norm, ffn_norm, gate, up, down;
+};
+
+int row_bytes(uint32_t type, uint64_t cols, uint64_t *out) {
+    switch (type) {
+    case ZIGGY_HIP_TYPE_F32: *out = cols * 4; return 0;
+    case ZIGGY_HIP_TYPE_F16: *out = cols * 2; return 0;
+    case ZIGGY_HIP_TYPE_Q8_0: if (cols % 32) return -1; *out = cols / 32 * 34; return 0;
+    case ZIGGY_HIP_TYPE_Q3_K: if (cols % 256) return -1; *out = cols / 256 * 110; return 0;
+    case ZIGGY_HIP_TYPE_Q4_K: if (cols % 256) return -1; *out = cols / 256 * 144; return 0;
+    case ZIGGY_HIP_TYPE_Q6_K: if (cols % 256) return -1; *out = cols / 256 * 210; return 0;
+    case ZIGGY_HIP_TYPE_IQ4_XS: if (cols % 256) return -1; *out = cols / 256 * 136; return 0;
+    default: return -1;
+    }
+}
+
+uint64_t now_ns() {
+    return (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+               std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+}
+
+}  // namespace
+
+struct ZiggyHipSession {
+    ZiggyHipContext *ctx = nullptr;
+    ZiggyHipModelDesc md{};
+    uint8_t *arena = nullptr;
+    size_t arena_len = 0;
+    DT embd, out_norm, out;
+    std::vector<LayerW> layers;
+    int q_size = 0, kv_size = 0, max_splits = 0;
+    float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr;
+    float *logits = nullptr, *part_o = nullptr, *part_ml = nullptr;
+    __half *kc = nullptr, *vc = nullptr;
+    StepState *st = nullptr;
+    StepState *st_host = nullptr;  // pinned staging for the host-driven step state
+    uint32_t *prompt = nullptr, *history = nullptr;
+    uint32_t prompt_cap = 0, history_cap = 0;
+    hipGraphExec_t graph = nullptr;
+    uint32_t position = 0;
+    bool logits_valid = false;
+    std::vector<void *> allocs;
+};
+
+namespace {
+
+int fail(char *err, size_t err_len, int code, const char *msg) {
+    set_err(err, err_len, "%s", msg);
+    return code;
+}
+
+// Plans a matvec over one or more row segments sharing the input.
+MvParams mv_params(const ZiggyHipSession *s, const DT *const *mats, float *const *ys, int n, int cols,
+                   const float *x) {
+    MvParams p{};
+    p.nseg = n;
+    for (int i = 0; i < n; i++) {
+        p.seg[i].w = mats[i]->p;
+        p.seg[i].stride = mats[i]->stride;
+        p.seg[i].y = ys[i];
+        p.seg[i].rows = (int)mats[i]->rows;
+        p.seg[i].fmt = mats[i]->type;
+    }
+    p.cols = cols;
+    p.x = x;
+    p.eps = s->md.rms_norm_eps;
+    plan_matvec(p, 1024);
+    return p;
+}
+
+// Enqueues one kernel of the step (ZIGGY_HIP_KERNEL_*) for layer l.  With
+// pos_dev set the position comes from device memory (graph replay).
+hipError_t enqueue_kernel(ZiggyHipSession *s, int id, int l, const int *pos_dev, int pos, hipStream_t st) {
+    const ZiggyHipModelDesc &md = s->md;
+    const int H = (int)md.embedding_length, F = (int)md.feed_forward_length;
+    const LayerW &L = s->layers[l < 0 ? 0 : l];
+    const size_t layer_base = (size_t)l * md.context_length * s->kv_size;
+    switch (id) {
+    case ZIGGY_HIP_KERNEL_QKV: {
+        const DT *m[3] = {&L.q, &L.k, &L.v};
+        float *ys[3] = {s->q, s->k, s->v};
+        MvParams p = mv_params(s, m, ys, 3, H, s->hidden);
+        p.norm_w = (const float *)L.attn_norm.p;
+        return launch_matvec(p, IN_NORM, OUT_STORE, st);
+    }
+    case ZIGGY_HIP_KERNEL_ROPE_KV: {
+        RopeKvParams r{};
+        r.q = s->q;
+        r.k = s->k;
+        r.v = s->v;
+        r.q_bias = L.q_bias.present ? (const float *)L.q_bias.p : nullptr;
+        r.k_bias = L.k_bias.present ? (const float *)L.k_bias.p : nullptr;
+        r.v_bias = L.v_bias.present ? (const float *)L.v_bias.p : nullptr;
+        r.q_norm = L.q_norm.present ? (const float *)L.q_norm.p : nullptr;
+        r.k_norm = L.k_norm.present ? (const float *)L.k_norm.p : nullptr;
+        r.k_cache = s->kc + layer_base;
+        r.v_cache = s->vc + layer_base;
+        r.heads = (int)md.head_count;
+        r.kv_heads = (int)md.head_count_kv;
+        r.hd = (int)md.head_dim;
+        r.rope_dim = (int)md.rope_dim;
+        r.style = (int)md.rope_style;
+        r.ctx = (int)md.context_length;
+        r.base = md.rope_freq_base;
+        r.eps = md.rms_norm_eps;
+        r.pos_dev = pos_dev;
+        r.pos = pos;
+        return launch_rope_kv(r, st);
+    }
+    case ZIGGY_HIP_KERNEL_ATTENTION: {
+        AttnParams a{};
+        a.q = s->q;
+        a.k_cache = s->kc + layer_base;
+        a.v_cache = s->vc + layer_base;
+        a.out = s->attn;
+        a.part_o = s->part_o;
+        a.part_ml = s->part_ml;
+        a.head_count = (int)md.head_count;
+        a.head_count_kv = (int)md.head_count_kv;
+        a.head_dim = (int)md.head_dim;
+        a.kv_dim = s->kv_size;
+        a.position = pos;
+        a.position_dev = pos_dev;
+        a.window_start = 0;
+        a.scale = 1.0f / sqrtf((float)md.head_dim);
+        a.chunk = 64;
+        a.max_splits = pos_dev ? s->max_splits : pos / 64 + 1;
+        return launch_attention(a, st);
+    }
+    case ZIGGY_HIP_KERNEL_O_PROJ: {
+        const DT *m[1] = {&L.o};
+        float *ys[1] = {s->hidden};
+        MvParams p = mv_params(s, m, ys, 1, s->q_size, s->attn);
+        return launch_matvec(p, IN_PLAIN, OUT_ADD, st);
+    }
+    case ZIGGY_HIP_KERNEL_GATE_UP: {
+        const DT *m[1] = {&L.gate};
+        float *ys[1] = {s->act};
+        MvParams p = mv_params(s, m, ys, 1, H, s->hidden);
+        p.norm_w = (const float *)L.ffn_norm.p;
+        if (L.gate.type == L.up.type) {
+            p.seg[0].w2 = L.up.p;
+            return launch_matvec(p, IN_NORM, OUT_SWIGLU, st);
+        }
+        // gate and up in different formats: two projections; the down kernel gates
+        hipError_t e = launch_matvec(p, IN_NORM, OUT_STORE, st);
+        if (e != hipSuccess) return e;
+        const DT *mu[1] = {&L.up};
+        float *yu[1] = {s->logits};  // the logits buffer is at least F long (sized at create)
+        MvParams pu = mv_params(s, mu, yu, 1, H, s->hidden);
+        pu.norm_w = (const float *)L.ffn_norm.p;
+        return launch_matvec(pu, IN_NORM, OUT_STORE, st);
+    }
+    case ZIGGY_HIP_KERNEL_DOWN: {
+        const DT *m[1] = {&L.down};
+        float *ys[1] = {s->hidden};
+        MvParams p = mv_params(s, m, ys, 1, F, s->act);
+        if (L.gate.type == L.up.type) return launch_matvec(p, IN_PLAIN, OUT_ADD, st);
+        p.x2 = s->logits;
+        return launch_matvec(p, IN_SILU, OUT_ADD, st);
+    }
+    case ZIGGY_HIP_KERNEL_OUTPUT: {
+        // fused final RMSNorm + output matvec + argmax (session.zig:633-651);
+        // on the device-driven step it is skipped on prompt steps (out_flag)
+        const DT *m[1] = {&s->out};
+        float *ys[1] = {s->logits};
+        MvParams p = mv_params(s, m, ys, 1, H, s->hidden);
+        p.norm_w = (const float *)s->out_norm.p;
+        p.gate_flag = pos_dev ? &s->st->out_flag : nullptr;
+        p.argmax_slot = &s->st->argmax;
+        return launch_matvec(p, IN_NORM, OUT_ARGMAX, st);
+    }
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// The attention block of one layer (session.zig:339-466).
+hipError_t enqueue_attention_block(ZiggyHipSession *s, int l, const int *pos_dev, int pos, hipStream_t st) {
+    for (int id : {ZIGGY_HIP_KERNEL_QKV, ZIGGY_HIP_KERNEL_ROPE_KV, ZIGGY_HIP_KERNEL_ATTENTION, ZIGGY_HIP_KERNEL_O_PROJ}) {
+        hipError_t e = enqueue_kernel(s, id, l, pos_dev, pos, st);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// The FFN block of one layer (session.zig:468-513).
+hipError_t enqueue_ffn_block(ZiggyHipSession *s, int l, hipStream_t st) {
+    hipError_t e = enqueue_kernel(s, ZIGGY_HIP_KERNEL_GATE_UP, l, nullptr, 0, st);
+    if (e != hipSuccess) return e;
+    return enqueue_kernel(s, ZIGGY_HIP_KERNEL_DOWN, l, nullptr, 0, st);
+}
+
+// Output head into the logits buffer, without argmax (session.zig:615-631).
+hipError_t enqueue_output_logits(ZiggyHipSession *s, hipStream_t st) {
+    const DT *m[1] = {&s->out};
+    float *ys[1] = {s->logits};
+    MvParams p = mv_params(s, m, ys, 1, (int)s->md.embedding_length, s->hidden);
+    p.norm_w = (const float *)s->out_norm.p;
+    return launch_matvec(p, IN_NORM, OUT_STORE, st);
+}
+
+// Algorithmic HBM bytes one launch of kernel `id` streams at position pos.
+uint64_t kernel_bytes(const ZiggyHipSession *s, int id, int l, int pos) {
+    const LayerW &L = s->layers[l];
+    auto mb = [](const DT &d) { return d.stride * d.rows; };
+    switch (id) {
+    case ZIGGY_HIP_KERNEL_QKV: return mb(L.q) + mb(L.k) + mb(L.v);
+    case ZIGGY_HIP_KERNEL_ROPE_KV: return (uint64_t)s->kv_size * 2 * 2;
+    case ZIGGY_HIP_KERNEL_ATTENTION: return (uint64_t)(pos + 1) * s->kv_size * 2 * 2;
+    case ZIGGY_HIP_KERNEL_O_PROJ: return mb(L.o);
+    case ZIGGY_HIP_KERNEL_GATE_UP: return mb(L.gate) + mb(L.up);
+    case ZIGGY_HIP_KERNEL_DOWN: return mb(L.down);
+    case ZIGGY_HIP_KERNEL_OUTPUT: return mb(s->out);
+    default: return 0;
+    }
+}
+
+hipError_t enqueue_step(ZiggyHipSession *s, hipStream_t st) {
+    hipError_t e = launch_step_begin(s->st, s->prompt, s->history, s->embd.p, s->embd.stride, (int)s->embd.rows,
+                                     s->embd.type, (int)s->md.embedding_length, s->hidden, st);
+    if (e != hipSuccess) return e;
+    for (int l = 0; l < (int)s->md.block_count; l++) {
+        e = enqueue_attention_block(s, l, &s->st->pos, 0, st);
+        if (e != hipSuccess) return e;
+        e = enqueue_ffn_block(s, l, st);
+        if (e != hipSuccess) return e;
+    }
+    return enqueue_kernel(s, ZIGGY_HIP_KERNEL_OUTPUT, 0, &s->st->pos, 0, st);
+}
+
+int build_graph(ZiggyHipSession *s, char *err, size_t err_len) {
+    hipStream_t st = s->ctx->stream;
+    hipGraph_t g = nullptr;
+    ZH_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "graph capture begin");
+    hipError_t e = enqueue_step(s, st);
+    hipError_t e2 = hipStreamEndCapture(st, &g);
+    if (e != hipSuccess) {
+        if (g) hipGraphDestroy(g);
+        return hip_fail(e, "graph capture", err, err_len);
+    }
+    if (e2 != hipSuccess) return hip_fail(e2, "graph capture end", err, err_len);
+    e = hipGraphInstantiate(&s->graph, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "graph instantiate", err, err_len);
+    return ZIGGY_HIP_OK;
+}
+
+bool take_tensor(const ZiggyHipTensorDesc *d, uint64_t want_rows, uint64_t want_cols, bool required, bool f32_only,
+                 DT *out, size_t *arena_off, std::vector<std::pair<const ZiggyHipTensorDesc *, DT *>> &todo) {
+    if (!d || !d->data) return !required;
+    uint64_t stride;
+    if (row_bytes(d->tensor_type, d->cols, &stride)) return false;
+    if (f32_only && d->tensor_type != ZIGGY_HIP_TYPE_F32) return false;
+    if ((want_rows && d->rows != want_rows) || (want_cols && d->cols != want_cols)) return false;
+    if (!f32_only && (d->cols % 64 || d->cols / 64 > 256)) return false;
+    out->rows = d->rows;
+    out->cols = d->cols;
+    out->stride = stride;
+    out->type = (int)d->tensor_type;
+    out->present = true;
+    out->p = reinterpret_cast<const uint8_t *>(*arena_off);  // fixed up after the arena is allocated
+    *arena_off += (stride * d->rows + 255) & ~(size_t)255;
+    todo.push_back({d, out});
+    return true;
+}
+
+void free_session(ZiggyHipSession *s) {
+    if (!s) return;
+    if (s->ctx) {
+        hipSetDevice(s->ctx->device);
+        hipStreamSynchronize(s->ctx->stream);
+    }
+    if (s->graph) hipGraphExecDestroy(s->graph);
+    for (void *p : s->allocs) hipFree(p);
+    if (s->st_host) hipHostFree(s->st_host);
+    delete s;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *model, const ZiggyHipTensorDesc *token_embd,
+                             const ZiggyHipTensorDesc *output_norm, const ZiggyHipTensorDesc *output,
+                             const ZiggyHipLayerDesc *layers, ZiggyHipSession **out_session, char *err, size_t err_len) {
+    if (!ctx || !model || !token_embd || !output_norm || !output || !layers || !out_session)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "null argument");
+    *out_session = nullptr;
+    const ZiggyHipModelDesc &md = *model;
+    if (md.block_count == 0 || md.embedding_length == 0 || md.head_count == 0 || md.head_count_kv == 0 ||
+        md.head_count % md.head_count_kv || md.head_count / md.head_count_kv > 8 ||
+        (md.head_dim != 64 && md.head_dim != 128 && md.head_dim != 256) || md.rope_dim > md.head_dim || md.rope_style > 1 ||
+        md.context_length == 0 || md.embedding_length % 64 || md.feed_forward_length % 64 ||
+        md.embedding_length / 64 > 256 || md.feed_forward_length / 64 > 256 ||
+        (md.head_count * md.head_dim) % 64)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "unsupported model shape");
+    ZiggyHipSession *s = new (std::nothrow) ZiggyHipSession();
+    if (!s) return fail(err, err_len, ZIGGY_HIP_INITIALIZATION_FAILED, "out of host memory");
+    s->ctx = ctx;
+    s->md = md;
+    s->q_size = (int)(md.head_count * md.head_dim);
+    s->kv_size = (int)(md.head_count_kv * md.head_dim);
+    s->max_splits = (int)((md.context_length + 63) / 64);
+    const uint64_t H = md.embedding_length, F = md.feed_forward_length, Q = (uint64_t)s->q_size,
+                   KV = (uint64_t)s->kv_size;
+
+    // ---- weight residency: one arena, every tensor 256-byte aligned ----
+    size_t off = 0;
+    std::vector<std::pair<const ZiggyHipTensorDesc *, DT *>> todo;
+    bool ok = take_tensor(token_embd, 0, H, true, false, &s->embd, &off, todo) &&
+              take_tensor(output_norm, 1, H, true, true, &s->out_norm, &off, todo) &&
+              take_tensor(output, md.vocab_size, H, true, false, &s->out, &off, todo);
+    s->layers.resize(md.block_count);
+    for (uint32_t l = 0; l < md.block_count && ok; l++) {
+        const ZiggyHipLayerDesc &d = layers[l];
+        LayerW &L = s->layers[l];
+        ok = take_tensor(&d.attn_norm, 1, H, true, true, &L.attn_norm, &off, todo) &&
+             take_tensor(&d.attn_q, Q, H, true, false, &L.q, &off, todo) &&
+             take_tensor(&d.attn_k, KV, H, true, false, &L.k, &off, todo) &&
+             take_tensor(&d.attn_v, KV, H, true, false, &L.v, &off, todo) &&
+             take_tensor(&d.attn_output, H, Q, true, false, &L.o, &off, todo) &&
+             take_tensor(&d.attn_q_bias, 1, Q, false, true, &L.q_bias, &off, todo) &&
+             take_tensor(&d.attn_k_bias, 1, KV, false, true, &L.k_bias, &off, todo) &&
+             take_tensor(&d.attn_v_bias, 1, KV, false, true, &L.v_bias, &off, todo) &&
+             take_tensor(&d.attn_q_norm, 1, md.head_dim, false, true, &L.q_norm, &off, todo) &&
+             take_tensor(&d.attn_k_norm, 1, md.head_dim, false, true, &L.k_norm, &off, todo) &&
+             take_tensor(&d.ffn_norm, 1, H, true, true, &L.ffn_norm, &off, todo) &&
+             take_tensor(&d.ffn_gate, F, H, true, false, &L.gate, &off, todo) &&
+             take_tensor(&d.ffn_up, F, H, true, false, &L.up, &off, todo) &&
+             take_tensor(&d.ffn_down, H, F, true, false, &L.down, &off, todo);
+        // q, k and v share one launch: at most two distinct formats, Q4_K/Q6_K mixed only
+        if (ok) {
+            const int a = L.q.type, b = L.k.type, c = L.v.type;
+            const bool uniform = a == b && b == c;
+            const bool mixed = ((a == ZIGGY_HIP_TYPE_Q4_K || a == ZIGGY_HIP_TYPE_Q6_K) &&
+                                (b == ZIGGY_HIP_TYPE_Q4_K || b == ZIGGY_HIP_TYPE_Q6_K) &&
+                                (c == ZIGGY_HIP_TYPE_Q4_K || c == ZIGGY_HIP_TYPE_Q6_K));
+            if (!uniform && !mixed) ok = false;
+        }
+    }
+    if (!ok) {
+        free_session(s);
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT,
+                    "tensor missing, of an unsupported type, or of the wrong shape");
+    }
+    hipSetDevice(ctx->device);
+    hipError_t e = hipMalloc(&s->arena, off);
+    if (e != hipSuccess) {
+        free_session(s);
+        return hip_fail(e, "weight arena hipMalloc", err, err_len);
+    }
+    s->allocs.push_back(s->arena);
+    s->arena_len = off;
+    for (auto &t : todo) {
+        const size_t o = reinterpret_cast<size_t>(t.second->p);
+        t.second->p = s->arena + o;
+        e = hipMemcpyAsync(s->arena + o, t.first->data, t.second->stride * t.second->rows, hipMemcpyHostToDevice,
+                           ctx->stream);
+        if (e != hipSuccess) {
+            free_session(s);
+            return hip_fail(e, "weight upload", err, err_len);
+        }
+    }
+
+    // ---- activations, KV cache, step state ----
+    const size_t cache_elems = (size_t)md.block_count * md.context_length * KV;
+    const size_t logits_len = md.vocab_size > F ? md.vocab_size : F;
+    const size_t attn_scratch = attention_scratch_floats((int)md.head_count, (int)md.head_dim, s->max_splits);
+    struct {
+        void **p;
+        size_t bytes;
+    } reqs[] = {
+        {(void **)&s->hidden, H * 4}, {(void **)&s->q, Q * 4}, {(void **)&s->k, KV * 4}, {(void **)&s->v, KV * 4},
+        {(void **)&s->attn, Q * 4}, {(void **)&s->act, F * 4}, {(void **)&s->logits, logits_len * 4},
+        {(void **)&s->part_o, attn_scratch * 4}, {(void **)&s->kc, cache_elems * 2}, {(void **)&s->vc, cache_elems * 2},
+        {(void **)&s->st, sizeof(StepState)},
+    };
+    for (auto &r : reqs) {
+        e = hipMalloc(r.p, r.bytes);
+        if (e == hipSuccess) e = hipMemsetAsync(*r.p, 0, r.bytes, ctx->stream);
+        if (e != hipSuccess) {
+            free_session(s);
+            return hip_fail(e, "session buffer allocation", err, err_len);
+        }
+        s->allocs.push_back(*r.p);
+    }
+    s->part_ml = s->part_o + (size_t)md.head_count * s->max_splits * 8 * md.head_dim;
+    e = hipHostMalloc((void **)&s->st_host, sizeof(StepState), hipHostMallocDefault);
+    if (e != hipSuccess) {
+        free_session(s);
+        return hip_fail(e, "pinned step state", err, err_len);
+    }
+    memset(s->st_host, 0, sizeof(StepState));
+    e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        free_session(s);
+        return hip_fail(e, "session upload", err, err_len);
+    }
+    int st = build_graph(s, err, err_len);
+    if (st) {
+        free_session(s);
+        return st;
+    }
+    *out_session = s;
+    return ZIGGY_HIP_OK;
+}
+
+void ziggy_hip_session_destroy(ZiggyHipSession *s) { free_session(s); }
+
+int ziggy_hip_session_reset(ZiggyHipSession *s, char *err, size_t err_len) {
+    if (!s) return ZIGGY_HIP_INVALID_ARGUMENT;
+    const size_t cache_bytes = (size_t)s->md.block_count * s->md.context_length * s->kv_size * 2;
+    ZH_TRY(hipMemsetAsync(s->kc, 0, cache_bytes, s->ctx->stream), "reset");
+    ZH_TRY(hipMemsetAsync(s->vc, 0, cache_bytes, s->ctx->stream), "reset");
+    ZH_TRY(hipStreamSynchronize(s->ctx->stream), "reset");
+    s->position = 0;
+    s->logits_valid = false;
+    return ZIGGY_HIP_OK;
+}
+
+uint32_t ziggy_hip_session_position(const ZiggyHipSession *s) { return s ? s->position : 0; }
+
+// ---- per-layer contract (gpu.Session) ----
+
+int ziggy_hip_session_begin_token(ZiggyHipSession *s, const float *hidden, char *err, size_t err_len) {
+    if (!s || !hidden) return ZIGGY_HIP_INVALID_ARGUMENT;
+    ZH_TRY(hipMemcpyAsync(s->hidden, hidden, (size_t)s->md.embedding_length * 4, hipMemcpyHostToDevice,
+                          s->ctx->stream),
+           "begin_token");
+    ZH_TRY(hipStreamSynchronize(s->ctx->stream), "begin_token");
+    return ZIGGY_HIP_OK;
+}
+
+int ziggy_hip_session_run_attention_block(ZiggyHipSession *s, uint32_t layer, uint32_t position, char *err,
+                                          size_t err_len) {
+    if (!s || layer >= s->md.block_count) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "bad layer");
+    if (position >= s->md.context_length) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "context overflow");
+    ZH_TRY(enqueue_attention_block(s, (int)layer, nullptr, (int)position, s->ctx->stream), "attention block");
+    return finish_op(s->ctx, "attention block", err, err_len);
+}
+
+int ziggy_hip_session_run_ffn_block(ZiggyHipSession *s, uint32_t layer, char *err, size_t err_len) {
+    if (!s || layer >= s->md.block_count) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "bad layer");
+    ZH_TRY(enqueue_ffn_block(s, (int)layer, s->ctx->stream), "ffn block");
+    return finish_op(s->ctx, "ffn block", err, err_len);
+}
+
+int ziggy_hip_session_run_output(ZiggyHipSession *s, float *logits, char *err, size_t err_len) {
+    if (!s || !logits) return ZIGGY_HIP_INVALID_ARGUMENT;
+    ZH_TRY(enqueue_output_logits(s, s->ctx->stream), "output");
+    ZH_TRY(hipMemcpyAsync(logits, s->logits, (size_t)s->md.vocab_size * 4, hipMemcpyDeviceToHost, s->ctx->stream),
+           "output readback");
+    ZH_TRY(hipStreamSynchronize(s->ctx->stream), "output");
+    s->logits_valid = true;
+    return ZIGGY_HIP_OK;
+}
+
+int ziggy_hip_session_run_output_argmax(ZiggyHipSession *s, uint32_t *token, char *err, size_t err_len) {
+    if (!s || !token) return ZIGGY_HIP_INVALID_ARGUMENT;
+    ZH_TRY(launch_fill_u64(&s->st->argmax, 0ull, 1, s->ctx->stream), "output argmax reset");
+    ZH_TRY(enqueue_kernel(s, ZIGGY_HIP_KERNEL_OUTPUT, 0, nullptr, 0, s->ctx->stream), "output argmax");
+    unsigned long long k = 0;
+    ZH_TRY(hipMemcpyAsync(&k, &s->st->argmax, 8, hipMemcpyDeviceToHost, s->ctx->stream), "argmax readback");
+    ZH_TRY(hipStreamSynchronize(s->ctx->stream), "output argmax");
+    *token = 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull);
+    s->logits_valid = true;
+    return ZIGGY_HIP_OK;
+}
+
+int ziggy_hip_session_read_hidden(ZiggyHipSession *s, float *out, char *err, size_t err_len) {
+    if (!s || !out) return ZIGGY_HIP_INVALID_ARGUMENT;
+    ZH_TRY(hipMemcpyAsync(out, s->hidden, (size_t)s->md.embedding_length * 4, hipMemcpyDeviceToHost, s->ctx->stream),
+           "read_hidden");
+    ZH_TRY(hipStreamSynchronize(s->ctx->stream), "read_hidden");
+    return ZIGGY_HIP_OK;
+}
+
+int ziggy_hip_session_write_hidden(ZiggyHipSession *s, const float *v, char *err, size_t err_len) {
+    return ziggy_hip_session_begin_token(s, v, err, err_len);
+}
+
+int ziggy_hip_session_read_kv(ZiggyHipSession *s, uint32_t layer, uint32_t pos, float *k_out, float *v_out, char *err,
+                              size_t err_len) {
+    if (!s || layer >= s->md.block_count || pos >= s->md.context_length || !k_out || !v_out)
+        return ZIGGY_HIP_INVALID_ARGUMENT;
+    std::vector<__half> tmp(2 * (size_t)s->kv_size);
+    const size_t base = ((size_t)layer * s->md.context_length + pos) * s->kv_size;
+    ZH_TRY(hipMemcpyAsync(tmp.data(), s->kc + base, (size_t)s->kv_size * 2, hipMemcpyDeviceToHost, s->ctx->stream),
+           "read_kv");
+    ZH_TRY(hipMemcpyAsync(tmp.data() + s->kv_size, s->vc + base, (size_t)s->kv_size * 2, hipMemcpyDeviceToHost,
+                          s->ctx->stream),
+           "read_kv");
+    ZH_TRY(hipStreamSynchronize(s->ctx->stream), "read_kv");
+    for (int i = 0; i < s->kv_size; i++) {
+        k_out[i] = __half2float(tmp[i]);
+        v_out[i] = __half2float(tmp[s->kv_size + i]);
+    }
+    return ZIGGY_HIP_OK;
+}
+
+int ziggy_hip_session_read_logits(ZiggyHipSession *s, float *out, char *err, size_t err_len) {
+    if (!s || !out) return ZIGGY_HIP_INVALID_ARGUMENT;
+    if (!s->logits_valid) return fail(err, err_len, ZIGGY_HIP_EXECUTION_FAILED, "no logits computed yet");
+    ZH_TRY(hipMemcpyAsync(out, s->logits, (size_t)s->md.vocab_size * 4, hipMemcpyDeviceToHost, s->ctx->stream),
+           "read_logits");
+    ZH_TRY(hipStreamSynchronize(s->ctx->stream), "read_logits");
+    return ZIGGY_HIP_OK;
+}
+
+// ---- whole steps ----
+
+static int host_step(ZiggyHipSession *s, uint32_t token, bool output, uint32_t *next, char *err, size_t err_len) {
+    if (s->position >= s->md.context_length) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "context overflow");
+    if (token >= s->embd.rows) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "token id out of range");
+    StepState *h = s->st_host;
+    memset(h, 0, sizeof(*h));
+    h->mode = 0;
+    h->pos = (int)s->position;
+    h->out_flag = output ? 1 : 0;
+    h->token = token;
+    hipStream_t st = s->ctx->stream;
+    ZH_TRY(hipMemcpyAsync(s->st, h, sizeof(StepState), hipMemcpyHostToDevice, st), "step state");
+    ZH_TRY(hipGraphLaunch(s->graph, st), "step graph");
+    if (output) ZH_TRY(hipMemcpyAsync(h, s->st, sizeof(StepState), hipMemcpyDeviceToHost, st), "step readback");
+    ZH_TRY(hipStreamSynchronize(st), "step");
+    s->position++;
+    if (output) {
+        s->logits_valid = true;
+        if (next) *next = 0xFFFFFFFFu - (uint32_t)(h->argmax & 0xFFFFFFFFull);
+    }
+    return ZIGGY_HIP_OK;
+}
+
+int ziggy_hip_session_step_greedy(ZiggyHipSession *s, uint32_t token, uint32_t *out_next, char *err, size_t err_len) {
+    if (!s || !out_next) return ZIGGY_HIP_INVALID_ARGUMENT;
+    return host_step(s, token, true, out_next, err, err_len);
+}
+
+int ziggy_hip_session_step_no_output(ZiggyHipSession *s, uint32_t token, char *err, size_t err_len) {
+    if (!s) return ZIGGY_HIP_INVALID_ARGUMENT;
+    return host_step(s, token, false, nullptr, err, err_len);
+}
+
+int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint32_t prompt_len, uint32_t steps,
+                               uint32_t *out_tokens, ZiggyHipGenerateStats *stats, char *err, size_t err_len) {
+    if (!s || !prompt || prompt_len == 0 || (steps && !out_tokens))
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "invalid generate arguments");
+    const uint64_t total = (uint64_t)prompt_len + steps;
+    if (s->position + total > s->md.context_length)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "context overflow");
+    for (uint32_t i = 0; i < prompt_len; i++)
+        if (prompt[i] >= s->embd.rows) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "token id out of range");
+    hipStream_t st = s->ctx->stream;
+    if (prompt_len > s->prompt_cap) {
+        if (s->prompt) {
+            hipFree(s->prompt);
+            s->allocs.erase(std::find(s->allocs.begin(), s->allocs.end(), (void *)s->prompt));
+        }
+        ZH_TRY(hipMalloc(&s->prompt, (size_t)prompt_len * 4), "prompt buffer");
+        s->allocs.push_back(s->prompt);
+        s->prompt_cap = prompt_len;
+    }
+    if (steps > s->history_cap || !s->history) {
+        if (s->history) {
+            hipFree(s->history);
+            s->allocs.erase(std::find(s->allocs.begin(), s->allocs.end(), (void *)s->history));
+        }
+        const uint32_t cap = steps ? steps : 1;
+        ZH_TRY(hipMalloc(&s->history, (size_t)cap * 4), "history buffer");
+        s->allocs.push_back(s->history);
+        s->history_cap = cap;
+    }
+    // step_begin reads the prompt/history pointers baked into the graph: rebuild it if they moved
+    if (s->graph) {
+        hipGraphExecDestroy(s->graph);
+        s->graph = nullptr;
+    }
+    int bst = build_graph(s, err, err_len);
+    if (bst) return bst;
+    ZH_TRY(hipMemcpyAsync(s->prompt, prompt, (size_t)prompt_len * 4, hipMemcpyHostToDevice, st), "prompt upload");
+    StepState *h = s->st_host;
+    memset(h, 0, sizeof(*h));
+    h->mode = 1;
+    h->base_pos = (int)s->position;
+    h->n_prompt = (int)prompt_len;
+    h->n_gen = (int)steps;
+    ZH_TRY(hipMemcpyAsync(s->st, h, sizeof(StepState), hipMemcpyHostToDevice, st), "step state");
+    ZH_TRY(hipStreamSynchronize(st), "generate setup");
+    // prompt steps, then the timed decode steps (the decode_ns bracket of model/loader.zig:2135-2257)
+    for (uint32_t i = 0; i < prompt_len; i++) ZH_TRY(hipGraphLaunch(s->graph, st), "prompt step");
+    ZH_TRY(hipStreamSynchronize(st), "prompt");
+    ZH_TRY(hipEventRecord(s->ctx->seq_begin, st), "generate");
+    const uint64_t t0 = now_ns();
+    for (uint32_t i = 0; i < steps; i++) ZH_TRY(hipGraphLaunch(s->graph, st), "decode step");
+    ZH_TRY(hipEventRecord(s->ctx->seq_end, st), "generate");
+    ZH_TRY(hipStreamSynchronize(st), "decode");
+    const uint64_t t1 = now_ns();
+    if (steps) ZH_TRY(hipMemcpy(out_tokens, s->history, (size_t)steps * 4, hipMemcpyDeviceToHost), "history");
+    ZH_TRY(hipMemcpy(h, s->st, sizeof(StepState), hipMemcpyDeviceToHost), "state readback");
+    if (h->error) return fail(err, err_len, ZIGGY_HIP_EXECUTION_FAILED, "a generated token was out of range");
+    s->position += (uint32_t)total;
+    s->logits_valid = true;
+    if (stats) {
+        float ms = 0.f;
+        hipEventElapsedTime(&ms, s->ctx->seq_begin, s->ctx->seq_end);
+        stats->steps = steps;
+        stats->gpu_elapsed_ns = (uint64_t)((double)ms * 1e6);
+        stats->wall_ns = t1 - t0;
+        stats->next_token = 0xFFFFFFFFu - (uint32_t)(h->argmax & 0xFFFFFFFFull);
+    }
+    return ZIGGY_HIP_OK;
+}
+
+int ziggy_hip_session_time_kernel(ZiggyHipSession *s, uint32_t kernel, uint32_t iterations, uint64_t *avg_ns,
+                                  uint64_t *bytes_per_launch, char *err, size_t err_len) {
+    if (!s || kernel > ZIGGY_HIP_KERNEL_OUTPUT || iterations == 0 || !avg_ns || !bytes_per_launch)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "invalid time_kernel arguments");
+    if (s->position >= s->md.context_length)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "no free cache row to time at");
+    const int pos = (int)s->position, L = (int)s->md.block_count;
+    hipStream_t st = s->ctx->stream;
+    hipEvent_t e0, e1;
+    ZH_TRY(hipEventCreate(&e0), "time_kernel");
+    if (hipEventCreate(&e1) != hipSuccess) {
+        hipEventDestroy(e0);
+        return fail(err, err_len, ZIGGY_HIP_EXECUTION_FAILED, "event creation failed");
+    }
+    double total_ms = 0.0;
+    uint64_t bytes = 0;
+    hipError_t e = hipSuccess;
+    for (uint32_t i = 0; i < iterations && e == hipSuccess; i++) {
+        const int l = (int)(i % (uint32_t)L);
+        e = hipEventRecord(e0, st);
+        if (e == hipSuccess) e = enqueue_kernel(s, (int)kernel, l, nullptr, pos, st);
+        if (e == hipSuccess) e = hipEventRecord(e1, st);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        float ms = 0.f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+        total_ms += ms;
+        bytes += kernel_bytes(s, (int)kernel, l, pos);
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (e != hipSuccess) return hip_fail(e, "time_kernel", err, err_len);
+    *avg_ns = (uint64_t)(total_ms * 1e6 / iterations);
+    *bytes_per_launch = bytes / iterations;
+    return ZIGGY_HIP_OK;
+}
+
+}  // extern "C"

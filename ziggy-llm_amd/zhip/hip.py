@@ -1,0 +1,442 @@
+"""ctypes binding of libziggy_hip's C ABI (include/ziggy_hip.h).
+
+This plays the role the reference's Zig wrapper (src/runtime/metal_backend.zig)
+plays for Metal: it owns handles, checks sizes, and turns status codes into
+exceptions carrying the library's error message (metal_backend.zig:2027-2047).
+There is no fallback: if the library is missing or no gfx950 device is
+present, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+from . import gguf
+from ._lib import HIP_LIB, load
+
+ERR_LEN = 256
+STATUS = {0: "OK", 1: "UNAVAILABLE", 2: "INITIALIZATION_FAILED", 3: "COMPILATION_FAILED", 4: "BUFFER_FAILED",
+          5: "EXECUTION_FAILED", 6: "INVALID_ARGUMENT"}
+
+
+class HipError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"{STATUS.get(status, status)}: {msg}")
+        self.status = status
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 128), ("arch", ctypes.c_char * 64), ("total_memory", ctypes.c_uint64),
+                ("compute_units", ctypes.c_uint32), ("wavefront_size", ctypes.c_uint32),
+                ("clock_khz", ctypes.c_uint32), ("l2_bytes", ctypes.c_uint32)]
+
+
+class CommitStats(ctypes.Structure):
+    _fields_ = [("cpu_wait_ns", ctypes.c_uint64), ("gpu_elapsed_ns", ctypes.c_uint64),
+                ("gpu_timestamps_valid", ctypes.c_bool)]
+
+
+class TensorDesc(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("rows", ctypes.c_uint64), ("cols", ctypes.c_uint64),
+                ("tensor_type", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+LAYER_FIELDS = ["attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "attn_q_bias", "attn_k_bias",
+                "attn_v_bias", "attn_q_norm", "attn_k_norm", "ffn_norm", "ffn_gate", "ffn_up", "ffn_down"]
+
+
+class LayerDesc(ctypes.Structure):
+    _fields_ = [(n, TensorDesc) for n in LAYER_FIELDS]
+
+
+class ModelDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "embedding_length", "block_count", "context_length", "feed_forward_length", "head_count", "head_count_kv",
+        "head_dim", "rope_dim", "vocab_size", "rope_style")] + [("rms_norm_eps", ctypes.c_float),
+                                                               ("rope_freq_base", ctypes.c_float)]
+
+
+class GenerateStats(ctypes.Structure):
+    _fields_ = [("steps", ctypes.c_uint64), ("gpu_elapsed_ns", ctypes.c_uint64), ("wall_ns", ctypes.c_uint64),
+                ("next_token", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+KERNELS = {"qkv": 0, "rope_kv": 1, "attention": 2, "o_proj": 3, "gate_up": 4, "down": 5, "output": 6}
+
+
+_typed = False
+
+
+def lib() -> ctypes.CDLL:
+    global _typed
+    L = load(HIP_LIB)
+    if _typed:
+        return L
+    vp, sz, u32, i, f, ep = (ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_int, ctypes.c_float,
+                             ctypes.c_char_p)
+    E = [ep, sz]
+    sigs = {
+        "ziggy_hip_create_context": [i, ctypes.POINTER(vp), ctypes.POINTER(DeviceInfo)] + E,
+        "ziggy_hip_destroy_context": [vp],
+        "ziggy_hip_create_buffer": [vp, vp, sz, ctypes.POINTER(vp)] + E,
+        "ziggy_hip_create_empty_buffer": [vp, sz, ctypes.POINTER(vp)] + E,
+        "ziggy_hip_destroy_buffer": [vp],
+        "ziggy_hip_buffer_length": [vp],
+        "ziggy_hip_write_buffer": [vp, vp, sz, sz] + E,
+        "ziggy_hip_read_buffer": [vp, vp, sz, sz] + E,
+        "ziggy_hip_copy_buffer_region": [vp, vp, sz, vp, sz, sz] + E,
+        "ziggy_hip_begin_sequence": [vp] + E,
+        "ziggy_hip_commit_sequence": [vp] + E,
+        "ziggy_hip_commit_sequence_timed": [vp, ctypes.POINTER(CommitStats)] + E,
+        "ziggy_hip_run_matvec": [vp, u32, vp, sz, vp, vp, sz, u32, u32, i] + E,
+        "ziggy_hip_run_matvec_silu_down_add": [vp, u32, vp, vp, vp, vp, u32, u32] + E,
+        "ziggy_hip_run_matvec_argmax": [vp, u32, vp, vp, vp, u32, u32] + E,
+        "ziggy_hip_dequantize_rows": [vp, u32, vp, sz, vp, u32, u32] + E,
+        "ziggy_hip_indexed_matvec": [vp, u32, vp, vp, vp, u32, u32, vp, u32, u32, i] + E,
+        "ziggy_hip_dual_indexed_matvec": [vp, u32, vp, vp, vp, vp, vp, u32, u32, vp, u32, u32] + E,
+        "ziggy_hip_apply_rope_f32": [vp, vp, u32, u32, u32, u32, f, u32] + E,
+        "ziggy_hip_apply_rope_to_dst_f32": [vp, vp, vp, sz, u32, u32, u32, u32, f, u32] + E,
+        "ziggy_hip_store_kv_half": [vp, vp, vp, sz, u32] + E,
+        "ziggy_hip_attention_fused_f32": [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, u32, f, f] + E,
+        "ziggy_hip_silu_mul_f32": [vp, vp, vp, u32] + E,
+        "ziggy_hip_add_in_place_f32": [vp, vp, vp, u32] + E,
+        "ziggy_hip_rms_norm_f32": [vp, vp, vp, vp, u32, f, f] + E,
+        "ziggy_hip_rms_norm_per_head_f32": [vp, vp, vp, vp, u32, u32, f, f] + E,
+        "ziggy_hip_argmax_f32": [vp, vp, vp, u32] + E,
+        "ziggy_hip_topk_f32": [vp, vp, vp, u32, u32] + E,
+        "ziggy_hip_normalize_topk_f32": [vp, vp, u32, ctypes.c_bool, ctypes.c_bool, f] + E,
+        "ziggy_hip_weighted_sum_topk_f32": [vp, vp, vp, vp, u32, u32] + E,
+        "ziggy_hip_sigmoid_scale_add_f32": [vp, vp, vp, vp, u32] + E,
+        "ziggy_hip_session_create": [vp, ctypes.POINTER(ModelDesc), ctypes.POINTER(TensorDesc),
+                                     ctypes.POINTER(TensorDesc), ctypes.POINTER(TensorDesc),
+                                     ctypes.POINTER(LayerDesc), ctypes.POINTER(vp)] + E,
+        "ziggy_hip_session_destroy": [vp],
+        "ziggy_hip_session_reset": [vp] + E,
+        "ziggy_hip_session_position": [vp],
+        "ziggy_hip_session_begin_token": [vp, vp] + E,
+        "ziggy_hip_session_run_attention_block": [vp, u32, u32] + E,
+        "ziggy_hip_session_run_ffn_block": [vp, u32] + E,
+        "ziggy_hip_session_run_output": [vp, vp] + E,
+        "ziggy_hip_session_run_output_argmax": [vp, ctypes.POINTER(u32)] + E,
+        "ziggy_hip_session_read_hidden": [vp, vp] + E,
+        "ziggy_hip_session_write_hidden": [vp, vp] + E,
+        "ziggy_hip_session_read_kv": [vp, u32, u32, vp, vp] + E,
+        "ziggy_hip_session_step_greedy": [vp, u32, ctypes.POINTER(u32)] + E,
+        "ziggy_hip_session_step_no_output": [vp, u32] + E,
+        "ziggy_hip_session_generate": [vp, vp, u32, u32, vp, ctypes.POINTER(GenerateStats)] + E,
+        "ziggy_hip_session_read_logits": [vp, vp] + E,
+        "ziggy_hip_session_time_kernel": [vp, u32, u32, ctypes.POINTER(ctypes.c_uint64),
+                                          ctypes.POINTER(ctypes.c_uint64)] + E,
+        "ziggy_hip_version": [],
+    }
+    restypes = {"ziggy_hip_destroy_context": None, "ziggy_hip_destroy_buffer": None,
+                "ziggy_hip_session_destroy": None, "ziggy_hip_buffer_length": sz,
+                "ziggy_hip_session_position": u32, "ziggy_hip_version": ctypes.c_char_p}
+    for name, args in sigs.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = restypes.get(name, i)
+    _typed = True
+    return L
+
+
+def _call(fn_name: str, *args):
+    err = ctypes.create_string_buffer(ERR_LEN)
+    st = getattr(lib(), fn_name)(*args, err, ERR_LEN)
+    if st:
+        raise HipError(st, err.value.decode(errors="replace"))
+
+
+class Buffer:
+    def __init__(self, ctx: "Context", handle: ctypes.c_void_p, nbytes: int):
+        self.ctx, self.h, self.nbytes = ctx, handle, nbytes
+
+    def write(self, arr: np.ndarray, offset: int = 0):
+        arr = np.ascontiguousarray(arr)
+        _call("ziggy_hip_write_buffer", self.h, arr.ctypes.data, arr.nbytes, offset)
+
+    def read(self, dtype=np.float32, count: int | None = None, offset: int = 0) -> np.ndarray:
+        itemsize = np.dtype(dtype).itemsize
+        n = count if count is not None else (self.nbytes - offset) // itemsize
+        out = np.empty(n, dtype=dtype)
+        _call("ziggy_hip_read_buffer", self.h, out.ctypes.data, out.nbytes, offset)
+        return out
+
+    def free(self):
+        if self.h:
+            lib().ziggy_hip_destroy_buffer(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    """One device context (ziggy_hip_create_context)."""
+
+    def __init__(self, device: int = 0):
+        import weakref
+        h = ctypes.c_void_p()
+        self.info = DeviceInfo()
+        _call("ziggy_hip_create_context", device, ctypes.byref(h), ctypes.byref(self.info))
+        self.h = h
+        self._owned = weakref.WeakSet()  # buffers and sessions, released before the context
+
+    def buffer(self, data: np.ndarray) -> Buffer:
+        data = np.ascontiguousarray(data)
+        h = ctypes.c_void_p()
+        _call("ziggy_hip_create_buffer", self.h, data.ctypes.data, data.nbytes, ctypes.byref(h))
+        b = Buffer(self, h, data.nbytes)
+        self._owned.add(b)
+        return b
+
+    def empty(self, nbytes: int) -> Buffer:
+        h = ctypes.c_void_p()
+        _call("ziggy_hip_create_empty_buffer", self.h, nbytes, ctypes.byref(h))
+        b = Buffer(self, h, nbytes)
+        self._owned.add(b)
+        return b
+
+    # ---- primitive ops ----
+    def matvec(self, ttype, m: Buffer, x: Buffer, y: Buffer, rows, cols, add=False, m_off=0, y_off=0):
+        _call("ziggy_hip_run_matvec", self.h, ttype, m.h, m_off, x.h, y.h, y_off, rows, cols, int(add))
+
+    def matvec_silu_down_add(self, ttype, m, gate, up, y, rows, cols):
+        _call("ziggy_hip_run_matvec_silu_down_add", self.h, ttype, m.h, gate.h, up.h, y.h, rows, cols)
+
+    def matvec_argmax(self, ttype, m, x, state, rows, cols):
+        _call("ziggy_hip_run_matvec_argmax", self.h, ttype, m.h, x.h, state.h, rows, cols)
+
+    def dequantize(self, ttype, m: Buffer, out: Buffer, rows, cols, m_off=0):
+        _call("ziggy_hip_dequantize_rows", self.h, ttype, m.h, m_off, out.h, rows, cols)
+
+    def indexed_matvec(self, ttype, m, x, y, rows, cols, entries, slot, rows_per_expert, add_weighted=False):
+        _call("ziggy_hip_indexed_matvec", self.h, ttype, m.h, x.h, y.h, rows, cols, entries.h, slot,
+              rows_per_expert, int(add_weighted))
+
+    def dual_indexed_matvec(self, ttype, ma, mb, x, ya, yb, rows, cols, entries, slot, rows_per_expert):
+        _call("ziggy_hip_dual_indexed_matvec", self.h, ttype, ma.h, mb.h, x.h, ya.h, yb.h, rows, cols, entries.h,
+              slot, rows_per_expert)
+
+    def rope(self, v: Buffer, heads, hd, rope_dim, pos, base, style):
+        _call("ziggy_hip_apply_rope_f32", self.h, v.h, heads, hd, rope_dim, pos, base, style)
+
+    def rope_to_dst(self, src, dst, dst_off, heads, hd, rope_dim, pos, base, style):
+        _call("ziggy_hip_apply_rope_to_dst_f32", self.h, src.h, dst.h, dst_off, heads, hd, rope_dim, pos, base,
+              style)
+
+    def store_kv_half(self, src, dst, dst_off_el, count):
+        _call("ziggy_hip_store_kv_half", self.h, src.h, dst.h, dst_off_el, count)
+
+    def attention(self, q, kc, vc, out, heads, heads_kv, hd, kv_dim, ctx_len, pos, layer_base=0, window_start=0,
+                  scale=None, softcap=0.0):
+        scale = 1.0 / np.sqrt(hd) if scale is None else scale
+        _call("ziggy_hip_attention_fused_f32", self.h, q.h, kc.h, vc.h, out.h, heads, heads_kv, hd, kv_dim, ctx_len,
+              pos, layer_base, window_start, float(scale), float(softcap))
+
+    def silu_mul(self, g, u, n):
+        _call("ziggy_hip_silu_mul_f32", self.h, g.h, u.h, n)
+
+    def add(self, d, s, n):
+        _call("ziggy_hip_add_in_place_f32", self.h, d.h, s.h, n)
+
+    def rms_norm(self, x, w, out, n, eps, offset=0.0):
+        _call("ziggy_hip_rms_norm_f32", self.h, x.h, w.h, out.h, n, eps, offset)
+
+    def rms_norm_per_head(self, x, w, out, heads, hd, eps, offset=0.0):
+        _call("ziggy_hip_rms_norm_per_head_f32", self.h, x.h, w.h, out.h, heads, hd, eps, offset)
+
+    def argmax(self, x, tok, n):
+        _call("ziggy_hip_argmax_f32", self.h, x.h, tok.h, n)
+
+    def topk(self, x, entries, n, k):
+        _call("ziggy_hip_topk_f32", self.h, x.h, entries.h, n, k)
+
+    def normalize_topk(self, entries, k, softmax, normalize, scale):
+        _call("ziggy_hip_normalize_topk_f32", self.h, entries.h, k, bool(softmax), bool(normalize), scale)
+
+    def weighted_sum_topk(self, d, s, entries, n, slot):
+        _call("ziggy_hip_weighted_sum_topk_f32", self.h, d.h, s.h, entries.h, n, slot)
+
+    def sigmoid_scale_add(self, d, s, scalar, n):
+        _call("ziggy_hip_sigmoid_scale_add_f32", self.h, d.h, s.h, scalar.h, n)
+
+    def begin(self):
+        _call("ziggy_hip_begin_sequence", self.h)
+
+    def commit(self) -> CommitStats:
+        st = CommitStats()
+        _call("ziggy_hip_commit_sequence_timed", self.h, ctypes.byref(st))
+        return st
+
+    def close(self):
+        if self.h:
+            for obj in list(getattr(self, "_owned", ())):
+                obj.close() if isinstance(obj, Session) else obj.free()
+            lib().ziggy_hip_destroy_context(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _desc(img: gguf.GGUFImage, name: str) -> TensorDesc:
+    d = TensorDesc()
+    t = img.tensors.get(name)
+    if t is None:
+        return d
+    view = img.tensor_view(name)
+    d.data = view.ctypes.data
+    d.rows = t.rows
+    d.cols = t.row_len
+    d.tensor_type = t.ttype
+    return d
+
+
+def model_desc_from_gguf(img: gguf.GGUFImage, context: int | None = None) -> ModelDesc:
+    """Hyperparameters as loadModel derives them (model/loader.zig:2596-2640)."""
+    md = img.metadata
+    arch = md["general.architecture"]
+
+    def key(suffix, default=None):
+        for k, v in md.items():
+            if k.endswith(suffix):
+                return v
+        return default
+
+    H = int(key(".embedding_length"))
+    heads = int(key(".attention.head_count"))
+    hd = int(key(".attention.key_length", H // heads))
+    m = ModelDesc()
+    m.embedding_length = H
+    m.block_count = int(key(".block_count"))
+    m.context_length = int(context if context is not None else key(".context_length"))
+    m.feed_forward_length = int(key(".feed_forward_length"))
+    m.head_count = heads
+    m.head_count_kv = int(key(".attention.head_count_kv"))
+    m.head_dim = hd
+    m.rope_dim = int(key(".rope.dimension_count", hd))
+    m.vocab_size = img.tensors.get("output.weight", img.tensors["token_embd.weight"]).rows
+    m.rope_style = 1 if (arch.startswith("qwen") or arch.startswith("mistral")) else 0
+    m.rms_norm_eps = float(key(".attention.layer_norm_rms_epsilon", 1e-6))
+    m.rope_freq_base = float(key(".rope.freq_base", 10000.0))
+    return m
+
+
+class Session:
+    """Decode session over a GGUF image resident in host memory (weights are uploaded once)."""
+
+    def __init__(self, ctx: Context, img: gguf.GGUFImage, context: int | None = None):
+        self.ctx, self.img = ctx, img
+        self.md = model_desc_from_gguf(img, context)
+        n = self.md.block_count
+        layers = (LayerDesc * n)()
+        for i in range(n):
+            for f in LAYER_FIELDS:
+                nm = f"blk.{i}.{f}.weight" if not f.endswith("_bias") else f"blk.{i}.{f[:-5]}.bias"
+                setattr(layers[i], f, _desc(img, nm))
+        out_name = "output.weight" if "output.weight" in img.tensors else "token_embd.weight"
+        self._descs = (_desc(img, "token_embd.weight"), _desc(img, "output_norm.weight"), _desc(img, out_name),
+                       layers)
+        h = ctypes.c_void_p()
+        _call("ziggy_hip_session_create", ctx.h, ctypes.byref(self.md), ctypes.byref(self._descs[0]),
+              ctypes.byref(self._descs[1]), ctypes.byref(self._descs[2]), layers, ctypes.byref(h))
+        self.h = h
+        ctx._owned.add(self)
+
+    @property
+    def position(self) -> int:
+        return int(lib().ziggy_hip_session_position(self.h))
+
+    def reset(self):
+        _call("ziggy_hip_session_reset", self.h)
+
+    def step_greedy(self, token: int) -> int:
+        nxt = ctypes.c_uint32()
+        _call("ziggy_hip_session_step_greedy", self.h, token, ctypes.byref(nxt))
+        return nxt.value
+
+    def step_no_output(self, token: int):
+        _call("ziggy_hip_session_step_no_output", self.h, token)
+
+    def generate(self, prompt, steps: int):
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(max(steps, 1), dtype=np.uint32)
+        st = GenerateStats()
+        _call("ziggy_hip_session_generate", self.h, prompt.ctypes.data, prompt.size, steps, out.ctypes.data,
+              ctypes.byref(st))
+        return out[:steps].copy(), st
+
+    def time_kernel(self, name: str, iterations: int):
+        """Mean launch duration (ns) and algorithmic bytes per launch of one step kernel."""
+        ns, nb = ctypes.c_uint64(), ctypes.c_uint64()
+        _call("ziggy_hip_session_time_kernel", self.h, KERNELS[name], iterations, ctypes.byref(ns), ctypes.byref(nb))
+        return ns.value, nb.value
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.md.vocab_size, np.float32)
+        _call("ziggy_hip_session_read_logits", self.h, out.ctypes.data)
+        return out
+
+    def kv(self, layer: int, pos: int):
+        n = self.md.head_count_kv * self.md.head_dim
+        k, v = np.empty(n, np.float32), np.empty(n, np.float32)
+        _call("ziggy_hip_session_read_kv", self.h, layer, pos, k.ctypes.data, v.ctypes.data)
+        return k, v
+
+    # per-layer contract (gpu.Session)
+    def begin_token(self, hidden: np.ndarray):
+        hidden = np.ascontiguousarray(hidden, np.float32)
+        _call("ziggy_hip_session_begin_token", self.h, hidden.ctypes.data)
+
+    def run_attention_block(self, layer: int, position: int):
+        _call("ziggy_hip_session_run_attention_block", self.h, layer, position)
+
+    def run_ffn_block(self, layer: int):
+        _call("ziggy_hip_session_run_ffn_block", self.h, layer)
+
+    def run_output(self) -> np.ndarray:
+        out = np.empty(self.md.vocab_size, np.float32)
+        _call("ziggy_hip_session_run_output", self.h, out.ctypes.data)
+        return out
+
+    def run_output_argmax(self) -> int:
+        t = ctypes.c_uint32()
+        _call("ziggy_hip_session_run_output_argmax", self.h, ctypes.byref(t))
+        return t.value
+
+    def hidden(self) -> np.ndarray:
+        out = np.empty(self.md.embedding_length, np.float32)
+        _call("ziggy_hip_session_read_hidden", self.h, out.ctypes.data)
+        return out
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().ziggy_hip_session_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def exported_symbols() -> list:
+    """Every function name declared in include/ziggy_hip.h (for ABI checks)."""
+    import re
+    here = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    text = open(os.path.join(here, "include", "ziggy_hip.h")).read()
+    names = set(re.findall(r"\b(ziggy_hip_[a-z0-9_]+)\s*\(", text))
+    for sfx in ("q4k", "q6k", "q8_0", "q3k", "f16", "dense"):
+        names |= {f"ziggy_hip_run_matvec_{sfx}_f32", f"ziggy_hip_run_matvec_{sfx}_f32_to_dst",
+                  f"ziggy_hip_run_matvec_{sfx}_add_f32"}
+    return sorted(n for n in names if not n.endswith("_f32##") and "##" not in n)
