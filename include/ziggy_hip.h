@@ -159,6 +159,17 @@ int ziggy_hip_run_matvec_q6k_argmax_f32(ZiggyHipContext *ctx, const ZiggyHipBuff
                                         const ZiggyHipBuffer *input, ZiggyHipBuffer *output_state, uint32_t rows,
                                         uint32_t cols, char *error_message, size_t error_message_len);
 
+/* Times the matvec kernel (no counterpart in the reference): `iterations`
+ * launches of ziggy_hip_run_matvec's kernel, launch i reading copy
+ * (i % copies) of the matrix, copies laid out copy_stride bytes apart in
+ * `matrices`, so a copy set larger than the 256 MB Infinity Cache streams
+ * from HBM.  Each launch is bracketed by its own HIP events; *avg_ns is the
+ * mean launch duration. */
+int ziggy_hip_time_matvec(ZiggyHipContext *ctx, uint32_t tensor_type, const ZiggyHipBuffer *matrices,
+                          uint32_t copies, size_t copy_stride, const ZiggyHipBuffer *input, ZiggyHipBuffer *output,
+                          uint32_t rows, uint32_t cols, uint32_t iterations, uint64_t *avg_ns,
+                          char *error_message, size_t error_message_len);
+
 /* Bit-exact block decode of `rows` rows to f32 (debug/parity entry; the
  * reference's counterpart is the CPU dequantizeRow, model/loader.zig:3428-3459). */
 int ziggy_hip_dequantize_rows(ZiggyHipContext *ctx, uint32_t tensor_type, const ZiggyHipBuffer *matrix,

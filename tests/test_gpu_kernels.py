@@ -96,7 +96,8 @@ def test_q4k_reference_matrix(hip_ctx):
     assert np.array_equal(deq.read().view(np.uint32), zo.dequantize(Q4_K, m, rows, cols).ravel().view(np.uint32))
 
 
-SHAPES = [(96, 256), (300, 1024), (4096, 4096), (14336, 4096), (4096, 14336), (1024, 2048), (4096, 12288)]
+SHAPES = [(96, 256), (300, 1024), (4096, 4096), (14336, 4096), (4096, 14336), (1024, 2048), (4096, 12288),
+          (128256, 4096)]
 
 
 @pytest.mark.parametrize("ttype", [Q4_K, Q6_K, Q8_0, Q3_K, IQ4_XS, F16, F32])

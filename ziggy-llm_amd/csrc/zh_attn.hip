@@ -42,34 +42,50 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnParams p) {
     __shared__ float s_s[kMaxGroup][kChunk];
     __shared__ float red[256 / (HD / 2)][kMaxGroup][HD];
 
+    // Every K and V load of this workgroup is issued first; the q staging,
+    // the score math and the softmax statistics run while they are in flight.
+    constexpr int DPT = HD / 4;                 // K dims per lane (4 lanes per position)
+    constexpr int NP = HD / 2, NS = 256 / NP;   // V: lanes own a dim pair, NS position subsets
+    constexpr int PPT = kChunk / NS;            // V positions per lane
+    const int pi = tid >> 2, part = tid & 3;
+    const int dp = tid % NP, ps = tid / NP;
+    uint4 kraw[DPT / 8];
+    uint32_t vraw[PPT];
+    {
+        const __half *krow = p.k_cache + (size_t)(t0 + pi) * p.kv_dim + (size_t)kvh * HD + part * DPT;
+#pragma unroll
+        for (int c = 0; c < DPT / 8; c++)
+            kraw[c] = pi < n ? *reinterpret_cast<const uint4 *>(krow + 8 * c) : make_uint4(0, 0, 0, 0);
+        const __half *vcol = p.v_cache + (size_t)t0 * p.kv_dim + (size_t)kvh * HD + 2 * dp;
+#pragma unroll
+        for (int j = 0; j < PPT; j++) {
+            const int pv = ps + NS * j;
+            vraw[j] = pv < n ? *reinterpret_cast<const uint32_t *>(vcol + (size_t)pv * p.kv_dim) : 0u;
+        }
+    }
+
     for (int i = tid; i < G * HD; i += 256) q_s[i / HD][i % HD] = p.q[(size_t)(kvh * G) * HD + i];
     __syncthreads();
 
     // scores: 4 lanes per position, each covering HD/4 dimensions
     {
-        constexpr int DPT = HD / 4;
-        const int pi = tid >> 2, part = tid & 3;
         float acc[kMaxGroup];
 #pragma unroll
         for (int g = 0; g < kMaxGroup; g++) acc[g] = 0.f;
-        if (pi < n) {
-            const __half *krow = p.k_cache + (size_t)(t0 + pi) * p.kv_dim + (size_t)kvh * HD + part * DPT;
 #pragma unroll
-            for (int c = 0; c < DPT; c += 8) {
-                const uint4 raw = *reinterpret_cast<const uint4 *>(krow + c);
-                const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-                float k[8];
+        for (int c = 0; c < DPT / 8; c++) {
+            const uint32_t w[4] = {kraw[c].x, kraw[c].y, kraw[c].z, kraw[c].w};
+            float k[8];
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    k[2 * j] = h2f(w[j]);
-                    k[2 * j + 1] = h2f(w[j] >> 16);
-                }
+            for (int j = 0; j < 4; j++) {
+                k[2 * j] = h2f(w[j]);
+                k[2 * j + 1] = h2f(w[j] >> 16);
+            }
 #pragma unroll
-                for (int g = 0; g < kMaxGroup; g++) {
-                    if (g < G) {
+            for (int g = 0; g < kMaxGroup; g++) {
+                if (g < G) {
 #pragma unroll
-                        for (int j = 0; j < 8; j++) acc[g] = fmaf(q_s[g][part * DPT + c + j], k[j], acc[g]);
-                    }
+                    for (int j = 0; j < 8; j++) acc[g] = fmaf(q_s[g][part * DPT + 8 * c + j], k[j], acc[g]);
                 }
             }
         }
@@ -102,21 +118,19 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnParams p) {
     }
     __syncthreads();
 
-    // values: thread owns a dimension pair and a subset of positions
+    // values: unnormalised sum of exp(s - m) v over this lane's positions
     {
-        constexpr int NP = HD / 2, NS = 256 / NP;
-        const int dp = tid % NP, ps = tid / NP;
         float o0[kMaxGroup], o1[kMaxGroup];
 #pragma unroll
         for (int g = 0; g < kMaxGroup; g++) o0[g] = o1[g] = 0.f;
-        for (int pi = ps; pi < n; pi += NS) {
-            const uint32_t v2 =
-                *reinterpret_cast<const uint32_t *>(p.v_cache + (size_t)(t0 + pi) * p.kv_dim + (size_t)kvh * HD + 2 * dp);
-            const float v0 = h2f(v2), v1 = h2f(v2 >> 16);
+#pragma unroll
+        for (int j = 0; j < PPT; j++) {
+            const int pv = ps + NS * j;
+            const float v0 = h2f(vraw[j]), v1 = h2f(vraw[j] >> 16);
 #pragma unroll
             for (int g = 0; g < kMaxGroup; g++) {
                 if (g < G) {
-                    const float w = s_s[g][pi];
+                    const float w = pv < n ? s_s[g][pv] : 0.f;
                     o0[g] = fmaf(w, v0, o0[g]);
                     o1[g] = fmaf(w, v1, o1[g]);
                 }
@@ -133,10 +147,10 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnParams p) {
         float *po = p.part_o + ((size_t)kvh * p.max_splits + split) * kMaxGroup * HD;
         for (int i = tid; i < G * HD; i += 256) {
             const int g = i / HD, d = i % HD;
-            float s = 0.f;
+            float sacc = 0.f;
 #pragma unroll
-            for (int k = 0; k < NS; k++) s += red[k][g][d];
-            po[(size_t)g * HD + d] = s;
+            for (int k = 0; k < NS; k++) sacc += red[k][g][d];
+            po[(size_t)g * HD + d] = sacc;
         }
     }
 }

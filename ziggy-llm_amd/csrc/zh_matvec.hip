@@ -15,6 +15,9 @@
 //   * Input prologues: plain, fused RMSNorm (each workgroup recomputes the
 //     1/rms scale; rmsNorm order (scale * x) * w as model/loader.zig:3404-3426),
 //     fused SiLU(gate) * up (the silu_down path, matvec.metal:2229-2300).
+#include <mutex>
+#include <unordered_map>
+
 #include "zh_internal.h"
 #include "zh_quant.h"
 
@@ -103,12 +106,10 @@ __device__ __forceinline__ void stage_x(XSlot &xs, int s, bool active, const MvP
 }
 
 template <int F, int IN, int OUT>
-__device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int wg_in_seg, float nscale, float *lds) {
+__device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int wg_in_seg, float *lds) {
     const int tid = threadIdx.x, T = p.team, teams = kThreads / T;
     const int team = tid / T, lane = tid % T;
     const bool active = lane < p.slots;
-    XSlot xs;
-    stage_x<F, IN>(xs, lane, active, p, nscale);
 
     const uint8_t *wbase = sg.w, *wbase2 = sg.w2;
     float wscale = p.weight_scale;
@@ -123,15 +124,36 @@ __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int 
     }
     const int r_begin = wg_in_seg * sg.rows_per_wg;
     const int r_end = min(r_begin + sg.rows_per_wg, sg.rows);
+
+    // Issue the first row's weight loads before staging the input: they do
+    // not depend on it, so HBM latency overlaps the norm and the staging.
+    int r = r_begin + team;
+    bool valid = !skip && r < r_end;
+    Raw<F> cur{}, cur2{};
+    if (valid && active) {
+        cur = slot_load<F>(wbase + (uint64_t)r * sg.stride, lane);
+        if (OUT == OUT_SWIGLU) cur2 = slot_load<F>(wbase2 + (uint64_t)r * sg.stride, lane);
+    }
+    float nscale = 1.f;
+    if (IN == IN_NORM) nscale = rms_scale(p.x, p.cols, p.eps, lds);
+    XSlot xs;
+    stage_x<F, IN>(xs, lane, active, p, nscale);
+
     float best_v = -INFINITY;
     int best_r = 0x7fffffff;
     for (int it = 0; it < p.rows_per_team; ++it) {
-        const int r = r_begin + it * teams + team;
-        const bool valid = !skip && r < r_end;
+        // double buffering: the next row's loads are in flight during this row's math
+        const int rn = r + teams;
+        const bool vn = !skip && it + 1 < p.rows_per_team && rn < r_end;
+        Raw<F> nxt{}, nxt2{};
+        if (vn && active) {
+            nxt = slot_load<F>(wbase + (uint64_t)rn * sg.stride, lane);
+            if (OUT == OUT_SWIGLU) nxt2 = slot_load<F>(wbase2 + (uint64_t)rn * sg.stride, lane);
+        }
         float v = 0.f, v2 = 0.f;
         if (valid && active) {
-            v = slot_dot<F>(wbase + (uint64_t)r * sg.stride, lane, xs);
-            if (OUT == OUT_SWIGLU) v2 = slot_dot<F>(wbase2 + (uint64_t)r * sg.stride, lane, xs);
+            v = slot_dot<F>(cur, lane, xs);
+            if (OUT == OUT_SWIGLU) v2 = slot_dot<F>(cur2, lane, xs);
         }
         v = team_sum(v, T, lds);
         if (OUT == OUT_SWIGLU) v2 = team_sum(v2, T, lds);
@@ -152,6 +174,10 @@ __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int 
                 }
             }
         }
+        cur = nxt;
+        cur2 = nxt2;
+        r = rn;
+        valid = vn;
     }
     if (OUT == OUT_ARGMAX) {
         __shared__ unsigned long long keys[kThreads];
@@ -178,12 +204,10 @@ __global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
     for (int i = 1; i < 4; i++)
         if (i < p.nseg && wg >= p.seg[i].wg_begin) si = i;
     const MvSeg &sg = p.seg[si];
-    float nscale = 1.f;
-    if (IN == IN_NORM) nscale = rms_scale(p.x, p.cols, p.eps, lds);
     if (F1 == F2 || sg.fmt == F1)
-        mv_body<F1, IN, OUT>(p, sg, wg - sg.wg_begin, nscale, lds);
+        mv_body<F1, IN, OUT>(p, sg, wg - sg.wg_begin, lds);
     else
-        mv_body<F2, IN, OUT>(p, sg, wg - sg.wg_begin, nscale, lds);
+        mv_body<F2, IN, OUT>(p, sg, wg - sg.wg_begin, lds);
 }
 
 // ---------------- host-side planning and dispatch ----------------
@@ -194,16 +218,18 @@ static int next_pow2(int v) {
     return t;
 }
 
+// Rows per team so that the grid fits in one resident wave of workgroups
+// (no tail), or one row per team when the matrix is too small to fill it.
 void plan_matvec(MvParams &p, int target_wgs) {
     p.slots = p.cols / 64;
     p.team = next_pow2(p.slots);
     if (p.team > kThreads) p.team = kThreads;
     const int teams = kThreads / p.team;
-    int total_rows = 0;
-    for (int i = 0; i < p.nseg; i++) total_rows += p.seg[i].rows;
-    int rpt = total_rows / (teams * (target_wgs > 0 ? target_wgs : 1024));
+    int team_rows = 0;
+    for (int i = 0; i < p.nseg; i++) team_rows += (p.seg[i].rows + teams - 1) / teams;
+    if (target_wgs < 1) target_wgs = 1;
+    int rpt = (team_rows + target_wgs - 1) / target_wgs;
     if (rpt < 1) rpt = 1;
-    if (rpt > 16) rpt = 16;
     p.rows_per_team = rpt;
     int wg = 0;
     for (int i = 0; i < p.nseg; i++) {
@@ -235,7 +261,40 @@ template <int F1, int F2> static MvKernel pick(int in, int out) {
     return nullptr;
 }
 
-hipError_t launch_matvec(const MvParams &p, int in, int out, hipStream_t s) {
+// Resident workgroups of kernel k on the whole device (cached per kernel).
+static int resident_wgs(MvKernel k) {
+    static std::mutex mu;
+    static std::unordered_map<const void *, int> cache;
+    static int cus = 0;
+    std::lock_guard<std::mutex> g(mu);
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    auto it = cache.find((const void *)k);
+    if (it != cache.end()) return it->second;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, 0) != hipSuccess || per_cu <= 0) per_cu = 2;
+    const int n = per_cu * cus;
+    cache[(const void *)k] = n;
+    return n;
+}
+
+// Grid size in units of one resident wave of workgroups; ZIGGY_HIP_MATVEC_WAVES
+// overrides the default of 1 (a tuning knob for sweeps).
+static float waves_of_workgroups() {
+    static float w = [] {
+        const char *e = getenv("ZIGGY_HIP_MATVEC_WAVES");
+        const float v = e ? (float)atof(e) : 1.0f;
+        return v > 0.f ? v : 1.0f;
+    }();
+    return w;
+}
+
+hipError_t launch_matvec(const MvParams &p_in, int in, int out, hipStream_t s) {
+    MvParams p = p_in;
     int f1 = p.seg[0].fmt, f2 = f1;
     for (int i = 1; i < p.nseg; i++)
         if (p.seg[i].fmt != f1) f2 = p.seg[i].fmt;
@@ -259,6 +318,7 @@ hipError_t launch_matvec(const MvParams &p, int in, int out, hipStream_t s) {
         k = mv_kernel<Q6_K, Q4_K, IN_NORM, OUT_STORE>;
     }
     if (!k) return hipErrorInvalidValue;
+    plan_matvec(p, (int)(resident_wgs(k) * waves_of_workgroups()));
     const int grid = total_wgs(p);
     if (grid <= 0) return hipSuccess;
     hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), 0, s, p);

@@ -104,17 +104,34 @@ struct XSlot {
     float sum[4];
 };
 
-// ---------------- slot dots: dot(64 weights of slot s in `row`, xs) ----------------
+// ---------------- slots: raw load (registers) + dot ----------------
+//
+// slot_load<F>(row, s) issues the 16-byte loads of slot s of `row` and
+// returns the raw words; slot_dot<F>(raw, s, xs) decodes them and returns
+// dot(64 weights, xs).  Splitting the two lets a kernel keep the next row's
+// loads in flight while it computes the current one.
 
-template <int F> __device__ __forceinline__ float slot_dot(const uint8_t *__restrict__ row, int s, const XSlot &xs);
+template <int F> struct Raw;
+template <> struct Raw<Q4_K> { uint4 hd, qa, qb; };
+template <> struct Raw<Q6_K> { uint4 qa, qb, qh; uint2 sc; uint32_t d; };
+template <> struct Raw<Q8_0> { uint4 a, b, c, e; uint32_t f; };
+template <> struct Raw<Q3_K> { uint4 hm, qs; uint32_t r0, r1, r2, d; };
+template <> struct Raw<IQ4_XS> { uint4 q0, q1; uint32_t dsh, sl; };
+template <> struct Raw<F16> { uint4 w[8]; };
+template <> struct Raw<F32> { uint4 w[16]; };
+
+template <int F> __device__ __forceinline__ Raw<F> slot_load(const uint8_t *__restrict__ row, int s);
+template <int F> __device__ __forceinline__ float slot_dot(const Raw<F> &r, int s, const XSlot &xs);
 
 // Q4_K: slot = (block b, group g): 32 qs bytes -> sub-block 2g (low nibbles) and 2g+1 (high).
-template <> __device__ __forceinline__ float slot_dot<Q4_K>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
-    const int g = s & 3;
+template <> __device__ __forceinline__ Raw<Q4_K> slot_load<Q4_K>(const uint8_t *__restrict__ row, int s) {
     const uint8_t *blk = row + (s >> 2) * 144;
-    const uint4 hd = ld16(blk);
-    const uint4 qa = ld16(blk + 16 + 32 * g);
-    const uint4 qb = ld16(blk + 32 + 32 * g);
+    const int g = s & 3;
+    return {ld16(blk), ld16(blk + 16 + 32 * g), ld16(blk + 32 + 32 * g)};
+}
+template <> __device__ __forceinline__ float slot_dot<Q4_K>(const Raw<Q4_K> &r, int s, const XSlot &xs) {
+    const int g = s & 3;
+    const uint4 hd = r.hd;
     const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
     // getScaleMinK4 for j = 2g, 2g+1 with lane-uniform formulas
     const bool lo = g < 2;
@@ -125,7 +142,7 @@ template <> __device__ __forceinline__ float slot_dot<Q4_K>(const uint8_t *__res
     const uint32_t m0 = bfe(a_m, o0 + om, wa) | (bfe(hd.z, o0 + 6, wb) << 4);
     const uint32_t sc1 = bfe(a_sc, o1, wa) | (bfe(hd.y, o1 + 6, wb) << 4);
     const uint32_t m1 = bfe(a_m, o1 + om, wa) | (bfe(hd.z, o1 + 6, wb) << 4);
-    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
     float dl = 0.f, dh = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
@@ -138,24 +155,25 @@ template <> __device__ __forceinline__ float slot_dot<Q4_K>(const uint8_t *__res
         }
     }
     const float d1 = d * (float)sc0, mm1 = dmin * (float)m0, d2 = d * (float)sc1, mm2 = dmin * (float)m1;
-    float r = d1 * dl;
-    r = fmaf(-mm1, xs.sum[0] + xs.sum[1], r);
-    r = fmaf(d2, dh * 0.0625f, r);
-    r = fmaf(-mm2, xs.sum[2] + xs.sum[3], r);
-    return r;
+    float res = d1 * dl;
+    res = fmaf(-mm1, xs.sum[0] + xs.sum[1], res);
+    res = fmaf(d2, dh * 0.0625f, res);
+    res = fmaf(-mm2, xs.sum[2] + xs.sum[3], res);
+    return res;
 }
 
 // Q6_K: slot = (block b, half h, l0 in {0,16}): ql[64h+l0..], ql[64h+32+l0..], qh[32h+l0..].
-template <> __device__ __forceinline__ float slot_dot<Q6_K>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+template <> __device__ __forceinline__ Raw<Q6_K> slot_load<Q6_K>(const uint8_t *__restrict__ row, int s) {
     const uint8_t *blk = row + (s >> 2) * 210;
     const int h = (s >> 1) & 1, l0 = (s & 1) * 16;
-    const uint4 qa = ld16(blk + 64 * h + l0);
-    const uint4 qb = ld16(blk + 64 * h + 32 + l0);
-    const uint4 qh = ld16(blk + 128 + 32 * h + l0);
-    const uint2 scw = ld8(blk + 192 + 8 * h);
-    const float d = h2f(ld2(blk + 208));
+    return {ld16(blk + 64 * h + l0), ld16(blk + 64 * h + 32 + l0), ld16(blk + 128 + 32 * h + l0),
+            ld8(blk + 192 + 8 * h), ld2(blk + 208)};
+}
+template <> __device__ __forceinline__ float slot_dot<Q6_K>(const Raw<Q6_K> &r, int s, const XSlot &xs) {
+    const float d = h2f(r.d);
     const int sb0 = s & 1;
-    const uint32_t a[4] = {qa.x, qa.y, qa.z, qa.w}, bq[4] = {qb.x, qb.y, qb.z, qb.w}, hh[4] = {qh.x, qh.y, qh.z, qh.w};
+    const uint32_t a[4] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w}, bq[4] = {r.qb.x, r.qb.y, r.qb.z, r.qb.w};
+    const uint32_t hh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -171,22 +189,24 @@ template <> __device__ __forceinline__ float slot_dot<Q6_K>(const uint8_t *__res
             acc[3] = fmaf(ub(u3, b), xs.v[48 + 4 * k + b], acc[3]);
         }
     }
-    // sc[8h + l0/16 + 2w]: byte sb0 (+2) of scw.x (w = 0, 1) and scw.y (w = 2, 3)
-    const float s0 = d * sb(scw.x, sb0), s1 = d * sb(scw.x, sb0 + 2);
-    const float s2 = d * sb(scw.y, sb0), s3 = d * sb(scw.y, sb0 + 2);
-    float r = s0 * fmaf(-32.f, xs.sum[0], acc[0]);
-    r = fmaf(s1, fmaf(-32.f, xs.sum[1], acc[1]), r);
-    r = fmaf(s2, fmaf(-32.f, xs.sum[2], acc[2]), r);
-    r = fmaf(s3, fmaf(-32.f, xs.sum[3], acc[3]), r);
-    return r;
+    // sc[8h + l0/16 + 2w]: byte sb0 (+2) of sc.x (w = 0, 1) and sc.y (w = 2, 3); values are q + 32
+    const float s0 = d * sb(r.sc.x, sb0), s1 = d * sb(r.sc.x, sb0 + 2);
+    const float s2 = d * sb(r.sc.y, sb0), s3 = d * sb(r.sc.y, sb0 + 2);
+    float res = s0 * fmaf(-32.f, xs.sum[0], acc[0]);
+    res = fmaf(s1, fmaf(-32.f, xs.sum[1], acc[1]), res);
+    res = fmaf(s2, fmaf(-32.f, xs.sum[2], acc[2]), res);
+    res = fmaf(s3, fmaf(-32.f, xs.sum[3], acc[3]), res);
+    return res;
 }
 
 // Q8_0: slot = 2 consecutive 34-byte blocks (68 bytes, 4-byte aligned within a row).
-template <> __device__ __forceinline__ float slot_dot<Q8_0>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+template <> __device__ __forceinline__ Raw<Q8_0> slot_load<Q8_0>(const uint8_t *__restrict__ row, int s) {
     const uint8_t *p = row + 68 * s;
-    const uint4 a = ld16(p), b = ld16(p + 16), c = ld16(p + 32), e = ld16(p + 48);
-    const uint32_t f = ld4(p + 64);
-    const uint32_t w[17] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, e.x, e.y, e.z, e.w, f};
+    return {ld16(p), ld16(p + 16), ld16(p + 32), ld16(p + 48), ld4(p + 64)};
+}
+template <> __device__ __forceinline__ float slot_dot<Q8_0>(const Raw<Q8_0> &r, int s, const XSlot &xs) {
+    const uint32_t w[17] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c.x,
+                            r.c.y, r.c.z, r.c.w, r.e.x, r.e.y, r.e.z, r.e.w, r.f};
     const float d0 = h2f(w[0]), d1 = h2f(w[8] >> 16);
     // signed bytes read as unsigned q + 128 (xor 0x80); the 128 * sum(x) offset is removed below
     uint32_t u[17];
@@ -205,14 +225,16 @@ template <> __device__ __forceinline__ float slot_dot<Q8_0>(const uint8_t *__res
 }
 
 // Q3_K: slot = (block b, half h, 16-group sh): qs[32h+16sh..], hmask[16sh..], 4 shifts.
-template <> __device__ __forceinline__ float slot_dot<Q3_K>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+template <> __device__ __forceinline__ Raw<Q3_K> slot_load<Q3_K>(const uint8_t *__restrict__ row, int s) {
     const uint8_t *blk = row + (s >> 2) * 110;
     const int h = (s >> 1) & 1, sh = s & 1;
-    const uint4 hm = ld16(blk + 16 * sh);
-    const uint4 qs = ld16(blk + 32 + 32 * h + 16 * sh);
-    const uint32_t r0 = ld4(blk + 96), r1 = ld4(blk + 100), r2 = ld4(blk + 104);
-    const float dall = h2f(ld2(blk + 108));
-    const uint32_t hmw[4] = {hm.x, hm.y, hm.z, hm.w}, qw[4] = {qs.x, qs.y, qs.z, qs.w};
+    return {ld16(blk + 16 * sh), ld16(blk + 32 + 32 * h + 16 * sh), ld4(blk + 96), ld4(blk + 100), ld4(blk + 104),
+            ld2(blk + 108)};
+}
+template <> __device__ __forceinline__ float slot_dot<Q3_K>(const Raw<Q3_K> &r, int s, const XSlot &xs) {
+    const int h = (s >> 1) & 1, sh = s & 1;
+    const float dall = h2f(r.d);
+    const uint32_t hmw[4] = {r.hm.x, r.hm.y, r.hm.z, r.hm.w}, qw[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -225,54 +247,81 @@ template <> __device__ __forceinline__ float slot_dot<Q3_K>(const uint8_t *__res
             for (int b = 0; b < 4; b++) acc[j] = fmaf(ub(u, b), xs.v[16 * j + 4 * k + b], acc[j]);
         }
     }
-    float r = 0.f;
+    float res = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         // scale index i = 8h + 2j + sh (expandQ3KScales)
         const int i = 8 * h + 2 * j + sh, qd = i & 3, grp = i >> 2;
-        const uint32_t lowsrc = (grp & 1) ? r1 : r0;
+        const uint32_t lowsrc = (grp & 1) ? r.r1 : r.r0;
         const uint32_t low4 = bfe(lowsrc, 8 * qd + 4 * (grp >> 1), 4);
-        const uint32_t hi2 = bfe(r2, 8 * qd + 2 * grp, 2);
+        const uint32_t hi2 = bfe(r.r2, 8 * qd + 2 * grp, 2);
         const float sc = (float)((int)(low4 | (hi2 << 4)) - 32);
-        r = fmaf(dall * sc, fmaf(-4.f, xs.sum[j], acc[j]), r);
+        res = fmaf(dall * sc, fmaf(-4.f, xs.sum[j], acc[j]), res);
     }
-    return r;
+    return res;
 }
 
 __device__ __constant__ static const float kIq4nl[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
                                                          1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
 
+// kvalues_iq4nl + 128 as bytes, 4 entries per word, for register table lookups with v_perm
+#define ZH_IQ4_T0 (((uint32_t)(-127 + 128)) | ((uint32_t)(-104 + 128) << 8) | ((uint32_t)(-83 + 128) << 16) | ((uint32_t)(-65 + 128) << 24))
+#define ZH_IQ4_T1 (((uint32_t)(-49 + 128)) | ((uint32_t)(-35 + 128) << 8) | ((uint32_t)(-22 + 128) << 16) | ((uint32_t)(-10 + 128) << 24))
+#define ZH_IQ4_T2 (((uint32_t)(1 + 128)) | ((uint32_t)(13 + 128) << 8) | ((uint32_t)(25 + 128) << 16) | ((uint32_t)(38 + 128) << 24))
+#define ZH_IQ4_T3 (((uint32_t)(53 + 128)) | ((uint32_t)(69 + 128) << 8) | ((uint32_t)(89 + 128) << 16) | ((uint32_t)(113 + 128) << 24))
+
+// Looks up 4 nibbles (one per byte of n, each 0..15) in kvalues_iq4nl + 128.
+__device__ __forceinline__ uint32_t iq4_lookup4(uint32_t n) {
+    const uint32_t sel = n & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(ZH_IQ4_T1, ZH_IQ4_T0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(ZH_IQ4_T3, ZH_IQ4_T2, sel);
+    // byte i of the result: lo.byte[i] (selector i) or hi.byte[i] (selector 4 + i) by bit 3 of the nibble
+    const uint32_t pick = 0x03020100u + ((n & 0x08080808u) >> 1);
+    return opaque(__builtin_amdgcn_perm(hi, lo, pick));
+}
+
 // IQ4_XS: slot = (block b, sub-block pair k): sub-blocks 2k, 2k+1.
-template <> __device__ __forceinline__ float slot_dot<IQ4_XS>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+template <> __device__ __forceinline__ Raw<IQ4_XS> slot_load<IQ4_XS>(const uint8_t *__restrict__ row, int s) {
     const uint8_t *blk = row + (s >> 2) * 136;
     const int k = s & 3;
-    const float d = h2f(ld2(blk));
-    const uint32_t sh = ld2(blk + 2), sl = blk[4 + k];
-    const uint4 q0 = ld16(blk + 8 + 32 * k), q1 = ld16(blk + 24 + 32 * k);
+    return {ld16(blk + 8 + 32 * k), ld16(blk + 24 + 32 * k), ld4(blk), ld4(blk + 4)};
+}
+template <> __device__ __forceinline__ float slot_dot<IQ4_XS>(const Raw<IQ4_XS> &r, int s, const XSlot &xs) {
+    const int k = s & 3;
+    const float d = h2f(r.dsh);
+    const uint32_t sh = r.dsh >> 16, sl = bfe(r.sl, 8 * k, 8);
     const uint32_t ls0 = (sl & 0xF) | (bfe(sh, 4 * k, 2) << 4), ls1 = (sl >> 4) | (bfe(sh, 4 * k + 2, 2) << 4);
-    const uint32_t w0[4] = {q0.x, q0.y, q0.z, q0.w}, w1[4] = {q1.x, q1.y, q1.z, q1.w};
+    const uint32_t w0[4] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w}, w1[4] = {r.q1.x, r.q1.y, r.q1.z, r.q1.w};
     float a0 = 0.f, a1 = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
+        const uint32_t l0 = iq4_lookup4(w0[c] & 0x0F0F0F0Fu), h0 = iq4_lookup4((w0[c] >> 4) & 0x0F0F0F0Fu);
+        const uint32_t l1 = iq4_lookup4(w1[c] & 0x0F0F0F0Fu), h1 = iq4_lookup4((w1[c] >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-            const uint32_t y0 = (w0[c] >> (8 * b)) & 0xFFu, y1 = (w1[c] >> (8 * b)) & 0xFFu;
-            a0 = fmaf(kIq4nl[y0 & 0xF], xs.v[4 * c + b], a0);
-            a0 = fmaf(kIq4nl[y0 >> 4], xs.v[16 + 4 * c + b], a0);
-            a1 = fmaf(kIq4nl[y1 & 0xF], xs.v[32 + 4 * c + b], a1);
-            a1 = fmaf(kIq4nl[y1 >> 4], xs.v[48 + 4 * c + b], a1);
+            a0 = fmaf(ub(l0, b), xs.v[4 * c + b], a0);
+            a0 = fmaf(ub(h0, b), xs.v[16 + 4 * c + b], a0);
+            a1 = fmaf(ub(l1, b), xs.v[32 + 4 * c + b], a1);
+            a1 = fmaf(ub(h1, b), xs.v[48 + 4 * c + b], a1);
         }
     }
+    a0 = fmaf(-128.f, xs.sum[0] + xs.sum[1], a0);
+    a1 = fmaf(-128.f, xs.sum[2] + xs.sum[3], a1);
     return fmaf(d * (float)((int)ls1 - 32), a1, (d * (float)((int)ls0 - 32)) * a0);
 }
 
-template <> __device__ __forceinline__ float slot_dot<F16>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+template <> __device__ __forceinline__ Raw<F16> slot_load<F16>(const uint8_t *__restrict__ row, int s) {
+    Raw<F16> r;
     const uint8_t *p = row + 128 * s;
+#pragma unroll
+    for (int c = 0; c < 8; c++) r.w[c] = ld16(p + 16 * c);
+    return r;
+}
+template <> __device__ __forceinline__ float slot_dot<F16>(const Raw<F16> &r, int s, const XSlot &xs) {
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < 8; c++) {
-        const uint4 v = ld16(p + 16 * c);
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t w[4] = {r.w[c].x, r.w[c].y, r.w[c].z, r.w[c].w};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             acc = fmaf(h2f(w[k]), xs.v[8 * c + 2 * k], acc);
@@ -282,16 +331,21 @@ template <> __device__ __forceinline__ float slot_dot<F16>(const uint8_t *__rest
     return acc;
 }
 
-template <> __device__ __forceinline__ float slot_dot<F32>(const uint8_t *__restrict__ row, int s, const XSlot &xs) {
+template <> __device__ __forceinline__ Raw<F32> slot_load<F32>(const uint8_t *__restrict__ row, int s) {
+    Raw<F32> r;
     const uint8_t *p = row + 256 * s;
+#pragma unroll
+    for (int c = 0; c < 16; c++) r.w[c] = ld16(p + 16 * c);
+    return r;
+}
+template <> __device__ __forceinline__ float slot_dot<F32>(const Raw<F32> &r, int s, const XSlot &xs) {
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < 16; c++) {
-        const uint4 v = ld16(p + 16 * c);
-        acc = fmaf(__uint_as_float(v.x), xs.v[4 * c + 0], acc);
-        acc = fmaf(__uint_as_float(v.y), xs.v[4 * c + 1], acc);
-        acc = fmaf(__uint_as_float(v.z), xs.v[4 * c + 2], acc);
-        acc = fmaf(__uint_as_float(v.w), xs.v[4 * c + 3], acc);
+        acc = fmaf(__uint_as_float(r.w[c].x), xs.v[4 * c + 0], acc);
+        acc = fmaf(__uint_as_float(r.w[c].y), xs.v[4 * c + 1], acc);
+        acc = fmaf(__uint_as_float(r.w[c].z), xs.v[4 * c + 2], acc);
+        acc = fmaf(__uint_as_float(r.w[c].w), xs.v[4 * c + 3], acc);
     }
     return acc;
 }

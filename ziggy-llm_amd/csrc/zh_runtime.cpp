@@ -652,3 +652,53 @@ int ziggy_hip_sigmoid_scale_add_f32(ZiggyHipContext *ctx, ZiggyHipBuffer *d, con
 }
 
 }  // extern "C"
+
+extern "C" int ziggy_hip_time_matvec(ZiggyHipContext *ctx, uint32_t type, const ZiggyHipBuffer *m, uint32_t copies,
+                                     size_t copy_stride, const ZiggyHipBuffer *in, ZiggyHipBuffer *out, uint32_t rows,
+                                     uint32_t cols, uint32_t iterations, uint64_t *avg_ns, char *err,
+                                     size_t err_len) {
+    uint64_t stride;
+    if (copies == 0 || iterations == 0 || !avg_ns) {
+        set_err(err, err_len, "invalid time_matvec arguments");
+        return ZIGGY_HIP_INVALID_ARGUMENT;
+    }
+    int st = check_matvec(ctx, type, m, (size_t)(copies - 1) * copy_stride, in, out, 0, rows, cols, &stride, err,
+                          err_len);
+    if (st) return st;
+    if (copy_stride < stride * rows) {
+        set_err(err, err_len, "copy stride smaller than one matrix");
+        return ZIGGY_HIP_INVALID_ARGUMENT;
+    }
+    hipEvent_t e0, e1;
+    ZH_TRY(hipEventCreate(&e0), "time_matvec");
+    if (hipEventCreate(&e1) != hipSuccess) {
+        hipEventDestroy(e0);
+        set_err(err, err_len, "event creation failed");
+        return ZIGGY_HIP_EXECUTION_FAILED;
+    }
+    MvParams p{};
+    p.nseg = 1;
+    p.seg[0].stride = stride;
+    p.seg[0].y = (float *)out->ptr;
+    p.seg[0].rows = (int)rows;
+    p.seg[0].fmt = (int)type;
+    p.cols = (int)cols;
+    p.x = (const float *)in->ptr;
+    double total = 0.0;
+    hipError_t e = hipSuccess;
+    for (uint32_t i = 0; i < iterations && e == hipSuccess; i++) {
+        p.seg[0].w = (const uint8_t *)m->ptr + (size_t)(i % copies) * copy_stride;
+        e = hipEventRecord(e0, ctx->stream);
+        if (e == hipSuccess) e = launch_matvec(p, IN_PLAIN, OUT_STORE, ctx->stream);
+        if (e == hipSuccess) e = hipEventRecord(e1, ctx->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        float ms = 0.f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+        total += ms;
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (e != hipSuccess) return hip_fail(e, "time_matvec", err, err_len);
+    *avg_ns = (uint64_t)(total * 1e6 / iterations);
+    return ZIGGY_HIP_OK;
+}

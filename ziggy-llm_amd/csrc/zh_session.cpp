@@ -266,7 +266,20 @@ hipError_t enqueue_step(ZiggyHipSession *s, hipStream_t st) {
     return enqueue_kernel(s, ZIGGY_HIP_KERNEL_OUTPUT, 0, &s->st->pos, 0, st);
 }
 
+// One step: a replay of the captured graph, or (ZIGGY_HIP_GRAPH=0, e.g. under
+// a profiler that cannot intercept graph launches) the same kernels enqueued
+// directly; both read token and position from the device step state.
+hipError_t launch_step(ZiggyHipSession *s, hipStream_t st) {
+    return s->graph ? hipGraphLaunch(s->graph, st) : enqueue_step(s, st);
+}
+
+bool graphs_enabled() {
+    const char *e = getenv("ZIGGY_HIP_GRAPH");
+    return !(e && e[0] == '0');
+}
+
 int build_graph(ZiggyHipSession *s, char *err, size_t err_len) {
+    if (!graphs_enabled()) return ZIGGY_HIP_OK;
     hipStream_t st = s->ctx->stream;
     hipGraph_t g = nullptr;
     ZH_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "graph capture begin");
@@ -558,7 +571,7 @@ static int host_step(ZiggyHipSession *s, uint32_t token, bool output, uint32_t *
     h->token = token;
     hipStream_t st = s->ctx->stream;
     ZH_TRY(hipMemcpyAsync(s->st, h, sizeof(StepState), hipMemcpyHostToDevice, st), "step state");
-    ZH_TRY(hipGraphLaunch(s->graph, st), "step graph");
+    ZH_TRY(launch_step(s, st), "step graph");
     if (output) ZH_TRY(hipMemcpyAsync(h, s->st, sizeof(StepState), hipMemcpyDeviceToHost, st), "step readback");
     ZH_TRY(hipStreamSynchronize(st), "step");
     s->position++;
@@ -625,11 +638,11 @@ int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint3
     ZH_TRY(hipMemcpyAsync(s->st, h, sizeof(StepState), hipMemcpyHostToDevice, st), "step state");
     ZH_TRY(hipStreamSynchronize(st), "generate setup");
     // prompt steps, then the timed decode steps (the decode_ns bracket of model/loader.zig:2135-2257)
-    for (uint32_t i = 0; i < prompt_len; i++) ZH_TRY(hipGraphLaunch(s->graph, st), "prompt step");
+    for (uint32_t i = 0; i < prompt_len; i++) ZH_TRY(launch_step(s, st), "prompt step");
     ZH_TRY(hipStreamSynchronize(st), "prompt");
     ZH_TRY(hipEventRecord(s->ctx->seq_begin, st), "generate");
     const uint64_t t0 = now_ns();
-    for (uint32_t i = 0; i < steps; i++) ZH_TRY(hipGraphLaunch(s->graph, st), "decode step");
+    for (uint32_t i = 0; i < steps; i++) ZH_TRY(launch_step(s, st), "decode step");
     ZH_TRY(hipEventRecord(s->ctx->seq_end, st), "generate");
     ZH_TRY(hipStreamSynchronize(st), "decode");
     const uint64_t t1 = now_ns();

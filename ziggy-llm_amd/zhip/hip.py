@@ -94,6 +94,7 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_run_matvec_silu_down_add": [vp, u32, vp, vp, vp, vp, u32, u32] + E,
         "ziggy_hip_run_matvec_argmax": [vp, u32, vp, vp, vp, u32, u32] + E,
         "ziggy_hip_dequantize_rows": [vp, u32, vp, sz, vp, u32, u32] + E,
+        "ziggy_hip_time_matvec": [vp, u32, vp, u32, sz, vp, vp, u32, u32, u32, ctypes.POINTER(ctypes.c_uint64)] + E,
         "ziggy_hip_indexed_matvec": [vp, u32, vp, vp, vp, u32, u32, vp, u32, u32, i] + E,
         "ziggy_hip_dual_indexed_matvec": [vp, u32, vp, vp, vp, vp, vp, u32, u32, vp, u32, u32] + E,
         "ziggy_hip_apply_rope_f32": [vp, vp, u32, u32, u32, u32, f, u32] + E,
@@ -211,6 +212,15 @@ class Context:
 
     def matvec_argmax(self, ttype, m, x, state, rows, cols):
         _call("ziggy_hip_run_matvec_argmax", self.h, ttype, m.h, x.h, state.h, rows, cols)
+
+    def time_matvec(self, ttype, mats: Buffer, copies, copy_stride, x, y, rows, cols, iterations) -> int:
+        ns = ctypes.c_uint64()
+        _call("ziggy_hip_time_matvec", self.h, ttype, mats.h, copies, copy_stride, x.h, y.h, rows, cols, iterations,
+              ctypes.byref(ns))
+        return ns.value
+
+    def copy(self, src: Buffer, src_off: int, dst: Buffer, dst_off: int, nbytes: int):
+        _call("ziggy_hip_copy_buffer_region", self.h, src.h, src_off, dst.h, dst_off, nbytes)
 
     def dequantize(self, ttype, m: Buffer, out: Buffer, rows, cols, m_off=0):
         _call("ziggy_hip_dequantize_rows", self.h, ttype, m.h, m_off, out.h, rows, cols)
