@@ -96,8 +96,11 @@ def test_q4k_reference_matrix(hip_ctx):
     assert np.array_equal(deq.read().view(np.uint32), zo.dequantize(Q4_K, m, rows, cols).ravel().view(np.uint32))
 
 
-SHAPES = [(96, 256), (300, 1024), (4096, 4096), (14336, 4096), (4096, 14336), (1024, 2048), (4096, 12288),
-          (128256, 4096)]
+# cols 64..16384 cover every team width (1..256 lanes) and both partial
+# (slots < team) and exact teams; rows cover ragged workgroup tails.
+SHAPES = [(7, 64), (33, 128), (96, 256), (50, 512), (300, 1024), (4096, 4096), (14336, 4096), (4096, 14336),
+          (1024, 2048), (4096, 12288), (129, 8192), (65, 16384), (128256, 4096)]
+BLOCK_VALUES = {Q4_K: 256, Q6_K: 256, Q3_K: 256, IQ4_XS: 256, Q8_0: 32, F16: 1, F32: 1}
 
 
 @pytest.mark.parametrize("ttype", [Q4_K, Q6_K, Q8_0, Q3_K, IQ4_XS, F16, F32])
@@ -106,6 +109,8 @@ def test_matvec_parity(hip_ctx, ttype, shape):
     rows, cols = shape
     if ttype in (F16, F32, Q3_K, IQ4_XS) and rows * cols > 4096 * 4096:
         pytest.skip("large dense/extra-format shapes are covered by the smaller cases")
+    if cols % BLOCK_VALUES[ttype]:
+        pytest.skip("row length is not a whole number of blocks of this format")
     say(f"matvec {ttype} {rows}x{cols}")
     q = random_weights(ttype, rows, cols, rows + cols)
     x = synth.normal_row(77, 0, cols, 0.0, 1.0)

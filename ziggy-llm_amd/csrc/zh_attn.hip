@@ -155,23 +155,74 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnParams p) {
     }
 }
 
+// One workgroup per query head.  Thread (d, sg) folds splits sg, sg + S, ...
+// (S = 256 / HD split groups) for dimension d; the split statistics are
+// staged in LDS once, and the S partial sums are combined in LDS.
 template <int HD>
-__global__ void __launch_bounds__(HD) attn_merge_kernel(AttnParams p) {
-    const int h = blockIdx.x, d = threadIdx.x;
+__global__ void __launch_bounds__(256) attn_merge_kernel(AttnParams p) {
+    constexpr int S = 256 / HD;
+    const int h = blockIdx.x, tid = threadIdx.x, d = tid % HD, sg = tid / HD;
     const int pos = p.position_dev ? *p.position_dev : p.position;
     const int G = p.head_count / p.head_count_kv, kvh = h / G, g = h % G;
     const int nsplit = (pos - p.window_start) / kChunk + 1;
-    const float *ml = p.part_ml + (size_t)kvh * p.max_splits * kMaxGroup * 2;
-    const float *po = p.part_o + (size_t)kvh * p.max_splits * kMaxGroup * HD;
+    const float *ml = p.part_ml + (size_t)kvh * p.max_splits * kMaxGroup * 2 + 2 * g;
+    const float *po = p.part_o + (size_t)kvh * p.max_splits * kMaxGroup * HD + (size_t)g * HD + d;
+    constexpr int kStage = 1024;  // splits whose statistics fit the LDS stage
+    __shared__ float m_s[kStage], l_s[kStage], red[256];
+    __shared__ float wmax_s[4];
+
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, ml[(size_t)s * kMaxGroup * 2 + 2 * g]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < nsplit; s++) {
-        const float w = expf(ml[(size_t)s * kMaxGroup * 2 + 2 * g] - M);
-        den = fmaf(w, ml[(size_t)s * kMaxGroup * 2 + 2 * g + 1], den);
-        num = fmaf(w, po[(size_t)s * kMaxGroup * HD + (size_t)g * HD + d], num);
+    for (int s = tid; s < nsplit; s += 256) {
+        const float m = ml[(size_t)s * kMaxGroup * 2], l = ml[(size_t)s * kMaxGroup * 2 + 1];
+        if (s < kStage) m_s[s] = m, l_s[s] = l;
+        M = fmaxf(M, m);
     }
-    p.out[(size_t)h * HD + d] = num / den;
+    M = wmax(M);
+    if ((tid & 63) == 0) wmax_s[tid >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(wmax_s[0], wmax_s[1]), fmaxf(wmax_s[2], wmax_s[3]));
+
+    float num = 0.f, den = 0.f;
+    int s = sg;
+    // 4 splits per step: their loads are independent of each other
+    for (; s + 3 * S < nsplit; s += 4 * S) {
+        float o[4], m[4], l[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int su = s + u * S;
+            o[u] = po[(size_t)su * kMaxGroup * HD];
+            if (su < kStage) {
+                m[u] = m_s[su], l[u] = l_s[su];
+            } else {
+                m[u] = ml[(size_t)su * kMaxGroup * 2], l[u] = ml[(size_t)su * kMaxGroup * 2 + 1];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float w = expf(m[u] - M);
+            den = fmaf(w, l[u], den);
+            num = fmaf(w, o[u], num);
+        }
+    }
+    for (; s < nsplit; s += S) {
+        const float m = s < kStage ? m_s[s] : ml[(size_t)s * kMaxGroup * 2];
+        const float l = s < kStage ? l_s[s] : ml[(size_t)s * kMaxGroup * 2 + 1];
+        const float w = expf(m - M);
+        den = fmaf(w, l, den);
+        num = fmaf(w, po[(size_t)s * kMaxGroup * HD], num);
+    }
+    if (S > 1) {
+        red[tid] = num;
+        __syncthreads();
+        if (sg == 0)
+            for (int k = 1; k < S; k++) num += red[k * HD + d];
+        __syncthreads();
+        red[tid] = den;
+        __syncthreads();
+        if (sg == 0)
+            for (int k = 1; k < S; k++) den += red[k * HD + d];
+    }
+    if (sg == 0) p.out[(size_t)h * HD + d] = num / den;
 }
 
 size_t attention_scratch_floats(int head_count, int head_dim, int max_splits) {
@@ -185,10 +236,10 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
     const dim3 grid(p.max_splits, p.head_count_kv);
     if (p.head_dim == 128) {
         hipLaunchKernelGGL(attn_partial_kernel<128>, grid, dim3(256), 0, s, p);
-        hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(p.head_count), dim3(128), 0, s, p);
+        hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(p.head_count), dim3(256), 0, s, p);
     } else if (p.head_dim == 64) {
         hipLaunchKernelGGL(attn_partial_kernel<64>, grid, dim3(256), 0, s, p);
-        hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(p.head_count), dim3(64), 0, s, p);
+        hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(p.head_count), dim3(256), 0, s, p);
     } else if (p.head_dim == 256) {
         hipLaunchKernelGGL(attn_partial_kernel<256>, grid, dim3(256), 0, s, p);
         hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(p.head_count), dim3(256), 0, s, p);

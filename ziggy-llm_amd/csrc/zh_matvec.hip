@@ -1,20 +1,27 @@
 // zh_matvec.hip -- batch-1 dequant-matvec kernels for gfx950.
 //
-// Design (bandwidth-bound, VALU co-limited for Q4_K):
+// Design (HBM-bound; the point is to keep enough weight bytes in flight):
 //   * A row is processed by a "team" of T lanes (T = next power of two of
 //     cols/64, at most 256); lane j owns weight slot j (64 weights) of every
 //     row the team visits, so its 64 activations are loaded (and normalised /
-//     SiLU-gated when fused) once per workgroup and stay in VGPRs.
+//     SiLU-gated when fused) once per workgroup and stay in VGPRs.  A team
+//     covers the whole input vector, which lets the fused RMSNorm take its
+//     sum of squares from the staged slots (one pass over x).
 //   * Quant blocks are read in their native GGUF layout with 16-byte loads;
 //     scales are unpacked in registers (zh_quant.h).
-//   * Team partial sums are reduced with cross-lane shuffles; teams wider than
-//     a wavefront finish the reduction through LDS.
+//   * Weight loads run ring_depth() rows ahead through a ring of register buffers.
+//     Every load is unconditional (rows past the team's range re-read its
+//     last row), so the compiler's in-order vmcnt waits for the row being
+//     consumed only, never for the rows behind it.
+//   * Team sums use DPP row operations inside a wavefront (the total lands in
+//     the team's last lane); teams wider than a wavefront finish through LDS
+//     with one barrier per row (double-buffered slots).
 //   * Epilogues: store, residual add, SwiGLU pair (silu(gate) * up from two
 //     matrices sharing the staged input), greedy argmax (packed 64-bit
 //     atomicMax, ties to the lowest row), expert-weighted add.
-//   * Input prologues: plain, fused RMSNorm (each workgroup recomputes the
-//     1/rms scale; rmsNorm order (scale * x) * w as model/loader.zig:3404-3426),
-//     fused SiLU(gate) * up (the silu_down path, matvec.metal:2229-2300).
+//   * Input prologues: plain, fused RMSNorm (rmsNorm order (scale * x) * w as
+//     model/loader.zig:3404-3426), fused SiLU(gate) * up (the silu_down path,
+//     matvec.metal:2229-2300).
 #include <mutex>
 #include <unordered_map>
 
@@ -24,24 +31,38 @@
 namespace zh {
 
 constexpr int kThreads = 256;
+// Rows per team in flight (ring of register buffers); the dense formats hold
+// 128 / 256 bytes per lane and row, so their rings are shorter.
+template <int F> constexpr int ring_depth() { return F == F32 ? 1 : F == F16 ? 2 : 3; }
 
-__device__ __forceinline__ float wave_sum(float v, int width) {
-    for (int o = width >> 1; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+// v + (v permuted by a DPP control); rows outside ROW_MASK add 0.
+template <int CTRL, int ROW_MASK> __device__ __forceinline__ float dpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum over aligned groups of T lanes (T a power of two, <= 64) of a wavefront.
+// The group total is valid in the group's last lane (in every lane for T <= 16).
+__device__ __forceinline__ float group_sum(float v, int T) {
+    if (T >= 2) v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    if (T >= 4) v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    if (T >= 8) v = dpp_add<0x141, 0xF>(v);  // row_half_mirror
+    if (T >= 16) v = dpp_add<0x140, 0xF>(v); // row_mirror
+    if (T >= 32) v = dpp_add<0x142, 0xA>(v); // row_bcast:15 into rows 1 and 3
+    if (T >= 64) v = dpp_add<0x143, 0xC>(v); // row_bcast:31 into rows 2 and 3
     return v;
 }
 
-// Reduces v over a team of T lanes; valid result in every lane of the team
-// for T <= 64, in lane 0 of the team for T > 64 (uses lds[4], two barriers).
-__device__ __forceinline__ float team_sum(float v, int T, float *lds) {
-    if (T <= 64) return wave_sum(v, T);
-    v = wave_sum(v, 64);
+// Team sum; valid in the team's last lane.  Teams wider than a wavefront use
+// lds[slot*4 .. slot*4+3] and one barrier (callers alternate `slot`).
+__device__ __forceinline__ float team_sum(float v, int T, float *lds, int slot) {
+    if (T <= 64) return group_sum(v, T);
+    v = group_sum(v, 64);
     const int tid = threadIdx.x, wave = tid >> 6;
-    if ((tid & 63) == 0) lds[wave] = v;
+    if ((tid & 63) == 63) lds[slot * 4 + wave] = v;
     __syncthreads();
     const int per = T >> 6, first = (wave / per) * per;
     float r = 0.f;
-    for (int i = 0; i < per; i++) r += lds[first + i];
-    __syncthreads();
+    for (int i = 0; i < per; i++) r += lds[slot * 4 + first + i];
     return r;
 }
 
@@ -50,73 +71,61 @@ __device__ __forceinline__ uint32_t ordered_bits(float v) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// Workgroup-wide 1/sqrt(mean(x^2) + eps) (rmsNorm, model/loader.zig:3404-3426).
-__device__ float rms_scale(const float *__restrict__ x, int n, float eps, float *lds) {
-    float ss = 0.f;
-    for (int i = threadIdx.x * 4; i < n; i += kThreads * 4) {
-        const float4 v = *reinterpret_cast<const float4 *>(x + i);
-        ss = fmaf(v.x, v.x, ss);
-        ss = fmaf(v.y, v.y, ss);
-        ss = fmaf(v.z, v.z, ss);
-        ss = fmaf(v.w, v.w, ss);
-    }
-    ss = wave_sum(ss, 64);
-    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    const float tot = (lds[0] + lds[1]) + (lds[2] + lds[3]);
-    __syncthreads();
-    return 1.0f / sqrtf(tot / (float)n + eps);
-}
-
+// Stages the 64 activations of slot s (zeros for inactive lanes) with the
+// input prologue applied, in the slot representation of format F.
 template <int F, int IN>
-__device__ __forceinline__ void stage_x(XSlot &xs, int s, bool active, const MvParams &p, float nscale) {
-#pragma unroll
-    for (int w = 0; w < 4; w++) xs.sum[w] = 0.f;
-    if (!active) {
-#pragma unroll
-        for (int i = 0; i < 64; i++) xs.v[i] = 0.f;
-        return;
-    }
+__device__ __forceinline__ void stage_x(XOf_t<F> &xs, int s, bool active, const MvParams &p, int T, float *lds) {
+    float v[64], aux[64];
     const int base = Geom<F>::x_base(s);
 #pragma unroll
     for (int w = 0; w < 4; w++) {
         const int o = base + w * Geom<F>::kXStride;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const float4 a = *reinterpret_cast<const float4 *>(p.x + o + 4 * c);
-            float t[4] = {a.x, a.y, a.z, a.w};
-            if (IN == IN_NORM) {
-                const float4 nw = *reinterpret_cast<const float4 *>(p.norm_w + o + 4 * c);
-                const float ww[4] = {nw.x, nw.y, nw.z, nw.w};
-#pragma unroll
-                for (int k = 0; k < 4; k++) t[k] = (nscale * t[k]) * ww[k];
-            } else if (IN == IN_SILU) {
-                const float4 u = *reinterpret_cast<const float4 *>(p.x2 + o + 4 * c);
-                const float uu[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-                for (int k = 0; k < 4; k++) t[k] = (t[k] / (1.0f + expf(-t[k]))) * uu[k];
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+            if (active) {
+                a = *reinterpret_cast<const float4 *>(p.x + o + 4 * c);
+                if (IN == IN_NORM) b = *reinterpret_cast<const float4 *>(p.norm_w + o + 4 * c);
+                if (IN == IN_SILU) b = *reinterpret_cast<const float4 *>(p.x2 + o + 4 * c);
             }
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                xs.v[16 * w + 4 * c + k] = t[k];
-                xs.sum[w] += t[k];
-            }
+            const int i = 16 * w + 4 * c;
+            v[i] = a.x, v[i + 1] = a.y, v[i + 2] = a.z, v[i + 3] = a.w;
+            aux[i] = b.x, aux[i + 1] = b.y, aux[i + 2] = b.z, aux[i + 3] = b.w;
         }
     }
+    if (IN == IN_NORM) {
+        // the team covers every slot of x, so the team sum of squares is the full one
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 64; i++) ss = fmaf(v[i], v[i], ss);
+        ss = team_sum(ss, T, lds, 4);
+        // every team holds the same total: in lane 63 of each wavefront for
+        // T <= 64, in every lane for wider teams
+        const float tot = T <= 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 63)) : ss;
+        const float scale = 1.0f / sqrtf(tot / (float)p.cols + p.eps);
+#pragma unroll
+        for (int i = 0; i < 64; i++) v[i] = (scale * v[i]) * aux[i];
+    } else if (IN == IN_SILU) {
+#pragma unroll
+        for (int i = 0; i < 64; i++) v[i] = (v[i] / (1.0f + expf(-v[i]))) * aux[i];
+    }
+    to_slot(v, xs);
 }
 
 template <int F, int IN, int OUT>
 __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int wg_in_seg, float *lds) {
+    constexpr int D = ring_depth<F>();
     const int tid = threadIdx.x, T = p.team, teams = kThreads / T;
     const int team = tid / T, lane = tid % T;
     const bool active = lane < p.slots;
+    const int sl = active ? lane : p.slots - 1;  // inactive lanes re-read a valid slot
+    const bool writer = lane == T - 1;
 
     const uint8_t *wbase = sg.w, *wbase2 = sg.w2;
     float wscale = p.weight_scale;
-    bool skip = false;
     if (p.expert) {
         const uint32_t e = p.expert[2 * p.expert_slot];
-        skip = e >= (uint32_t)p.expert_limit;
+        if (e >= (uint32_t)p.expert_limit) return;  // uniform over the grid: no rows are read
         const uint64_t off = (uint64_t)e * (uint64_t)p.rows_per_expert * sg.stride;
         wbase += off;
         if (wbase2) wbase2 += off;
@@ -124,67 +133,73 @@ __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int 
     }
     const int r_begin = wg_in_seg * sg.rows_per_wg;
     const int r_end = min(r_begin + sg.rows_per_wg, sg.rows);
+    const int n = p.rows_per_team;
+    const int r0 = r_begin + team;
+    // row `it` of this team, clamped to the workgroup's last row (loads only)
+    auto row_of = [&](int it) { return min(r0 + it * teams, r_end - 1); };
 
-    // Issue the first row's weight loads before staging the input: they do
-    // not depend on it, so HBM latency overlaps the norm and the staging.
-    int r = r_begin + team;
-    bool valid = !skip && r < r_end;
-    Raw<F> cur{}, cur2{};
-    if (valid && active) {
-        cur = slot_load<F>(wbase + (uint64_t)r * sg.stride, lane);
-        if (OUT == OUT_SWIGLU) cur2 = slot_load<F>(wbase2 + (uint64_t)r * sg.stride, lane);
+    // Issue the first rows' weight loads before staging the input: they do not
+    // depend on it, so HBM latency overlaps the staging and the norm.
+    // The residual read of ADD / WADD rides in the same ring: a late load of
+    // y[r] would make the in-order vmcnt wait cover the prefetched rows too.
+    constexpr bool kReadY = OUT == OUT_ADD || OUT == OUT_WADD;
+    Raw<F> ra[D], rb[D];
+    float ry[D];
+#pragma unroll
+    for (int k = 0; k < D; k++) {
+        ra[k] = slot_load<F>(wbase + (uint64_t)row_of(k) * sg.stride, sl);
+        if (OUT == OUT_SWIGLU) rb[k] = slot_load<F>(wbase2 + (uint64_t)row_of(k) * sg.stride, sl);
+        if (kReadY) ry[k] = sg.y[row_of(k)];
     }
-    float nscale = 1.f;
-    if (IN == IN_NORM) nscale = rms_scale(p.x, p.cols, p.eps, lds);
-    XSlot xs;
-    stage_x<F, IN>(xs, lane, active, p, nscale);
+    XOf_t<F> xs;
+    stage_x<F, IN>(xs, lane, active, p, T, lds);
 
     float best_v = -INFINITY;
     int best_r = 0x7fffffff;
-    for (int it = 0; it < p.rows_per_team; ++it) {
-        // double buffering: the next row's loads are in flight during this row's math
-        const int rn = r + teams;
-        const bool vn = !skip && it + 1 < p.rows_per_team && rn < r_end;
-        Raw<F> nxt{}, nxt2{};
-        if (vn && active) {
-            nxt = slot_load<F>(wbase + (uint64_t)rn * sg.stride, lane);
-            if (OUT == OUT_SWIGLU) nxt2 = slot_load<F>(wbase2 + (uint64_t)rn * sg.stride, lane);
-        }
-        float v = 0.f, v2 = 0.f;
-        if (valid && active) {
-            v = slot_dot<F>(cur, lane, xs);
-            if (OUT == OUT_SWIGLU) v2 = slot_dot<F>(cur2, lane, xs);
-        }
-        v = team_sum(v, T, lds);
-        if (OUT == OUT_SWIGLU) v2 = team_sum(v2, T, lds);
-        if (valid && lane == 0) {
-            if (OUT == OUT_STORE) {
-                sg.y[r] = v;
-            } else if (OUT == OUT_ADD) {
-                sg.y[r] += v;
-            } else if (OUT == OUT_WADD) {
-                sg.y[r] = fmaf(v, wscale, sg.y[r]);
-            } else if (OUT == OUT_SWIGLU) {
-                sg.y[r] = (v / (1.0f + expf(-v))) * v2;  // siluInPlace then gate * up
-            } else if (OUT == OUT_ARGMAX) {
-                if (sg.y) sg.y[r] = v;
-                if (v > best_v || (v == best_v && r < best_r)) {
-                    best_v = v;
-                    best_r = r;
+    for (int it0 = 0; it0 < n; it0 += D) {
+#pragma unroll
+        for (int k = 0; k < D; k++) {
+            const int it = it0 + k;
+            if (it < n) {
+                float v = slot_dot<F>(ra[k], sl, xs), v2 = 0.f;
+                if (OUT == OUT_SWIGLU) v2 = slot_dot<F>(rb[k], sl, xs);
+                v = active ? v : 0.f;
+                v = team_sum(v, T, lds, it & 1);
+                if (OUT == OUT_SWIGLU) {
+                    v2 = active ? v2 : 0.f;
+                    v2 = team_sum(v2, T, lds, 2 + (it & 1));
+                }
+                const int r = r0 + it * teams;
+                if (writer && r < r_end) {
+                    if (OUT == OUT_STORE) {
+                        sg.y[r] = v;
+                    } else if (OUT == OUT_ADD) {
+                        sg.y[r] = ry[k] + v;
+                    } else if (OUT == OUT_WADD) {
+                        sg.y[r] = fmaf(v, wscale, ry[k]);
+                    } else if (OUT == OUT_SWIGLU) {
+                        sg.y[r] = (v / (1.0f + expf(-v))) * v2;  // siluInPlace then gate * up
+                    } else if (OUT == OUT_ARGMAX) {
+                        if (sg.y) sg.y[r] = v;
+                        if (v > best_v || (v == best_v && r < best_r)) {
+                            best_v = v;
+                            best_r = r;
+                        }
+                    }
                 }
             }
+            // refill this ring slot (unconditionally: keeps the vmcnt waits exact)
+            ra[k] = slot_load<F>(wbase + (uint64_t)row_of(it + D) * sg.stride, sl);
+            if (OUT == OUT_SWIGLU) rb[k] = slot_load<F>(wbase2 + (uint64_t)row_of(it + D) * sg.stride, sl);
+            if (kReadY) ry[k] = sg.y[row_of(it + D)];
         }
-        cur = nxt;
-        cur2 = nxt2;
-        r = rn;
-        valid = vn;
     }
     if (OUT == OUT_ARGMAX) {
         __shared__ unsigned long long keys[kThreads];
         unsigned long long key = 0ull;
-        if (lane == 0 && best_r != 0x7fffffff)
+        if (writer && best_r != 0x7fffffff)
             key = ((unsigned long long)ordered_bits(best_v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_r);
-        if (lane == 0) keys[team] = key;
+        if (writer) keys[team] = key;
         __syncthreads();
         if (tid == 0) {
             unsigned long long k = keys[0];
@@ -196,7 +211,7 @@ __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int 
 
 template <int F1, int F2, int IN, int OUT>
 __global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
-    __shared__ float lds[8];
+    __shared__ float lds[20];
     if (p.gate_flag && *p.gate_flag == 0) return;
     const int wg = blockIdx.x;
     int si = 0;

@@ -12,8 +12,10 @@
 //   Q3_K  model/quant_extra.zig:45-126, expandQ3KScales :248-279
 //   IQ4_XS model/quant_extra.zig:191-246, kvalues_iq4nl :8
 // The matvec dots factor the per-block scales out of the 16/32-value sums
-// (as the reference's own dotQ4KRow / dotQ6KRow do); unsigned-offset
-// encodings (Q6_K q+32, Q3_K q+4) are corrected with per-run activation sums.
+// (as the reference's own dotQ4KRow / dotQ6KRow do) and form those sums with
+// integer dot products against a fixed-point copy of the activations (XDig);
+// unsigned-offset codes (Q6_K q+32, Q3_K q+4) are corrected with per-run
+// activation sums.
 // The dequant_* functions reproduce the reference's exact binary32 operation
 // order (no contraction) and are bit-exact with the CPU decoder.
 #pragma once
@@ -98,17 +100,100 @@ template <> struct Geom<F32> {
     static constexpr int kXStride = 16;
 };
 
-// The 64 activations a lane owns, plus per-run sums.
+// ---------------- activation slots ----------------
+//
+// The float formats (F16, F32) keep a lane's 64 activations as f32 (XSlot).
+// The quantized formats use XDig: the lane's activations as 22-bit fixed
+// point, x_i ~= scale * (65536 * d2 + 256 * d1 + d0), with a per-lane
+// power-of-two scale chosen from max|x| and balanced base-256 digits
+// d0, d1 in [-128, 127], d2 in [-64, 64].  A quant block's integer codes
+// then meet the digits in v_dot4_i32_i8 (four products per instruction,
+// exact int32 sums), and each sub-block's three digit sums are recombined in
+// f32.  The only approximation is the fixed-point rounding of x, at most
+// 2^-22 * max|x| per value (the size of binary32 rounding of the largest
+// term); sums of products are exact before the recombination.
+
 struct XSlot {
     float v[64];
     float sum[4];
+};
+
+struct XDig {
+    uint32_t d[3][16];  // digit j of slot values 4c..4c+3, one signed byte each, in d[j][c]
+    float scale;        // 2^-k (non-finite when an activation is)
+    float sum[4];       // per-run f32 sums of the activations
+};
+
+template <int F> struct XOf { using type = XDig; };
+template <> struct XOf<F16> { using type = XSlot; };
+template <> struct XOf<F32> { using type = XSlot; };
+template <int F> using XOf_t = typename XOf<F>::type;
+
+__device__ __forceinline__ void run_sums(const float (&v)[64], float (&sum)[4]) {
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; k++) t += v[16 * w + k];
+        sum[w] = t;
+    }
+}
+
+__device__ __forceinline__ void to_slot(const float (&v)[64], XSlot &xs) {
+#pragma unroll
+    for (int i = 0; i < 64; i++) xs.v[i] = v[i];
+    run_sums(v, xs.sum);
+}
+
+__device__ __forceinline__ void to_slot(const float (&v)[64], XDig &xd) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64; i++) m = fmaxf(m, fabsf(v[i]));
+    // m = f * 2^e with f in [0.5, 1): |v * 2^(22 - e)| < 2^22
+    const int k = 22 - __builtin_amdgcn_frexp_expf(m);
+    run_sums(v, xd.sum);
+    // a NaN or infinite activation makes every dot NaN (the digits cannot carry it)
+    const float tot = (xd.sum[0] + xd.sum[1]) + (xd.sum[2] + xd.sum[3]);
+    xd.scale = (m <= 3.4028235e38f && fabsf(tot) <= 3.4028235e38f) ? ldexpf(1.0f, -k) : __builtin_nanf("");
+#pragma unroll
+    for (int c = 0; c < 16; c++) {
+        // u = xi + 0x808080 has the balanced digits + 128 as its bytes 0..2
+        uint32_t u[4];
+#pragma unroll
+        for (int b = 0; b < 4; b++) u[b] = (uint32_t)(int)ldexpf(v[4 * c + b], k) + 0x808080u;
+        const uint32_t a = __builtin_amdgcn_perm(u[1], u[0], 0x05010400u);  // u0.b0 u1.b0 u0.b1 u1.b1
+        const uint32_t b = __builtin_amdgcn_perm(u[3], u[2], 0x05010400u);  // u2.b0 u3.b0 u2.b1 u3.b1
+        const uint32_t c2 = __builtin_amdgcn_perm(u[1], u[0], 0x07030602u); // u0.b2 u1.b2 u0.b3 u1.b3
+        const uint32_t e2 = __builtin_amdgcn_perm(u[3], u[2], 0x07030602u);
+        xd.d[0][c] = __builtin_amdgcn_perm(b, a, 0x05040100u) ^ 0x80808080u;
+        xd.d[1][c] = __builtin_amdgcn_perm(b, a, 0x07060302u) ^ 0x80808080u;
+        xd.d[2][c] = __builtin_amdgcn_perm(e2, c2, 0x05040100u) ^ 0x80808080u;
+    }
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Three-digit integer dot of 4 code words with slot words c0..c0+3 of xd,
+// recombined to f32 (without the scale).
+struct Dig3 {
+    int a0 = 0, a1 = 0, a2 = 0;
+    __device__ __forceinline__ void add(uint32_t q, const XDig &xd, int c) {
+        a0 = sdot4(q, xd.d[0][c], a0);
+        a1 = sdot4(q, xd.d[1][c], a1);
+        a2 = sdot4(q, xd.d[2][c], a2);
+    }
+    __device__ __forceinline__ float value() const {
+        return fmaf((float)a2, 65536.f, fmaf((float)a1, 256.f, (float)a0));
+    }
 };
 
 // ---------------- slots: raw load (registers) + dot ----------------
 //
 // slot_load<F>(row, s) issues the 16-byte loads of slot s of `row` and
 // returns the raw words; slot_dot<F>(raw, s, xs) decodes them and returns
-// dot(64 weights, xs).  Splitting the two lets a kernel keep the next row's
+// dot(64 weights, x).  Splitting the two lets a kernel keep the next rows'
 // loads in flight while it computes the current one.
 
 template <int F> struct Raw;
@@ -121,7 +206,7 @@ template <> struct Raw<F16> { uint4 w[8]; };
 template <> struct Raw<F32> { uint4 w[16]; };
 
 template <int F> __device__ __forceinline__ Raw<F> slot_load(const uint8_t *__restrict__ row, int s);
-template <int F> __device__ __forceinline__ float slot_dot(const Raw<F> &r, int s, const XSlot &xs);
+template <int F> __device__ __forceinline__ float slot_dot(const Raw<F> &r, int s, const XOf_t<F> &xs);
 
 // Q4_K: slot = (block b, group g): 32 qs bytes -> sub-block 2g (low nibbles) and 2g+1 (high).
 template <> __device__ __forceinline__ Raw<Q4_K> slot_load<Q4_K>(const uint8_t *__restrict__ row, int s) {
@@ -129,7 +214,7 @@ template <> __device__ __forceinline__ Raw<Q4_K> slot_load<Q4_K>(const uint8_t *
     const int g = s & 3;
     return {ld16(blk), ld16(blk + 16 + 32 * g), ld16(blk + 32 + 32 * g)};
 }
-template <> __device__ __forceinline__ float slot_dot<Q4_K>(const Raw<Q4_K> &r, int s, const XSlot &xs) {
+template <> __device__ __forceinline__ float slot_dot<Q4_K>(const Raw<Q4_K> &r, int s, const XDig &xs) {
     const int g = s & 3;
     const uint4 hd = r.hd;
     const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
@@ -143,21 +228,15 @@ template <> __device__ __forceinline__ float slot_dot<Q4_K>(const Raw<Q4_K> &r, 
     const uint32_t sc1 = bfe(a_sc, o1, wa) | (bfe(hd.y, o1 + 6, wb) << 4);
     const uint32_t m1 = bfe(a_m, o1 + om, wa) | (bfe(hd.z, o1 + 6, wb) << 4);
     const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
-    float dl = 0.f, dh = 0.f;
+    Dig3 lo_acc, hi_acc;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-        // high nibbles are converted in place as 16 * q (exact), undone by the 1/16 below
-        const uint32_t l4 = opaque(q[k] & 0x0F0F0F0Fu), h4 = opaque(q[k] & 0xF0F0F0F0u);
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            dl = fmaf(ub(l4, b), xs.v[4 * k + b], dl);
-            dh = fmaf(ub(h4, b), xs.v[32 + 4 * k + b], dh);
-        }
+        lo_acc.add(q[k] & 0x0F0F0F0Fu, xs, k);
+        hi_acc.add((q[k] >> 4) & 0x0F0F0F0Fu, xs, 8 + k);
     }
     const float d1 = d * (float)sc0, mm1 = dmin * (float)m0, d2 = d * (float)sc1, mm2 = dmin * (float)m1;
-    float res = d1 * dl;
+    float res = fmaf(d1, lo_acc.value(), d2 * hi_acc.value()) * xs.scale;
     res = fmaf(-mm1, xs.sum[0] + xs.sum[1], res);
-    res = fmaf(d2, dh * 0.0625f, res);
     res = fmaf(-mm2, xs.sum[2] + xs.sum[3], res);
     return res;
 }
@@ -169,33 +248,27 @@ template <> __device__ __forceinline__ Raw<Q6_K> slot_load<Q6_K>(const uint8_t *
     return {ld16(blk + 64 * h + l0), ld16(blk + 64 * h + 32 + l0), ld16(blk + 128 + 32 * h + l0),
             ld8(blk + 192 + 8 * h), ld2(blk + 208)};
 }
-template <> __device__ __forceinline__ float slot_dot<Q6_K>(const Raw<Q6_K> &r, int s, const XSlot &xs) {
+template <> __device__ __forceinline__ float slot_dot<Q6_K>(const Raw<Q6_K> &r, int s, const XDig &xs) {
     const float d = h2f(r.d);
     const int sb0 = s & 1;
     const uint32_t a[4] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w}, bq[4] = {r.qb.x, r.qb.y, r.qb.z, r.qb.w};
     const uint32_t hh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    Dig3 acc[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        const uint32_t u0 = opaque((a[k] & 0x0F0F0F0Fu) | ((hh[k] & 0x03030303u) << 4));
-        const uint32_t u1 = opaque((bq[k] & 0x0F0F0F0Fu) | ((hh[k] & 0x0C0C0C0Cu) << 2));
-        const uint32_t u2 = opaque(((a[k] >> 4) & 0x0F0F0F0Fu) | (hh[k] & 0x30303030u));
-        const uint32_t u3 = opaque(((bq[k] >> 4) & 0x0F0F0F0Fu) | ((hh[k] >> 2) & 0x30303030u));
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            acc[0] = fmaf(ub(u0, b), xs.v[0 + 4 * k + b], acc[0]);
-            acc[1] = fmaf(ub(u1, b), xs.v[16 + 4 * k + b], acc[1]);
-            acc[2] = fmaf(ub(u2, b), xs.v[32 + 4 * k + b], acc[2]);
-            acc[3] = fmaf(ub(u3, b), xs.v[48 + 4 * k + b], acc[3]);
-        }
+        // codes q + 32 in 0..63, one run (sub-block of 16) per word group
+        acc[0].add((a[k] & 0x0F0F0F0Fu) | ((hh[k] & 0x03030303u) << 4), xs, k);
+        acc[1].add((bq[k] & 0x0F0F0F0Fu) | ((hh[k] & 0x0C0C0C0Cu) << 2), xs, 4 + k);
+        acc[2].add(((a[k] >> 4) & 0x0F0F0F0Fu) | (hh[k] & 0x30303030u), xs, 8 + k);
+        acc[3].add(((bq[k] >> 4) & 0x0F0F0F0Fu) | ((hh[k] >> 2) & 0x30303030u), xs, 12 + k);
     }
-    // sc[8h + l0/16 + 2w]: byte sb0 (+2) of sc.x (w = 0, 1) and sc.y (w = 2, 3); values are q + 32
+    // sc[8h + l0/16 + 2w]: byte sb0 (+2) of sc.x (w = 0, 1) and sc.y (w = 2, 3)
     const float s0 = d * sb(r.sc.x, sb0), s1 = d * sb(r.sc.x, sb0 + 2);
     const float s2 = d * sb(r.sc.y, sb0), s3 = d * sb(r.sc.y, sb0 + 2);
-    float res = s0 * fmaf(-32.f, xs.sum[0], acc[0]);
-    res = fmaf(s1, fmaf(-32.f, xs.sum[1], acc[1]), res);
-    res = fmaf(s2, fmaf(-32.f, xs.sum[2], acc[2]), res);
-    res = fmaf(s3, fmaf(-32.f, xs.sum[3], acc[3]), res);
+    float res = s0 * fmaf(acc[0].value(), xs.scale, -32.f * xs.sum[0]);
+    res = fmaf(s1, fmaf(acc[1].value(), xs.scale, -32.f * xs.sum[1]), res);
+    res = fmaf(s2, fmaf(acc[2].value(), xs.scale, -32.f * xs.sum[2]), res);
+    res = fmaf(s3, fmaf(acc[3].value(), xs.scale, -32.f * xs.sum[3]), res);
     return res;
 }
 
@@ -204,24 +277,17 @@ template <> __device__ __forceinline__ Raw<Q8_0> slot_load<Q8_0>(const uint8_t *
     const uint8_t *p = row + 68 * s;
     return {ld16(p), ld16(p + 16), ld16(p + 32), ld16(p + 48), ld4(p + 64)};
 }
-template <> __device__ __forceinline__ float slot_dot<Q8_0>(const Raw<Q8_0> &r, int s, const XSlot &xs) {
+template <> __device__ __forceinline__ float slot_dot<Q8_0>(const Raw<Q8_0> &r, int s, const XDig &xs) {
     const uint32_t w[17] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c.x,
                             r.c.y, r.c.z, r.c.w, r.e.x, r.e.y, r.e.z, r.e.w, r.f};
     const float d0 = h2f(w[0]), d1 = h2f(w[8] >> 16);
-    // signed bytes read as unsigned q + 128 (xor 0x80); the 128 * sum(x) offset is removed below
-    uint32_t u[17];
+    Dig3 b0, b1;
 #pragma unroll
-    for (int k = 0; k < 17; k++) u[k] = opaque(w[k] ^ 0x80808080u);
-    float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-        const int bi = 2 + i;  // block 0 quants start at byte 2
-        s0 = fmaf(ub(u[bi >> 2], bi & 3), xs.v[i], s0);
-        s1 = fmaf(ub(u[9 + (i >> 2)], i & 3), xs.v[32 + i], s1);
+    for (int m = 0; m < 8; m++) {
+        b0.add(__builtin_amdgcn_alignbyte(w[m + 1], w[m], 2), xs, m);  // block 0 quants: bytes 2..33
+        b1.add(w[9 + m], xs, 8 + m);                                    // block 1 quants: bytes 36..67
     }
-    s0 = fmaf(-128.f, xs.sum[0] + xs.sum[1], s0);
-    s1 = fmaf(-128.f, xs.sum[2] + xs.sum[3], s1);
-    return fmaf(d1, s1, d0 * s0);
+    return fmaf(d1, b1.value(), d0 * b0.value()) * xs.scale;
 }
 
 // Q3_K: slot = (block b, half h, 16-group sh): qs[32h+16sh..], hmask[16sh..], 4 shifts.
@@ -231,20 +297,18 @@ template <> __device__ __forceinline__ Raw<Q3_K> slot_load<Q3_K>(const uint8_t *
     return {ld16(blk + 16 * sh), ld16(blk + 32 + 32 * h + 16 * sh), ld4(blk + 96), ld4(blk + 100), ld4(blk + 104),
             ld2(blk + 108)};
 }
-template <> __device__ __forceinline__ float slot_dot<Q3_K>(const Raw<Q3_K> &r, int s, const XSlot &xs) {
+template <> __device__ __forceinline__ float slot_dot<Q3_K>(const Raw<Q3_K> &r, int s, const XDig &xs) {
     const int h = (s >> 1) & 1, sh = s & 1;
     const float dall = h2f(r.d);
     const uint32_t hmw[4] = {r.hm.x, r.hm.y, r.hm.z, r.hm.w}, qw[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    Dig3 acc[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             // (q + 4) = low 2 bits | high-mask bit << 2, per byte
-            const uint32_t u =
-                opaque(((qw[k] >> (2 * j)) & 0x03030303u) | (((hmw[k] >> (4 * h + j)) & 0x01010101u) << 2));
-#pragma unroll
-            for (int b = 0; b < 4; b++) acc[j] = fmaf(ub(u, b), xs.v[16 * j + 4 * k + b], acc[j]);
+            acc[j].add(((qw[k] >> (2 * j)) & 0x03030303u) | (((hmw[k] >> (4 * h + j)) & 0x01010101u) << 2), xs,
+                       4 * j + k);
         }
     }
     float res = 0.f;
@@ -256,7 +320,7 @@ template <> __device__ __forceinline__ float slot_dot<Q3_K>(const Raw<Q3_K> &r, 
         const uint32_t low4 = bfe(lowsrc, 8 * qd + 4 * (grp >> 1), 4);
         const uint32_t hi2 = bfe(r.r2, 8 * qd + 2 * grp, 2);
         const float sc = (float)((int)(low4 | (hi2 << 4)) - 32);
-        res = fmaf(dall * sc, fmaf(-4.f, xs.sum[j], acc[j]), res);
+        res = fmaf(dall * sc, fmaf(acc[j].value(), xs.scale, -4.f * xs.sum[j]), res);
     }
     return res;
 }
@@ -264,20 +328,21 @@ template <> __device__ __forceinline__ float slot_dot<Q3_K>(const Raw<Q3_K> &r, 
 __device__ __constant__ static const float kIq4nl[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
                                                          1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
 
-// kvalues_iq4nl + 128 as bytes, 4 entries per word, for register table lookups with v_perm
-#define ZH_IQ4_T0 (((uint32_t)(-127 + 128)) | ((uint32_t)(-104 + 128) << 8) | ((uint32_t)(-83 + 128) << 16) | ((uint32_t)(-65 + 128) << 24))
-#define ZH_IQ4_T1 (((uint32_t)(-49 + 128)) | ((uint32_t)(-35 + 128) << 8) | ((uint32_t)(-22 + 128) << 16) | ((uint32_t)(-10 + 128) << 24))
-#define ZH_IQ4_T2 (((uint32_t)(1 + 128)) | ((uint32_t)(13 + 128) << 8) | ((uint32_t)(25 + 128) << 16) | ((uint32_t)(38 + 128) << 24))
-#define ZH_IQ4_T3 (((uint32_t)(53 + 128)) | ((uint32_t)(69 + 128) << 8) | ((uint32_t)(89 + 128) << 16) | ((uint32_t)(113 + 128) << 24))
+// kvalues_iq4nl as signed bytes, 4 entries per word, for register table lookups with v_perm
+#define ZH_IQ4_B(v, i) (((uint32_t)(uint8_t)(int8_t)(v)) << (8 * (i)))
+#define ZH_IQ4_T0 (ZH_IQ4_B(-127, 0) | ZH_IQ4_B(-104, 1) | ZH_IQ4_B(-83, 2) | ZH_IQ4_B(-65, 3))
+#define ZH_IQ4_T1 (ZH_IQ4_B(-49, 0) | ZH_IQ4_B(-35, 1) | ZH_IQ4_B(-22, 2) | ZH_IQ4_B(-10, 3))
+#define ZH_IQ4_T2 (ZH_IQ4_B(1, 0) | ZH_IQ4_B(13, 1) | ZH_IQ4_B(25, 2) | ZH_IQ4_B(38, 3))
+#define ZH_IQ4_T3 (ZH_IQ4_B(53, 0) | ZH_IQ4_B(69, 1) | ZH_IQ4_B(89, 2) | ZH_IQ4_B(113, 3))
 
-// Looks up 4 nibbles (one per byte of n, each 0..15) in kvalues_iq4nl + 128.
+// Looks up 4 nibbles (one per byte of n, each 0..15) in kvalues_iq4nl (signed bytes).
 __device__ __forceinline__ uint32_t iq4_lookup4(uint32_t n) {
     const uint32_t sel = n & 0x07070707u;
     const uint32_t lo = __builtin_amdgcn_perm(ZH_IQ4_T1, ZH_IQ4_T0, sel);
     const uint32_t hi = __builtin_amdgcn_perm(ZH_IQ4_T3, ZH_IQ4_T2, sel);
     // byte i of the result: lo.byte[i] (selector i) or hi.byte[i] (selector 4 + i) by bit 3 of the nibble
     const uint32_t pick = 0x03020100u + ((n & 0x08080808u) >> 1);
-    return opaque(__builtin_amdgcn_perm(hi, lo, pick));
+    return __builtin_amdgcn_perm(hi, lo, pick);
 }
 
 // IQ4_XS: slot = (block b, sub-block pair k): sub-blocks 2k, 2k+1.
@@ -286,28 +351,21 @@ template <> __device__ __forceinline__ Raw<IQ4_XS> slot_load<IQ4_XS>(const uint8
     const int k = s & 3;
     return {ld16(blk + 8 + 32 * k), ld16(blk + 24 + 32 * k), ld4(blk), ld4(blk + 4)};
 }
-template <> __device__ __forceinline__ float slot_dot<IQ4_XS>(const Raw<IQ4_XS> &r, int s, const XSlot &xs) {
+template <> __device__ __forceinline__ float slot_dot<IQ4_XS>(const Raw<IQ4_XS> &r, int s, const XDig &xs) {
     const int k = s & 3;
     const float d = h2f(r.dsh);
     const uint32_t sh = r.dsh >> 16, sl = bfe(r.sl, 8 * k, 8);
     const uint32_t ls0 = (sl & 0xF) | (bfe(sh, 4 * k, 2) << 4), ls1 = (sl >> 4) | (bfe(sh, 4 * k + 2, 2) << 4);
     const uint32_t w0[4] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w}, w1[4] = {r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-    float a0 = 0.f, a1 = 0.f;
+    Dig3 a0, a1;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        const uint32_t l0 = iq4_lookup4(w0[c] & 0x0F0F0F0Fu), h0 = iq4_lookup4((w0[c] >> 4) & 0x0F0F0F0Fu);
-        const uint32_t l1 = iq4_lookup4(w1[c] & 0x0F0F0F0Fu), h1 = iq4_lookup4((w1[c] >> 4) & 0x0F0F0F0Fu);
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            a0 = fmaf(ub(l0, b), xs.v[4 * c + b], a0);
-            a0 = fmaf(ub(h0, b), xs.v[16 + 4 * c + b], a0);
-            a1 = fmaf(ub(l1, b), xs.v[32 + 4 * c + b], a1);
-            a1 = fmaf(ub(h1, b), xs.v[48 + 4 * c + b], a1);
-        }
+        a0.add(iq4_lookup4(w0[c] & 0x0F0F0F0Fu), xs, c);
+        a0.add(iq4_lookup4((w0[c] >> 4) & 0x0F0F0F0Fu), xs, 4 + c);
+        a1.add(iq4_lookup4(w1[c] & 0x0F0F0F0Fu), xs, 8 + c);
+        a1.add(iq4_lookup4((w1[c] >> 4) & 0x0F0F0F0Fu), xs, 12 + c);
     }
-    a0 = fmaf(-128.f, xs.sum[0] + xs.sum[1], a0);
-    a1 = fmaf(-128.f, xs.sum[2] + xs.sum[3], a1);
-    return fmaf(d * (float)((int)ls1 - 32), a1, (d * (float)((int)ls0 - 32)) * a0);
+    return fmaf(d * (float)((int)ls1 - 32), a1.value(), (d * (float)((int)ls0 - 32)) * a0.value()) * xs.scale;
 }
 
 template <> __device__ __forceinline__ Raw<F16> slot_load<F16>(const uint8_t *__restrict__ row, int s) {
@@ -456,6 +514,54 @@ template <> __device__ void dequant_block<IQ4_XS>(const uint8_t *blk, float *out
         }
         qs += 16;
     }
+}
+
+// Value i of one block, with the same operation order as dequant_block
+// (bit-exact with it); lets one thread decode one value.
+template <int F> __device__ float dequant_value(const uint8_t *blk, int i);
+
+template <> __device__ __forceinline__ float dequant_value<Q4_K>(const uint8_t *blk, int i) {
+    const int g = i >> 6, hi = (i >> 5) & 1, l = i & 31;
+    int sc, m;
+    scale_min_k4(2 * g + hi, blk + 4, sc, m);
+    const float d1 = __fmul_rn(h2f(ld2(blk)), (float)sc), mm = __fmul_rn(h2f(ld2(blk + 2)), (float)m);
+    const uint8_t q = blk[16 + 32 * g + l];
+    return __fsub_rn(__fmul_rn(d1, (float)(hi ? q >> 4 : q & 0x0F)), mm);
+}
+
+template <> __device__ __forceinline__ float dequant_value<Q6_K>(const uint8_t *blk, int i) {
+    const int half = i >> 7, quarter = (i >> 5) & 3, l = i & 31;
+    const uint8_t *ql = blk + 64 * half, *qh = blk + 128 + 32 * half, *sc = blk + 192 + 8 * half;
+    const uint8_t lq = ql[l + ((quarter & 1) ? 32 : 0)];
+    const int nib = (quarter & 2) ? lq >> 4 : lq & 0x0F;
+    const int q = (nib | (((qh[l] >> (2 * quarter)) & 3) << 4)) - 32;
+    const float sd = __fmul_rn(h2f(ld2(blk + 208)), (float)(int8_t)sc[l / 16 + 2 * quarter]);
+    return __fmul_rn(sd, (float)q);
+}
+
+template <> __device__ __forceinline__ float dequant_value<Q8_0>(const uint8_t *blk, int i) {
+    return __fmul_rn(h2f(ld2(blk)), (float)(int8_t)blk[2 + i]);
+}
+
+template <> __device__ __forceinline__ float dequant_value<Q3_K>(const uint8_t *blk, int i) {
+    const int h = i >> 7, j = (i >> 5) & 3, half16 = (i >> 4) & 1, l = i & 15;
+    const int si = 8 * h + 2 * j + half16, qd = si & 3, grp = si >> 2;
+    const uint8_t *raw = blk + 96;
+    const int low4 = (raw[(grp & 1) * 4 + qd] >> (4 * (grp >> 1))) & 0xF;
+    const int hi2 = (raw[8 + qd] >> (2 * grp)) & 3;
+    const int scv = (low4 | (hi2 << 4)) - 32;
+    const int idx = 32 * h + 16 * half16 + l;
+    const int v = (int)((blk[32 + idx] >> (2 * j)) & 3) - ((blk[16 * half16 + l] & (1 << (4 * h + j))) ? 0 : 4);
+    return __fmul_rn(__fmul_rn(h2f(ld2(blk + 108)), (float)scv), (float)v);
+}
+
+template <> __device__ __forceinline__ float dequant_value<IQ4_XS>(const uint8_t *blk, int i) {
+    const int ib = i >> 5, j = i & 31;
+    const int low = (blk[4 + ib / 2] >> (4 * (ib % 2))) & 0x0f;
+    const int high = (ld2(blk + 2) >> (2 * ib)) & 0x03;
+    const float dl = __fmul_rn(h2f(ld2(blk)), (float)((low | (high << 4)) - 32));
+    const uint8_t qb = blk[8 + 16 * ib + (j & 15)];
+    return __fmul_rn(dl, kIq4nl[j < 16 ? qb & 0x0f : qb >> 4]);
 }
 
 #pragma clang fp contract(on)

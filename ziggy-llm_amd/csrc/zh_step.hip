@@ -16,7 +16,7 @@ namespace zh {
 // (embeddingLookup, model/loader.zig:3391-3402); bit-exact decode.
 template <int F> __device__ void embed_row(const uint8_t *row, int cols, float *out) {
     constexpr int V = Geom<F>::kValues, B = Geom<F>::kBytes;
-    for (int b = threadIdx.x; b < cols / V; b += blockDim.x) dequant_block<F>(row + (size_t)b * B, out + (size_t)b * V);
+    for (int i = threadIdx.x; i < cols; i += blockDim.x) out[i] = dequant_value<F>(row + (size_t)(i / V) * B, i % V);
 }
 
 __global__ void step_begin_kernel(StepState *st, const uint32_t *prompt, uint32_t *history, const uint8_t *embd,
