@@ -10,6 +10,7 @@ GB/s counts the weight bytes plus x and y (rows*cols*bytes_per_weight +
 4*(rows+cols)).
 
 Usage: python -m zhip.microbench [--iters N] [--formats q4_k,q6_k,q8_0]
+                                 [--shapes 4096x4096,14336x4096]
 Prints one JSON object per case.
 """
 from __future__ import annotations
@@ -56,10 +57,13 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--formats", default="q4_k,q6_k,q8_0")
+    ap.add_argument("--shapes", default=",".join(f"{r}x{c}" for r, c in SHAPES),
+                    help="comma-separated ROWSxCOLS list")
     args = ap.parse_args()
+    shapes = [tuple(int(v) for v in s.split("x")) for s in args.shapes.split(",")]
     ctx = hip.Context(0)
     for f in args.formats.split(","):
-        for rows, cols in SHAPES:
+        for rows, cols in shapes:
             print(json.dumps(run(ctx, FORMATS[f], rows, cols, args.iters)), flush=True)
     ctx.close()
 
