@@ -88,7 +88,7 @@ def main():
         f" ms/step), {bytes_per_token / 1e9:.3f} GB/token -> {100 * hbm_frac:.1f}% of HBM peak")
 
     kernels = {}
-    for name in ("qkv", "rope_kv", "attention", "o_proj", "gate_up", "down", "output"):
+    for name in ("qkv", "attention", "o_proj", "gate_up", "down", "output"):
         iters = args.kernel_iters if name != "output" else max(4, args.kernel_iters // 8)
         ns, nb = sess.time_kernel(name, iters)
         kernels[name] = {"avg_us": round(ns / 1e3, 2), "bytes": nb, "gbs": round(nb / ns, 1) if ns else None}

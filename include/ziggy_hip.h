@@ -308,8 +308,9 @@ typedef struct {
 /* Kernels of one decode step, for ziggy_hip_session_time_kernel. */
 enum {
     ZIGGY_HIP_KERNEL_QKV = 0,      /* fused RMSNorm + q/k/v projections */
-    ZIGGY_HIP_KERNEL_ROPE_KV = 1,  /* bias, QK-norm, RoPE, binary16 K/V store */
-    ZIGGY_HIP_KERNEL_ATTENTION = 2,/* split-K partials + merge */
+    ZIGGY_HIP_KERNEL_ROPE_KV = 1,  /* folded into ATTENTION: launches nothing (id kept stable) */
+    ZIGGY_HIP_KERNEL_ATTENTION = 2,/* q/k bias, QK-norm, RoPE, binary16 K/V store, split-K
+                                      attention with the merge in the last split */
     ZIGGY_HIP_KERNEL_O_PROJ = 3,   /* output projection + residual */
     ZIGGY_HIP_KERNEL_GATE_UP = 4,  /* fused RMSNorm + gate/up + SiLU(gate) * up */
     ZIGGY_HIP_KERNEL_DOWN = 5,     /* down projection + residual */

@@ -155,7 +155,11 @@ def test_silu_down_add(hip_ctx):
     assert rel_l2(y.read(), want) < REL_L2
 
 
-@pytest.mark.parametrize("heads,kv_heads,hd", [(32, 8, 128), (32, 4, 64), (3, 1, 128), (1, 1, 256)])
+# Splits hold one or more 64-position chunks: with 256 / kv_heads splits at
+# most, (16, 16, 128) and (64, 64, 64) fold several chunks per split (online
+# softmax across chunks) from positions 1024 and 256 on.
+@pytest.mark.parametrize("heads,kv_heads,hd", [(32, 8, 128), (32, 4, 64), (3, 1, 128), (1, 1, 256), (16, 16, 128),
+                                               (64, 64, 64)])
 @pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 200, 1000, 4095])
 def test_attention_parity(hip_ctx, heads, kv_heads, hd, pos):
     say(f"attention {heads}/{kv_heads}x{hd} pos {pos}")

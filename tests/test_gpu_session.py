@@ -77,6 +77,26 @@ def test_small_model_stream_and_logits(hip_ctx, name):
     s.close()
 
 
+def test_long_prompt_logits(hip_ctx):
+    # 16 kv heads give 16 attention splits, so 1090 positions fold two 64-position
+    # chunks into a split (online softmax inside a split, merge across splits)
+    # in the session's fused attention (q/k RoPE + K/V store in-kernel)
+    say("long prompt")
+    spec = synth.small_spec(hidden=1024, ffn=1024, n_head=16, n_kv=16, head_dim=64, n_layers=2, context=1100)
+    img = synth.build(spec, seed=37)
+    prompt = synth.prompt_tokens(7, 1090, spec.vocab)
+    o = zo.Session(zo.Model(img.buf), context=spec.context, kv_f16=True)
+    s = hip.Session(hip_ctx, img, context=spec.context)
+    for t in prompt[:-1]:
+        o.step_no_output(int(t))
+        s.step_no_output(int(t))
+    nxt = s.step_greedy(int(prompt[-1]))
+    ol = o.step(int(prompt[-1]))
+    assert nxt == zo.argmax(ol)
+    assert rel_l2(s.logits(), ol) < 1e-4
+    s.close()
+
+
 def test_per_layer_contract_matches_step(hip_ctx):
     # the gpu.Session contract (begin_token / run_attention_block / run_ffn_block /
     # run_output_argmax, runtime/gpu/session.zig:258-651) gives the step's token

@@ -21,6 +21,8 @@ struct ZiggyHipContext {
     // device scratch shared by the primitive ops (attention partials, argmax slot)
     void *scratch = nullptr;
     size_t scratch_len = 0;
+    // zeroed arrival counters of the attention kernel (each launch leaves them zero)
+    unsigned *counters = nullptr;
 };
 
 struct ZiggyHipBuffer {
@@ -128,21 +130,30 @@ hipError_t launch_fill_u64(unsigned long long *p, unsigned long long v, int n, h
 
 // attention (zh_attn.hip)
 struct AttnParams {
-    const float *q;            // [head_count * head_dim]
-    const __half *k_cache;     // layer base applied: [ctx][kv_dim]
-    const __half *v_cache;
+    const float *q;            // [head_count * head_dim]: raw projection (fused) or roped q (plain)
+    __half *k_cache;           // layer base applied: [ctx][kv_dim]
+    __half *v_cache;
     float *out;                // [head_count * head_dim]
-    float *part_o;             // [kv_heads][max_splits][group][head_dim]
-    float *part_ml;            // [kv_heads][max_splits][group][2]
+    float *part_o;             // [kv_heads][max_splits][8][head_dim]
+    float *part_ml;            // [kv_heads][max_splits][8][2]
+    unsigned *counters;        // [kv_heads] arrival counters, zero between launches
     int head_count, head_count_kv, head_dim, kv_dim;
     int position;              // attend to [window_start, position]
     const int *position_dev;   // if set, position is read from device memory (graph replay)
     int window_start;
     float scale;
-    int chunk;                 // positions per split
-    int max_splits;
+    int max_splits;            // grid width; splits used grow with the position up to this
+    // fused mode (k_new set): q/k/v epilogue of the projection and the K/V store
+    const float *k_new, *v_new;              // [kv_dim] raw k and v of this step
+    const float *q_bias, *k_bias, *v_bias;   // optional
+    const float *q_norm, *k_norm;            // optional per-head RMSNorm weights [head_dim]
+    float eps, rope_base;
+    int rope_dim, rope_style;
+    int ctx;                   // cache capacity in positions (no store at or past it)
 };
 hipError_t launch_attention(const AttnParams &p, hipStream_t s);
+// Splits of the attention grid for kv_heads heads and up to max_positions keys.
+int attention_splits(int kv_heads, int max_positions);
 size_t attention_scratch_floats(int head_count, int head_dim, int max_splits);
 
 }  // namespace zh

@@ -16,6 +16,7 @@ using namespace zh;
 namespace {
 
 constexpr size_t kCtxScratch = 64u << 20;  // attention partials + argmax/topk slots
+constexpr size_t kCtxCounters = 1024;      // attention arrival counters (one per kv head)
 
 int gguf_row_bytes(uint32_t type, uint32_t cols, uint64_t *out) {
     switch (type) {
@@ -110,7 +111,9 @@ int ziggy_hip_create_context(int device_index, ZiggyHipContext **out_ctx, ZiggyH
     ctx->info.l2_bytes = (uint32_t)prop.l2CacheSize;
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&ctx->seq_begin) != hipSuccess || hipEventCreate(&ctx->seq_end) != hipSuccess ||
-        hipMalloc(&ctx->scratch, kCtxScratch) != hipSuccess) {
+        hipMalloc(&ctx->scratch, kCtxScratch) != hipSuccess ||
+        hipMalloc((void **)&ctx->counters, kCtxCounters * sizeof(unsigned)) != hipSuccess ||
+        hipMemset(ctx->counters, 0, kCtxCounters * sizeof(unsigned)) != hipSuccess) {
         set_err(err, err_len, "stream/event/scratch creation failed");
         ziggy_hip_destroy_context(ctx);
         return ZIGGY_HIP_INITIALIZATION_FAILED;
@@ -126,6 +129,7 @@ void ziggy_hip_destroy_context(ZiggyHipContext *ctx) {
     hipSetDevice(ctx->device);
     if (ctx->stream) hipStreamSynchronize(ctx->stream);
     if (ctx->scratch) hipFree(ctx->scratch);
+    if (ctx->counters) hipFree(ctx->counters);
     if (ctx->seq_begin) hipEventDestroy(ctx->seq_begin);
     if (ctx->seq_end) hipEventDestroy(ctx->seq_end);
     if (ctx->stream) hipStreamDestroy(ctx->stream);
@@ -520,7 +524,7 @@ int ziggy_hip_attention_fused_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *q,
                                   const ZiggyHipBuffer *vc, ZiggyHipBuffer *out, uint32_t heads, uint32_t heads_kv,
                                   uint32_t hd, uint32_t kv_dim, uint32_t ctx_len, uint32_t pos, uint32_t layer_base,
                                   uint32_t window_start, float scale, float softcap, char *err, size_t err_len) {
-    if (!ctx || heads == 0 || heads_kv == 0 || heads % heads_kv || heads / heads_kv > 8 || (hd != 64 && hd != 128 && hd != 256) ||
+    if (!ctx || heads == 0 || heads_kv == 0 || heads_kv > kCtxCounters || heads % heads_kv || heads / heads_kv > 8 || (hd != 64 && hd != 128 && hd != 256) ||
         kv_dim != heads_kv * hd || pos >= ctx_len || window_start > pos) {
         set_err(err, err_len, "unsupported attention shape");
         return ZIGGY_HIP_INVALID_ARGUMENT;
@@ -537,8 +541,8 @@ int ziggy_hip_attention_fused_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *q,
     }
     AttnParams p{};
     p.q = (const float *)q->ptr;
-    p.k_cache = (const __half *)kc->ptr + layer_base;
-    p.v_cache = (const __half *)vc->ptr + layer_base;
+    p.k_cache = (__half *)kc->ptr + layer_base;
+    p.v_cache = (__half *)vc->ptr + layer_base;
     p.out = (float *)out->ptr;
     p.head_count = (int)heads;
     p.head_count_kv = (int)heads_kv;
@@ -547,8 +551,8 @@ int ziggy_hip_attention_fused_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *q,
     p.position = (int)pos;
     p.window_start = (int)window_start;
     p.scale = scale;
-    p.chunk = 64;
-    p.max_splits = (int)((pos - window_start) / 64 + 1);
+    p.max_splits = attention_splits((int)heads_kv, (int)(pos + 1 - window_start));
+    p.counters = ctx->counters;
     const size_t need = attention_scratch_floats((int)heads, (int)hd, p.max_splits) * 4;
     if (need > ctx->scratch_len) {
         set_err(err, err_len, "context too long for the context scratch (%zu bytes)", need);

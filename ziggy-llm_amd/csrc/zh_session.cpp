@@ -69,6 +69,7 @@ struct ZiggyHipSession {
     int q_size = 0, kv_size = 0, max_splits = 0;
     float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr;
     float *logits = nullptr, *part_o = nullptr, *part_ml = nullptr;
+    unsigned *counters = nullptr;  // attention arrival counters (zero between launches)
     __half *kc = nullptr, *vc = nullptr;
     StepState *st = nullptr;
     StepState *st_host = nullptr;  // pinned staging for the host-driven step state
@@ -121,38 +122,25 @@ hipError_t enqueue_kernel(ZiggyHipSession *s, int id, int l, const int *pos_dev,
         p.norm_w = (const float *)L.attn_norm.p;
         return launch_matvec(p, IN_NORM, OUT_STORE, st);
     }
-    case ZIGGY_HIP_KERNEL_ROPE_KV: {
-        RopeKvParams r{};
-        r.q = s->q;
-        r.k = s->k;
-        r.v = s->v;
-        r.q_bias = L.q_bias.present ? (const float *)L.q_bias.p : nullptr;
-        r.k_bias = L.k_bias.present ? (const float *)L.k_bias.p : nullptr;
-        r.v_bias = L.v_bias.present ? (const float *)L.v_bias.p : nullptr;
-        r.q_norm = L.q_norm.present ? (const float *)L.q_norm.p : nullptr;
-        r.k_norm = L.k_norm.present ? (const float *)L.k_norm.p : nullptr;
-        r.k_cache = s->kc + layer_base;
-        r.v_cache = s->vc + layer_base;
-        r.heads = (int)md.head_count;
-        r.kv_heads = (int)md.head_count_kv;
-        r.hd = (int)md.head_dim;
-        r.rope_dim = (int)md.rope_dim;
-        r.style = (int)md.rope_style;
-        r.ctx = (int)md.context_length;
-        r.base = md.rope_freq_base;
-        r.eps = md.rms_norm_eps;
-        r.pos_dev = pos_dev;
-        r.pos = pos;
-        return launch_rope_kv(r, st);
-    }
+    case ZIGGY_HIP_KERNEL_ROPE_KV:
+        // the q/k/v epilogue and the K/V store run inside the attention kernel
+        return hipSuccess;
     case ZIGGY_HIP_KERNEL_ATTENTION: {
         AttnParams a{};
         a.q = s->q;
+        a.k_new = s->k;
+        a.v_new = s->v;
+        a.q_bias = L.q_bias.present ? (const float *)L.q_bias.p : nullptr;
+        a.k_bias = L.k_bias.present ? (const float *)L.k_bias.p : nullptr;
+        a.v_bias = L.v_bias.present ? (const float *)L.v_bias.p : nullptr;
+        a.q_norm = L.q_norm.present ? (const float *)L.q_norm.p : nullptr;
+        a.k_norm = L.k_norm.present ? (const float *)L.k_norm.p : nullptr;
         a.k_cache = s->kc + layer_base;
         a.v_cache = s->vc + layer_base;
         a.out = s->attn;
         a.part_o = s->part_o;
         a.part_ml = s->part_ml;
+        a.counters = s->counters;
         a.head_count = (int)md.head_count;
         a.head_count_kv = (int)md.head_count_kv;
         a.head_dim = (int)md.head_dim;
@@ -161,8 +149,12 @@ hipError_t enqueue_kernel(ZiggyHipSession *s, int id, int l, const int *pos_dev,
         a.position_dev = pos_dev;
         a.window_start = 0;
         a.scale = 1.0f / sqrtf((float)md.head_dim);
-        a.chunk = 64;
-        a.max_splits = pos_dev ? s->max_splits : pos / 64 + 1;
+        a.max_splits = s->max_splits;
+        a.eps = md.rms_norm_eps;
+        a.rope_base = md.rope_freq_base;
+        a.rope_dim = (int)md.rope_dim;
+        a.rope_style = (int)md.rope_style;
+        a.ctx = (int)md.context_length;
         return launch_attention(a, st);
     }
     case ZIGGY_HIP_KERNEL_O_PROJ: {
@@ -243,7 +235,7 @@ uint64_t kernel_bytes(const ZiggyHipSession *s, int id, int l, int pos) {
     auto mb = [](const DT &d) { return d.stride * d.rows; };
     switch (id) {
     case ZIGGY_HIP_KERNEL_QKV: return mb(L.q) + mb(L.k) + mb(L.v);
-    case ZIGGY_HIP_KERNEL_ROPE_KV: return (uint64_t)s->kv_size * 2 * 2;
+    case ZIGGY_HIP_KERNEL_ROPE_KV: return 0;
     case ZIGGY_HIP_KERNEL_ATTENTION: return (uint64_t)(pos + 1) * s->kv_size * 2 * 2;
     case ZIGGY_HIP_KERNEL_O_PROJ: return mb(L.o);
     case ZIGGY_HIP_KERNEL_GATE_UP: return mb(L.gate) + mb(L.up);
@@ -351,7 +343,7 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
     s->md = md;
     s->q_size = (int)(md.head_count * md.head_dim);
     s->kv_size = (int)(md.head_count_kv * md.head_dim);
-    s->max_splits = (int)((md.context_length + 63) / 64);
+    s->max_splits = attention_splits((int)md.head_count_kv, (int)md.context_length);
     const uint64_t H = md.embedding_length, F = md.feed_forward_length, Q = (uint64_t)s->q_size,
                    KV = (uint64_t)s->kv_size;
 
@@ -424,7 +416,7 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
         {(void **)&s->hidden, H * 4}, {(void **)&s->q, Q * 4}, {(void **)&s->k, KV * 4}, {(void **)&s->v, KV * 4},
         {(void **)&s->attn, Q * 4}, {(void **)&s->act, F * 4}, {(void **)&s->logits, logits_len * 4},
         {(void **)&s->part_o, attn_scratch * 4}, {(void **)&s->kc, cache_elems * 2}, {(void **)&s->vc, cache_elems * 2},
-        {(void **)&s->st, sizeof(StepState)},
+        {(void **)&s->st, sizeof(StepState)}, {(void **)&s->counters, md.head_count_kv * sizeof(unsigned)},
     };
     for (auto &r : reqs) {
         e = hipMalloc(r.p, r.bytes);

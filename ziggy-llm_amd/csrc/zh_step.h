@@ -1,4 +1,4 @@
-// zh_step.h -- device-resident step state and the per-step kernel launchers.
+// zh_step.h -- device-resident step state and the step-begin kernel launcher.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -21,21 +21,9 @@ struct StepState {
     int pad[5];
 };
 
-struct RopeKvParams {
-    float *q, *k;
-    float *v;
-    const float *q_bias, *k_bias, *v_bias;  // optional, [heads*hd] / [kv_heads*hd]
-    const float *q_norm, *k_norm;           // optional per-head RMSNorm weights [hd]
-    __half *k_cache, *v_cache;              // this layer: [ctx][kv_heads*hd]
-    int heads, kv_heads, hd, rope_dim, style, ctx;
-    float base, eps;
-    const int *pos_dev;
-    int pos;
-};
 
 hipError_t launch_step_begin(StepState *st, const uint32_t *prompt, uint32_t *history, const uint8_t *embd,
                              uint64_t embd_stride, int embd_rows, int embd_type, int cols, float *hidden,
                              hipStream_t s);
-hipError_t launch_rope_kv(const RopeKvParams &p, hipStream_t s);
 
 }  // namespace zh
