@@ -21,6 +21,7 @@
 // holds the current position, which stores k and v to the cache as binary16
 // (store_kv_half, matvec.metal:246-255) and uses the stored values for that
 // position.  The position may be read from device memory (graph replay).
+#include <cstdlib>
 #include <type_traits>
 
 #include "zh_internal.h"
@@ -452,11 +453,22 @@ size_t attention_scratch_floats(int head_count, int head_dim, int max_splits) {
     return (size_t)head_count * max_splits * kMaxGroup * (head_dim + 2);
 }
 
+// Target workgroups of the attention grid at the longest context;
+// ZIGGY_HIP_ATTN_WGS overrides it (a tuning knob).
+static int attention_target_wgs() {
+    static int t = [] {
+        const char *e = getenv("ZIGGY_HIP_ATTN_WGS");
+        const int v = e ? atoi(e) : 256;
+        return v > 0 ? v : 256;
+    }();
+    return t;
+}
+
 int attention_splits(int kv_heads, int max_positions) {
-    // about one workgroup per CU at the longest context; never more splits
-    // than 64-position chunks
+    // a bounded number of splits (the merge reads them all); never more
+    // splits than 64-position chunks
     const int chunks = (max_positions + kChunk - 1) / kChunk;
-    int s = 256 / (kv_heads > 0 ? kv_heads : 1);
+    int s = attention_target_wgs() / (kv_heads > 0 ? kv_heads : 1);
     if (s < 1) s = 1;
     return s < chunks ? s : chunks;
 }
