@@ -11,9 +11,15 @@ synthetic.
 
 Also reported, on the same JSON line:
   hbm_fraction  -- (weight + KV bytes per token) x tok/s / 8 TB/s;
-  roofline      -- the dominant kernel (fused RMSNorm + gate/up + SwiGLU, Q4_K),
-                   timed with HIP events rotating over the 32 layers so its
-                   weights stream from HBM, against the 8 TB/s HBM peak;
+  roofline      -- the dominant kernel (fused RMSNorm + gate/up + SwiGLU, Q4_K):
+                   its algorithmic bytes per launch (66,060,288 B: 2 x 14336 x
+                   4096 weights at 144 B per 256) over its mean launch time,
+                   measured here with one pair of HIP events on the session
+                   stream around back-to-back launches rotating over the 32
+                   layers (weights stream from HBM), against the 8 TB/s peak;
+                   `traffic` is the HBM bytes per launch from the committed
+                   rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+                   (profiles/gate_up_llama8b_hbm_traffic.md), else null;
   cpu_baseline  -- the CPU oracle (a C restatement of the reference's CPU
                    decode path, same threads policy: 1 + min(11, ncpu - 1))
                    decoding the same model at the same context on host cores.
@@ -94,9 +100,13 @@ def main():
         kernels[name] = {"avg_us": round(ns / 1e3, 2), "bytes": nb, "gbs": round(nb / ns, 1) if ns else None}
         log(f"kernel {name}: {ns / 1e3:.2f} us, {nb / 1e6:.2f} MB -> {nb / max(ns, 1):.0f} GB/s")
     dom = kernels["gate_up"]
+    traffic = None
+    if args.model == "llama8b":
+        from zhip import pmc
+        traffic = pmc.read_traffic(os.path.join(REPO, "profiles", "gate_up_llama8b_hbm_traffic.md"))
     roofline = {"bound": "hbm", "kernel": "gate_up (fused RMSNorm + Q4_K gate/up + SwiGLU)",
                 "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "bytes_per_launch": dom["bytes"], "avg_launch_us": dom["avg_us"]}
     sess.close()
     ctx.close()

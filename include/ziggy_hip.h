@@ -163,8 +163,8 @@ int ziggy_hip_run_matvec_q6k_argmax_f32(ZiggyHipContext *ctx, const ZiggyHipBuff
  * launches of ziggy_hip_run_matvec's kernel, launch i reading copy
  * (i % copies) of the matrix, copies laid out copy_stride bytes apart in
  * `matrices`, so a copy set larger than the 256 MB Infinity Cache streams
- * from HBM.  Each launch is bracketed by its own HIP events; *avg_ns is the
- * mean launch duration. */
+ * from HBM.  The launches run back to back between one pair of HIP events;
+ * *avg_ns is the elapsed time divided by `iterations`. */
 int ziggy_hip_time_matvec(ZiggyHipContext *ctx, uint32_t tensor_type, const ZiggyHipBuffer *matrices,
                           uint32_t copies, size_t copy_stride, const ZiggyHipBuffer *input, ZiggyHipBuffer *output,
                           uint32_t rows, uint32_t cols, uint32_t iterations, uint64_t *avg_ns,
@@ -369,12 +369,13 @@ int ziggy_hip_session_read_logits(ZiggyHipSession *session, float *out, char *er
 
 /* Times one kernel of the decode step (no counterpart in the reference; its
  * Metal profiler times host-side encode, runtime/metal_profile.zig:80-315):
- * `iterations` launches at the session's current position, rotating over the
- * layers so successive launches read distinct weights from HBM; each launch
- * is bracketed by its own HIP events on the session stream.  Reports the
- * mean launch duration and the algorithmic bytes one launch streams
- * (weights + binary16 KV; activations excluded).  Leaves the KV cache and
- * position as they were, but overwrites the hidden state. */
+ * one warm-up launch, then `iterations` back-to-back launches at the
+ * session's current position, rotating over the layers so successive launches
+ * read distinct weights from HBM, between one pair of HIP events on the
+ * session stream.  Reports the mean launch duration and the algorithmic bytes
+ * one launch streams (weights + binary16 KV; activations excluded).  Leaves
+ * the position as it was; overwrites the hidden state and (ATTENTION) the
+ * cache row of the current position, which the next step writes anyway. */
 int ziggy_hip_session_time_kernel(ZiggyHipSession *session, uint32_t kernel, uint32_t iterations,
                                   uint64_t *avg_ns, uint64_t *bytes_per_launch, char *error_message,
                                   size_t error_message_len);

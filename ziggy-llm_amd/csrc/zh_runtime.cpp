@@ -688,21 +688,19 @@ extern "C" int ziggy_hip_time_matvec(ZiggyHipContext *ctx, uint32_t type, const 
     p.seg[0].fmt = (int)type;
     p.cols = (int)cols;
     p.x = (const float *)in->ptr;
-    double total = 0.0;
-    hipError_t e = hipSuccess;
+    // back-to-back launches rotating over the copies, between one event pair
+    float ms = 0.f;
+    hipError_t e = hipEventRecord(e0, ctx->stream);
     for (uint32_t i = 0; i < iterations && e == hipSuccess; i++) {
         p.seg[0].w = (const uint8_t *)m->ptr + (size_t)(i % copies) * copy_stride;
-        e = hipEventRecord(e0, ctx->stream);
-        if (e == hipSuccess) e = launch_matvec(p, IN_PLAIN, OUT_STORE, ctx->stream);
-        if (e == hipSuccess) e = hipEventRecord(e1, ctx->stream);
-        if (e == hipSuccess) e = hipEventSynchronize(e1);
-        float ms = 0.f;
-        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
-        total += ms;
+        e = launch_matvec(p, IN_PLAIN, OUT_STORE, ctx->stream);
     }
+    if (e == hipSuccess) e = hipEventRecord(e1, ctx->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
     hipEventDestroy(e0);
     hipEventDestroy(e1);
     if (e != hipSuccess) return hip_fail(e, "time_matvec", err, err_len);
-    *avg_ns = (uint64_t)(total * 1e6 / iterations);
+    *avg_ns = (uint64_t)((double)ms * 1e6 / iterations);
     return ZIGGY_HIP_OK;
 }

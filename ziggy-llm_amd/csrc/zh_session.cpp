@@ -668,24 +668,24 @@ int ziggy_hip_session_time_kernel(ZiggyHipSession *s, uint32_t kernel, uint32_t 
         hipEventDestroy(e0);
         return fail(err, err_len, ZIGGY_HIP_EXECUTION_FAILED, "event creation failed");
     }
-    double total_ms = 0.0;
+    // one warm-up launch, then `iterations` back-to-back launches (rotating
+    // over the layers so weights stream from HBM) between one event pair
     uint64_t bytes = 0;
-    hipError_t e = hipSuccess;
+    float ms = 0.f;
+    hipError_t e = enqueue_kernel(s, (int)kernel, 0, nullptr, pos, st);
+    if (e == hipSuccess) e = hipEventRecord(e0, st);
     for (uint32_t i = 0; i < iterations && e == hipSuccess; i++) {
-        const int l = (int)(i % (uint32_t)L);
-        e = hipEventRecord(e0, st);
-        if (e == hipSuccess) e = enqueue_kernel(s, (int)kernel, l, nullptr, pos, st);
-        if (e == hipSuccess) e = hipEventRecord(e1, st);
-        if (e == hipSuccess) e = hipEventSynchronize(e1);
-        float ms = 0.f;
-        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
-        total_ms += ms;
+        const int l = (int)((i + 1) % (uint32_t)L);
+        e = enqueue_kernel(s, (int)kernel, l, nullptr, pos, st);
         bytes += kernel_bytes(s, (int)kernel, l, pos);
     }
+    if (e == hipSuccess) e = hipEventRecord(e1, st);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
     hipEventDestroy(e0);
     hipEventDestroy(e1);
     if (e != hipSuccess) return hip_fail(e, "time_kernel", err, err_len);
-    *avg_ns = (uint64_t)(total_ms * 1e6 / iterations);
+    *avg_ns = (uint64_t)((double)ms * 1e6 / iterations);
     *bytes_per_launch = bytes / iterations;
     return ZIGGY_HIP_OK;
 }
