@@ -367,3 +367,44 @@ def test_moe_routing_closed_form():
     assert list(idx) == list(top)
     e = np.exp(logits[top].astype(np.float64) - logits[top].max())
     assert np.allclose(w, e / e.sum(), rtol=1e-5)
+
+
+def test_f16_to_f32_matches_numpy_for_every_bit_pattern():
+    # readF16AsF32 (model/loader.zig:4484-4488) is an exact widening, subnormals,
+    # infinities and NaN payload class included: numpy's binary16 is the pin
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    want = bits.astype(np.uint16).view(np.float16).astype(np.float32)
+    got = np.array([zo.lib().zo_f16_to_f32(int(b)) for b in bits], np.float32)
+    finite = np.isfinite(want)
+    assert np.array_equal(got[finite].view(np.uint32), want[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[np.isinf(want)], want[np.isinf(want)])
+
+
+def test_silu_and_sigmoid_closed_forms():
+    # siluInPlace / sigmoidScalar (model/loader.zig:4004-4029) against float64
+    x = np.concatenate([np.linspace(-30, 30, 601), [0.0, -0.0, 1e-30, -88.0, 88.0]]).astype(np.float32)
+    got = zo.silu(x)
+    xd = x.astype(np.float64)
+    want = xd / (1.0 + np.exp(-xd))
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-30)) < 4e-7
+    for v in (-20.0, -1.5, 0.0, 0.25, 3.0, 20.0):
+        s = zo.lib().zo_sigmoid(float(np.float32(v)))
+        assert abs(s - 1.0 / (1.0 + np.exp(-v))) < 1e-7
+
+
+def test_rms_norm_per_head_closed_form():
+    # rmsNormPerHeadWithOffset (model/loader.zig:1777-1812): each head slice is
+    # normalised on its own (its own mean square) with the shared weights
+    rng = np.random.default_rng(13)
+    heads, hd = 5, 64
+    x = rng.standard_normal(heads * hd).astype(np.float32)
+    w = rng.standard_normal(hd).astype(np.float32)
+    got = zo.rms_norm_per_head(x, w, heads, hd, 1e-6)
+    # heads are independent: a head computed alone gives the same bits
+    for h in range(heads):
+        alone = zo.rms_norm_per_head(x[h * hd:(h + 1) * hd].copy(), w, 1, hd, 1e-6)
+        assert np.array_equal(got[h * hd:(h + 1) * hd], alone)
+    xd = x.reshape(heads, hd).astype(np.float64)
+    want = xd / np.sqrt((xd ** 2).mean(axis=1, keepdims=True) + 1e-6) * w
+    assert np.max(np.abs(got.reshape(heads, hd) - want)) < 1e-5
