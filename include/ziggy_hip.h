@@ -228,9 +228,11 @@ int ziggy_hip_apply_rope_to_dst_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *
 int ziggy_hip_store_kv_half(ZiggyHipContext *ctx, const ZiggyHipBuffer *src, ZiggyHipBuffer *dst,
                             size_t dst_offset_elements, uint32_t count, char *error_message,
                             size_t error_message_len);
-/* GQA decode attention over the binary16 cache; split-K flash decoding with a
- * merge pass (replaces ziggy_metal_attention_fused_f32, bridge.h:459-477).
- * softcap must be 0 (softcapping belongs to Gemma, outside this path). */
+/* GQA decode attention over the binary16 cache; split-K flash decoding whose
+ * last split to finish merges the others (replaces
+ * ziggy_metal_attention_fused_f32, bridge.h:459-477).  q is the roped query;
+ * the cache already holds the current position.  softcap must be 0
+ * (softcapping belongs to Gemma, outside this path). */
 int ziggy_hip_attention_fused_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *q, const ZiggyHipBuffer *k_cache,
                                   const ZiggyHipBuffer *v_cache, ZiggyHipBuffer *output, uint32_t head_count,
                                   uint32_t head_count_kv, uint32_t head_dim, uint32_t kv_dim,

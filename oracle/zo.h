@@ -17,6 +17,17 @@
  * cannot fuse on its own.  Zig's @reduce(.Add) over an 8-lane f32 vector is
  * restated as a sequential left-to-right sum (the reference does not pin the
  * order; results agree with it to tolerance, not to the last ulp).
+ *
+ * Parity unpinned (no reference-held vector, closed form or brute force can
+ * fix these without running the Zig binary):
+ *   - the summation order of the matvec dots (zo_dot_*, zo_matvec): pinned
+ *     only to a float64 dot of the dequantized row, not to the last ulp;
+ *   - the ulps of pow / sin / cos inside zo_apply_rope (Zig std.math vs
+ *     glibc): pinned by closed forms (position 0, partial rotary) and
+ *     tolerance only.
+ * Everything else is pinned by the reference's known-answer tests, its
+ * fixture blocks and golden text, closed forms and brute-force layouts
+ * (tests/test_oracle_pins.py, tests/test_golden.py).
  */
 #ifndef ZIGGY_ORACLE_H
 #define ZIGGY_ORACLE_H
