@@ -99,27 +99,41 @@ __device__ __forceinline__ uint32_t ordered_bits(float v) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// Stages the 64 activations of slot s (zeros for inactive lanes) with the
-// input prologue applied, in the slot representation of format F.
+// The raw activations of a lane's slot (and the norm weights or the up half
+// for the fused prologues), loaded before the weight ring so that waiting for
+// them does not wait for the ring (vmcnt completes in order).
+struct XRaw {
+    float4 a[16], b[16];
+};
+
 template <int F, int IN>
-__device__ __forceinline__ void stage_x(XOf_t<F> &xs, int s, bool active, const MvParams &p, int T, float *lds) {
-    float v[64], aux[64];
+__device__ __forceinline__ void stage_load(XRaw &r, int s, bool active, const MvParams &p) {
     const int base = Geom<F>::x_base(s);
 #pragma unroll
     for (int w = 0; w < 4; w++) {
         const int o = base + w * Geom<F>::kXStride;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+            r.a[4 * w + c] = make_float4(0.f, 0.f, 0.f, 0.f);
+            r.b[4 * w + c] = r.a[4 * w + c];
             if (active) {
-                a = *reinterpret_cast<const float4 *>(p.x + o + 4 * c);
-                if (IN == IN_NORM) b = *reinterpret_cast<const float4 *>(p.norm_w + o + 4 * c);
-                if (IN == IN_SILU) b = *reinterpret_cast<const float4 *>(p.x2 + o + 4 * c);
+                r.a[4 * w + c] = *reinterpret_cast<const float4 *>(p.x + o + 4 * c);
+                if (IN == IN_NORM) r.b[4 * w + c] = *reinterpret_cast<const float4 *>(p.norm_w + o + 4 * c);
+                if (IN == IN_SILU) r.b[4 * w + c] = *reinterpret_cast<const float4 *>(p.x2 + o + 4 * c);
             }
-            const int i = 16 * w + 4 * c;
-            v[i] = a.x, v[i + 1] = a.y, v[i + 2] = a.z, v[i + 3] = a.w;
-            aux[i] = b.x, aux[i + 1] = b.y, aux[i + 2] = b.z, aux[i + 3] = b.w;
         }
+    }
+}
+
+// Applies the input prologue to the loaded slot and converts it to the slot
+// representation of format F.
+template <int F, int IN>
+__device__ __forceinline__ void stage_finish(XOf_t<F> &xs, const XRaw &r, const MvParams &p, int T, float *lds) {
+    float v[64], aux[64];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        v[4 * k] = r.a[k].x, v[4 * k + 1] = r.a[k].y, v[4 * k + 2] = r.a[k].z, v[4 * k + 3] = r.a[k].w;
+        aux[4 * k] = r.b[k].x, aux[4 * k + 1] = r.b[k].y, aux[4 * k + 2] = r.b[k].z, aux[4 * k + 3] = r.b[k].w;
     }
     if (IN == IN_NORM) {
         // the team covers every slot of x, so the team sum of squares is the full one
@@ -138,6 +152,15 @@ __device__ __forceinline__ void stage_x(XOf_t<F> &xs, int s, bool active, const 
         for (int i = 0; i < 64; i++) v[i] = (v[i] / (1.0f + expf(-v[i]))) * aux[i];
     }
     to_slot(v, xs);
+}
+
+// Stages the 64 activations of slot s (zeros for inactive lanes) with the
+// input prologue applied, in the slot representation of format F.
+template <int F, int IN>
+__device__ __forceinline__ void stage_x(XOf_t<F> &xs, int s, bool active, const MvParams &p, int T, float *lds) {
+    XRaw r;
+    stage_load<F, IN>(r, s, active, p);
+    stage_finish<F, IN>(xs, r, p, T, lds);
 }
 
 template <int F, int IN, int OUT>
@@ -272,6 +295,9 @@ __device__ __forceinline__ void mv_body_fast(const MvParams &p, const MvSeg &sg,
     // It is loaded after the previous batch's epilogue, so the waits for it
     // only cover weight loads issued a batch earlier.
     constexpr bool kReadY = OUT == OUT_ADD || OUT == OUT_WADD;
+    XRaw xr;
+    stage_load<F, IN>(xr, lane, active, p);
+    __builtin_amdgcn_sched_barrier(0);  // keep the x loads ahead of the ring loads
     Raw<F> ra[D], rb[D];
 #pragma unroll
     for (int k = 0; k < D; k++) {
@@ -280,8 +306,9 @@ __device__ __forceinline__ void mv_body_fast(const MvParams &p, const MvSeg &sg,
     }
     float ry = 0.f;
     if (kReadY) ry = sg.y[row_of(l4)];
+    __builtin_amdgcn_sched_barrier(0);  // all loads issued before the staging math
     XOf_t<F> xs;
-    stage_x<F, IN>(xs, lane, active, p, TT, lds);
+    stage_finish<F, IN>(xs, xr, p, TT, lds);
 
     float best_v = -INFINITY;
     int best_r = 0x7fffffff;
