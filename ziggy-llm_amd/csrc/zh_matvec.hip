@@ -1,423 +1,9 @@
-// zh_matvec.hip -- batch-1 dequant-matvec kernels for gfx950.
-//
-// Design (HBM-bound; the point is to keep enough weight bytes in flight):
-//   * A row is processed by a "team" of T lanes (T = next power of two of
-//     cols/64, at most 256); lane j owns weight slot j (64 weights) of every
-//     row the team visits, so its 64 activations are loaded (and normalised /
-//     SiLU-gated when fused) once per workgroup and stay in VGPRs.  A team
-//     covers the whole input vector, which lets the fused RMSNorm take its
-//     sum of squares from the staged slots (one pass over x).
-//   * Quant blocks are read in their native GGUF layout with 16-byte loads;
-//     scales are unpacked in registers (zh_quant.h).
-//   * Weight loads run ring_depth() rows ahead through a ring of register buffers.
-//     Every load is unconditional (rows past the team's range re-read its
-//     last row), so the compiler's in-order vmcnt waits for the row being
-//     consumed only, never for the rows behind it.
-//   * Team sums use DPP row operations inside a wavefront (the total lands in
-//     the team's last lane); teams wider than a wavefront finish through LDS
-//     with one barrier per row (double-buffered slots).
-//   * Epilogues: store, residual add, SwiGLU pair (silu(gate) * up from two
-//     matrices sharing the staged input), greedy argmax (packed 64-bit
-//     atomicMax, ties to the lowest row), expert-weighted add.
-//   * Input prologues: plain, fused RMSNorm (rmsNorm order (scale * x) * w as
-//     model/loader.zig:3404-3426), fused SiLU(gate) * up (the silu_down path,
-//     matvec.metal:2229-2300).
-
-#include "zh_internal.h"
-#include "zh_quant.h"
+// zh_matvec.hip -- host-side planning and dispatch of the batch-1
+// dequant-matvec kernels (templates in zh_mv.h, instantiated by the
+// zh_mv_*.hip files), and the bit-exact dequant kernels.
+#include "zh_mv.h"
 
 namespace zh {
-
-constexpr int kThreads = 256;
-// Rows per team in flight (ring of register buffers).  The dense formats hold
-// 128 / 256 bytes per lane and row, and SwiGLU rings carry two matrices, so
-// their rings are shorter.
-#ifndef ZH_RING_QUANT
-#define ZH_RING_QUANT 4
-#endif
-#ifndef ZH_RING_PAIR
-#define ZH_RING_PAIR 3
-#endif
-template <int F, int OUT> constexpr int ring_depth() {
-    return F == F32 ? 1 : F == F16 ? 2 : OUT == OUT_SWIGLU ? ZH_RING_PAIR : ZH_RING_QUANT;
-}
-
-// v + (v permuted by a DPP control); rows outside ROW_MASK add 0.
-template <int CTRL, int ROW_MASK> __device__ __forceinline__ float dpp_add(float v) {
-    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
-}
-
-// Sum over aligned groups of T lanes (T a power of two, <= 64) of a wavefront.
-// The group total is valid in the group's last lane (in every lane for T <= 16).
-__device__ __forceinline__ float group_sum(float v, int T) {
-    if (T >= 2) v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
-    if (T >= 4) v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
-    if (T >= 8) v = dpp_add<0x141, 0xF>(v);  // row_half_mirror
-    if (T >= 16) v = dpp_add<0x140, 0xF>(v); // row_mirror
-    if (T >= 32) v = dpp_add<0x142, 0xA>(v); // row_bcast:15 into rows 1 and 3
-    if (T >= 64) v = dpp_add<0x143, 0xC>(v); // row_bcast:31 into rows 2 and 3
-    return v;
-}
-
-// Team sum; valid in the team's last lane.  Teams wider than a wavefront use
-// lds[slot*4 .. slot*4+3] and one barrier (callers alternate `slot`).
-__device__ __forceinline__ float team_sum(float v, int T, float *lds, int slot) {
-    if (T <= 64) return group_sum(v, T);
-    v = group_sum(v, 64);
-    const int tid = threadIdx.x, wave = tid >> 6;
-    if ((tid & 63) == 63) lds[slot * 4 + wave] = v;
-    __syncthreads();
-    const int per = T >> 6, first = (wave / per) * per;
-    float r = 0.f;
-    for (int i = 0; i < per; i++) r += lds[slot * 4 + first + i];
-    return r;
-}
-
-// Batched team sums for the fast paths (T = 64 or 256): four per-lane values
-// (rows or gate/up halves) reduce together.  Two DPP transposition steps
-// leave each lane one value for value index (lane & 3); row_ror and two
-// swizzles finish the sums over the wavefront.  On return every lane holds
-// the wavefront total of value (lane & 3).
-template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float reduce4_wave(float v0, float v1, float v2, float v3) {
-    const int l = threadIdx.x;
-    const bool b0 = l & 1, b1 = l & 2;
-    const float a = (b0 ? v1 : v0) + dpp_mov<0xB1>(b0 ? v0 : v1);  // lane ^ 1
-    const float b = (b0 ? v3 : v2) + dpp_mov<0xB1>(b0 ? v2 : v3);
-    float c = (b1 ? b : a) + dpp_mov<0x4E>(b1 ? a : b);            // lane ^ 2
-    c += dpp_mov<0x124>(c);                                       // row_ror:4
-    c += dpp_mov<0x128>(c);                                       // row_ror:8
-    c += __shfl_xor(c, 16, 64);
-    c += __shfl_xor(c, 32, 64);
-    return c;
-}
-
-__device__ __forceinline__ uint32_t ordered_bits(float v) {
-    const uint32_t b = __float_as_uint(v);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-// The raw activations of a lane's slot (and the norm weights or the up half
-// for the fused prologues), loaded before the weight ring so that waiting for
-// them does not wait for the ring (vmcnt completes in order).
-struct XRaw {
-    float4 a[16], b[16];
-};
-
-template <int F, int IN>
-__device__ __forceinline__ void stage_load(XRaw &r, int s, bool active, const MvParams &p) {
-    const int base = Geom<F>::x_base(s);
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-        const int o = base + w * Geom<F>::kXStride;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            r.a[4 * w + c] = make_float4(0.f, 0.f, 0.f, 0.f);
-            r.b[4 * w + c] = r.a[4 * w + c];
-            if (active) {
-                r.a[4 * w + c] = *reinterpret_cast<const float4 *>(p.x + o + 4 * c);
-                if (IN == IN_NORM) r.b[4 * w + c] = *reinterpret_cast<const float4 *>(p.norm_w + o + 4 * c);
-                if (IN == IN_SILU) r.b[4 * w + c] = *reinterpret_cast<const float4 *>(p.x2 + o + 4 * c);
-            }
-        }
-    }
-}
-
-// Applies the input prologue to the loaded slot and converts it to the slot
-// representation of format F.
-template <int F, int IN>
-__device__ __forceinline__ void stage_finish(XOf_t<F> &xs, const XRaw &r, const MvParams &p, int T, float *lds) {
-    float v[64], aux[64];
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-        v[4 * k] = r.a[k].x, v[4 * k + 1] = r.a[k].y, v[4 * k + 2] = r.a[k].z, v[4 * k + 3] = r.a[k].w;
-        aux[4 * k] = r.b[k].x, aux[4 * k + 1] = r.b[k].y, aux[4 * k + 2] = r.b[k].z, aux[4 * k + 3] = r.b[k].w;
-    }
-    if (IN == IN_NORM) {
-        // the team covers every slot of x, so the team sum of squares is the full one
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < 64; i++) ss = fmaf(v[i], v[i], ss);
-        ss = team_sum(ss, T, lds, 8);  // lds[32..35]: clear of the row-sum slots
-        // every team holds the same total: in lane 63 of each wavefront for
-        // T <= 64, in every lane for wider teams
-        const float tot = T <= 64 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 63)) : ss;
-        const float scale = 1.0f / sqrtf(tot / (float)p.cols + p.eps);
-#pragma unroll
-        for (int i = 0; i < 64; i++) v[i] = (scale * v[i]) * aux[i];
-    } else if (IN == IN_SILU) {
-#pragma unroll
-        for (int i = 0; i < 64; i++) v[i] = (v[i] / (1.0f + expf(-v[i]))) * aux[i];
-    }
-    to_slot(v, xs);
-}
-
-// Stages the 64 activations of slot s (zeros for inactive lanes) with the
-// input prologue applied, in the slot representation of format F.
-template <int F, int IN>
-__device__ __forceinline__ void stage_x(XOf_t<F> &xs, int s, bool active, const MvParams &p, int T, float *lds) {
-    XRaw r;
-    stage_load<F, IN>(r, s, active, p);
-    stage_finish<F, IN>(xs, r, p, T, lds);
-}
-
-template <int F, int IN, int OUT>
-__device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int wg_in_seg, float *lds) {
-    constexpr int D = ring_depth<F, OUT>();
-    const int tid = threadIdx.x, T = p.team, teams = kThreads / T;
-    const int team = tid / T, lane = tid % T;
-    const bool active = lane < p.slots;
-    const int sl = active ? lane : p.slots - 1;  // inactive lanes re-read a valid slot
-    const bool writer = lane == T - 1;
-
-    const uint8_t *wbase = sg.w, *wbase2 = sg.w2;
-    float wscale = p.weight_scale;
-    if (p.expert) {
-        const uint32_t e = p.expert[2 * p.expert_slot];
-        if (e >= (uint32_t)p.expert_limit) return;  // uniform over the grid: no rows are read
-        const uint64_t off = (uint64_t)e * (uint64_t)p.rows_per_expert * sg.stride;
-        wbase += off;
-        if (wbase2) wbase2 += off;
-        wscale = __uint_as_float(p.expert[2 * p.expert_slot + 1]);
-    }
-    const int r_begin = wg_in_seg * sg.rows_per_wg;
-    const int r_end = min(r_begin + sg.rows_per_wg, sg.rows);
-    const int n = p.rows_per_team;
-    const int r0 = r_begin + team;
-    // row `it` of this team, clamped to the workgroup's last row (loads only)
-    auto row_of = [&](int it) { return min(r0 + it * teams, r_end - 1); };
-
-    // Issue the first rows' weight loads before staging the input: they do not
-    // depend on it, so HBM latency overlaps the staging and the norm.
-    // The residual read of ADD / WADD rides in the same ring: a late load of
-    // y[r] would make the in-order vmcnt wait cover the prefetched rows too.
-    constexpr bool kReadY = OUT == OUT_ADD || OUT == OUT_WADD;
-    Raw<F> ra[D], rb[D];
-    float ry[D];
-#pragma unroll
-    for (int k = 0; k < D; k++) {
-        ra[k] = slot_load<F>(wbase + (uint64_t)row_of(k) * sg.stride, sl);
-        if (OUT == OUT_SWIGLU) rb[k] = slot_load<F>(wbase2 + (uint64_t)row_of(k) * sg.stride, sl);
-        if (kReadY) ry[k] = sg.y[row_of(k)];
-    }
-    XOf_t<F> xs;
-    stage_x<F, IN>(xs, lane, active, p, T, lds);
-
-    float best_v = -INFINITY;
-    int best_r = 0x7fffffff;
-    for (int it0 = 0; it0 < n; it0 += D) {
-#pragma unroll
-        for (int k = 0; k < D; k++) {
-            const int it = it0 + k;
-            if (it < n) {
-                float v = slot_dot<F>(ra[k], sl, xs), v2 = 0.f;
-                if (OUT == OUT_SWIGLU) v2 = slot_dot<F>(rb[k], sl, xs);
-                v = active ? v : 0.f;
-                v = team_sum(v, T, lds, it & 1);
-                if (OUT == OUT_SWIGLU) {
-                    v2 = active ? v2 : 0.f;
-                    v2 = team_sum(v2, T, lds, 2 + (it & 1));
-                }
-                const int r = r0 + it * teams;
-                if (writer && r < r_end) {
-                    if (OUT == OUT_STORE) {
-                        sg.y[r] = v;
-                    } else if (OUT == OUT_ADD) {
-                        sg.y[r] = ry[k] + v;
-                    } else if (OUT == OUT_WADD) {
-                        sg.y[r] = fmaf(v, wscale, ry[k]);
-                    } else if (OUT == OUT_SWIGLU) {
-                        sg.y[r] = (v / (1.0f + expf(-v))) * v2;  // siluInPlace then gate * up
-                    } else if (OUT == OUT_ARGMAX) {
-                        if (sg.y) sg.y[r] = v;
-                        if (v > best_v || (v == best_v && r < best_r)) {
-                            best_v = v;
-                            best_r = r;
-                        }
-                    }
-                }
-            }
-            // refill this ring slot (unconditionally: keeps the vmcnt waits exact)
-            ra[k] = slot_load<F>(wbase + (uint64_t)row_of(it + D) * sg.stride, sl);
-            if (OUT == OUT_SWIGLU) rb[k] = slot_load<F>(wbase2 + (uint64_t)row_of(it + D) * sg.stride, sl);
-            if (kReadY) ry[k] = sg.y[row_of(it + D)];
-        }
-    }
-    if (OUT == OUT_ARGMAX) {
-        __shared__ unsigned long long keys[kThreads];
-        unsigned long long key = 0ull;
-        if (writer && best_r != 0x7fffffff)
-            key = ((unsigned long long)ordered_bits(best_v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_r);
-        if (writer) keys[team] = key;
-        __syncthreads();
-        if (tid == 0) {
-            unsigned long long k = keys[0];
-            for (int i = 1; i < teams; i++) k = keys[i] > k ? keys[i] : k;
-            if (k) atomicMax(p.argmax_slot, k);
-        }
-    }
-}
-
-// Fast path for teams of TT = 64 lanes (one team per wavefront) or 256 lanes
-// (one team per workgroup).  Rows are consumed four at a time (two gate/up
-// pairs for SwiGLU), each ring slot is refilled as soon as its dot is done,
-// and the four sums reduce together.  Residual reads (ADD / WADD) use scalar
-// loads, which count on lgkmcnt and so never wait on the weight ring.
-template <int F, int IN, int OUT, int TT>
-__device__ __forceinline__ void mv_body_fast(const MvParams &p, const MvSeg &sg, int wg_in_seg, float *lds) {
-    constexpr bool kPair = OUT == OUT_SWIGLU;
-    constexpr int D = kPair ? 2 : 4;  // ring slots: rows (or gate/up row pairs) per batch
-    constexpr int teams = kThreads / TT;
-    const int tid = threadIdx.x, lane = tid % TT, wave = tid >> 6, l4 = tid & 3;
-    const int team = __builtin_amdgcn_readfirstlane(tid / TT);
-    const bool active = lane < p.slots;
-    const int sl = active ? lane : p.slots - 1;  // inactive lanes re-read a valid slot
-
-    const uint8_t *wbase = sg.w, *wbase2 = sg.w2;
-    float wscale = p.weight_scale;
-    if (p.expert) {
-        const uint32_t e = p.expert[2 * p.expert_slot];
-        if (e >= (uint32_t)p.expert_limit) return;  // uniform over the grid: no rows are read
-        const uint64_t off = (uint64_t)e * (uint64_t)p.rows_per_expert * sg.stride;
-        wbase += off;
-        if (wbase2) wbase2 += off;
-        wscale = __uint_as_float(p.expert[2 * p.expert_slot + 1]);
-    }
-    const int r_begin = wg_in_seg * sg.rows_per_wg;
-    const int r_end = min(r_begin + sg.rows_per_wg, sg.rows);
-    const int n = p.rows_per_team;
-    const int r0 = r_begin + team;
-    auto row_of = [&](int it) { return min(r0 + it * teams, r_end - 1); };
-
-    // The residual of ADD / WADD: lane l reads y of row (l & 3) of the batch.
-    // It is loaded after the previous batch's epilogue, so the waits for it
-    // only cover weight loads issued a batch earlier.
-    constexpr bool kReadY = OUT == OUT_ADD || OUT == OUT_WADD;
-    XRaw xr;
-    stage_load<F, IN>(xr, lane, active, p);
-    __builtin_amdgcn_sched_barrier(0);  // keep the x loads ahead of the ring loads
-    Raw<F> ra[D], rb[D];
-#pragma unroll
-    for (int k = 0; k < D; k++) {
-        ra[k] = slot_load<F>(wbase + (uint64_t)row_of(k) * sg.stride, sl);
-        if (kPair) rb[k] = slot_load<F>(wbase2 + (uint64_t)row_of(k) * sg.stride, sl);
-    }
-    float ry = 0.f;
-    if (kReadY) ry = sg.y[row_of(l4)];
-    __builtin_amdgcn_sched_barrier(0);  // all loads issued before the staging math
-    XOf_t<F> xs;
-    stage_finish<F, IN>(xs, xr, p, TT, lds);
-
-    float best_v = -INFINITY;
-    int best_r = 0x7fffffff;
-    for (int it0 = 0; it0 < n; it0 += D) {
-        float v[4];
-#pragma unroll
-        for (int k = 0; k < D; k++) {
-            float a = 0.f, b = 0.f;
-            if (it0 + k < n) {
-                a = slot_dot<F>(ra[k], sl, xs);
-                if (kPair) b = slot_dot<F>(rb[k], sl, xs);
-            }
-            if (kPair) {
-                v[2 * k] = active ? a : 0.f;
-                v[2 * k + 1] = active ? b : 0.f;
-            } else {
-                v[k] = active ? a : 0.f;
-            }
-            // Refill this ring slot (unconditionally: keeps the vmcnt waits
-            // exact).  The scheduling barrier keeps the loads after the dot
-            // that reads the slot, so the ring stays in place across iterations.
-            __builtin_amdgcn_sched_barrier(0);
-            ra[k] = slot_load<F>(wbase + (uint64_t)row_of(it0 + k + D) * sg.stride, sl);
-            if (kPair) rb[k] = slot_load<F>(wbase2 + (uint64_t)row_of(it0 + k + D) * sg.stride, sl);
-        }
-        float c = reduce4_wave(v[0], v[1], v[2], v[3]);
-        if (TT == 256) {
-            // one team per workgroup: combine the four wavefront totals
-            const int slot = (it0 / D) & 1;
-            if ((tid & 63) < 4) lds[slot * 16 + wave * 4 + l4] = c;
-            __syncthreads();
-            c = (lds[slot * 16 + l4] + lds[slot * 16 + 4 + l4]) + (lds[slot * 16 + 8 + l4] + lds[slot * 16 + 12 + l4]);
-        }
-        // value (lane & 3) of the batch: row it0 + l4 (single) or half l4 & 1 of row it0 + l4 / 2 (pair)
-        if (kPair) {
-            const float up = dpp_mov<0xF5>(c);  // quad_perm [1,1,3,3]: the up half next to its gate
-            const int k = l4 >> 1;
-            const int r = r0 + (it0 + k) * teams;
-            if (lane < 4 && !(l4 & 1) && it0 + k < n && r < r_end) sg.y[r] = (c / (1.0f + expf(-c))) * up;
-        } else {
-            const float yk = ry;
-            const int r = r0 + (it0 + l4) * teams;
-            if (lane < 4 && it0 + l4 < n && r < r_end) {
-                if (OUT == OUT_STORE) {
-                    sg.y[r] = c;
-                } else if (OUT == OUT_ADD) {
-                    sg.y[r] = yk + c;
-                } else if (OUT == OUT_WADD) {
-                    sg.y[r] = fmaf(c, wscale, yk);
-                } else if (OUT == OUT_ARGMAX) {
-                    if (sg.y) sg.y[r] = c;
-                    if (c > best_v || (c == best_v && r < best_r)) {
-                        best_v = c;
-                        best_r = r;
-                    }
-                }
-            }
-            if (kReadY) ry = sg.y[row_of(it0 + D + l4)];
-        }
-    }
-    if (OUT == OUT_ARGMAX) {
-        __shared__ unsigned long long keys[16];
-        unsigned long long key = 0ull;
-        if (best_r != 0x7fffffff)
-            key = ((unsigned long long)ordered_bits(best_v) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_r);
-        if ((tid & 63) < 4) keys[wave * 4 + l4] = TT == 64 || wave == 0 ? key : 0ull;
-        __syncthreads();
-        if (tid == 0) {
-            unsigned long long k = 0ull;
-            for (int i = 0; i < 16; i++) k = keys[i] > k ? keys[i] : k;
-            if (k) atomicMax(p.argmax_slot, k);
-        }
-    }
-}
-
-template <int F, int IN, int OUT, int TT>
-__device__ __forceinline__ void mv_dispatch(const MvParams &p, const MvSeg &sg, int wg_in_seg, float *lds) {
-    if constexpr (TT != 0)
-        mv_body_fast<F, IN, OUT, TT>(p, sg, wg_in_seg, lds);
-    else
-        mv_body<F, IN, OUT>(p, sg, wg_in_seg, lds);
-}
-
-// TT: compile-time team width (64 or 256) of the fast path, 0 for any width.
-template <int F1, int F2, int IN, int OUT, int TT>
-__global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
-    __shared__ float lds[36];
-    if (p.gate_flag && *p.gate_flag == 0) return;
-    const int wg = blockIdx.x;
-    int si = 0;
-#pragma unroll
-    for (int i = 1; i < 4; i++)
-        if (i < p.nseg && wg >= p.seg[i].wg_begin) si = i;
-    const MvSeg &sg = p.seg[si];
-    if (F1 == F2 || sg.fmt == F1)
-        mv_dispatch<F1, IN, OUT, TT>(p, sg, wg - sg.wg_begin, lds);
-    else
-        mv_dispatch<F2, IN, OUT, TT>(p, sg, wg - sg.wg_begin, lds);
-}
-
-// ---------------- host-side planning and dispatch ----------------
-
-// Team width of a row of `cols` values: next power of two of the slot count,
-// at most one workgroup.
-static int team_width(int cols) {
-    int t = 1;
-    while (t < cols / 64) t <<= 1;
-    return t > kThreads ? kThreads : t;
-}
 
 // Rows per team so that the grid has at most target_wgs workgroups, or one
 // row per team when the matrix is too small to fill them.
@@ -446,26 +32,14 @@ static int total_wgs(const MvParams &p) {
     return wg;
 }
 
-typedef void (*MvKernel)(MvParams);
-
-template <int F1, int F2, int TT> static MvKernel pick_tt(int in, int out) {
-    if (in == IN_PLAIN && out == OUT_STORE) return mv_kernel<F1, F2, IN_PLAIN, OUT_STORE, TT>;
-    if (in == IN_PLAIN && out == OUT_ADD) return mv_kernel<F1, F2, IN_PLAIN, OUT_ADD, TT>;
-    if (in == IN_NORM && out == OUT_STORE) return mv_kernel<F1, F2, IN_NORM, OUT_STORE, TT>;
-    if (in == IN_NORM && out == OUT_SWIGLU) return mv_kernel<F1, F2, IN_NORM, OUT_SWIGLU, TT>;
-    if (in == IN_PLAIN && out == OUT_SWIGLU) return mv_kernel<F1, F2, IN_PLAIN, OUT_SWIGLU, TT>;
-    if (in == IN_PLAIN && out == OUT_ARGMAX) return mv_kernel<F1, F2, IN_PLAIN, OUT_ARGMAX, TT>;
-    if (in == IN_NORM && out == OUT_ARGMAX) return mv_kernel<F1, F2, IN_NORM, OUT_ARGMAX, TT>;
-    if (in == IN_SILU && out == OUT_ADD) return mv_kernel<F1, F2, IN_SILU, OUT_ADD, TT>;
-    if (in == IN_PLAIN && out == OUT_WADD) return mv_kernel<F1, F2, IN_PLAIN, OUT_WADD, TT>;
-    return nullptr;
-}
-
-template <int F1, int F2> static MvKernel pick(int in, int out, int cols) {
-    const int T = team_width(cols);
-    if (T == 64) return pick_tt<F1, F2, 64>(in, out);
-    if (T == 256) return pick_tt<F1, F2, 256>(in, out);
-    return pick_tt<F1, F2, 0>(in, out);
+// Ring batches of the fast path; ZIGGY_HIP_MATVEC_NB forces 1, 2 or 3 (a tuning knob).
+int forced_nb() {
+    static int v = [] {
+        const char *e = getenv("ZIGGY_HIP_MATVEC_NB");
+        const int n = e ? atoi(e) : 0;
+        return n >= 1 && n <= 3 ? n : 0;
+    }();
+    return v;
 }
 
 static int device_cus() {
@@ -499,27 +73,21 @@ hipError_t launch_matvec(const MvParams &p_in, int in, int out, hipStream_t s) {
         if (p.seg[i].fmt != f1) f2 = p.seg[i].fmt;
     for (int i = 0; i < p.nseg; i++)
         if (p.seg[i].fmt != f1 && p.seg[i].fmt != f2) return hipErrorInvalidValue;
+    plan_matvec(p, (int)(device_cus() * workgroups_per_cu() + 0.5f));
+    const int n = p.rows_per_team;
     MvKernel k = nullptr;
     if (f1 == f2) {
         switch (f1) {
-        case Q4_K: k = pick<Q4_K, Q4_K>(in, out, p.cols); break;
-        case Q6_K: k = pick<Q6_K, Q6_K>(in, out, p.cols); break;
-        case Q8_0: k = pick<Q8_0, Q8_0>(in, out, p.cols); break;
-        case Q3_K: k = pick<Q3_K, Q3_K>(in, out, p.cols); break;
-        case IQ4_XS: k = pick<IQ4_XS, IQ4_XS>(in, out, p.cols); break;
-        case F16: k = pick_tt<F16, F16, 0>(in, out); break;
-        case F32: k = pick_tt<F32, F32, 0>(in, out); break;
-        default: break;
+        case Q4_K: k = pick_mv_q4k(in, out, p.cols, n); break;
+        case Q6_K: k = pick_mv_q6k(in, out, p.cols, n); break;
+        case Q8_0: k = pick_mv_q8_0(in, out, p.cols, n); break;
+        default: k = pick_mv_other(f1, in, out, p.cols, n); break;
         }
-    } else if (f1 == Q4_K && f2 == Q6_K && in == IN_NORM && out == OUT_STORE) {
-        k = team_width(p.cols) == 64 ? mv_kernel<Q4_K, Q6_K, IN_NORM, OUT_STORE, 64>
-                                     : mv_kernel<Q4_K, Q6_K, IN_NORM, OUT_STORE, 0>;
-    } else if (f1 == Q6_K && f2 == Q4_K && in == IN_NORM && out == OUT_STORE) {
-        k = team_width(p.cols) == 64 ? mv_kernel<Q6_K, Q4_K, IN_NORM, OUT_STORE, 64>
-                                     : mv_kernel<Q6_K, Q4_K, IN_NORM, OUT_STORE, 0>;
+    } else if (in == IN_NORM && out == OUT_STORE) {
+        // the q/k/v launch of a Q4_K_M layer: Q4_K and Q6_K segments
+        k = pick_mv_mixed(f1, f2, p.cols, n);
     }
     if (!k) return hipErrorInvalidValue;
-    plan_matvec(p, (int)(device_cus() * workgroups_per_cu() + 0.5f));
     const int grid = total_wgs(p);
     if (grid <= 0) return hipSuccess;
     hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), 0, s, p);

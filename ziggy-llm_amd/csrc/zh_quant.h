@@ -68,26 +68,36 @@ template <> struct Geom<Q4_K> {
     static constexpr int kValues = 256, kBytes = 144, kSlotsPerBlock = 4;
     __device__ static int x_base(int s) { return (s >> 2) * 256 + (s & 3) * 64; }
     static constexpr int kXStride = 16;
+    // slot s and run w of the 16-value run R (x[16R .. 16R + 15])
+    __device__ static void run_slot(int R, int &s, int &w) { s = (R >> 4) * 4 + ((R >> 2) & 3), w = R & 3; }
 };
 template <> struct Geom<Q6_K> {
     static constexpr int kValues = 256, kBytes = 210, kSlotsPerBlock = 4;
     __device__ static int x_base(int s) { return (s >> 2) * 256 + ((s >> 1) & 1) * 128 + (s & 1) * 16; }
     static constexpr int kXStride = 32;
+    __device__ static void run_slot(int R, int &s, int &w) {
+        s = (R >> 4) * 4 + ((R >> 3) & 1) * 2 + (R & 1), w = (R & 7) >> 1;
+    }
 };
 template <> struct Geom<Q3_K> {
     static constexpr int kValues = 256, kBytes = 110, kSlotsPerBlock = 4;
     __device__ static int x_base(int s) { return (s >> 2) * 256 + ((s >> 1) & 1) * 128 + (s & 1) * 16; }
     static constexpr int kXStride = 32;
+    __device__ static void run_slot(int R, int &s, int &w) {
+        s = (R >> 4) * 4 + ((R >> 3) & 1) * 2 + (R & 1), w = (R & 7) >> 1;
+    }
 };
 template <> struct Geom<IQ4_XS> {
     static constexpr int kValues = 256, kBytes = 136, kSlotsPerBlock = 4;
     __device__ static int x_base(int s) { return (s >> 2) * 256 + (s & 3) * 64; }
     static constexpr int kXStride = 16;
+    __device__ static void run_slot(int R, int &s, int &w) { s = (R >> 4) * 4 + ((R >> 2) & 3), w = R & 3; }
 };
 template <> struct Geom<Q8_0> {
     static constexpr int kValues = 32, kBytes = 34, kSlotsPerBlock = 1;  // a slot spans 2 blocks
     __device__ static int x_base(int s) { return s * 64; }
     static constexpr int kXStride = 16;
+    __device__ static void run_slot(int R, int &s, int &w) { s = R >> 2, w = R & 3; }
 };
 template <> struct Geom<F16> {
     static constexpr int kValues = 1, kBytes = 2, kSlotsPerBlock = 1;
@@ -145,30 +155,40 @@ __device__ __forceinline__ void to_slot(const float (&v)[64], XSlot &xs) {
     run_sums(v, xs.sum);
 }
 
+// The three balanced base-256 digit words of four activations scaled by 2^k.
+__device__ __forceinline__ void digits4(float v0, float v1, float v2, float v3, int k, uint32_t &d0, uint32_t &d1,
+                                        uint32_t &d2) {
+    // u = xi + 0x808080 has the balanced digits + 128 as its bytes 0..2
+    const uint32_t u0 = (uint32_t)(int)ldexpf(v0, k) + 0x808080u, u1 = (uint32_t)(int)ldexpf(v1, k) + 0x808080u;
+    const uint32_t u2 = (uint32_t)(int)ldexpf(v2, k) + 0x808080u, u3 = (uint32_t)(int)ldexpf(v3, k) + 0x808080u;
+    const uint32_t a = __builtin_amdgcn_perm(u1, u0, 0x05010400u);   // u0.b0 u1.b0 u0.b1 u1.b1
+    const uint32_t b = __builtin_amdgcn_perm(u3, u2, 0x05010400u);   // u2.b0 u3.b0 u2.b1 u3.b1
+    const uint32_t c2 = __builtin_amdgcn_perm(u1, u0, 0x07030602u);  // u0.b2 u1.b2 u0.b3 u1.b3
+    const uint32_t e2 = __builtin_amdgcn_perm(u3, u2, 0x07030602u);
+    d0 = __builtin_amdgcn_perm(b, a, 0x05040100u) ^ 0x80808080u;
+    d1 = __builtin_amdgcn_perm(b, a, 0x07060302u) ^ 0x80808080u;
+    d2 = __builtin_amdgcn_perm(e2, c2, 0x05040100u) ^ 0x80808080u;
+}
+
+// Scale exponent k of a slot: |v * 2^k| < 2^22 for max|v| = m; and the scale
+// 2^-k, or NaN when an activation (m, or the slot total tot) is not finite
+// (the digits cannot carry it, so every dot is NaN).
+__device__ __forceinline__ int slot_exponent(float m) { return 22 - __builtin_amdgcn_frexp_expf(m); }
+__device__ __forceinline__ float slot_scale(float m, float tot, int k) {
+    return (m <= 3.4028235e38f && fabsf(tot) <= 3.4028235e38f) ? ldexpf(1.0f, -k) : __builtin_nanf("");
+}
+
 __device__ __forceinline__ void to_slot(const float (&v)[64], XDig &xd) {
     float m = 0.f;
 #pragma unroll
     for (int i = 0; i < 64; i++) m = fmaxf(m, fabsf(v[i]));
     // m = f * 2^e with f in [0.5, 1): |v * 2^(22 - e)| < 2^22
-    const int k = 22 - __builtin_amdgcn_frexp_expf(m);
+    const int k = slot_exponent(m);
     run_sums(v, xd.sum);
-    // a NaN or infinite activation makes every dot NaN (the digits cannot carry it)
     const float tot = (xd.sum[0] + xd.sum[1]) + (xd.sum[2] + xd.sum[3]);
-    xd.scale = (m <= 3.4028235e38f && fabsf(tot) <= 3.4028235e38f) ? ldexpf(1.0f, -k) : __builtin_nanf("");
+    xd.scale = slot_scale(m, tot, k);
 #pragma unroll
-    for (int c = 0; c < 16; c++) {
-        // u = xi + 0x808080 has the balanced digits + 128 as its bytes 0..2
-        uint32_t u[4];
-#pragma unroll
-        for (int b = 0; b < 4; b++) u[b] = (uint32_t)(int)ldexpf(v[4 * c + b], k) + 0x808080u;
-        const uint32_t a = __builtin_amdgcn_perm(u[1], u[0], 0x05010400u);  // u0.b0 u1.b0 u0.b1 u1.b1
-        const uint32_t b = __builtin_amdgcn_perm(u[3], u[2], 0x05010400u);  // u2.b0 u3.b0 u2.b1 u3.b1
-        const uint32_t c2 = __builtin_amdgcn_perm(u[1], u[0], 0x07030602u); // u0.b2 u1.b2 u0.b3 u1.b3
-        const uint32_t e2 = __builtin_amdgcn_perm(u[3], u[2], 0x07030602u);
-        xd.d[0][c] = __builtin_amdgcn_perm(b, a, 0x05040100u) ^ 0x80808080u;
-        xd.d[1][c] = __builtin_amdgcn_perm(b, a, 0x07060302u) ^ 0x80808080u;
-        xd.d[2][c] = __builtin_amdgcn_perm(e2, c2, 0x05040100u) ^ 0x80808080u;
-    }
+    for (int c = 0; c < 16; c++) digits4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3], k, xd.d[0][c], xd.d[1][c], xd.d[2][c]);
 }
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
