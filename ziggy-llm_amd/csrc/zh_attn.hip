@@ -7,9 +7,8 @@
 // matvec.metal:1274-1389) runs one threadgroup per query head.
 //
 // Here one workgroup handles one kv head (all G query heads of its group)
-// over a contiguous range of 64-position chunks, with an online softmax
-// across its chunks; the number of splits grows with the position up to
-// max_splits, so long contexts keep about one workgroup per CU busy.  Each
+// over a contiguous range of positions; the number of splits grows with the
+// position up to max_splits, so long contexts keep every CU busy.  Each
 // split writes (m, l, unnormalised o) per query head; the last workgroup of
 // a kv head to finish (arrival counter) merges the splits with log-sum-exp
 // and resets the counter, so replays of a captured graph need no memset.
@@ -33,10 +32,6 @@ constexpr int kChunk = 64;
 constexpr int kMaxGroup = 8;
 constexpr int QV_MAX = 8;  // q values per thread at most (8 heads of 256)
 
-__device__ __forceinline__ float wmax(float v) {
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
 __device__ __forceinline__ float wsum(float v) {
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
@@ -101,77 +96,94 @@ __device__ __forceinline__ void norm_rope(float (&x)[V], int n, const float *nor
     __syncthreads();
 }
 
-// Sum / max over the 16 position quads of a wavefront (lane bits 2..5).
-__device__ __forceinline__ float quads_sum(float v) {
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));  // row_ror:4
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
+// Sum over aligned groups of n lanes (n = 4, 8 or 16) of a 16-lane row; the
+// total is valid in every lane of the group.
+__device__ __forceinline__ float group_sum16(float v, int n) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+    if (n >= 8) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+    if (n >= 16) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)); // row_mirror
     return v;
 }
-__device__ __forceinline__ float quads_max(float v) {
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
+// Sum over the lanes of a 16-lane row with the same (lane mod n) (n = 4, 8
+// or 16): every such lane holds the total.
+__device__ __forceinline__ float rows_sum16(float v, int n) {
+    if (n <= 8) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+    if (n <= 4) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));  // row_ror:4
     return v;
 }
 
-// Workgroup (split, kv head).  Wavefront w takes positions 16w..16w+15 of
-// every 64-position chunk of the split and keeps its own online softmax
-// (running max m, sum l, unnormalised o per query head): no workgroup
-// barrier inside the chunk loop.  Scores: lane = (position, quarter of the
-// head dims), a quad reduction finishes each dot.  Values: lane owns HD/64
-// dims and takes the probabilities of the 16 positions by readlane.
+// Max / sum over aligned groups of 32 lanes (half wavefronts); the total is
+// valid in every lane of the group.
+__device__ __forceinline__ float half_max32(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+    return fmaxf(v, __shfl_xor(v, 16, 64));
+}
+__device__ __forceinline__ float half_sum32(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+    return v + __shfl_xor(v, 16, 64);
+}
+
+// Workgroup (split, kv head) attends over a contiguous range of positions,
+// in passes of PPP positions: lane (position pw, dims block sub) of wavefront
+// w takes position pw + PPW w of each pass and dims 16 sub .. 16 sub + 15
+// (LP = HD / 16 lanes per position, PPW = 64 / LP positions per wavefront).
+// The K and V loads of NP passes are in flight at once (a ring refilled in
+// place; short ranges issue all their loads up front).  Scores finish with
+// an LP-lane DPP sum; every lane keeps an online softmax (m, l, o) for its
+// own position stream, so the pass loop has no cross-lane traffic beyond
+// the score sum.  The workgroup then merges its streams (max through LDS,
+// row sums by DPP, row partials through LDS).  With several splits, each
+// writes (m, l, unnormalised o) per query head with write-through stores;
+// the last workgroup of a kv head to arrive (arrival counter) merges the
+// splits with log-sum-exp and resets the counter, so replays of a captured
+// graph need no memset.
 // GG: query heads per kv head when it is 1, 2, 4 or 8 (compile-time loops),
 // 0 for any group size up to 8.
 template <int HD, int GG>
 __global__ void __launch_bounds__(256) attn_kernel(AttnParams p) {
+    constexpr int LP = HD / 16;   // lanes per position
+    constexpr int PPW = 64 / LP;  // positions per wavefront and pass
+    constexpr int PPP = 4 * PPW;  // positions per pass
+    constexpr int NP = 4;         // passes in flight
+    constexpr int KG = GG ? GG : kMaxGroup;  // head loop bound
     const int split = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, sub = lane % LP, pw = lane / LP;
     const int pos = p.position_dev ? *p.position_dev : p.position;
     const int n_total = pos + 1 - p.window_start;
-    const int nch = (n_total + kChunk - 1) / kChunk;
-    const int per = (nch + p.max_splits - 1) / p.max_splits;  // chunks per split
-    const int nsplit = (nch + per - 1) / per;
+    const int units = (n_total + PPP - 1) / PPP;
+    const int per = (units + p.max_splits - 1) / p.max_splits;  // passes per split
+    const int nsplit = (units + per - 1) / per;
     if (split >= nsplit) return;
-    const int c_begin = split * per, c_end = min(c_begin + per, nch);
-    constexpr int KG = GG ? GG : kMaxGroup;  // head loop bound
+    const int u_begin = split * per, npass = min(per, units - u_begin);
     const int G = GG ? GG : p.head_count / p.head_count_kv;
     const bool fused = p.k_new != nullptr;
-    const int wave = tid >> 6, lane = tid & 63;
+    const bool own_pos = fused && u_begin + npass == units;  // this split holds the current position
 
-    constexpr int DQ = HD / 4;    // K dims per lane
-    constexpr int DPL = HD / 64;  // V dims per lane
     __shared__ float q_s[kMaxGroup][HD];
-    __shared__ float wo[4][kMaxGroup][HD];
-    __shared__ float wm[4][kMaxGroup], wl[4][kMaxGroup];
     __shared__ float kn_s[HD], vn_s[HD];  // this step's k and v (binary16-rounded)
     __shared__ float red16[4 * QV_MAX];
     __shared__ float cs_s[HD / 2], sn_s[HD / 2];
+    __shared__ float ml_s[PPP][kMaxGroup][2];
     __shared__ float fm_s[kMaxGroup], fl_s[kMaxGroup];
+    constexpr int NR = 16;  // row partials of the stream sums (4 per wavefront)
+    __shared__ float rows_s[NR][KG * HD <= 512 ? KG * HD : 512];
     __shared__ int last_s;
 
-    const int pk = lane >> 2, quarter = lane & 3;
     const size_t kv_off = (size_t)kvh * HD;
+    // stream position of pass i (may pass the end: loads clamp, scores mask)
+    auto pos_of = [&](int i) { return p.window_start + (u_begin + i) * PPP + wave * PPW + pw; };
 
-    // Loads of one chunk for this wavefront.  Positions past the end re-read
-    // position `pos` (valid memory; masked below), so the loads are unconditional.
-    using VW = typename std::conditional<DPL == 1, uint16_t, typename std::conditional<DPL == 2, uint32_t, uint2>::type>::type;
-    auto load_chunk = [&](int c, uint4 (&kr)[DQ / 8], VW (&vr)[16]) {
-        const int tw = p.window_start + c * kChunk + 16 * wave;
-        const __half *krow = p.k_cache + (size_t)min(tw + pk, pos) * p.kv_dim + kv_off + quarter * DQ;
-#pragma unroll
-        for (int j = 0; j < DQ / 8; j++) kr[j] = *reinterpret_cast<const uint4 *>(krow + 8 * j);
-#pragma unroll
-        for (int j = 0; j < 16; j++)
-            vr[j] = *reinterpret_cast<const VW *>(p.v_cache + (size_t)min(tw + j, pos) * p.kv_dim + kv_off + lane * DPL);
-    };
-
-    // q (and this step's k / v) first, so waiting for them does not wait
-    // for the K/V chunk loads issued next.
-    constexpr int QV = kMaxGroup * HD / 256;  // q values per thread at most
+    // q (and this step's k / v) first: waiting for them must not wait for
+    // the K/V loads issued next (vmcnt completes in order)
+    constexpr int QV = kMaxGroup * HD / 256;
     const int nq = G * HD;
-    const bool own_pos = fused && c_end == nch;  // this split holds the current position
     float qv[QV], kx[1] = {0.f}, vx = 0.f;
 #pragma unroll
     for (int i = 0; i < QV; i++) {
@@ -188,9 +200,30 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnParams p) {
         if (p.k_bias) kx[0] += p.k_bias[kv_off + tid];
         if (p.v_bias) vx += p.v_bias[kv_off + tid];
     }
-    uint4 kraw[DQ / 8];
-    VW vraw[16];
-    load_chunk(c_begin, kraw, vraw);
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 kr[NP][2], vr[NP][2];
+    auto row_off = [&](int i) { return (size_t)min(pos_of(min(i, npass - 1)), pos) * p.kv_dim + kv_off + 16 * sub; };
+    auto load_k = [&](int i, uint4 (&k)[2]) {
+        const uint4 *kp = reinterpret_cast<const uint4 *>(p.k_cache + row_off(i));
+        k[0] = kp[0];
+        k[1] = kp[1];
+    };
+    auto load_v = [&](int i, uint4 (&v)[2]) {
+        const uint4 *vp = reinterpret_cast<const uint4 *>(p.v_cache + row_off(i));
+        v[0] = vp[0];
+        v[1] = vp[1];
+    };
+    // all K slots, then all V slots: the order the group loop consumes them
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+        load_k(j, kr[j]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int j = 0; j < NP; j++) {
+        load_v(j, vr[j]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     if (fused) {
         const int n_rot = p.rope_dim < HD ? p.rope_dim : HD;
@@ -218,232 +251,232 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnParams p) {
     }
     __syncthreads();
 
-    float m[KG], l[KG], o[KG][DPL];
+    // Softmax in base 2: scores carry scale * log2(e), so exp2 gives the
+    // exponentials (the max-subtracted arguments stay in [-126, 0]).
+    const float sl2 = p.scale * 1.44269504088896340736f;
+    float m[KG], l[KG], o[KG][16];
 #pragma unroll
     for (int g = 0; g < KG; g++) {
         m[g] = -INFINITY;
         l[g] = 0.f;
 #pragma unroll
-        for (int d = 0; d < DPL; d++) o[g][d] = 0.f;
+        for (int d = 0; d < 16; d++) o[g][d] = 0.f;
     }
-
-    auto process = [&](int c, const uint4 (&kr)[DQ / 8], const VW (&vr)[16]) {
-        const int tw = p.window_start + c * kChunk + 16 * wave;
-        const int nw = min(16, pos + 1 - tw);  // valid positions of this wavefront (uniform)
-        if (nw <= 0) return;
-        // scores
-        const bool kcur = fused && tw + pk == pos;  // this step's k, from LDS
-        float acc[KG];
+    // Groups of NP passes: the scores of the whole group first (each K slot
+    // is refilled as soon as its scores are done), then one rescale of the
+    // stream state to the group max, then the values (each V slot refilled
+    // after use).
+    for (int i0 = 0; i0 < npass; i0 += NP) {
+        float sc[NP][KG];
 #pragma unroll
-        for (int g = 0; g < KG; g++) acc[g] = 0.f;
+        for (int j = 0; j < NP; j++) {
+            const int i = i0 + j;
+            const int ps = pos_of(i);
+            const bool valid = i < npass && ps <= pos;
+            float k[16];
 #pragma unroll
-        for (int j = 0; j < DQ / 8; j++) {
-            const uint32_t w[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
-            float k[8];
+            for (int c = 0; c < 2; c++) {
+                const uint32_t kw[4] = {kr[j][c].x, kr[j][c].y, kr[j][c].z, kr[j][c].w};
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                k[2 * i] = h2f(w[i]);
-                k[2 * i + 1] = h2f(w[i] >> 16);
+                for (int e = 0; e < 4; e++) {
+                    k[8 * c + 2 * e] = h2f(kw[e]);
+                    k[8 * c + 2 * e + 1] = h2f(kw[e] >> 16);
+                }
             }
-            if (kcur) {
+            if (fused && ps == pos) {  // this step's k (the cache row was loaded before the store)
 #pragma unroll
-                for (int i = 0; i < 8; i++) k[i] = kn_s[quarter * DQ + 8 * j + i];
+                for (int d = 0; d < 16; d++) k[d] = kn_s[16 * sub + d];
             }
+            __builtin_amdgcn_sched_barrier(0);
+            load_k(i + NP, kr[j]);  // unconditional (clamped): keeps the slot in place
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int g = 0; g < KG; g++) {
+                float acc = 0.f;
+                if (g < G) {
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const float4 qq = *reinterpret_cast<const float4 *>(&q_s[g][16 * sub + 4 * c]);
+                        acc = fmaf(qq.x, k[4 * c], acc);
+                        acc = fmaf(qq.y, k[4 * c + 1], acc);
+                        acc = fmaf(qq.z, k[4 * c + 2], acc);
+                        acc = fmaf(qq.w, k[4 * c + 3], acc);
+                    }
+                    acc = group_sum16(acc, LP);  // the position's score in every lane of its group
+                }
+                sc[j][g] = valid ? acc * sl2 : -INFINITY;
+            }
+        }
+        float alpha[KG];
+#pragma unroll
+        for (int g = 0; g < KG; g++) {
+            float gm = m[g];
+#pragma unroll
+            for (int j = 0; j < NP; j++) gm = fmaxf(gm, sc[j][g]);
+            alpha[g] = gm == -INFINITY ? 1.f : exp2f(m[g] - gm);  // 0 on the stream's first scores
+            m[g] = gm;
+            l[g] *= alpha[g];
+        }
+#pragma unroll
+        for (int g = 0; g < KG; g++)
+            if (g < G) {
+#pragma unroll
+                for (int d = 0; d < 16; d++) o[g][d] *= alpha[g];
+            }
+#pragma unroll
+        for (int j = 0; j < NP; j++) {
+            const int i = i0 + j;
+            const int ps = pos_of(i);
+            float v[16];
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const uint32_t vw[4] = {vr[j][c].x, vr[j][c].y, vr[j][c].z, vr[j][c].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    v[8 * c + 2 * e] = h2f(vw[e]);
+                    v[8 * c + 2 * e + 1] = h2f(vw[e] >> 16);
+                }
+            }
+            if (fused && ps == pos) {
+#pragma unroll
+                for (int d = 0; d < 16; d++) v[d] = vn_s[16 * sub + d];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_v(i + NP, vr[j]);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int g = 0; g < KG; g++) {
                 if (g < G) {
-                    const float4 qa = *reinterpret_cast<const float4 *>(&q_s[g][quarter * DQ + 8 * j]);
-                    const float4 qb = *reinterpret_cast<const float4 *>(&q_s[g][quarter * DQ + 8 * j + 4]);
-                    acc[g] = fmaf(qa.x, k[0], acc[g]);
-                    acc[g] = fmaf(qa.y, k[1], acc[g]);
-                    acc[g] = fmaf(qa.z, k[2], acc[g]);
-                    acc[g] = fmaf(qa.w, k[3], acc[g]);
-                    acc[g] = fmaf(qb.x, k[4], acc[g]);
-                    acc[g] = fmaf(qb.y, k[5], acc[g]);
-                    acc[g] = fmaf(qb.z, k[6], acc[g]);
-                    acc[g] = fmaf(qb.w, k[7], acc[g]);
+                    const float e = sc[j][g] == -INFINITY ? 0.f : exp2f(sc[j][g] - m[g]);
+                    l[g] += e;
+#pragma unroll
+                    for (int d = 0; d < 16; d++) o[g][d] = fmaf(e, v[d], o[g][d]);
                 }
             }
         }
-        float e[KG];
+    }
+
+    // ---- merge the workgroup's PPP position streams ----
+    const int stream = wave * PPW + pw;
+    if (sub == 0) {
+#pragma unroll
+        for (int g = 0; g < KG; g++)
+            if (g < G) ml_s[stream][g][0] = m[g], ml_s[stream][g][1] = l[g];
+    }
+    __syncthreads();
+    {
+        // 32 lanes per head g: lane (tid & 31) folds streams tid & 31,
+        // + 32, ...; then a 32-lane max and sum, and one lane writes the
+        // head's (M, L)
+        const int g = tid >> 5, r = tid & 31;
+        float mm = -INFINITY;
+        if (g < G)
+            for (int st = r; st < PPP; st += 32) mm = fmaxf(mm, ml_s[st][g][0]);
+        mm = half_max32(mm);
+        float ll = 0.f;
+        if (g < G)
+            for (int st = r; st < PPP; st += 32) {
+                const float ms = ml_s[st][g][0];
+                ll += ms == -INFINITY ? 0.f : ml_s[st][g][1] * exp2f(ms - mm);
+            }
+        ll = half_sum32(ll);
+        if (g < G && r == 31) {
+            fm_s[g] = mm;
+            fl_s[g] = ll;
+        }
+    }
+    __syncthreads();
+    // scale each stream to the workgroup max, sum the streams of a 16-lane
+    // row by DPP, then the 16 row partials through LDS (in head blocks of
+    // at most 512 values)
+    for (int gb = 0; gb < KG; gb += (512 / HD > 0 ? 512 / HD : 1)) {
+        const int gn = min(512 / HD > 0 ? 512 / HD : 1, G - gb);  // heads in this block
+        if (gn <= 0) break;
 #pragma unroll
         for (int g = 0; g < KG; g++) {
-            if (g < G) {
-                float sc = acc[g];
-                sc += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sc), 0xB1, 0xF, 0xF, false));
-                sc += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sc), 0x4E, 0xF, 0xF, false));
-                sc = pk < nw ? sc * p.scale : -INFINITY;
-                const float m_new = fmaxf(m[g], quads_max(sc));
-                const float alpha = expf(m[g] - m_new);  // 0 on the first chunk
-                e[g] = pk < nw ? expf(sc - m_new) : 0.f;
-                l[g] = fmaf(l[g], alpha, quads_sum(quarter == 0 ? e[g] : 0.f));
-                m[g] = m_new;
+            if (g >= gb && g < gb + gn) {
+                const float w = m[g] == -INFINITY ? 0.f : exp2f(m[g] - fm_s[g]);
 #pragma unroll
-                for (int d = 0; d < DPL; d++) o[g][d] *= alpha;
-            }
-        }
-        // values
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            if (j < nw) {
-                float v[DPL];
-                const VW raw = vr[j];
-                if constexpr (DPL == 1) {
-                    v[0] = h2f((uint32_t)raw);
-                } else if constexpr (DPL == 2) {
-                    v[0] = h2f((uint32_t)raw);
-                    v[1] = h2f((uint32_t)raw >> 16);
-                } else {
-                    v[0] = h2f(raw.x);
-                    v[1] = h2f(raw.x >> 16);
-                    v[2] = h2f(raw.y);
-                    v[3] = h2f(raw.y >> 16);
-                }
-                if (fused && tw + j == pos) {
-#pragma unroll
-                    for (int d = 0; d < DPL; d++) v[d] = vn_s[lane * DPL + d];
-                }
-#pragma unroll
-                for (int g = 0; g < KG; g++) {
-                    if (g < G) {
-                        const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[g]), 4 * j));
-#pragma unroll
-                        for (int d = 0; d < DPL; d++) o[g][d] = fmaf(pj, v[d], o[g][d]);
-                    }
+                for (int d = 0; d < 16; d++) {
+                    float t = o[g][d] * w;
+                    t = rows_sum16(t, LP);  // sum over the row's position streams
+                    if ((lane & 15) < LP) rows_s[wave * 4 + (lane >> 4)][(g - gb) * HD + 16 * sub + d] = t;
                 }
             }
         }
-    };
-
-    // Two chunk buffers alternate, so a buffer is never copied (a copy would
-    // wait for the loads in flight into its source).
-    uint4 kb[DQ / 8];
-    VW vb[16];
-    for (int c = c_begin; c < c_end; c += 2) {
-        load_chunk(min(c + 1, c_end - 1), kb, vb);
-        process(c, kraw, vraw);
-        if (c + 1 < c_end) {
-            load_chunk(min(c + 2, c_end - 1), kraw, vraw);
-            process(c + 1, kb, vb);
-        }
-    }
-
-    // combine the four wavefronts' softmax states
+        __syncthreads();
+        for (int it = tid; it < gn * HD; it += 256) {
+            float acc = 0.f;
 #pragma unroll
-    for (int g = 0; g < KG; g++) {
-        if (g < G) {
-#pragma unroll
-            for (int d = 0; d < DPL; d++) wo[wave][g][lane * DPL + d] = o[g][d];
-            if (lane == 0) {
-                wm[wave][g] = m[g];
-                wl[wave][g] = l[g];
+            for (int r = 0; r < NR; r++) acc += rows_s[r][it];
+            const int g = gb + it / HD, d = it % HD;
+            if (nsplit == 1) {
+                p.out[(size_t)(kvh * G + g) * HD + d] = acc / fl_s[g];
+            } else {
+                const size_t e = (((size_t)kvh * p.max_splits + split) * kMaxGroup + g) * HD + d;
+                __hip_atomic_store(p.part_o + e, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
-    }
-    __syncthreads();
-    if (tid < G) {
-        const int g = tid;
-        const float M = fmaxf(fmaxf(wm[0][g], wm[1][g]), fmaxf(wm[2][g], wm[3][g]));
-        float L = 0.f;
-        for (int w = 0; w < 4; w++) L = fmaf(wl[w][g], expf(wm[w][g] - M), L);  // empty wavefronts: exp(-inf) = 0
-        fm_s[g] = M;
-        fl_s[g] = L;
-    }
-    __syncthreads();
-    const size_t pbase = ((size_t)kvh * p.max_splits + split) * kMaxGroup;
-    for (int i = tid; i < G * HD; i += 256) {
-        const int g = i / HD, d = i % HD;
-        const float M = fm_s[g];
-        float sacc = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; w++) sacc = fmaf(wo[w][g][d], expf(wm[w][g] - M), sacc);
-        if (nsplit == 1) {
-            p.out[(size_t)(kvh * G + g) * HD + d] = sacc / fl_s[g];
-        } else {
-            p.part_o[(pbase + g) * HD + d] = sacc;
-        }
+        __syncthreads();
     }
     if (nsplit == 1) return;
     if (tid < G) {
-        p.part_ml[(pbase + tid) * 2] = fm_s[tid];
-        p.part_ml[(pbase + tid) * 2 + 1] = fl_s[tid];
+        const size_t e = ((size_t)kvh * p.max_splits + split) * kMaxGroup + tid;
+        const unsigned long long v = (unsigned long long)__float_as_uint(fm_s[tid]) |
+                                     ((unsigned long long)__float_as_uint(fl_s[tid]) << 32);
+        __hip_atomic_store(reinterpret_cast<unsigned long long *>(p.part_ml) + e, v, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    // Arrival: the workgroup barrier orders every thread's partial stores
-    // before thread 0's agent-scope release (one L2 write-back per workgroup);
-    // the counter tells the last arrival of this kv head, which acquires
-    // (invalidates its stale cache lines) and merges.
+    // Arrival: every thread's partial stores (agent scope, write-through)
+    // complete before the workgroup barrier; thread 0 then releases and
+    // counts.  The last arrival of this kv head acquires and merges.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads();
     if (tid == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        const unsigned old = __hip_atomic_fetch_add(&p.counters[kvh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned old = __hip_atomic_fetch_add(&p.counters[kvh], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         last_s = old == (unsigned)(nsplit - 1);
         if (last_s) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
     if (!last_s) return;
 
-    // Merge: item (quad of 4 dims of one head, split group sg) folds splits
-    // sg, sg + SG, ... with an online log-sum-exp, four splits' loads at a
-    // time; the SG groups then combine through LDS (the wo buffer is free).
-    const float *ml = p.part_ml + (size_t)kvh * p.max_splits * kMaxGroup * 2;
-    const float *po = p.part_o + (size_t)kvh * p.max_splits * kMaxGroup * HD;
-    constexpr int Q4 = HD / 4;
-    const int nquads = G * Q4;
-    const int SG = nquads >= 256 ? 1 : 256 / nquads;
-    float *mg = &wo[0][0][0];  // [SG][nquads][6]: M, L, O[4]
-    for (int it = tid; it < nquads * SG; it += 256) {
-        const int quad = it % nquads, sg = it / nquads, g = quad / Q4, d4 = (quad % Q4) * 4;
-        float M = -INFINITY, L = 0.f, O[4] = {0.f, 0.f, 0.f, 0.f};
-        auto fold = [&](float m, float l, const float4 o) {
-            const float Mn = fmaxf(M, m);
-            const float a = expf(M - Mn), b = expf(m - Mn);
-            L = fmaf(L, a, l * b);
-            O[0] = fmaf(O[0], a, o.x * b);
-            O[1] = fmaf(O[1], a, o.y * b);
-            O[2] = fmaf(O[2], a, o.z * b);
-            O[3] = fmaf(O[3], a, o.w * b);
-            M = Mn;
-        };
-        int sp = sg;
-        for (; sp + 3 * SG < nsplit; sp += 4 * SG) {
-            float m4[4], l4[4];
-            float4 o4[4];
+    // Merge: item (pair of dims of one head) folds every split with an
+    // online log-sum-exp (base 2), sixteen splits' loads in flight.
+    const unsigned long long *ml = reinterpret_cast<const unsigned long long *>(p.part_ml) +
+                                   (size_t)kvh * p.max_splits * kMaxGroup;
+    const unsigned long long *po = reinterpret_cast<const unsigned long long *>(p.part_o) +
+                                   (size_t)kvh * p.max_splits * kMaxGroup * (HD / 2);
+    for (int it = tid; it < G * HD / 2; it += 256) {
+        const int g = it / (HD / 2), d2 = it % (HD / 2);
+        float M = -INFINITY, L = 0.f, O0 = 0.f, O1 = 0.f;
+        for (int s0 = 0; s0 < nsplit; s0 += 16) {
+            unsigned long long mlv[16], ov[16];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const size_t e = (size_t)(sp + u * SG) * kMaxGroup + g;
-                m4[u] = ml[e * 2];
-                l4[u] = ml[e * 2 + 1];
-                o4[u] = *reinterpret_cast<const float4 *>(po + e * HD + d4);
+            for (int u = 0; u < 16; u++) {
+                const size_t e = (size_t)min(s0 + u, nsplit - 1) * kMaxGroup + g;
+                mlv[u] = __hip_atomic_load(ml + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ov[u] = __hip_atomic_load(po + e * (HD / 2) + d2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
 #pragma unroll
-            for (int u = 0; u < 4; u++) fold(m4[u], l4[u], o4[u]);
+            for (int u = 0; u < 16; u++) {
+                if (s0 + u < nsplit) {
+                    const float ms = __uint_as_float((uint32_t)mlv[u]), ls = __uint_as_float((uint32_t)(mlv[u] >> 32));
+                    const float o0 = __uint_as_float((uint32_t)ov[u]), o1 = __uint_as_float((uint32_t)(ov[u] >> 32));
+                    const float Mn = fmaxf(M, ms);  // every split holds a position: ms is finite
+                    const float a = exp2f(M - Mn), b = exp2f(ms - Mn);
+                    L = fmaf(L, a, ls * b);
+                    O0 = fmaf(O0, a, o0 * b);
+                    O1 = fmaf(O1, a, o1 * b);
+                    M = Mn;
+                }
+            }
         }
-        for (; sp < nsplit; sp += SG) {
-            const size_t e = (size_t)sp * kMaxGroup + g;
-            fold(ml[e * 2], ml[e * 2 + 1], *reinterpret_cast<const float4 *>(po + e * HD + d4));
-        }
-        float *dst = mg + ((size_t)sg * nquads + quad) * 6;
-        dst[0] = M;
-        dst[1] = L;
-        dst[2] = O[0], dst[3] = O[1], dst[4] = O[2], dst[5] = O[3];
-    }
-    __syncthreads();
-    for (int quad = tid; quad < nquads; quad += 256) {
-        float M = -INFINITY;
-        for (int sg = 0; sg < SG; sg++) M = fmaxf(M, mg[((size_t)sg * nquads + quad) * 6]);
-        float L = 0.f, O[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int sg = 0; sg < SG; sg++) {
-            const float *src = mg + ((size_t)sg * nquads + quad) * 6;
-            const float w = expf(src[0] - M);  // split groups without splits: exp(-inf) = 0
-            L = fmaf(src[1], w, L);
-#pragma unroll
-            for (int k = 0; k < 4; k++) O[k] = fmaf(src[2 + k], w, O[k]);
-        }
-        const int g = quad / Q4, d4 = (quad % Q4) * 4;
-        float *dst = p.out + (size_t)(kvh * G + g) * HD + d4;
-#pragma unroll
-        for (int k = 0; k < 4; k++) dst[k] = O[k] / L;
+        float *dst = p.out + (size_t)(kvh * G + g) * HD + 2 * d2;
+        dst[0] = O0 / L;
+        dst[1] = O1 / L;
     }
     if (tid == 0) __hip_atomic_store(&p.counters[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
