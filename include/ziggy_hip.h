@@ -382,6 +382,51 @@ int ziggy_hip_session_time_kernel(ZiggyHipSession *session, uint32_t kernel, uin
                                   uint64_t *avg_ns, uint64_t *bytes_per_launch, char *error_message,
                                   size_t error_message_len);
 
+/* ---- MoE FFN layer stack (batch-1 decode) ----
+ * The MoE FFN block of a layer, hidden += computeMoeFfn(rmsNorm(hidden,
+ * ffn_norm)) (model/loader.zig:1262-1285, 1718-1749), as the Metal session
+ * runs it (runMoeFfnBlock, runtime/gpu/session.zig:515-613), for a stack of
+ * layers: router, softmax / top-k / normalise routing, the k routed experts'
+ * SwiGLU FFNs (expert rows offset by the routed id) and the shared expert
+ * scaled by sigmoid of its gate row (computeSharedFfn, :1679-1697).  The
+ * reference's session keeps these tensors in gpu/types.zig:48-67 (the moe
+ * fields); this stack uploads them once and runs every layer as one
+ * captured HIP graph. */
+typedef struct ZiggyHipMoeStack ZiggyHipMoeStack;
+
+typedef struct {
+    ZiggyHipTensorDesc ffn_norm;        /* f32, [1][hidden] */
+    ZiggyHipTensorDesc router;          /* ffn_gate_inp: [expert_count][hidden] */
+    ZiggyHipTensorDesc gate_exps;       /* ffn_gate_exps: [expert_count * expert_ff][hidden] */
+    ZiggyHipTensorDesc up_exps;         /* ffn_up_exps: same shape and type */
+    ZiggyHipTensorDesc down_exps;       /* ffn_down_exps: [expert_count * hidden][expert_ff] */
+    ZiggyHipTensorDesc gate_shexp;      /* optional: [shared_ff][hidden] */
+    ZiggyHipTensorDesc up_shexp;        /* optional: same */
+    ZiggyHipTensorDesc down_shexp;      /* optional: [hidden][shared_ff] */
+    ZiggyHipTensorDesc gate_inp_shexp;  /* optional: [1][hidden], same type as router */
+} ZiggyHipMoeLayerDesc;
+
+typedef struct {
+    uint32_t hidden, expert_count, expert_used_count, expert_ff_length, shared_ff_length;
+    uint32_t gating_func;    /* 0: raw logits, 1 / 2: softmax over all experts */
+    uint32_t weights_norm;   /* normalizePositiveWeights over the selected weights */
+    float weights_scale, rms_norm_eps;
+} ZiggyHipMoeDesc;
+
+int ziggy_hip_moe_stack_create(ZiggyHipContext *ctx, const ZiggyHipMoeDesc *desc, const ZiggyHipMoeLayerDesc *layers,
+                               uint32_t layer_count, ZiggyHipMoeStack **out_stack, char *error_message,
+                               size_t error_message_len);
+void ziggy_hip_moe_stack_destroy(ZiggyHipMoeStack *stack);
+/* Runs one token's hidden state (f32, [hidden]) through every layer; selected
+ * (optional, [layer_count][expert_used_count] u32) and weights (optional,
+ * same shape, f32) receive each layer's routing. */
+int ziggy_hip_moe_stack_forward(ZiggyHipMoeStack *stack, const float *hidden_in, float *hidden_out,
+                                uint32_t *selected, float *weights, char *error_message, size_t error_message_len);
+/* Mean time of one pass through the stack: `iterations` graph replays back to
+ * back between one pair of HIP events (no counterpart in the reference). */
+int ziggy_hip_moe_stack_time(ZiggyHipMoeStack *stack, uint32_t iterations, uint64_t *avg_ns, char *error_message,
+                             size_t error_message_len);
+
 /* Library build tag, for logs. */
 const char *ziggy_hip_version(void);
 

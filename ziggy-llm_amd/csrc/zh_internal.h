@@ -77,14 +77,18 @@ struct MvSeg {
     uint64_t stride;        // bytes per row
     float *y;               // output (STORE/ADD/SWIGLU/ARGMAX logits; may be null for ARGMAX)
     const uint8_t *w2;      // SWIGLU: the "up" matrix (same format/shape as w)
+    const float *x;         // input of this segment (null: MvParams::x)
     int rows;
     int fmt;
     int wg_begin;           // first workgroup of this segment
     int rows_per_wg;
+    int expert_slot;        // >= 0: rows offset by entries[slot].id * rows_per_expert (MvParams::expert)
 };
 
+constexpr int kMaxSeg = 10;  // segments of one matvec launch (8 routed experts + shared + spare)
+
 struct MvParams {
-    MvSeg seg[4];
+    MvSeg seg[kMaxSeg];
     int nseg;
     int cols;
     int slots;              // cols / 64
@@ -95,8 +99,7 @@ struct MvParams {
     const float *norm_w;    // NORM: f32 weights
     float eps;
     unsigned long long *argmax_slot;  // ARGMAX: packed (ordered value << 32 | ~row)
-    const uint32_t *expert;           // indexed: entries (ShortlistEntry) + slot
-    int expert_slot;
+    const uint32_t *expert;           // indexed: entries (ShortlistEntry {u32 id, f32 weight})
     int rows_per_expert;
     int expert_limit;                 // expert ids >= this are ignored (no rows are read)
     float weight_scale;               // WADD: y += scale * dot (scale from entries if expert set)
@@ -127,6 +130,12 @@ hipError_t launch_weighted_sum_topk(float *dst, const float *src, const void *en
 hipError_t launch_sigmoid_scale_add(float *dst, const float *src, const float *scalar, int n, hipStream_t s);
 hipError_t launch_argmax_finalize(const unsigned long long *slot, uint32_t *state, hipStream_t s);
 hipError_t launch_fill_u64(unsigned long long *p, unsigned long long v, int n, hipStream_t s);
+
+// MoE routing and combine (zh_moe.hip)
+hipError_t launch_moe_route(const float *logits, int E, int k, int gating, int weights_norm, float weights_scale,
+                            int has_shared_gate, uint32_t *route, hipStream_t s);
+hipError_t launch_moe_combine(float *hidden, const float *tmp, const uint32_t *route, int H, int k, int has_shared,
+                              hipStream_t s);
 
 // attention (zh_attn.hip)
 struct AttnParams {

@@ -23,7 +23,7 @@ void plan_matvec(MvParams &p, int target_wgs) {
         p.seg[i].wg_begin = wg;
         wg += (p.seg[i].rows + teams * rpt - 1) / (teams * rpt);
     }
-    for (int i = p.nseg; i < 4; i++) p.seg[i].wg_begin = 0x7fffffff;
+    for (int i = p.nseg; i < kMaxSeg; i++) p.seg[i].wg_begin = 0x7fffffff;
 }
 
 static int total_wgs(const MvParams &p) {
@@ -83,9 +83,12 @@ hipError_t launch_matvec(const MvParams &p_in, int in, int out, hipStream_t s) {
         case Q8_0: k = pick_mv_q8_0(in, out, p.cols, n); break;
         default: k = pick_mv_other(f1, in, out, p.cols, n); break;
         }
-    } else if (in == IN_NORM && out == OUT_STORE) {
+    } else if (in == IN_NORM && out == OUT_STORE && (f1 == Q4_K || f1 == Q6_K)) {
         // the q/k/v launch of a Q4_K_M layer: Q4_K and Q6_K segments
         k = pick_mv_mixed(f1, f2, p.cols, n);
+    } else {
+        // routed (IQ4_XS) and shared (Q3_K) experts of an MoE layer
+        k = pick_mv_moe(f1, f2, in, out, p.cols);
     }
     if (!k) return hipErrorInvalidValue;
     const int grid = total_wgs(p);

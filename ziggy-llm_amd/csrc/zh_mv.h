@@ -111,7 +111,7 @@ struct XRaw {
 };
 
 template <int F, int IN>
-__device__ __forceinline__ void stage_load(XRaw &r, int s, bool active, const MvParams &p) {
+__device__ __forceinline__ void stage_load(XRaw &r, int s, bool active, const MvParams &p, const float *x) {
     const int base = Geom<F>::x_base(s);
 #pragma unroll
     for (int w = 0; w < 4; w++) {
@@ -121,7 +121,7 @@ __device__ __forceinline__ void stage_load(XRaw &r, int s, bool active, const Mv
             r.a[4 * w + c] = make_float4(0.f, 0.f, 0.f, 0.f);
             r.b[4 * w + c] = r.a[4 * w + c];
             if (active) {
-                r.a[4 * w + c] = *reinterpret_cast<const float4 *>(p.x + o + 4 * c);
+                r.a[4 * w + c] = *reinterpret_cast<const float4 *>(x + o + 4 * c);
                 if (IN == IN_NORM) r.b[4 * w + c] = *reinterpret_cast<const float4 *>(p.norm_w + o + 4 * c);
                 if (IN == IN_SILU) r.b[4 * w + c] = *reinterpret_cast<const float4 *>(p.x2 + o + 4 * c);
             }
@@ -161,9 +161,10 @@ __device__ __forceinline__ void stage_finish(XOf_t<F> &xs, const XRaw &r, const 
 // Stages the 64 activations of slot s (zeros for inactive lanes) with the
 // input prologue applied, in the slot representation of format F.
 template <int F, int IN>
-__device__ __forceinline__ void stage_x(XOf_t<F> &xs, int s, bool active, const MvParams &p, int T, float *lds) {
+__device__ __forceinline__ void stage_x(XOf_t<F> &xs, int s, bool active, const MvParams &p, const float *x, int T,
+                                        float *lds) {
     XRaw r;
-    stage_load<F, IN>(r, s, active, p);
+    stage_load<F, IN>(r, s, active, p, x);
     stage_finish<F, IN>(xs, r, p, T, lds);
 }
 
@@ -191,14 +192,14 @@ struct XRun {
 };
 
 template <int IN>
-__device__ __forceinline__ void coop_load(XRun &r, int nruns, const MvParams &p) {
+__device__ __forceinline__ void coop_load(XRun &r, int nruns, const MvParams &p, const float *x) {
     const int t = threadIdx.x;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         r.a[c] = make_float4(0.f, 0.f, 0.f, 0.f);
         r.b[c] = r.a[c];
         if (t < nruns) {
-            r.a[c] = *reinterpret_cast<const float4 *>(p.x + 16 * t + 4 * c);
+            r.a[c] = *reinterpret_cast<const float4 *>(x + 16 * t + 4 * c);
             if (IN == IN_NORM) r.b[c] = *reinterpret_cast<const float4 *>(p.norm_w + 16 * t + 4 * c);
             if (IN == IN_SILU) r.b[c] = *reinterpret_cast<const float4 *>(p.x2 + 16 * t + 4 * c);
         }
@@ -279,13 +280,13 @@ __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int 
 
     const uint8_t *wbase = sg.w, *wbase2 = sg.w2;
     float wscale = p.weight_scale;
-    if (p.expert) {
-        const uint32_t e = p.expert[2 * p.expert_slot];
-        if (e >= (uint32_t)p.expert_limit) return;  // uniform over the grid: no rows are read
+    if (p.expert && sg.expert_slot >= 0) {
+        const uint32_t e = p.expert[2 * sg.expert_slot];
+        if (e >= (uint32_t)p.expert_limit) return;  // uniform over the segment: no rows are read
         const uint64_t off = (uint64_t)e * (uint64_t)p.rows_per_expert * sg.stride;
         wbase += off;
         if (wbase2) wbase2 += off;
-        wscale = __uint_as_float(p.expert[2 * p.expert_slot + 1]);
+        wscale = __uint_as_float(p.expert[2 * sg.expert_slot + 1]);
     }
     const int r_begin = wg_in_seg * sg.rows_per_wg;
     const int r_end = min(r_begin + sg.rows_per_wg, sg.rows);
@@ -308,7 +309,7 @@ __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int 
         if (kReadY) ry[k] = sg.y[row_of(k)];
     }
     XOf_t<F> xs;
-    stage_x<F, IN>(xs, lane, active, p, T, lds);
+    stage_x<F, IN>(xs, lane, active, p, sg.x ? sg.x : p.x, T, lds);
 
     float best_v = -INFINITY;
     int best_r = 0x7fffffff;
@@ -387,13 +388,13 @@ __device__ __forceinline__ void mv_body_fast(const MvParams &p, const MvSeg &sg,
 
     const uint8_t *wbase = sg.w, *wbase2 = sg.w2;
     float wscale = p.weight_scale;
-    if (p.expert) {
-        const uint32_t e = p.expert[2 * p.expert_slot];
-        if (e >= (uint32_t)p.expert_limit) return;  // uniform over the grid: no rows are read
+    if (p.expert && sg.expert_slot >= 0) {
+        const uint32_t e = p.expert[2 * sg.expert_slot];
+        if (e >= (uint32_t)p.expert_limit) return;  // uniform over the segment: no rows are read
         const uint64_t off = (uint64_t)e * (uint64_t)p.rows_per_expert * sg.stride;
         wbase += off;
         if (wbase2) wbase2 += off;
-        wscale = __uint_as_float(p.expert[2 * p.expert_slot + 1]);
+        wscale = __uint_as_float(p.expert[2 * sg.expert_slot + 1]);
     }
     const int r_begin = wg_in_seg * sg.rows_per_wg;
     const int r_end = min(r_begin + sg.rows_per_wg, sg.rows);
@@ -407,10 +408,11 @@ __device__ __forceinline__ void mv_body_fast(const MvParams &p, const MvSeg &sg,
     const int nruns = p.slots * 4;
     XRaw xr;
     XRun xrun;
+    const float *xin = sg.x ? sg.x : p.x;
     if constexpr (kCoop)
-        coop_load<IN>(xrun, nruns, p);
+        coop_load<IN>(xrun, nruns, p, xin);
     else
-        stage_load<F, IN>(xr, lane, active, p);
+        stage_load<F, IN>(xr, lane, active, p, xin);
     // residual of row (4b + l4) of the team for batch b (lane l serves value l & 3)
     float ry[kReadY ? kMaxYB : 1];
     if (kReadY) {
@@ -534,7 +536,7 @@ __global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
     const int wg = blockIdx.x;
     int si = 0;
 #pragma unroll
-    for (int i = 1; i < 4; i++)
+    for (int i = 1; i < kMaxSeg; i++)
         if (i < p.nseg && wg >= p.seg[i].wg_begin) si = i;
     const MvSeg &sg = p.seg[si];
     if (F1 == F2 || sg.fmt == F1)
@@ -608,11 +610,21 @@ template <int F1, int F2> MvKernel pick_mixed(int cols, int rows_per_team) {
     return mv_kernel<F1, F2, IN_NORM, OUT_STORE, 0, 1>;
 }
 
+// Two formats in one launch for a fixed prologue / epilogue (the q/k/v launch
+// of a Q4_K_M layer; the routed + shared experts of an MoE layer).
+template <int F1, int F2, int IN, int OUT> MvKernel pick_two(int cols) {
+    const int T = team_width(cols);
+    if (T == 64) return mv_kernel<F1, F2, IN, OUT, 64, 1>;
+    if (T == 256) return mv_kernel<F1, F2, IN, OUT, 256, 1>;
+    return mv_kernel<F1, F2, IN, OUT, 0, 1>;
+}
+
 // Kernel pickers, one per group of formats (zh_mv_*.hip).
 MvKernel pick_mv_q4k(int in, int out, int cols, int rows_per_team);
 MvKernel pick_mv_q6k(int in, int out, int cols, int rows_per_team);
 MvKernel pick_mv_q8_0(int in, int out, int cols, int rows_per_team);
 MvKernel pick_mv_other(int fmt, int in, int out, int cols, int rows_per_team);
 MvKernel pick_mv_mixed(int f1, int f2, int cols, int rows_per_team);
+MvKernel pick_mv_moe(int f1, int f2, int in, int out, int cols);
 
 }  // namespace zh

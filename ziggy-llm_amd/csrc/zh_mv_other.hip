@@ -1,4 +1,5 @@
-// zh_mv_other.hip -- Q3_K, IQ4_XS, F16 and F32 matvec kernel instantiations (zh_mv.h).
+// zh_mv_other.hip -- Q3_K, IQ4_XS, F16 and F32 matvec kernel instantiations (zh_mv.h),
+// and the mixed IQ4_XS / Q3_K launches of an MoE layer (routed and shared experts).
 #include "zh_mv.h"
 
 namespace zh {
@@ -11,6 +12,14 @@ MvKernel pick_mv_other(int fmt, int in, int out, int cols, int n) {
     case F32: return pick<F32, F32, false>(in, out, cols, n);
     default: return nullptr;
     }
+}
+
+MvKernel pick_mv_moe(int f1, int f2, int in, int out, int cols) {
+    if (f1 == IQ4_XS && f2 == Q3_K) {
+        if (in == IN_NORM && out == OUT_SWIGLU) return pick_two<IQ4_XS, Q3_K, IN_NORM, OUT_SWIGLU>(cols);
+        if (in == IN_PLAIN && out == OUT_STORE) return pick_two<IQ4_XS, Q3_K, IN_PLAIN, OUT_STORE>(cols);
+    }
+    return nullptr;
 }
 
 }  // namespace zh

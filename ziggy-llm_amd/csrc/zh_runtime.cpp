@@ -416,7 +416,6 @@ static int indexed_common(ZiggyHipContext *ctx, uint32_t type, const ZiggyHipBuf
     p.cols = (int)cols;
     p.x = (const float *)in->ptr;
     p.expert = (const uint32_t *)entries->ptr;
-    p.expert_slot = (int)slot;
     p.rows_per_expert = (int)rpe;
     // the number of whole experts the matrix holds bounds the device-side expert id
     p.expert_limit = (int)(ma->len / (stride * rpe));
@@ -427,6 +426,7 @@ static int indexed_common(ZiggyHipContext *ctx, uint32_t type, const ZiggyHipBuf
     p.seg[0].y = (float *)outa->ptr;
     p.seg[0].rows = (int)rows;
     p.seg[0].fmt = (int)type;
+    p.seg[0].expert_slot = (int)slot;
     plan_matvec(p, 512);
     ZH_TRY(launch_matvec(p, IN_PLAIN, out_mode, ctx->stream), what);
     if (mb) {

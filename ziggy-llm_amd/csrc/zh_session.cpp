@@ -19,6 +19,7 @@
 #include <new>
 #include <vector>
 
+#include "zh_arena.h"
 #include "zh_internal.h"
 #include "zh_quant.h"
 #include "zh_step.h"
@@ -27,29 +28,9 @@ using namespace zh;
 
 namespace {
 
-struct DT {
-    const uint8_t *p = nullptr;
-    uint64_t rows = 0, cols = 0, stride = 0;
-    int type = -1;
-    bool present = false;
-};
-
 struct LayerW {
     DT attn_norm, q, k, v, o, q_bias, k_bias, v_bias, q_norm, k_norm, ffn_norm, gate, up, down;
 };
-
-int row_bytes(uint32_t type, uint64_t cols, uint64_t *out) {
-    switch (type) {
-    case ZIGGY_HIP_TYPE_F32: *out = cols * 4; return 0;
-    case ZIGGY_HIP_TYPE_F16: *out = cols * 2; return 0;
-    case ZIGGY_HIP_TYPE_Q8_0: if (cols % 32) return -1; *out = cols / 32 * 34; return 0;
-    case ZIGGY_HIP_TYPE_Q3_K: if (cols % 256) return -1; *out = cols / 256 * 110; return 0;
-    case ZIGGY_HIP_TYPE_Q4_K: if (cols % 256) return -1; *out = cols / 256 * 144; return 0;
-    case ZIGGY_HIP_TYPE_Q6_K: if (cols % 256) return -1; *out = cols / 256 * 210; return 0;
-    case ZIGGY_HIP_TYPE_IQ4_XS: if (cols % 256) return -1; *out = cols / 256 * 136; return 0;
-    default: return -1;
-    }
-}
 
 uint64_t now_ns() {
     return (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
@@ -286,25 +267,6 @@ int build_graph(ZiggyHipSession *s, char *err, size_t err_len) {
     hipGraphDestroy(g);
     if (e != hipSuccess) return hip_fail(e, "graph instantiate", err, err_len);
     return ZIGGY_HIP_OK;
-}
-
-bool take_tensor(const ZiggyHipTensorDesc *d, uint64_t want_rows, uint64_t want_cols, bool required, bool f32_only,
-                 DT *out, size_t *arena_off, std::vector<std::pair<const ZiggyHipTensorDesc *, DT *>> &todo) {
-    if (!d || !d->data) return !required;
-    uint64_t stride;
-    if (row_bytes(d->tensor_type, d->cols, &stride)) return false;
-    if (f32_only && d->tensor_type != ZIGGY_HIP_TYPE_F32) return false;
-    if ((want_rows && d->rows != want_rows) || (want_cols && d->cols != want_cols)) return false;
-    if (!f32_only && (d->cols % 64 || d->cols / 64 > 256)) return false;
-    out->rows = d->rows;
-    out->cols = d->cols;
-    out->stride = stride;
-    out->type = (int)d->tensor_type;
-    out->present = true;
-    out->p = reinterpret_cast<const uint8_t *>(*arena_off);  // fixed up after the arena is allocated
-    *arena_off += (stride * d->rows + 255) & ~(size_t)255;
-    todo.push_back({d, out});
-    return true;
 }
 
 void free_session(ZiggyHipSession *s) {

@@ -63,6 +63,20 @@ class GenerateStats(ctypes.Structure):
                 ("next_token", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
 
 
+MOE_LAYER_FIELDS = ["ffn_norm", "router", "gate_exps", "up_exps", "down_exps", "gate_shexp", "up_shexp",
+                    "down_shexp", "gate_inp_shexp"]
+
+
+class MoeLayerDesc(ctypes.Structure):
+    _fields_ = [(n, TensorDesc) for n in MOE_LAYER_FIELDS]
+
+
+class MoeDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("hidden", "expert_count", "expert_used_count", "expert_ff_length",
+                                               "shared_ff_length", "gating_func", "weights_norm")] + [
+        ("weights_scale", ctypes.c_float), ("rms_norm_eps", ctypes.c_float)]
+
+
 KERNELS = {"qkv": 0, "rope_kv": 1, "attention": 2, "o_proj": 3, "gate_up": 4, "down": 5, "output": 6}
 
 
@@ -130,10 +144,15 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_session_read_logits": [vp, vp] + E,
         "ziggy_hip_session_time_kernel": [vp, u32, u32, ctypes.POINTER(ctypes.c_uint64),
                                           ctypes.POINTER(ctypes.c_uint64)] + E,
+        "ziggy_hip_moe_stack_create": [vp, ctypes.POINTER(MoeDesc), ctypes.POINTER(MoeLayerDesc), u32,
+                                       ctypes.POINTER(vp)] + E,
+        "ziggy_hip_moe_stack_destroy": [vp],
+        "ziggy_hip_moe_stack_forward": [vp, vp, vp, vp, vp] + E,
+        "ziggy_hip_moe_stack_time": [vp, u32, ctypes.POINTER(ctypes.c_uint64)] + E,
         "ziggy_hip_version": [],
     }
     restypes = {"ziggy_hip_destroy_context": None, "ziggy_hip_destroy_buffer": None,
-                "ziggy_hip_session_destroy": None, "ziggy_hip_buffer_length": sz,
+                "ziggy_hip_session_destroy": None, "ziggy_hip_moe_stack_destroy": None, "ziggy_hip_buffer_length": sz,
                 "ziggy_hip_session_position": u32, "ziggy_hip_version": ctypes.c_char_p}
     for name, args in sigs.items():
         fn = getattr(L, name)
@@ -450,3 +469,46 @@ def exported_symbols() -> list:
         names |= {f"ziggy_hip_run_matvec_{sfx}_f32", f"ziggy_hip_run_matvec_{sfx}_f32_to_dst",
                   f"ziggy_hip_run_matvec_{sfx}_add_f32"}
     return sorted(n for n in names if not n.endswith("_f32##") and "##" not in n)
+
+
+class MoeStack:
+    """A stack of MoE FFN blocks (ziggy_hip_moe_stack_*) over host-resident tensors.
+
+    `layers` holds one dict per layer mapping MOE_LAYER_FIELDS names to
+    (uint8 bytes, rows, cols, tensor type); optional tensors may be absent.
+    """
+
+    def __init__(self, ctx: Context, desc: MoeDesc, layers):
+        self.ctx, self.desc, self._keep = ctx, desc, layers
+        arr = (MoeLayerDesc * len(layers))()
+        for i, lay in enumerate(layers):
+            for f in MOE_LAYER_FIELDS:
+                if f in lay:
+                    data, rows, cols, ttype = lay[f]
+                    setattr(arr[i], f, TensorDesc(data.ctypes.data, rows, cols, ttype, 0))
+        self._arr = arr
+        h = ctypes.c_void_p()
+        _call("ziggy_hip_moe_stack_create", ctx.h, ctypes.byref(desc), arr, len(layers), ctypes.byref(h))
+        self.h = h
+        ctx._owned.add(self)
+
+    def forward(self, hidden: np.ndarray):
+        """(hidden after every layer, selected experts [layers, k], their weights)."""
+        hidden = np.ascontiguousarray(hidden, np.float32)
+        out = np.empty_like(hidden)
+        n, k = len(self._keep), self.desc.expert_used_count
+        sel = np.empty((n, k), np.uint32)
+        w = np.empty((n, k), np.float32)
+        _call("ziggy_hip_moe_stack_forward", self.h, hidden.ctypes.data, out.ctypes.data, sel.ctypes.data,
+              w.ctypes.data)
+        return out, sel, w
+
+    def time(self, iterations: int) -> int:
+        ns = ctypes.c_uint64()
+        _call("ziggy_hip_moe_stack_time", self.h, iterations, ctypes.byref(ns))
+        return ns.value
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().ziggy_hip_moe_stack_destroy(self.h)
+            self.h = None

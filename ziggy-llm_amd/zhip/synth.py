@@ -321,3 +321,73 @@ def toy_llama_fixture(embedding_length: int = 14, feed_forward_length: int = 4, 
 
 def toy_detokenize(ids) -> str:
     return "".join(TOY_VOCAB[i].replace(METASPACE, " ") for i in ids)
+
+
+@dataclass
+class MoeSpec:
+    """A stack of Qwen3.5-MoE-style sparse FFN layers (BASELINE config 5 at full size)."""
+    name: str
+    n_layers: int
+    hidden: int
+    n_experts: int
+    top_k: int
+    expert_ff: int
+    shared_ff: int
+    expert_type: int = IQ4_XS
+    shared_type: int = Q3_K
+    router_type: int = F32
+    shared_gate: bool = True
+    gating_func: int = 1          # softmax over all experts
+    weights_norm: int = 1         # expert_weights_norm (true for qwen35moe)
+    weights_scale: float = 1.0
+    eps: float = 1e-6
+
+    def weight_bytes_per_token(self) -> int:
+        """Bytes one decode token streams: router (+ shared gate row), k routed experts, shared expert, norm."""
+        H, F, S, k = self.hidden, self.expert_ff, self.shared_ff, self.top_k
+        rb = gguf.row_bytes
+        per = (rb(self.router_type, H) * (self.n_experts + (1 if self.shared_gate else 0)) + 4 * H +
+               k * (2 * F * rb(self.expert_type, H) + H * rb(self.expert_type, F)) +
+               (2 * S * rb(self.shared_type, H) + H * rb(self.shared_type, S) if S else 0))
+        return per * self.n_layers
+
+
+def moe_config5_spec(n_layers: int = 40) -> MoeSpec:
+    return MoeSpec("qwen3.5-moe-ffn-stack", n_layers, 2048, 256, 8, 512, 512)
+
+
+def small_moe_spec(n_layers: int = 3) -> MoeSpec:
+    return MoeSpec("small-moe", n_layers, 256, 16, 4, 256, 256)
+
+
+def build_moe_stack(spec: MoeSpec, seed: int, threads: int | None = None):
+    """Per-layer tensors {name: (bytes, rows, cols, type)}: N(0, 0.02) expert weights quantized by this
+    package, router rows N(0, 1/sqrt(hidden)) so normed inputs give ~N(0, 1) logits, norm weights 1."""
+    H, E, F, S = spec.hidden, spec.n_experts, spec.expert_ff, spec.shared_ff
+    layers = []
+
+    def t(name, rows, cols, ttype, std):
+        buf = np.zeros(gguf.row_bytes(ttype, cols) * rows, np.uint8)
+        fill_tensor(buf, ttype, rows, cols, tensor_seed(seed, name), 0.0, std, threads)
+        return (buf, rows, cols, ttype)
+
+    for i in range(spec.n_layers):
+        lay = {"ffn_norm": (np.ones(H, np.float32).view(np.uint8), 1, H, F32),
+               "router": t(f"blk.{i}.ffn_gate_inp", E, H, spec.router_type, H ** -0.5),
+               "gate_exps": t(f"blk.{i}.ffn_gate_exps", E * F, H, spec.expert_type, 0.02),
+               "up_exps": t(f"blk.{i}.ffn_up_exps", E * F, H, spec.expert_type, 0.02),
+               "down_exps": t(f"blk.{i}.ffn_down_exps", E * H, F, spec.expert_type, 0.02)}
+        if S:
+            lay["gate_shexp"] = t(f"blk.{i}.ffn_gate_shexp", S, H, spec.shared_type, 0.02)
+            lay["up_shexp"] = t(f"blk.{i}.ffn_up_shexp", S, H, spec.shared_type, 0.02)
+            lay["down_shexp"] = t(f"blk.{i}.ffn_down_shexp", H, S, spec.shared_type, 0.02)
+            if spec.shared_gate:
+                lay["gate_inp_shexp"] = t(f"blk.{i}.ffn_gate_inp_shexp", 1, H, spec.router_type, H ** -0.5)
+        layers.append(lay)
+    return layers
+
+
+def moe_desc(spec: MoeSpec):
+    from .hip import MoeDesc
+    return MoeDesc(spec.hidden, spec.n_experts, spec.top_k, spec.expert_ff, spec.shared_ff, spec.gating_func,
+                   spec.weights_norm, spec.weights_scale, spec.eps)
