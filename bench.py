@@ -49,7 +49,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--seed", type=int, default=1)
-    ap.add_argument("--model", default="llama8b", choices=["llama8b", "tinyllama", "qwen3"])
+    ap.add_argument("--model", default="llama8b", choices=["llama8b", "tinyllama", "qwen3", "moe"],
+                    help="llama8b: the headline (config 3); tinyllama, qwen3: configs 1 and 4; "
+                         "moe: config 5, the 40-layer MoE FFN stack at batch-1 decode")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=64)
@@ -63,6 +65,9 @@ def main():
     import numpy as np
 
     from zhip import hip, synth
+
+    if args.model == "moe":
+        return bench_moe(args)
 
     ctx_len = args.prompt + args.warmup + args.steps + 8
     spec = {"llama8b": synth.llama8b_spec, "tinyllama": synth.tinyllama_spec,
@@ -134,8 +139,17 @@ def main():
                          f"C restatement of the reference CPU path, {threads} threads of {ncpu} host cores"}
         log(f"cpu baseline: {cpu['value']} tok/s over {n} steps ({t_cpu:.1f}s)")
 
+    if args.model == "llama8b":
+        metric = "decode tok/s + % of HBM roofline, Llama-3.1-8B-shaped Q4_K_M, batch 1, 4k ctx"
+        weights = "Q4_K (Q6_K attn_v, 16/32 ffn_down, output), random N(0,0.02)"
+    elif args.model == "qwen3":
+        metric = "decode tok/s + % of HBM roofline, Qwen3-8B-shaped Q8_0, batch 1"
+        weights = "Q8_0 throughout, per-head QK RMSNorm, random N(0,0.02)"
+    else:
+        metric = "decode tok/s + % of HBM roofline, TinyLlama-1.1B-shaped Q4_K_M, batch 1"
+        weights = "Q4_K (Q6_K attn_v, 10/22 ffn_down, output), random N(0,0.02)"
     line = {
-        "metric": "decode tok/s + % of HBM roofline, Llama-3.1-8B-shaped Q4_K_M, batch 1, 4k ctx",
+        "metric": metric,
         "value": round(tok_s, 3),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -147,9 +161,9 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": f"{spec.name} Q4_K_M greedy decode, batch 1, positions {pos0}-{pos0 + args.steps - 1}"
+        "config": {"workload": f"{spec.name} greedy decode, batch 1, positions {pos0}-{pos0 + args.steps - 1}"
                                f" after a {args.prompt}-token prompt",
-                   "weights": "Q4_K (Q6_K attn_v, 16/32 ffn_down, output), random N(0,0.02)",
+                   "weights": weights,
                    "kv_cache": "binary16", "batch": 1, "context": pos0 + args.steps, "parallelism": "none"},
         "hbm_fraction": round(hbm_frac, 4),
         "bytes_per_token": bytes_per_token,
@@ -157,6 +171,72 @@ def main():
         "cpu_baseline": cpu,
         "kernels": kernels,
         "tokens_head": [int(t) for t in toks[:8]],
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_moe(args):
+    """Config 5: 40 Qwen3.5-MoE-style sparse FFN layers (hidden 2048, 256 IQ4_XS experts of FFN 512, top-8
+    softmax routing, a Q3_K shared expert with a sigmoid gate) at batch-1 decode.  A step is one token's
+    hidden state through the whole stack (one graph replay); weights resident in HBM."""
+    import numpy as np
+
+    from zhip import hip, synth
+
+    spec = synth.moe_config5_spec(40)
+    t0 = time.time()
+    layers = synth.build_moe_stack(spec, seed=args.seed)
+    log(f"built {spec.name}: {spec.n_layers} layers in {time.time() - t0:.1f}s")
+    ctx = hip.Context(0)
+    st = hip.MoeStack(ctx, synth.moe_desc(spec), layers)
+    x = synth.normal_row(args.seed, 0, spec.hidden, 0.0, 1.0)
+    for _ in range(max(1, args.warmup)):
+        x, _, _ = st.forward(x)
+    ns = st.time(args.steps)
+    tok_s = 1e9 / ns
+    bpt = spec.weight_bytes_per_token()
+    frac = bpt * tok_s / (HBM_PEAK_GBS * 1e9)
+    log(f"moe stack: {ns / 1e3:.1f} us per token, {tok_s:.1f} tok/s, {bpt / 1e6:.1f} MB/token -> "
+        f"{100 * frac:.1f}% of HBM peak")
+    st.close()
+    ctx.close()
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the oracle's MoE path (computeMoeFfn restated, zo_moe_ffn), layer by layer, with the
+        # reference's matvec thread policy, on a bounded sample of tokens
+        from oracle import zo
+        ncpu = os.cpu_count() or 1
+        threads = 1 + min(11, ncpu - 1)
+
+        def ptr(lay, name):
+            return lay[name][0].ctypes.data if name in lay else None
+
+        descs = [zo.MoeDesc(spec.router_type, ptr(l, "router"), spec.expert_type, ptr(l, "gate_exps"),
+                            ptr(l, "up_exps"), ptr(l, "down_exps"), spec.shared_type, ptr(l, "gate_shexp"),
+                            ptr(l, "up_shexp"), ptr(l, "down_shexp"), spec.router_type, ptr(l, "gate_inp_shexp"),
+                            spec.hidden, spec.expert_ff, spec.shared_ff, spec.n_experts, spec.top_k,
+                            spec.gating_func, spec.weights_norm, spec.weights_scale) for l in layers]
+        h = synth.normal_row(args.seed, 0, spec.hidden, 0.0, 1.0)
+        n, t_cpu = 0, 0.0
+        while (t_cpu < args.cpu_seconds or n < 2) and n < 64:
+            t1 = time.perf_counter()
+            for lay, d in zip(layers, descs):
+                normed = zo.rms_norm(h, lay["ffn_norm"][0].view(np.float32), spec.eps)
+                out, _, _ = zo.moe_ffn(d, normed, threads=threads)
+                h = (h + out).astype(np.float32)
+            t_cpu += time.perf_counter() - t1
+            n += 1
+        cpu = {"value": round(n / t_cpu, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"{n} tokens through the same {spec.n_layers}-layer stack, C restatement of the "
+                         f"reference's CPU MoE path, {threads} threads of {ncpu} host cores"}
+        log(f"cpu baseline: {cpu['value']} tok/s over {n} tokens ({t_cpu:.1f}s)")
+    line = {
+        "metric": "MoE FFN stack decode tok/s + % of HBM roofline, 40 x (256 IQ4_XS experts top-8 + Q3_K shared)",
+        "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ns / 1e6, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"{spec.name}, {spec.n_layers} layers, batch 1", "batch": 1, "parallelism": "none"},
+        "hbm_fraction": round(frac, 4), "bytes_per_token": bpt, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 

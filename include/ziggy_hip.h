@@ -176,6 +176,15 @@ int ziggy_hip_dequantize_rows(ZiggyHipContext *ctx, uint32_t tensor_type, const 
                               size_t matrix_offset, ZiggyHipBuffer *output, uint32_t rows, uint32_t cols,
                               char *error_message, size_t error_message_len);
 
+/* ---- dense path for M >= 8 tokens on the matrix cores (the batched matvecs of the
+ * reference's speculative verify, ziggy_metal_batch_matvec_*_f32, bridge.h:622-700, which
+ * run one token per dispatch):
+ *   output[t][r] (=|+=) dot(row r of matrix, input[t][0..cols)),  t < tokens,
+ * input [tokens][cols] and output [tokens][rows] row-major f32. ---- */
+int ziggy_hip_run_gemm(ZiggyHipContext *ctx, uint32_t tensor_type, const ZiggyHipBuffer *matrix,
+                       const ZiggyHipBuffer *input, ZiggyHipBuffer *output, uint32_t tokens, uint32_t rows,
+                       uint32_t cols, int add, char *error_message, size_t error_message_len);
+
 /* ---- expert-indexed matvec (replace bridge.h:294-336, 701-757).  The expert id
  * is entries[slot_idx].token_id of a ShortlistEntry{u32, f32} array; rows
  * are offset by expert_id * rows_per_expert. ---- */

@@ -1,0 +1,226 @@
+// zh_gemm.hip -- the dense path for M >= 8 tokens (speculative verify,
+// prefill, grouped MoE experts) on the matrix cores.
+//
+//   Y[m][n] (=, +=) sum_k W[n][k] * X[m][k]     for tokens m < M, rows n < N
+//
+// W is a quantized (or f16/f32) GGUF matrix in its native row layout; each
+// lane decodes the four consecutive weights its MFMA A fragment needs with
+// the bit-exact decoders of zh_quant.h (dequant_value: the reference's own
+// binary32 operation order).  Weights and activations enter the matrix
+// cores as bf16 pairs: v = hi + lo with hi = bf16(v), lo = bf16(v - hi),
+// and each 16x16x16 tile accumulates hi*hi + hi*lo + lo*hi in f32 -- about
+// 16 significant bits per operand, so the products carry ~2^-16 relative
+// error (lo*lo, below that, is dropped).  Accumulation is f32.
+//
+// Tiling: a workgroup computes 16 rows x 16 tokens over the whole reduction
+// dimension; its four wavefronts take interleaved 16-value steps of K and
+// their partial tiles meet in LDS.  The grid has up to 1024 row tiles (more
+// rows loop) by ceil(M / 16) token tiles.  Decode-sized M (8 .. 16) keeps
+// the kernel bound by the weight stream; the token tile is re-read from L2.
+//
+// MFMA operand layout (v_mfma_f32_16x16x16_bf16, wave64): lane l holds
+// A[l % 16][4 (l / 16) + 0..3], B[4 (l / 16) + 0..3][l % 16], and the result
+// D[4 (l / 16) + 0..3][l % 16].  Here A = the row tile of W, B = the token
+// tile of X transposed, D[i][j] = Y[token j][row i].
+#include "zh_internal.h"
+#include "zh_quant.h"
+
+namespace zh {
+
+typedef short bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// bf16 round-to-nearest-even of a finite f32 (the bits of the upper half).
+__device__ __forceinline__ uint32_t bf16_bits(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+// hi / lo bf16 halves of four values, packed as MFMA operands.
+__device__ __forceinline__ void split4(const float (&v)[4], bf16x4 &hi, bf16x4 &lo) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t h = bf16_bits(v[i]);
+        const float r = v[i] - __uint_as_float(h << 16);
+        hi[i] = (short)h;
+        lo[i] = (short)bf16_bits(r);
+    }
+}
+
+// Weights k .. k+3 (k a multiple of 4) of one row, bit-exact.
+template <int F> __device__ __forceinline__ void weights4(const uint8_t *__restrict__ row, int k, float (&w)[4]) {
+    if constexpr (F == F32) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[i] = __uint_as_float(ld4(row + 4 * (k + i)));
+    } else if constexpr (F == F16) {
+        const uint2 v = ld8(row + 2 * k);
+        w[0] = h2f(v.x), w[1] = h2f(v.x >> 16), w[2] = h2f(v.y), w[3] = h2f(v.y >> 16);
+    } else {
+        constexpr int V = Geom<F>::kValues, B = Geom<F>::kBytes;
+        const uint8_t *blk = row + (size_t)(k / V) * B;
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[i] = dequant_value<F>(blk, k % V + i);
+    }
+}
+
+struct GemmParams {
+    const uint8_t *w;     // W row 0
+    const uint8_t *w2;    // SWIGLU: the up matrix (same format and shape)
+    uint64_t stride;      // bytes per W row
+    const float *x;       // [M][ldx]
+    float *y;             // [M][ldy]
+    int M, N, K, ldx, ldy;
+    unsigned long long *argmax;  // ARGMAX: [M] packed (ordered value << 32 | ~row)
+};
+
+__device__ __forceinline__ uint32_t ordered_bits_g(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+template <int F, int OUT>
+__global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
+    constexpr bool kPair = OUT == OUT_SWIGLU;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int m0 = blockIdx.y * 16;
+    const int li = lane & 15, lq = lane >> 4;
+    const int m = min(m0 + li, p.M - 1);  // this lane's X token (clamped; dropped at the store)
+    const float *xrow = p.x + (size_t)m * p.ldx;
+    const int j = m0 + li;                // token of this lane's results
+    __shared__ float part[4][kPair ? 2 : 1][64][4];
+    float best = -INFINITY;
+    int best_n = 0x7fffffff;
+    const int ntiles = (p.N + 15) / 16;
+    // row tiles n0 = 16 * (blockIdx.x + t * gridDim.x)
+    for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        const int n0 = 16 * tile;
+        const int n = min(n0 + li, p.N - 1);  // this lane's W row (clamped)
+        const uint8_t *wrow = p.w + (uint64_t)n * p.stride;
+        const uint8_t *wrow2 = kPair ? p.w2 + (uint64_t)n * p.stride : nullptr;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 16 * wave + 4 * lq; k < p.K; k += 64) {
+            float wv[4], xv[4];
+            weights4<F>(wrow, k, wv);
+            const float4 xx = *reinterpret_cast<const float4 *>(xrow + k);
+            xv[0] = xx.x, xv[1] = xx.y, xv[2] = xx.z, xv[3] = xx.w;
+            bf16x4 ah, al, bh, bl;
+            split4(wv, ah, al);
+            split4(xv, bh, bl);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
+            if (kPair) {
+                weights4<F>(wrow2, k, wv);
+                split4(wv, ah, al);
+                acc2 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc2, 0, 0, 0);
+                acc2 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc2, 0, 0, 0);
+                acc2 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc2, 0, 0, 0);
+            }
+        }
+        // the four wavefronts' partial tiles meet in LDS
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            part[wave][0][lane][r] = acc[r];
+            if (kPair) part[wave][kPair ? 1 : 0][lane][r] = acc2[r];
+        }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float v = (part[0][0][lane][r] + part[1][0][lane][r]) + (part[2][0][lane][r] + part[3][0][lane][r]);
+                const int nn = n0 + 4 * lq + r;  // row of result r
+                if (j >= p.M || nn >= p.N) continue;
+                float *dst = p.y ? p.y + (size_t)j * p.ldy + nn : nullptr;
+                if (OUT == OUT_STORE) {
+                    *dst = v;
+                } else if (OUT == OUT_ADD) {
+                    *dst = *dst + v;
+                } else if (OUT == OUT_SWIGLU) {
+                    const int c = kPair ? 1 : 0;
+                    const float u =
+                        (part[0][c][lane][r] + part[1][c][lane][r]) + (part[2][c][lane][r] + part[3][c][lane][r]);
+                    *dst = (v / (1.0f + expf(-v))) * u;
+                } else if (OUT == OUT_ARGMAX) {
+                    if (dst) *dst = v;
+                    if (v > best || (v == best && nn < best_n)) {
+                        best = v;
+                        best_n = nn;
+                    }
+                }
+            }
+        }
+        __syncthreads();  // part is reused by the next tile
+    }
+    if (OUT == OUT_ARGMAX && wave == 0) {
+        // lanes j, j + 16, j + 32, j + 48 hold this token's rows; the packed
+        // maximum picks the largest value, then the lowest row
+        unsigned long long key = best_n == 0x7fffffff ? 0ull
+                                 : ((unsigned long long)ordered_bits_g(best) << 32) |
+                                       (unsigned long long)(0xFFFFFFFFu - (uint32_t)best_n);
+        unsigned long long o = __shfl_xor(key, 16, 64);
+        key = o > key ? o : key;
+        o = __shfl_xor(key, 32, 64);
+        key = o > key ? o : key;
+        if (lq == 0 && j < p.M && key) atomicMax(p.argmax + j, key);
+    }
+}
+
+typedef void (*GemmKernel)(GemmParams);
+
+template <int F> static GemmKernel pick_gemm(int out) {
+    switch (out) {
+    case OUT_STORE: return gemm_kernel<F, OUT_STORE>;
+    case OUT_ADD: return gemm_kernel<F, OUT_ADD>;
+    case OUT_SWIGLU: return gemm_kernel<F, OUT_SWIGLU>;
+    case OUT_ARGMAX: return gemm_kernel<F, OUT_ARGMAX>;
+    default: return nullptr;
+    }
+}
+
+hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
+                       float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s) {
+    if (M < 1 || N < 1 || K < 16 || K % 16 || ldx % 4) return hipErrorInvalidValue;
+    GemmKernel k = nullptr;
+    switch (fmt) {
+    case Q4_K: k = pick_gemm<Q4_K>(out); break;
+    case Q6_K: k = pick_gemm<Q6_K>(out); break;
+    case Q8_0: k = pick_gemm<Q8_0>(out); break;
+    case Q3_K: k = pick_gemm<Q3_K>(out); break;
+    case IQ4_XS: k = pick_gemm<IQ4_XS>(out); break;
+    case F16: k = pick_gemm<F16>(out); break;
+    case F32: k = pick_gemm<F32>(out); break;
+    default: break;
+    }
+    if (!k) return hipErrorInvalidValue;
+    GemmParams p{w, w2, stride, x, y, M, N, K, ldx, ldy, argmax};
+    // at most 1024 row tiles in flight per token tile; larger N loops (grid-stride)
+    const int tiles = (N + 15) / 16;
+    hipLaunchKernelGGL(k, dim3(tiles < 1024 ? tiles : 1024, (M + 15) / 16), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+// Per-token RMSNorm of M rows (rmsNorm, model/loader.zig:3404-3426, for each
+// token): out[m] = (scale_m * x[m]) * w; one workgroup per token.
+__global__ void __launch_bounds__(256) rms_norm_rows_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                            float *__restrict__ out, int n, float eps) {
+    const float *xr = x + (size_t)blockIdx.x * n;
+    float *orow = out + (size_t)blockIdx.x * n;
+    __shared__ float red[4];
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float scale = 1.0f / sqrtf(tot / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 256) orow[i] = (scale * xr[i]) * w[i];
+}
+
+hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps,
+                                hipStream_t s) {
+    if (rows < 1 || n < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rms_norm_rows_kernel, dim3(rows), dim3(256), 0, s, x, w, out, n, eps);
+    return hipGetLastError();
+}
+
+}  // namespace zh

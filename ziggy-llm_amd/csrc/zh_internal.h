@@ -131,6 +131,13 @@ hipError_t launch_sigmoid_scale_add(float *dst, const float *src, const float *s
 hipError_t launch_argmax_finalize(const unsigned long long *slot, uint32_t *state, hipStream_t s);
 hipError_t launch_fill_u64(unsigned long long *p, unsigned long long v, int n, hipStream_t s);
 
+// MFMA GEMM for M >= 8 tokens (zh_gemm.hip): Y[m][n] (=, +=) sum_k W[n][k] X[m][k]
+// (OUT_STORE / OUT_ADD / OUT_SWIGLU with w2 / OUT_ARGMAX into argmax[M]).
+hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
+                       float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s);
+hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps,
+                                hipStream_t s);
+
 // MoE routing and combine (zh_moe.hip)
 hipError_t launch_moe_route(const float *logits, int E, int k, int gating, int weights_norm, float weights_scale,
                             int has_shared_gate, uint32_t *route, hipStream_t s);

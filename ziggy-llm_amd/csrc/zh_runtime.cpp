@@ -395,6 +395,25 @@ int ziggy_hip_dequantize_rows(ZiggyHipContext *ctx, uint32_t type, const ZiggyHi
     return finish_op(ctx, "dequantize_rows", err, err_len);
 }
 
+// ---------------- MFMA GEMM for M >= 8 tokens ----------------
+
+extern "C" int ziggy_hip_run_gemm(ZiggyHipContext *ctx, uint32_t type, const ZiggyHipBuffer *m,
+                                  const ZiggyHipBuffer *in, ZiggyHipBuffer *out, uint32_t tokens, uint32_t rows,
+                                  uint32_t cols, int add, char *err, size_t err_len) {
+    uint64_t stride;
+    int st = check_matvec(ctx, type, m, 0, in, out, 0, rows, cols, &stride, err, err_len);
+    if (st) return st;
+    if (tokens == 0 || cols % 16 || !buf_ok(in, (size_t)tokens * cols * 4) || !buf_ok(out, (size_t)tokens * rows * 4)) {
+        set_err(err, err_len, "buffers too small for a %u-token %ux%u GEMM", tokens, rows, cols);
+        return ZIGGY_HIP_INVALID_ARGUMENT;
+    }
+    ZH_TRY(launch_gemm((int)type, (const uint8_t *)m->ptr, nullptr, stride, (const float *)in->ptr, (int)cols,
+                       (float *)out->ptr, (int)rows, (int)tokens, (int)rows, (int)cols, add ? OUT_ADD : OUT_STORE,
+                       nullptr, ctx->stream),
+           "gemm");
+    return finish_op(ctx, "gemm", err, err_len);
+}
+
 // ---------------- expert-indexed matvec ----------------
 
 static int indexed_common(ZiggyHipContext *ctx, uint32_t type, const ZiggyHipBuffer *ma, const ZiggyHipBuffer *mb,

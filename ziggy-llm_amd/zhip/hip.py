@@ -110,6 +110,7 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_dequantize_rows": [vp, u32, vp, sz, vp, u32, u32] + E,
         "ziggy_hip_time_matvec": [vp, u32, vp, u32, sz, vp, vp, u32, u32, u32, ctypes.POINTER(ctypes.c_uint64)] + E,
         "ziggy_hip_indexed_matvec": [vp, u32, vp, vp, vp, u32, u32, vp, u32, u32, i] + E,
+        "ziggy_hip_run_gemm": [vp, u32, vp, vp, vp, u32, u32, u32, i] + E,
         "ziggy_hip_dual_indexed_matvec": [vp, u32, vp, vp, vp, vp, vp, u32, u32, vp, u32, u32] + E,
         "ziggy_hip_apply_rope_f32": [vp, vp, u32, u32, u32, u32, f, u32] + E,
         "ziggy_hip_apply_rope_to_dst_f32": [vp, vp, vp, sz, u32, u32, u32, u32, f, u32] + E,
@@ -244,6 +245,9 @@ class Context:
     def dequantize(self, ttype, m: Buffer, out: Buffer, rows, cols, m_off=0):
         _call("ziggy_hip_dequantize_rows", self.h, ttype, m.h, m_off, out.h, rows, cols)
 
+    def gemm(self, ttype, m: Buffer, x: Buffer, y: Buffer, tokens: int, rows: int, cols: int, add=False):
+        _call("ziggy_hip_run_gemm", self.h, ttype, m.h, x.h, y.h, tokens, rows, cols, 1 if add else 0)
+
     def indexed_matvec(self, ttype, m, x, y, rows, cols, entries, slot, rows_per_expert, add_weighted=False):
         _call("ziggy_hip_indexed_matvec", self.h, ttype, m.h, x.h, y.h, rows, cols, entries.h, slot,
               rows_per_expert, int(add_weighted))
@@ -306,7 +310,7 @@ class Context:
     def close(self):
         if self.h:
             for obj in list(getattr(self, "_owned", ())):
-                obj.close() if isinstance(obj, Session) else obj.free()
+                obj.free() if isinstance(obj, Buffer) else obj.close()
             lib().ziggy_hip_destroy_context(self.h)
             self.h = None
 
