@@ -69,7 +69,7 @@ def main():
     if args.model == "moe":
         return bench_moe(args)
 
-    ctx_len = args.prompt + args.warmup + args.steps + 8
+    ctx_len = args.prompt + args.warmup + args.steps + 8 + (64 if args.model == "qwen3" else 0)
     spec = {"llama8b": synth.llama8b_spec, "tinyllama": synth.tinyllama_spec,
             "qwen3": synth.qwen3_8b_spec}[args.model](context=ctx_len)
     t0 = time.time()
@@ -97,6 +97,26 @@ def main():
     hbm_frac = bytes_per_token * tok_s / (HBM_PEAK_GBS * 1e9)
     log(f"decode: {tok_s:.1f} tok/s ({ms_per_step:.3f} ms/step, gpu events {st.gpu_elapsed_ns / 1e6 / args.steps:.3f}"
         f" ms/step), {bytes_per_token / 1e9:.3f} GB/token -> {100 * hbm_frac:.1f}% of HBM peak")
+
+    verify = None
+    if args.model == "qwen3":
+        # config 4's speculative-verify step: the pending token and 8 drafts (the stream's own next
+        # tokens, so all are accepted) in one batched pass on the matrix cores, against the 9 decode
+        # steps it replaces
+        stream, st2 = sess.generate(np.array([st.next_token], np.uint32), 9)
+        times = []
+        cur = int(st2.next_token)
+        for _ in range(3):
+            drafts, st3 = sess.generate(np.array([cur], np.uint32), 8)
+            cur_v = int(st3.next_token)
+            t1 = time.perf_counter()
+            pred, n = sess.verify(cur_v, [int(t) for t in drafts])
+            times.append(time.perf_counter() - t1)
+            cur = int(pred[n - 1])
+        tv = sorted(times)[1]
+        verify = {"tokens": 9, "drafts": 8, "ms": round(1e3 * tv, 3), "accepted_last": n,
+                  "tok_s_equiv": round(9 / tv, 1), "decode_ms_for_9": round(9 * ms_per_step, 3)}
+        log(f"verify (1 + 8 drafts, MFMA GEMMs): {1e3 * tv:.3f} ms vs {9 * ms_per_step:.3f} ms for 9 decode steps")
 
     kernels = {}
     for name in ("qkv", "attention", "o_proj", "gate_up", "down", "output"):
@@ -170,6 +190,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "verify": verify,
         "tokens_head": [int(t) for t in toks[:8]],
     }
     print(json.dumps(line), flush=True)

@@ -374,6 +374,20 @@ int ziggy_hip_session_step_no_output(ZiggyHipSession *session, uint32_t token, c
 int ziggy_hip_session_generate(ZiggyHipSession *session, const uint32_t *prompt, uint32_t prompt_len,
                                uint32_t steps, uint32_t *out_tokens, ZiggyHipGenerateStats *stats,
                                char *error_message, size_t error_message_len);
+/* Speculative verify in one batched pass (the reference's
+ * verifyDraftTokensBatchGpu / gpu.Session.runBatchSpeculativeDecode,
+ * model/loader.zig:1153-1190, runtime/gpu/session.zig:1525-1650, with the
+ * acceptance of verifyDraftTokensSequential, model/loader.zig:1131-1151):
+ * current_token and the draft_count (<= 15) drafts run at positions
+ * position .. position + draft_count on the matrix cores (GEMMs of M =
+ * draft_count + 1 tokens), writing their K/V rows.  out_predicted[i]
+ * (draft_count + 1 entries) is the greedy token after input i;
+ * *out_count = the predictions emitted: up to and including the first that
+ * differs from its draft, or all of them.  The position advances by
+ * *out_count (later steps overwrite the K/V of rejected drafts). */
+int ziggy_hip_session_verify(ZiggyHipSession *session, uint32_t current_token, const uint32_t *drafts,
+                             uint32_t draft_count, uint32_t *out_predicted, uint32_t *out_count,
+                             char *error_message, size_t error_message_len);
 /* Logits of the most recent step that ran the output head (f32, vocab_size). */
 int ziggy_hip_session_read_logits(ZiggyHipSession *session, float *out, char *error_message,
                                   size_t error_message_len);

@@ -1,0 +1,87 @@
+"""GPU parity of the batched speculative verify (ziggy_hip_session_verify).
+
+The verify pass runs the current token and its drafts through the model in
+one batch on the matrix cores.  Its predictions must be the oracle's greedy
+stream (the reference's verifyDraftTokensSequential is numerically a plain
+greedy stream, model/loader.zig:1131-1151), the emitted count must follow
+the reference's acceptance rule, and decoding after the pass (over the K/V
+rows the pass wrote) must continue the oracle's stream.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import zo
+from zhip import hip, synth
+from zhip.gguf import Q8_0
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+SMALL = {
+    "llama-q4km": dict(arch="llama", down_q6k_layers=[1]),
+    "qwen3-q8": dict(arch="qwen3", qk_norm=True, default_type=Q8_0, attn_v_type=Q8_0, output_type=Q8_0,
+                     embd_type=Q8_0, rope_theta=1000000.0),
+    "llama-hd128-g4": dict(arch="llama", hidden=512, ffn=1024, n_head=4, n_kv=1, head_dim=128, n_layers=3,
+                           context=160),
+}
+
+
+@pytest.mark.parametrize("name", list(SMALL))
+def test_verify_accepts_the_greedy_stream(hip_ctx, name):
+    say(f"verify {name}")
+    spec = synth.small_spec(**SMALL[name])
+    img = synth.build(spec, seed=23)
+    prompt = synth.prompt_tokens(5, 9, spec.vocab)
+    want, _ = zo.Session(zo.Model(img.buf), context=spec.context, kv_f16=True).generate(prompt, 40)
+    want = [int(t) for t in want]
+    s = hip.Session(hip_ctx, img, context=spec.context)
+    _, st = s.generate(prompt, 0)
+    assert st.next_token == want[0]
+    # eight drafts, all right: nine predictions emitted (the last one the bonus)
+    pred, n = s.verify(want[0], want[1:9])
+    assert n == 9 and list(pred) == want[1:10]
+    assert s.position == len(prompt) + 9
+    # decoding continues the stream over the K/V rows the pass wrote
+    got, _ = s.generate(np.array([want[9]], np.uint32), 8)
+    assert [int(t) for t in got] == want[10:18]
+    s.close()
+
+
+def test_verify_rejects_at_the_first_wrong_draft(hip_ctx):
+    spec = synth.small_spec(**SMALL["llama-q4km"])
+    img = synth.build(spec, seed=29)
+    prompt = synth.prompt_tokens(6, 7, spec.vocab)
+    want, _ = zo.Session(zo.Model(img.buf), context=spec.context, kv_f16=True).generate(prompt, 30)
+    want = [int(t) for t in want]
+    s = hip.Session(hip_ctx, img, context=spec.context)
+    s.generate(prompt, 0)
+    drafts = want[1:9]
+    drafts[2] = (drafts[2] + 1) % spec.vocab  # the third draft is wrong
+    pred, n = s.verify(want[0], drafts)
+    assert n == 3 and list(pred[:3]) == want[1:4]
+    assert s.position == len(prompt) + 3
+    # the rejected rows are overwritten: the stream goes on from the emitted token
+    got, _ = s.generate(np.array([want[3]], np.uint32), 10)
+    assert [int(t) for t in got] == want[4:14]
+    # no drafts: one greedy step (want[14] is the pending token after the generated ones)
+    pred, n = s.verify(want[14], [])
+    assert n == 1 and int(pred[0]) == want[15]
+    s.close()
+
+
+def test_verify_rejects_bad_arguments(hip_ctx):
+    spec = synth.small_spec()
+    img = synth.build(spec, seed=1)
+    s = hip.Session(hip_ctx, img, context=spec.context)
+    with pytest.raises(hip.HipError):
+        s.verify(1, list(range(16)))  # 17 tokens > one 16-token pass
+    with pytest.raises(hip.HipError):
+        s.verify(spec.vocab, [1, 2])  # out-of-range id
+    s.close()

@@ -57,6 +57,11 @@ struct ZiggyHipSession {
     uint32_t *prompt = nullptr, *history = nullptr;
     uint32_t prompt_cap = 0, history_cap = 0;
     hipGraphExec_t graph = nullptr;
+    // batched verify (allocated on first use): [kVerifyMax] rows each
+    float *b_hidden = nullptr, *b_normed = nullptr, *b_q = nullptr, *b_k = nullptr, *b_v = nullptr;
+    float *b_attn = nullptr, *b_act = nullptr, *b_up = nullptr;
+    uint32_t *b_tokens = nullptr;
+    unsigned long long *b_argmax = nullptr;
     uint32_t position = 0;
     bool logits_valid = false;
     std::vector<void *> allocs;
@@ -613,6 +618,132 @@ int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint3
         stats->wall_ns = t1 - t0;
         stats->next_token = 0xFFFFFFFFu - (uint32_t)(h->argmax & 0xFFFFFFFFull);
     }
+    return ZIGGY_HIP_OK;
+}
+
+// ---- speculative verify: a batch of tokens in one pass ----
+
+constexpr uint32_t kVerifyMax = 16;  // tokens of one verify pass (one MFMA token tile)
+
+static hipError_t verify_alloc(ZiggyHipSession *s) {
+    if (s->b_hidden) return hipSuccess;
+    const size_t H = s->md.embedding_length, F = s->md.feed_forward_length, Q = (size_t)s->q_size,
+                 KV = (size_t)s->kv_size, M = kVerifyMax;
+    struct {
+        void **p;
+        size_t bytes;
+    } reqs[] = {{(void **)&s->b_hidden, M * H * 4}, {(void **)&s->b_normed, M * H * 4}, {(void **)&s->b_q, M * Q * 4},
+                {(void **)&s->b_k, M * KV * 4},      {(void **)&s->b_v, M * KV * 4},      {(void **)&s->b_attn, M * Q * 4},
+                {(void **)&s->b_act, M * F * 4},     {(void **)&s->b_up, M * F * 4},      {(void **)&s->b_tokens, M * 4},
+                {(void **)&s->b_argmax, M * 8}};
+    for (auto &r : reqs) {
+        hipError_t e = hipMalloc(r.p, r.bytes);
+        if (e != hipSuccess) return e;
+        s->allocs.push_back(*r.p);
+    }
+    return hipSuccess;
+}
+
+// One batched pass of M tokens at positions pos .. pos + M - 1: embedding,
+// per layer per-token RMSNorm + q/k/v GEMMs, attention query by query (each
+// stores its K/V row, in order), o_proj / gate-up / down GEMMs with the
+// residual adds, final norm and the output GEMM fused with a per-token argmax.
+static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t st) {
+    const ZiggyHipModelDesc &md = s->md;
+    const int H = (int)md.embedding_length, F = (int)md.feed_forward_length, Q = s->q_size, KV = s->kv_size;
+    const float eps = md.rms_norm_eps;
+    hipError_t e = launch_embed_rows(s->b_tokens, M, s->embd.p, s->embd.stride, (int)s->embd.rows, s->embd.type, H,
+                                     s->b_hidden, st);
+    auto gemm = [&](const DT &w, const DT *w2, const float *x, int ldx, float *y, int ldy, int out) {
+        if (e != hipSuccess) return;
+        e = launch_gemm(w.type, w.p, w2 ? w2->p : nullptr, w.stride, x, ldx, y, ldy, M, (int)w.rows, (int)w.cols,
+                        out, s->b_argmax, st);
+    };
+    for (int l = 0; l < (int)md.block_count && e == hipSuccess; l++) {
+        const LayerW &L = s->layers[l];
+        e = launch_rms_norm_rows(s->b_hidden, (const float *)L.attn_norm.p, s->b_normed, M, H, eps, st);
+        gemm(L.q, nullptr, s->b_normed, H, s->b_q, Q, OUT_STORE);
+        gemm(L.k, nullptr, s->b_normed, H, s->b_k, KV, OUT_STORE);
+        gemm(L.v, nullptr, s->b_normed, H, s->b_v, KV, OUT_STORE);
+        const size_t layer_base = (size_t)l * md.context_length * s->kv_size;
+        for (int m = 0; m < M && e == hipSuccess; m++) {
+            AttnParams a{};
+            a.q = s->b_q + (size_t)m * Q;
+            a.k_new = s->b_k + (size_t)m * KV;
+            a.v_new = s->b_v + (size_t)m * KV;
+            a.q_bias = L.q_bias.present ? (const float *)L.q_bias.p : nullptr;
+            a.k_bias = L.k_bias.present ? (const float *)L.k_bias.p : nullptr;
+            a.v_bias = L.v_bias.present ? (const float *)L.v_bias.p : nullptr;
+            a.q_norm = L.q_norm.present ? (const float *)L.q_norm.p : nullptr;
+            a.k_norm = L.k_norm.present ? (const float *)L.k_norm.p : nullptr;
+            a.k_cache = s->kc + layer_base;
+            a.v_cache = s->vc + layer_base;
+            a.out = s->b_attn + (size_t)m * Q;
+            a.part_o = s->part_o;
+            a.part_ml = s->part_ml;
+            a.counters = s->counters;
+            a.head_count = (int)md.head_count;
+            a.head_count_kv = (int)md.head_count_kv;
+            a.head_dim = (int)md.head_dim;
+            a.kv_dim = s->kv_size;
+            a.position = pos + m;
+            a.window_start = 0;
+            a.scale = 1.0f / sqrtf((float)md.head_dim);
+            a.max_splits = s->max_splits;
+            a.eps = eps;
+            a.rope_base = md.rope_freq_base;
+            a.rope_dim = (int)md.rope_dim;
+            a.rope_style = (int)md.rope_style;
+            a.ctx = (int)md.context_length;
+            e = launch_attention(a, st);
+        }
+        gemm(L.o, nullptr, s->b_attn, Q, s->b_hidden, H, OUT_ADD);
+        if (e == hipSuccess) e = launch_rms_norm_rows(s->b_hidden, (const float *)L.ffn_norm.p, s->b_normed, M, H, eps, st);
+        if (L.gate.type == L.up.type) {
+            gemm(L.gate, &L.up, s->b_normed, H, s->b_act, F, OUT_SWIGLU);
+        } else {
+            gemm(L.gate, nullptr, s->b_normed, H, s->b_act, F, OUT_STORE);
+            gemm(L.up, nullptr, s->b_normed, H, s->b_up, F, OUT_STORE);
+            if (e == hipSuccess) e = launch_silu_mul(s->b_act, s->b_up, M * F, st);
+        }
+        gemm(L.down, nullptr, s->b_act, F, s->b_hidden, H, OUT_ADD);
+    }
+    if (e == hipSuccess) e = launch_rms_norm_rows(s->b_hidden, (const float *)s->out_norm.p, s->b_normed, M, H, eps, st);
+    if (e == hipSuccess) e = launch_fill_u64(s->b_argmax, 0ull, M, st);
+    gemm(s->out, nullptr, s->b_normed, H, nullptr, 0, OUT_ARGMAX);
+    return e;
+}
+
+int ziggy_hip_session_verify(ZiggyHipSession *s, uint32_t current_token, const uint32_t *drafts, uint32_t draft_count,
+                             uint32_t *out_predicted, uint32_t *out_count, char *err, size_t err_len) {
+    if (!s || !out_predicted || !out_count || (draft_count && !drafts))
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "null argument");
+    const uint32_t M = draft_count + 1;
+    if (M > kVerifyMax) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "at most 15 draft tokens");
+    if (s->position + M > s->md.context_length) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "context overflow");
+    uint32_t toks[kVerifyMax];
+    toks[0] = current_token;
+    for (uint32_t i = 0; i < draft_count; i++) toks[i + 1] = drafts[i];
+    for (uint32_t i = 0; i < M; i++)
+        if (toks[i] >= s->embd.rows) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "token id out of range");
+    hipStream_t st = s->ctx->stream;
+    ZH_TRY(verify_alloc(s), "verify buffers");
+    ZH_TRY(hipMemcpyAsync(s->b_tokens, toks, M * 4, hipMemcpyHostToDevice, st), "verify tokens");
+    ZH_TRY(verify_enqueue(s, (int)M, (int)s->position, st), "verify");
+    unsigned long long keys[kVerifyMax];
+    ZH_TRY(hipMemcpyAsync(keys, s->b_argmax, M * 8, hipMemcpyDeviceToHost, st), "verify readback");
+    ZH_TRY(hipStreamSynchronize(st), "verify");
+    // verifyDraftTokensSequential (model/loader.zig:1131-1151): emit predictions until one
+    // differs from its draft; all drafts accepted adds the bonus prediction
+    for (uint32_t i = 0; i < M; i++) out_predicted[i] = 0xFFFFFFFFu - (uint32_t)(keys[i] & 0xFFFFFFFFull);
+    uint32_t n = 0;
+    for (uint32_t i = 0; i < M; i++) {
+        n = i + 1;
+        if (i < draft_count && out_predicted[i] != drafts[i]) break;
+    }
+    *out_count = n;
+    s->position += n;
+    s->logits_valid = false;
     return ZIGGY_HIP_OK;
 }
 

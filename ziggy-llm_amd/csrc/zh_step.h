@@ -22,6 +22,9 @@ struct StepState {
 };
 
 
+hipError_t launch_embed_rows(const uint32_t *tokens, int count, const uint8_t *embd, uint64_t embd_stride,
+                             int embd_rows, int embd_type, int cols, float *hidden, hipStream_t s);
+
 hipError_t launch_step_begin(StepState *st, const uint32_t *prompt, uint32_t *history, const uint8_t *embd,
                              uint64_t embd_stride, int embd_rows, int embd_type, int cols, float *hidden,
                              hipStream_t s);

@@ -63,6 +63,38 @@ __global__ void step_begin_kernel(StepState *st, const uint32_t *prompt, uint32_
     }
 }
 
+// Embedding rows of `count` tokens (the batched verify / prefill input):
+// hidden[m] = dequant(token_embd[tokens[m]]), one workgroup per token;
+// out-of-range ids embed row 0 (the host checks them first).
+__global__ void embed_rows_kernel(const uint32_t *tokens, const uint8_t *embd, uint64_t embd_stride, int embd_rows,
+                                  int embd_type, int cols, float *hidden) {
+    uint32_t t = tokens[blockIdx.x];
+    if (t >= (uint32_t)embd_rows) t = 0;
+    const uint8_t *row = embd + (uint64_t)t * embd_stride;
+    float *out = hidden + (size_t)blockIdx.x * cols;
+    switch (embd_type) {
+    case Q4_K: embed_row<Q4_K>(row, cols, out); break;
+    case Q6_K: embed_row<Q6_K>(row, cols, out); break;
+    case Q8_0: embed_row<Q8_0>(row, cols, out); break;
+    case Q3_K: embed_row<Q3_K>(row, cols, out); break;
+    case IQ4_XS: embed_row<IQ4_XS>(row, cols, out); break;
+    case F16:
+        for (int i = threadIdx.x; i < cols; i += blockDim.x) out[i] = h2f(ld2(row + 2 * i));
+        break;
+    default:
+        for (int i = threadIdx.x; i < cols; i += blockDim.x) out[i] = __uint_as_float(ld4(row + 4 * i));
+        break;
+    }
+}
+
+hipError_t launch_embed_rows(const uint32_t *tokens, int count, const uint8_t *embd, uint64_t embd_stride,
+                             int embd_rows, int embd_type, int cols, float *hidden, hipStream_t s) {
+    if (count < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(count), dim3(256), 0, s, tokens, embd, embd_stride, embd_rows,
+                       embd_type, cols, hidden);
+    return hipGetLastError();
+}
+
 hipError_t launch_step_begin(StepState *st, const uint32_t *prompt, uint32_t *history, const uint8_t *embd,
                              uint64_t embd_stride, int embd_rows, int embd_type, int cols, float *hidden,
                              hipStream_t s) {

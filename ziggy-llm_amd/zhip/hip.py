@@ -143,6 +143,7 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_session_step_no_output": [vp, u32] + E,
         "ziggy_hip_session_generate": [vp, vp, u32, u32, vp, ctypes.POINTER(GenerateStats)] + E,
         "ziggy_hip_session_read_logits": [vp, vp] + E,
+        "ziggy_hip_session_verify": [vp, u32, vp, u32, vp, ctypes.POINTER(u32)] + E,
         "ziggy_hip_session_time_kernel": [vp, u32, u32, ctypes.POINTER(ctypes.c_uint64),
                                           ctypes.POINTER(ctypes.c_uint64)] + E,
         "ziggy_hip_moe_stack_create": [vp, ctypes.POINTER(MoeDesc), ctypes.POINTER(MoeLayerDesc), u32,
@@ -407,6 +408,15 @@ class Session:
         _call("ziggy_hip_session_generate", self.h, prompt.ctypes.data, prompt.size, steps, out.ctypes.data,
               ctypes.byref(st))
         return out[:steps].copy(), st
+
+    def verify(self, current: int, drafts):
+        """(predicted tokens [len(drafts) + 1], emitted count) of one batched verify pass."""
+        drafts = np.ascontiguousarray(drafts, dtype=np.uint32)
+        pred = np.zeros(drafts.size + 1, np.uint32)
+        n = ctypes.c_uint32()
+        _call("ziggy_hip_session_verify", self.h, current, drafts.ctypes.data if drafts.size else None,
+              drafts.size, pred.ctypes.data, ctypes.byref(n))
+        return pred, n.value
 
     def time_kernel(self, name: str, iterations: int):
         """Mean launch duration (ns) and algorithmic bytes per launch of one step kernel."""
