@@ -36,6 +36,7 @@ for _p in (REPO, os.path.join(REPO, "ziggy-llm_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_TFLOPS = 2500.0  # dense bf16 matrix-core peak
 
 
 def log(msg):
@@ -219,6 +220,22 @@ def bench_moe(args):
     frac = bpt * tok_s / (HBM_PEAK_GBS * 1e9)
     log(f"moe stack: {ns / 1e3:.1f} us per token, {tok_s:.1f} tok/s, {bpt / 1e6:.1f} MB/token -> "
         f"{100 * frac:.1f}% of HBM peak")
+    # the 512-token prefill: rows grouped by routed expert per layer, expert GEMMs on the matrix cores
+    ptok = 512
+    xs = np.stack([synth.normal_row(args.seed + 1, t, spec.hidden, 0.0, 1.0) for t in range(ptok)])
+    _, psel, _ = st.prefill(xs)
+    pns = st.time_prefill(ptok, max(1, min(args.steps, 8)))
+    touched = float(np.mean([len(np.unique(psel[:, l, :])) for l in range(spec.n_layers)]))
+    pbytes = spec.weight_bytes_all()
+    pflops = spec.flops_per_token() * ptok
+    prefill = {"tokens": ptok, "ms": round(pns / 1e6, 3), "tok_s": round(ptok * 1e9 / pns, 1),
+               "weight_bytes": pbytes, "experts_touched_per_layer": round(touched, 1),
+               "hbm_fraction": round(pbytes / (pns * 1e-9) / (HBM_PEAK_GBS * 1e9), 4),
+               "tflops": round(pflops / (pns * 1e-9) / 1e12, 2),
+               "mfma_fraction_bf16": round(pflops / (pns * 1e-9) / (MFMA_BF16_TFLOPS * 1e12), 5)}
+    log(f"moe prefill: {ptok} rows in {pns / 1e6:.2f} ms ({prefill['tok_s']} tok/s), "
+        f"{pbytes / 1e9:.2f} GB of weights -> {100 * prefill['hbm_fraction']:.1f}% of HBM peak, "
+        f"{prefill['tflops']} TFLOP/s")
     st.close()
     ctx.close()
     cpu = None
@@ -257,7 +274,7 @@ def bench_moe(args):
         "ms_per_step": round(ns / 1e6, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"{spec.name}, {spec.n_layers} layers, batch 1", "batch": 1, "parallelism": "none"},
-        "hbm_fraction": round(frac, 4), "bytes_per_token": bpt, "cpu_baseline": cpu,
+        "hbm_fraction": round(frac, 4), "bytes_per_token": bpt, "cpu_baseline": cpu, "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
 

@@ -449,6 +449,20 @@ int ziggy_hip_moe_stack_forward(ZiggyHipMoeStack *stack, const float *hidden_in,
  * back between one pair of HIP events (no counterpart in the reference). */
 int ziggy_hip_moe_stack_time(ZiggyHipMoeStack *stack, uint32_t iterations, uint64_t *avg_ns, char *error_message,
                              size_t error_message_len);
+/* Prefill: `tokens` independent hidden rows (f32, [tokens][hidden]) through
+ * every layer, each row exactly as ziggy_hip_moe_stack_forward would take it,
+ * with the routed experts run grouped by expert on the matrix cores.
+ * selected / weights (optional) are [tokens][layer_count][expert_used_count].
+ * The reference prefills token by token (runPrompt, model/loader.zig:1016-1036,
+ * each token through computeMoeFfn :1718-1749); rows are taken in batches of
+ * up to 4096 / expert_used_count (at most 512). */
+int ziggy_hip_moe_stack_prefill(ZiggyHipMoeStack *stack, const float *hidden_in, uint32_t tokens, float *hidden_out,
+                                uint32_t *selected, float *weights, char *error_message, size_t error_message_len);
+/* Mean time of one prefill of the first `tokens` rows of the last prefill's
+ * input (tokens <= one batch), `iterations` passes between one pair of HIP
+ * events (no counterpart in the reference). */
+int ziggy_hip_moe_stack_time_prefill(ZiggyHipMoeStack *stack, uint32_t tokens, uint32_t iterations, uint64_t *avg_ns,
+                                     char *error_message, size_t error_message_len);
 
 /* Library build tag, for logs. */
 const char *ziggy_hip_version(void);

@@ -103,3 +103,71 @@ def test_moe_stack_rejects_bad_shapes(hip_ctx):
     d.expert_used_count = 9
     with pytest.raises(hip.HipError):
         hip.MoeStack(hip_ctx, d, layers)
+
+
+def check_prefill(spec, layers, xs, got, sel, w):
+    """Each prefill row against the oracle's token-by-token path (the reference
+    prefills one token at a time, model/loader.zig:1016-1036)."""
+    for t in range(xs.shape[0]):
+        want, want_sel, want_w = oracle_stack(spec, layers, xs[t])
+        assert np.array_equal(sel[t], want_sel), (t, sel[t], want_sel)
+        # weights within 1e-5, relative above magnitude 1 (raw logits x scale reach ~8, where the
+        # GEMM path's 1e-6-relative hidden-state difference from the previous layer shows)
+        assert np.max(np.abs(w[t] - want_w) / np.maximum(1.0, np.abs(want_w))) < 1e-5, t
+        assert rel_l2(got[t], want) < 1e-4, (t, rel_l2(got[t], want))
+
+
+@pytest.mark.parametrize("name", ["small", "small-q8-router-rawlogits", "small-no-shared"])
+def test_moe_prefill_matches_oracle(hip_ctx, name):
+    spec = CASES[name]()
+    tokens = 37  # ragged: expert tiles of 1 .. 16 rows
+    say(f"moe prefill {name}: {tokens} rows")
+    layers = synth.build_moe_stack(spec, seed=11)
+    xs = np.stack([synth.normal_row(5, t, spec.hidden, 0.0, 1.0) for t in range(tokens)])
+    st = hip.MoeStack(hip_ctx, synth.moe_desc(spec), layers)
+    got, sel, w = st.prefill(xs)
+    # row 0 of the batch also matches the single-token decode forward's routing
+    one, one_sel, _ = st.forward(xs[0])
+    st.close()
+    check_prefill(spec, layers, xs, got, sel, w)
+    assert np.array_equal(one_sel, sel[0]) and rel_l2(got[0], one) < 1e-4
+
+
+def test_moe_prefill_config5_shape(hip_ctx):
+    # config 5 layer shape, two layers of the forty, 48 rows (about 1.5 rows per expert)
+    spec = synth.moe_config5_spec(2)
+    tokens = 48
+    say(f"moe prefill config-5 shape: {tokens} rows")
+    layers = synth.build_moe_stack(spec, seed=3)
+    xs = np.stack([synth.normal_row(9, t, spec.hidden, 0.0, 1.0) for t in range(tokens)])
+    st = hip.MoeStack(hip_ctx, synth.moe_desc(spec), layers)
+    got, sel, w = st.prefill(xs)
+    got2, sel2, _ = st.prefill(xs)
+    ns = st.time_prefill(tokens, 2)
+    st.close()
+    check_prefill(spec, layers, xs, got, sel, w)
+    assert np.array_equal(got, got2) and np.array_equal(sel, sel2)
+    assert ns > 0
+
+
+def test_moe_prefill_batches_past_one_pass(hip_ctx):
+    # top-4 of 16: 512 rows per pass; 600 rows take two passes, the second ragged
+    spec = synth.small_moe_spec(2)
+    tokens = 600
+    say(f"moe prefill two passes: {tokens} rows")
+    layers = synth.build_moe_stack(spec, seed=17)
+    xs = np.stack([synth.normal_row(3, t, spec.hidden, 0.0, 1.0) for t in range(tokens)])
+    st = hip.MoeStack(hip_ctx, synth.moe_desc(spec), layers)
+    got, sel, w = st.prefill(xs)
+    with pytest.raises(hip.HipError):
+        st.time_prefill(513, 1)  # more rows than one pass holds
+    st.close()
+    check_prefill(spec, layers, xs, got, sel, w)
+
+
+def test_moe_time_prefill_needs_a_prefill_first(hip_ctx):
+    spec = synth.small_moe_spec(1)
+    st = hip.MoeStack(hip_ctx, synth.moe_desc(spec), synth.build_moe_stack(spec, seed=1))
+    with pytest.raises(hip.HipError):
+        st.time_prefill(8, 1)
+    st.close()

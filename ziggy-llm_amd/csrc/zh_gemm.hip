@@ -71,6 +71,11 @@ struct GemmParams {
     float *y;             // [M][ldy]
     int M, N, K, ldx, ldy;
     unsigned long long *argmax;  // ARGMAX: [M] packed (ordered value << 32 | ~row)
+    // grouped (experts): token tile t of blockIdx.y is group_tiles[t] = {expert, first, count};
+    // its tokens are group_list[first .. first + count), x row = id / x_div, y row = id
+    const int *group_tiles, *group_list, *group_ntiles;
+    int x_div;
+    uint64_t expert_stride;  // bytes between consecutive experts' W
 };
 
 __device__ __forceinline__ uint32_t ordered_bits_g(float v) {
@@ -78,15 +83,32 @@ __device__ __forceinline__ uint32_t ordered_bits_g(float v) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-template <int F, int OUT>
+// PRECISE: f32 operands on v_mfma_f32_16x16x4_f32 (products as exact as the
+// matvec path's fmaf), four instructions per 16-value step: instruction i
+// takes value 4 (l / 16) + i of each lane, so the four together cover the
+// same 16 reduction indices as the bf16 instructions.  Used where a result
+// feeds a discrete choice (the MoE router's top-k).
+template <int F, int OUT, bool GROUPED, bool PRECISE = false>
 __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
     constexpr bool kPair = OUT == OUT_SWIGLU;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int m0 = blockIdx.y * 16;
     const int li = lane & 15, lq = lane >> 4;
-    const int m = min(m0 + li, p.M - 1);  // this lane's X token (clamped; dropped at the store)
-    const float *xrow = p.x + (size_t)m * p.ldx;
+    int m0 = blockIdx.y * 16, M = p.M;
+    const int *ids = nullptr;
+    if (GROUPED) {
+        // one expert's token tile: up to 16 of its routed (token, slot) ids
+        if ((int)blockIdx.y >= *p.group_ntiles) return;
+        const int *gt = p.group_tiles + 3 * blockIdx.y;
+        p.w += (uint64_t)gt[0] * p.expert_stride;
+        if (kPair) p.w2 += (uint64_t)gt[0] * p.expert_stride;
+        ids = p.group_list + gt[1];
+        m0 = 0;
+        M = gt[2];
+    }
+    const int m = min(m0 + li, M - 1);  // this lane's X token (clamped; dropped at the store)
+    const float *xrow = p.x + (size_t)(GROUPED ? ids[m] / p.x_div : m) * p.ldx;
     const int j = m0 + li;                // token of this lane's results
+    const int jrow = GROUPED ? (j < M ? ids[j] : 0) : j;  // its y row
     __shared__ float part[4][kPair ? 2 : 1][64][4];
     float best = -INFINITY;
     int best_n = 0x7fffffff;
@@ -103,6 +125,11 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
             weights4<F>(wrow, k, wv);
             const float4 xx = *reinterpret_cast<const float4 *>(xrow + k);
             xv[0] = xx.x, xv[1] = xx.y, xv[2] = xx.z, xv[3] = xx.w;
+            if constexpr (PRECISE && !kPair) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[i], xv[i], acc, 0, 0, 0);
+                continue;
+            }
             bf16x4 ah, al, bh, bl;
             split4(wv, ah, al);
             split4(xv, bh, bl);
@@ -129,8 +156,8 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
             for (int r = 0; r < 4; r++) {
                 const float v = (part[0][0][lane][r] + part[1][0][lane][r]) + (part[2][0][lane][r] + part[3][0][lane][r]);
                 const int nn = n0 + 4 * lq + r;  // row of result r
-                if (j >= p.M || nn >= p.N) continue;
-                float *dst = p.y ? p.y + (size_t)j * p.ldy + nn : nullptr;
+                if (j >= M || nn >= p.N) continue;
+                float *dst = p.y ? p.y + (size_t)jrow * p.ldy + nn : nullptr;
                 if (OUT == OUT_STORE) {
                     *dst = v;
                 } else if (OUT == OUT_ADD) {
@@ -161,7 +188,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
         key = o > key ? o : key;
         o = __shfl_xor(key, 32, 64);
         key = o > key ? o : key;
-        if (lq == 0 && j < p.M && key) atomicMax(p.argmax + j, key);
+        if (lq == 0 && j < M && key) atomicMax(p.argmax + jrow, key);
     }
 }
 
@@ -169,18 +196,43 @@ typedef void (*GemmKernel)(GemmParams);
 
 template <int F> static GemmKernel pick_gemm(int out) {
     switch (out) {
-    case OUT_STORE: return gemm_kernel<F, OUT_STORE>;
-    case OUT_ADD: return gemm_kernel<F, OUT_ADD>;
-    case OUT_SWIGLU: return gemm_kernel<F, OUT_SWIGLU>;
-    case OUT_ARGMAX: return gemm_kernel<F, OUT_ARGMAX>;
+    case OUT_STORE: return gemm_kernel<F, OUT_STORE, false>;
+    case OUT_ADD: return gemm_kernel<F, OUT_ADD, false>;
+    case OUT_SWIGLU: return gemm_kernel<F, OUT_SWIGLU, false>;
+    case OUT_ARGMAX: return gemm_kernel<F, OUT_ARGMAX, false>;
+    default: return nullptr;
+    }
+}
+template <int F> static GemmKernel pick_grouped(int out) {
+    switch (out) {
+    case OUT_STORE: return gemm_kernel<F, OUT_STORE, true>;
+    case OUT_SWIGLU: return gemm_kernel<F, OUT_SWIGLU, true>;
     default: return nullptr;
     }
 }
 
+template <int F> static GemmKernel pick_precise(int out) {
+    return out == OUT_STORE ? gemm_kernel<F, OUT_STORE, false, true> : nullptr;
+}
+
 hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
-                       float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s) {
+                       float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
+                       bool precise) {
     if (M < 1 || N < 1 || K < 16 || K % 16 || ldx % 4) return hipErrorInvalidValue;
     GemmKernel k = nullptr;
+    if (precise) {
+        switch (fmt) {
+        case Q4_K: k = pick_precise<Q4_K>(out); break;
+        case Q6_K: k = pick_precise<Q6_K>(out); break;
+        case Q8_0: k = pick_precise<Q8_0>(out); break;
+        case Q3_K: k = pick_precise<Q3_K>(out); break;
+        case IQ4_XS: k = pick_precise<IQ4_XS>(out); break;
+        case F16: k = pick_precise<F16>(out); break;
+        case F32: k = pick_precise<F32>(out); break;
+        default: break;
+        }
+        fmt = -1;  // chosen
+    }
     switch (fmt) {
     case Q4_K: k = pick_gemm<Q4_K>(out); break;
     case Q6_K: k = pick_gemm<Q6_K>(out); break;
@@ -192,10 +244,98 @@ hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t st
     default: break;
     }
     if (!k) return hipErrorInvalidValue;
-    GemmParams p{w, w2, stride, x, y, M, N, K, ldx, ldy, argmax};
+    GemmParams p{w, w2, stride, x, y, M, N, K, ldx, ldy, argmax, nullptr, nullptr, nullptr, 1, 0};
     // at most 1024 row tiles in flight per token tile; larger N loops (grid-stride)
     const int tiles = (N + 15) / 16;
     hipLaunchKernelGGL(k, dim3(tiles < 1024 ? tiles : 1024, (M + 15) / 16), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, uint64_t expert_stride,
+                               const float *x, int ldx, int x_div, float *y, int ldy, int N, int K, int out,
+                               const int *tiles, const int *list, const int *ntiles, int max_tiles, hipStream_t s) {
+    if (N < 1 || K < 16 || K % 16 || ldx % 4 || max_tiles < 1 || x_div < 1) return hipErrorInvalidValue;
+    GemmKernel k = nullptr;
+    switch (fmt) {
+    case Q4_K: k = pick_grouped<Q4_K>(out); break;
+    case Q6_K: k = pick_grouped<Q6_K>(out); break;
+    case Q8_0: k = pick_grouped<Q8_0>(out); break;
+    case Q3_K: k = pick_grouped<Q3_K>(out); break;
+    case IQ4_XS: k = pick_grouped<IQ4_XS>(out); break;
+    default: break;
+    }
+    if (!k) return hipErrorInvalidValue;
+    GemmParams p{w, w2, stride, x, y, 16, N, K, ldx, ldy, nullptr, tiles, list, ntiles, x_div, expert_stride};
+    const int rt = (N + 15) / 16;
+    hipLaunchKernelGGL(k, dim3(rt < 1024 ? rt : 1024, max_tiles), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+// Groups the routed (token, slot) assignments of M tokens by expert.  Route
+// row t (route_stride words) holds the k {id, weight} entries of token t;
+// assignment a = t * k + s.  Writes list (the assignments grouped by expert;
+// within an expert in arrival order, which does not change any result: each
+// token's output column depends only on its own operands), tiles
+// {expert, first, count} of at most 16 assignments in expert order, and
+// their number.  One workgroup of 1024: one expert per thread for the
+// counts' scan, up to four assignments per thread.
+constexpr int kGroupMaxAssign = 4096;
+
+__global__ void __launch_bounds__(1024) moe_group_kernel(const uint32_t *__restrict__ route, int route_stride, int M,
+                                                         int k, int E, int *__restrict__ list, int *__restrict__ tiles,
+                                                         int *__restrict__ ntiles) {
+    __shared__ int cnt[1024];
+    __shared__ int wsum[2][16];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int n = M * k;
+    cnt[t] = 0;
+    __syncthreads();
+    int pos[4], ex[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int a = t + 1024 * i;
+        ex[i] = -1;
+        pos[i] = 0;
+        if (a < n) {
+            const uint32_t e = route[(size_t)(a / k) * route_stride + 2 * (a % k)];
+            if (e < (uint32_t)E) {
+                ex[i] = (int)e;
+                pos[i] = atomicAdd(&cnt[e], 1);
+            }
+        }
+    }
+    __syncthreads();
+    // inclusive scans of the counts and of the tiles per expert
+    const int c = t < E ? cnt[t] : 0, tc = (c + 15) >> 4;
+    int sc = c, st = tc;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int vc = __shfl_up(sc, o, 64), vt = __shfl_up(st, o, 64);
+        if (lane >= o) sc += vc, st += vt;
+    }
+    if (lane == 63) wsum[0][wave] = sc, wsum[1][wave] = st;
+    __syncthreads();
+    for (int w = 0; w < wave; w++) sc += wsum[0][w], st += wsum[1][w];
+    const int off = sc - c, toff = st - tc;
+    if (t == 1023) *ntiles = st;
+    __syncthreads();  // every count read before the offsets replace them
+    cnt[t] = off;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (ex[i] >= 0) list[cnt[ex[i]] + pos[i]] = t + 1024 * i;
+    for (int f = 0; f < tc; f++) {
+        int *d = tiles + 3 * (toff + f);
+        d[0] = t;
+        d[1] = off + 16 * f;
+        d[2] = min(16, c - 16 * f);
+    }
+}
+
+hipError_t launch_moe_group(const uint32_t *route, int route_stride, int M, int k, int E, int *list, int *tiles,
+                            int *ntiles, hipStream_t s) {
+    if (E < 1 || E > 1024 || M < 1 || k < 1 || M * k > kGroupMaxAssign) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(1024), 0, s, route, route_stride, M, k, E, list, tiles, ntiles);
     return hipGetLastError();
 }
 

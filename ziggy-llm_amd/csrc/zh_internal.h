@@ -134,15 +134,26 @@ hipError_t launch_fill_u64(unsigned long long *p, unsigned long long v, int n, h
 // MFMA GEMM for M >= 8 tokens (zh_gemm.hip): Y[m][n] (=, +=) sum_k W[n][k] X[m][k]
 // (OUT_STORE / OUT_ADD / OUT_SWIGLU with w2 / OUT_ARGMAX into argmax[M]).
 hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
-                       float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s);
+                       float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
+                       bool precise = false);
 hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps,
                                 hipStream_t s);
+// Grouped by expert (MoE prefill): token tiles from launch_moe_group; W of expert e
+// starts expert_stride bytes after W of expert e - 1; x row = id / x_div, y row = id.
+hipError_t launch_gemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, uint64_t expert_stride,
+                               const float *x, int ldx, int x_div, float *y, int ldy, int N, int K, int out,
+                               const int *tiles, const int *list, const int *ntiles, int max_tiles, hipStream_t s);
+hipError_t launch_moe_group(const uint32_t *route, int route_stride, int M, int k, int E, int *list, int *tiles,
+                            int *ntiles, hipStream_t s);
 
 // MoE routing and combine (zh_moe.hip)
+// `tokens` rows: logits row t at logits + t * logits_stride, route row t at route + t * (2k + 2)
 hipError_t launch_moe_route(const float *logits, int E, int k, int gating, int weights_norm, float weights_scale,
-                            int has_shared_gate, uint32_t *route, hipStream_t s);
+                            int has_shared_gate, uint32_t *route, hipStream_t s, int tokens = 1,
+                            int logits_stride = 0);
+// hidden[t] += combine of tmp rows t * k .. t * k + k - 1 (and shared row sh_tmp[t]) for `tokens` rows
 hipError_t launch_moe_combine(float *hidden, const float *tmp, const uint32_t *route, int H, int k, int has_shared,
-                              hipStream_t s);
+                              hipStream_t s, int tokens = 1, const float *sh_tmp = nullptr);
 
 // attention (zh_attn.hip)
 struct AttnParams {

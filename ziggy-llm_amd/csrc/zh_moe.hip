@@ -38,7 +38,10 @@ __device__ __forceinline__ uint32_t ordered_bits_moe(float v) {
 // route: [2k] {u32 id, f32 weight} entries, then the shared expert's scale.
 __global__ void __launch_bounds__(256) moe_route_kernel(const float *__restrict__ logits, int E, int k, int gating,
                                                         int weights_norm, float weights_scale, int has_shared_gate,
-                                                        uint32_t *__restrict__ route) {
+                                                        uint32_t *__restrict__ route, int logits_stride) {
+    // one workgroup per token
+    logits += (size_t)blockIdx.x * logits_stride;
+    route += (size_t)blockIdx.x * (2 * k + 2);
     __shared__ float pr[kMoeMaxExperts];
     __shared__ float red[4];
     __shared__ unsigned long long keys[4];
@@ -131,33 +134,41 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const float *__restrict_
 }
 
 __global__ void moe_combine_kernel(float *__restrict__ hidden, const float *__restrict__ tmp,
-                                   const uint32_t *__restrict__ route, int H, int k, int has_shared) {
+                                   const uint32_t *__restrict__ route, int H, int k, int has_shared,
+                                   const float *__restrict__ sh_tmp) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= H) return;
+    // token blockIdx.y: its k routed rows, its route row, its hidden row
+    const int t = blockIdx.y;
+    hidden += (size_t)t * H;
+    route += (size_t)t * (2 * k + 2);
+    tmp += (size_t)t * k * H;
+    const float *sh = sh_tmp ? sh_tmp + (size_t)t * H : tmp + (size_t)k * H;
     float out = 0.f;
     for (int s = 0; s < k; s++) {
         const float w = __uint_as_float(route[2 * s + 1]), d = tmp[(size_t)s * H + r];
         out = w == 1.0f ? out + d : fmaf(d, w, out);
     }
     if (has_shared) {
-        const float g = __uint_as_float(route[2 * k]), d = tmp[(size_t)k * H + r];
+        const float g = __uint_as_float(route[2 * k]), d = sh[r];
         out = g == 1.0f ? out + d : fmaf(d, g, out);
     }
     hidden[r] = hidden[r] + out;
 }
 
 hipError_t launch_moe_route(const float *logits, int E, int k, int gating, int weights_norm, float weights_scale,
-                            int has_shared_gate, uint32_t *route, hipStream_t s) {
-    if (E < 1 || E > kMoeMaxExperts || k < 1 || k > kMoeMaxK || k > E) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(256), 0, s, logits, E, k, gating, weights_norm, weights_scale,
-                       has_shared_gate, route);
+                            int has_shared_gate, uint32_t *route, hipStream_t s, int tokens, int logits_stride) {
+    if (E < 1 || E > kMoeMaxExperts || k < 1 || k > kMoeMaxK || k > E || tokens < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_route_kernel, dim3(tokens), dim3(256), 0, s, logits, E, k, gating, weights_norm,
+                       weights_scale, has_shared_gate, route, logits_stride);
     return hipGetLastError();
 }
 
 hipError_t launch_moe_combine(float *hidden, const float *tmp, const uint32_t *route, int H, int k, int has_shared,
-                              hipStream_t s) {
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((H + 255) / 256), dim3(256), 0, s, hidden, tmp, route, H, k,
-                       has_shared);
+                              hipStream_t s, int tokens, const float *sh_tmp) {
+    if (tokens < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((H + 255) / 256, tokens), dim3(256), 0, s, hidden, tmp, route, H, k,
+                       has_shared, sh_tmp);
     return hipGetLastError();
 }
 

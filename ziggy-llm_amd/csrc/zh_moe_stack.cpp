@@ -28,6 +28,12 @@ struct ZiggyHipMoeStack {
     bool shared = false, shared_gate = false;
     hipGraphExec_t graph = nullptr;
     std::vector<void *> allocs;
+    // prefill (token batches of up to pre_max rows), allocated at the first call
+    int pre_max = 0;
+    float *p_input = nullptr, *p_hidden = nullptr, *p_normed = nullptr, *p_logits = nullptr, *p_act = nullptr,
+          *p_act_sh = nullptr, *p_tmp = nullptr, *p_sh = nullptr;
+    uint32_t *p_route = nullptr;  // [layers][pre_max][2k + 2]
+    int *p_list = nullptr, *p_tiles = nullptr, *p_ntiles = nullptr;
 };
 
 namespace {
@@ -142,6 +148,96 @@ hipError_t enqueue_layer(ZiggyHipMoeStack *s, int l, hipStream_t st) {
         }
     }
     return launch_moe_combine(s->hidden, s->tmp, route, H, K, s->shared ? 1 : 0, st);
+}
+
+// One layer over M token rows (prefill): the rows are independent, so each
+// goes through the same operations as the decode path; the routed experts
+// run grouped (launch_moe_group), one expert's token tile per GEMM workgroup,
+// so every routed expert's weights stream once per tile.
+//   norm     per-row RMSNorm into p_normed
+//   router   f32-exact MFMA GEMM (the top-k must see the matvec's logits),
+//            plus the shared expert's gate row into column E
+//   route    per row, as in decode; group: assignments by expert
+//   gate/up  grouped SWIGLU GEMM -> p_act[t * k + s]; shared -> p_act_sh[t]
+//   down     grouped GEMM -> p_tmp[t * k + s]; shared -> p_sh[t]
+//   combine  per row, slot order as in decode
+hipError_t enqueue_prefill_layer(ZiggyHipMoeStack *s, int l, int M, hipStream_t st) {
+    const MoeLayerW &L = s->layers[l];
+    const ZiggyHipMoeDesc &d = s->d;
+    const int H = (int)d.hidden, E = (int)d.expert_count, K = (int)d.expert_used_count, FF = (int)d.expert_ff_length,
+              SF = (int)d.shared_ff_length;
+    uint32_t *route = s->p_route + (size_t)l * s->pre_max * s->route_stride;
+    hipError_t e = launch_rms_norm_rows(s->p_hidden, (const float *)L.norm.p, s->p_normed, M, H, d.rms_norm_eps, st);
+    if (e == hipSuccess)
+        e = launch_gemm(L.router.type, L.router.p, nullptr, L.router.stride, s->p_normed, H, s->p_logits, E + 1, M, E,
+                        H, OUT_STORE, nullptr, st, true);
+    if (e == hipSuccess && s->shared_gate)
+        e = launch_gemm(L.gate_inp_sh.type, L.gate_inp_sh.p, nullptr, L.gate_inp_sh.stride, s->p_normed, H,
+                        s->p_logits + E, E + 1, M, 1, H, OUT_STORE, nullptr, st, true);
+    if (e == hipSuccess)
+        e = launch_moe_route(s->p_logits, E, K, (int)d.gating_func, (int)d.weights_norm, d.weights_scale,
+                             s->shared_gate ? 1 : 0, route, st, M, E + 1);
+    if (e == hipSuccess) e = launch_moe_group(route, s->route_stride, M, K, E, s->p_list, s->p_tiles, s->p_ntiles, st);
+    // tiles <= assignments / 16 + one partial tile per expert touched
+    const int max_tiles = M * K / 16 + (E < M * K ? E : M * K);
+    if (e == hipSuccess)
+        e = launch_gemm_grouped(L.gate.type, L.gate.p, L.up.p, L.gate.stride, (uint64_t)FF * L.gate.stride,
+                                s->p_normed, H, K, s->p_act, FF, FF, H, OUT_SWIGLU, s->p_tiles, s->p_list,
+                                s->p_ntiles, max_tiles, st);
+    if (e == hipSuccess && s->shared)
+        e = launch_gemm(L.gate_sh.type, L.gate_sh.p, L.up_sh.p, L.gate_sh.stride, s->p_normed, H, s->p_act_sh, SF, M,
+                        SF, H, OUT_SWIGLU, nullptr, st);
+    if (e == hipSuccess)
+        e = launch_gemm_grouped(L.down.type, L.down.p, nullptr, L.down.stride, (uint64_t)H * L.down.stride, s->p_act,
+                                FF, 1, s->p_tmp, H, H, FF, OUT_STORE, s->p_tiles, s->p_list, s->p_ntiles, max_tiles,
+                                st);
+    if (e == hipSuccess && s->shared)
+        e = launch_gemm(L.down_sh.type, L.down_sh.p, nullptr, L.down_sh.stride, s->p_act_sh, SF, s->p_sh, H, M, H, SF,
+                        OUT_STORE, nullptr, st);
+    if (e == hipSuccess)
+        e = launch_moe_combine(s->p_hidden, s->p_tmp, route, H, K, s->shared ? 1 : 0, st, M,
+                               s->shared ? s->p_sh : nullptr);
+    return e;
+}
+
+hipError_t prefill_alloc(ZiggyHipMoeStack *s) {
+    if (s->pre_max) return hipSuccess;
+    const ZiggyHipMoeDesc &d = s->d;
+    const size_t H = d.hidden, E = d.expert_count, K = d.expert_used_count, FF = d.expert_ff_length,
+                 SF = d.shared_ff_length, NL = s->layers.size();
+    const size_t Mc = 4096 / K < 512 ? 4096 / K : 512;
+    const size_t tiles = Mc * K / 16 + E;
+    struct {
+        void **p;
+        size_t bytes;
+    } reqs[] = {
+        {(void **)&s->p_input, Mc * H * 4},
+        {(void **)&s->p_hidden, Mc * H * 4},
+        {(void **)&s->p_normed, Mc * H * 4},
+        {(void **)&s->p_logits, Mc * (E + 1) * 4},
+        {(void **)&s->p_act, Mc * K * FF * 4},
+        {(void **)&s->p_act_sh, Mc * (SF ? SF : 1) * 4},
+        {(void **)&s->p_tmp, Mc * K * H * 4},
+        {(void **)&s->p_sh, Mc * H * 4},
+        {(void **)&s->p_route, NL * Mc * s->route_stride * 4},
+        {(void **)&s->p_list, Mc * K * 4},
+        {(void **)&s->p_tiles, tiles * 3 * 4},
+        {(void **)&s->p_ntiles, 256},
+    };
+    for (auto &r : reqs) {
+        hipError_t e = hipMalloc(r.p, r.bytes);
+        if (e == hipSuccess) e = hipMemsetAsync(*r.p, 0, r.bytes, s->ctx->stream);
+        if (e != hipSuccess) return e;
+        s->allocs.push_back(*r.p);
+    }
+    s->pre_max = (int)Mc;
+    return hipSuccess;
+}
+
+hipError_t enqueue_prefill(ZiggyHipMoeStack *s, int M, hipStream_t st) {
+    hipError_t e = hipMemcpyAsync(s->p_hidden, s->p_input, (size_t)M * s->d.hidden * 4, hipMemcpyDeviceToDevice, st);
+    for (int l = 0; l < (int)s->layers.size() && e == hipSuccess; l++) e = enqueue_prefill_layer(s, l, M, st);
+    return e;
 }
 
 hipError_t enqueue_stack(ZiggyHipMoeStack *s, hipStream_t st) {
@@ -291,6 +387,66 @@ int ziggy_hip_moe_stack_forward(ZiggyHipMoeStack *s, const float *hidden_in, flo
             if (selected) selected[l * K + k] = e[0];
             if (weights) memcpy(&weights[l * K + k], &e[1], 4);
         }
+    return ZIGGY_HIP_OK;
+}
+
+int ziggy_hip_moe_stack_prefill(ZiggyHipMoeStack *s, const float *hidden_in, uint32_t tokens, float *hidden_out,
+                                uint32_t *selected, float *weights, char *err, size_t err_len) {
+    if (!s || !hidden_in || !hidden_out || tokens == 0)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "invalid arguments");
+    hipSetDevice(s->ctx->device);
+    hipStream_t st = s->ctx->stream;
+    ZH_TRY(prefill_alloc(s), "MoE prefill buffers");
+    const size_t H = s->d.hidden, K = s->d.expert_used_count, NL = s->layers.size(), RS = s->route_stride;
+    std::vector<uint32_t> r;
+    for (uint32_t t0 = 0; t0 < tokens; t0 += (uint32_t)s->pre_max) {
+        const uint32_t M = tokens - t0 < (uint32_t)s->pre_max ? tokens - t0 : (uint32_t)s->pre_max;
+        ZH_TRY(hipMemcpyAsync(s->p_input, hidden_in + (size_t)t0 * H, M * H * 4, hipMemcpyHostToDevice, st),
+               "MoE prefill input");
+        ZH_TRY(enqueue_prefill(s, (int)M, st), "MoE prefill");
+        ZH_TRY(hipMemcpyAsync(hidden_out + (size_t)t0 * H, s->p_hidden, M * H * 4, hipMemcpyDeviceToHost, st),
+               "MoE prefill output");
+        if (selected || weights) {
+            r.resize(NL * s->pre_max * RS);
+            ZH_TRY(hipMemcpyAsync(r.data(), s->p_route, r.size() * 4, hipMemcpyDeviceToHost, st), "MoE routing");
+        }
+        ZH_TRY(hipStreamSynchronize(st), "MoE prefill");
+        if (!r.empty())
+            for (size_t t = 0; t < M; t++)
+                for (size_t l = 0; l < NL; l++)
+                    for (size_t k = 0; k < K; k++) {
+                        const uint32_t *e = &r[(l * s->pre_max + t) * RS + 2 * k];
+                        const size_t o = ((t0 + t) * NL + l) * K + k;
+                        if (selected) selected[o] = e[0];
+                        if (weights) memcpy(&weights[o], &e[1], 4);
+                    }
+    }
+    return ZIGGY_HIP_OK;
+}
+
+int ziggy_hip_moe_stack_time_prefill(ZiggyHipMoeStack *s, uint32_t tokens, uint32_t iterations, uint64_t *avg_ns,
+                                     char *err, size_t err_len) {
+    if (!s || !iterations || !avg_ns || tokens == 0)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "invalid arguments");
+    if (!s->pre_max || tokens > (uint32_t)s->pre_max)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT,
+                    "time_prefill replays the last prefill input: run a prefill of at least `tokens` rows first");
+    hipSetDevice(s->ctx->device);
+    hipStream_t st = s->ctx->stream;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    ZH_TRY(hipEventCreate(&e0), "MoE prefill time");
+    hipError_t e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = enqueue_prefill(s, (int)tokens, st);  // warm-up
+    if (e == hipSuccess) e = hipEventRecord(e0, st);
+    for (uint32_t i = 0; i < iterations && e == hipSuccess; i++) e = enqueue_prefill(s, (int)tokens, st);
+    if (e == hipSuccess) e = hipEventRecord(e1, st);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    if (e != hipSuccess) return hip_fail(e, "MoE prefill time", err, err_len);
+    *avg_ns = (uint64_t)((double)ms * 1e6 / iterations);
     return ZIGGY_HIP_OK;
 }
 

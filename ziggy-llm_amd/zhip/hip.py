@@ -151,6 +151,8 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_moe_stack_destroy": [vp],
         "ziggy_hip_moe_stack_forward": [vp, vp, vp, vp, vp] + E,
         "ziggy_hip_moe_stack_time": [vp, u32, ctypes.POINTER(ctypes.c_uint64)] + E,
+        "ziggy_hip_moe_stack_prefill": [vp, vp, u32, vp, vp, vp] + E,
+        "ziggy_hip_moe_stack_time_prefill": [vp, u32, u32, ctypes.POINTER(ctypes.c_uint64)] + E,
         "ziggy_hip_version": [],
     }
     restypes = {"ziggy_hip_destroy_context": None, "ziggy_hip_destroy_buffer": None,
@@ -520,6 +522,25 @@ class MoeStack:
     def time(self, iterations: int) -> int:
         ns = ctypes.c_uint64()
         _call("ziggy_hip_moe_stack_time", self.h, iterations, ctypes.byref(ns))
+        return ns.value
+
+    def prefill(self, hidden: np.ndarray):
+        """Rows [tokens][hidden] through every layer:
+        (hidden rows after the stack, selected [tokens, layers, k], weights)."""
+        hidden = np.ascontiguousarray(hidden, np.float32)
+        assert hidden.ndim == 2 and hidden.shape[1] == self.desc.hidden
+        tokens = hidden.shape[0]
+        out = np.empty_like(hidden)
+        n, k = len(self._keep), self.desc.expert_used_count
+        sel = np.empty((tokens, n, k), np.uint32)
+        w = np.empty((tokens, n, k), np.float32)
+        _call("ziggy_hip_moe_stack_prefill", self.h, hidden.ctypes.data, tokens, out.ctypes.data, sel.ctypes.data,
+              w.ctypes.data)
+        return out, sel, w
+
+    def time_prefill(self, tokens: int, iterations: int) -> int:
+        ns = ctypes.c_uint64()
+        _call("ziggy_hip_moe_stack_time_prefill", self.h, tokens, iterations, ctypes.byref(ns))
         return ns.value
 
     def close(self):

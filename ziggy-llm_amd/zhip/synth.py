@@ -351,6 +351,21 @@ class MoeSpec:
                (2 * S * rb(self.shared_type, H) + H * rb(self.shared_type, S) if S else 0))
         return per * self.n_layers
 
+    def weight_bytes_all(self) -> int:
+        """Bytes of every layer's weights: what one prefill pass streams when every expert is routed to."""
+        H, F, S, E = self.hidden, self.expert_ff, self.shared_ff, self.n_experts
+        rb = gguf.row_bytes
+        per = (rb(self.router_type, H) * (E + (1 if self.shared_gate else 0)) + 4 * H +
+               E * (2 * F * rb(self.expert_type, H) + H * rb(self.expert_type, F)) +
+               (2 * S * rb(self.shared_type, H) + H * rb(self.shared_type, S) if S else 0))
+        return per * self.n_layers
+
+    def flops_per_token(self) -> int:
+        """Multiply-adds x 2 of one token through the stack (router, k routed + shared SwiGLU experts)."""
+        H, F, S, E, k = self.hidden, self.expert_ff, self.shared_ff, self.n_experts, self.top_k
+        per = 2 * H * (E + (1 if self.shared_gate else 0)) + 2 * 3 * H * (k * F + S)
+        return per * self.n_layers
+
 
 def moe_config5_spec(n_layers: int = 40) -> MoeSpec:
     return MoeSpec("qwen3.5-moe-ffn-stack", n_layers, 2048, 256, 8, 512, 512)
