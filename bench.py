@@ -101,18 +101,19 @@ def main():
 
     verify = None
     if args.model == "qwen3":
-        # config 4's speculative-verify step: the pending token and 8 drafts (the stream's own next
-        # tokens, so all are accepted) in one batched pass on the matrix cores, against the 9 decode
-        # steps it replaces
-        stream, st2 = sess.generate(np.array([st.next_token], np.uint32), 9)
+        # config 4's speculative-verify step: the pending token and 8 drafts in one batched pass on the
+        # matrix cores, against the 9 decode steps it replaces.  The drafts are the stream's own next
+        # tokens (decoded, then the position rewound), so all are accepted.
         times = []
-        cur = int(st2.next_token)
+        cur = int(st.next_token)
         for _ in range(3):
-            drafts, st3 = sess.generate(np.array([cur], np.uint32), 8)
-            cur_v = int(st3.next_token)
+            p0 = sess.position
+            drafts, _ = sess.generate(np.array([cur], np.uint32), 8)
+            sess.rewind(p0)
             t1 = time.perf_counter()
-            pred, n = sess.verify(cur_v, [int(t) for t in drafts])
+            pred, n = sess.verify(cur, [int(t) for t in drafts])
             times.append(time.perf_counter() - t1)
+            assert n == 9 and [int(t) for t in pred[:8]] == [int(t) for t in drafts], "verify diverged from decode"
             cur = int(pred[n - 1])
         tv = sorted(times)[1]
         verify = {"tokens": 9, "drafts": 8, "ms": round(1e3 * tv, 3), "accepted_last": n,

@@ -336,6 +336,13 @@ void ziggy_hip_session_destroy(ZiggyHipSession *session);
 /* Clears the cache and the position (ReusableSession.reset, model/loader.zig:857-868). */
 int ziggy_hip_session_reset(ZiggyHipSession *session, char *error_message, size_t error_message_len);
 uint32_t ziggy_hip_session_position(const ZiggyHipSession *session);
+/* Moves the position back to `position` (<= the current one), keeping the
+ * cache rows before it: the reuse of a cached prompt prefix
+ * (generateLoadedStreamingCached, model/loader.zig:2281-2336, which resumes at
+ * the common-prefix length).  Rows at and past `position` are overwritten by
+ * the steps that follow. */
+int ziggy_hip_session_rewind(ZiggyHipSession *session, uint32_t position, char *error_message,
+                             size_t error_message_len);
 
 /* Per-layer contract of gpu.Session (session.zig:258-261, 339-513, 615-651): the
  * host computes the embedding and drives the layers one call at a time. */

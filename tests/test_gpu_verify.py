@@ -85,3 +85,22 @@ def test_verify_rejects_bad_arguments(hip_ctx):
     with pytest.raises(hip.HipError):
         s.verify(spec.vocab, [1, 2])  # out-of-range id
     s.close()
+
+
+def test_rewind_then_verify_accepts_the_decoded_drafts(hip_ctx):
+    # drafts decoded by the session itself, the position moved back, then verified: all accepted
+    spec = synth.small_spec(**SMALL["qwen3-q8"])
+    img = synth.build(spec, seed=31)
+    prompt = synth.prompt_tokens(8, 11, spec.vocab)
+    s = hip.Session(hip_ctx, img, context=spec.context)
+    _, st = s.generate(prompt, 0)
+    p0 = s.position
+    drafts, st2 = s.generate(np.array([st.next_token], np.uint32), 8)
+    s.rewind(p0)
+    assert s.position == p0
+    pred, n = s.verify(st.next_token, [int(t) for t in drafts])
+    assert n == 9 and [int(t) for t in pred[:8]] == [int(t) for t in drafts]
+    assert int(pred[8]) == st2.next_token
+    with pytest.raises(hip.HipError):
+        s.rewind(s.position + 1)
+    s.close()

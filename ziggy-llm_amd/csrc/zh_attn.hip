@@ -21,6 +21,7 @@
 // (store_kv_half, matvec.metal:246-255) and uses the stored values for that
 // position.  The position may be read from device memory (graph replay).
 #include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "zh_internal.h"
@@ -29,6 +30,7 @@
 namespace zh {
 
 constexpr int kChunk = 64;
+constexpr int kMergeSplits = 32;  // splits the merge folds per round of loads
 constexpr int kMaxGroup = 8;
 constexpr int QV_MAX = 8;  // q values per thread at most (8 heads of 256)
 
@@ -57,11 +59,26 @@ __device__ __forceinline__ void rope_table(int n_rot, float base, int pos, float
 // a wavefront never spans two heads since HD >= 64), then the values go to
 // dst (LDS) and are rotated pairwise with the RoPE table.  `n` elements in all.
 template <int HD, int V>
+__device__ __forceinline__ void norm_rope_w(float (&x)[V], int n, bool has_norm, const float (&nw)[V], float eps,
+                                            int n_rot, int style, const float *cs, const float *sn, float *dst,
+                                            float *red);
+template <int HD, int V>
 __device__ __forceinline__ void norm_rope(float (&x)[V], int n, const float *norm_w, float eps, int n_rot, int style,
                                           const float *cs, const float *sn, float *dst, float *red) {
+    float nw[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) nw[i] = norm_w && threadIdx.x + 256 * i < n ? norm_w[(threadIdx.x + 256 * i) % HD] : 0.f;
+    norm_rope_w<HD, V>(x, n, norm_w != nullptr, nw, eps, n_rot, style, cs, sn, dst, red);
+}
+// The same with the norm weights of this thread's values already loaded
+// (nw[i] = norm_w[(tid + 256 i) % HD]), so that no load waits inside.
+template <int HD, int V>
+__device__ __forceinline__ void norm_rope_w(float (&x)[V], int n, bool has_norm, const float (&nw)[V], float eps,
+                                            int n_rot, int style, const float *cs, const float *sn, float *dst,
+                                            float *red) {
     const int tid = threadIdx.x, wave = tid >> 6;
     constexpr int WPH = HD / 64;  // wavefronts per head
-    if (norm_w) {
+    if (has_norm) {
 #pragma unroll
         for (int i = 0; i < V; i++) {
             const int idx = tid + 256 * i;
@@ -76,7 +93,7 @@ __device__ __forceinline__ void norm_rope(float (&x)[V], int n, const float *nor
             const int w0 = wave / WPH * WPH;
             for (int w = 0; w < WPH; w++) tot += red[4 * i + w0 + w];
             const float scale = 1.0f / sqrtf(tot / (float)HD + eps);
-            if (idx < n) x[i] = (scale * x[i]) * norm_w[idx % HD];
+            if (idx < n) x[i] = (scale * x[i]) * nw[i];
         }
     }
 #pragma unroll
@@ -128,6 +145,121 @@ __device__ __forceinline__ float half_sum32(float v) {
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
     return v + __shfl_xor(v, 16, 64);
+}
+
+// Arrival of a split and, in the last workgroup of a kv head to arrive, the
+// merge of every split (partials stored with agent-scope write-through).
+template <int HD, int KG>
+__device__ __forceinline__ void split_merge(const AttnParams &p, int kvh, int G, int nsplit, int *last_ptr) {
+    const int tid = threadIdx.x;
+    int &last_s = *last_ptr;
+    constexpr int IPTM = (KG * HD / 2 + 255) / 256;
+    __shared__ float fm_merge[kMaxGroup], fl_merge[kMaxGroup], fa_merge[kMaxGroup];
+    float acc_merge[IPTM][2];
+    // Every thread's partial stores (agent scope, write-through)
+    // complete before the workgroup barrier; thread 0 then releases and
+    // counts.  The last arrival of this kv head acquires and merges.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned old = __hip_atomic_fetch_add(&p.counters[kvh], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        last_s = old == (unsigned)(nsplit - 1);
+        if (last_s) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    if (!last_s) return;
+
+    // Merge, one round of loads: every split's (m, l) of every head (one per
+    // thread) and, for each item (pair of dims of one head), every split's
+    // partial, all in flight together; the weights exp2(m_s - M) / L go
+    // through LDS.
+    __shared__ float wt_s[kMaxGroup][kMergeSplits];
+    const unsigned long long *ml = reinterpret_cast<const unsigned long long *>(p.part_ml) +
+                                   (size_t)kvh * p.max_splits * kMaxGroup;
+    const unsigned long long *po = reinterpret_cast<const unsigned long long *>(p.part_o) +
+                                   (size_t)kvh * p.max_splits * kMaxGroup * (HD / 2);
+    constexpr int IPT = IPTM;  // items per thread at most
+    for (int s0 = 0; s0 < nsplit; s0 += kMergeSplits) {
+        const int ns = min(kMergeSplits, nsplit - s0);
+        unsigned long long ov[IPT][kMergeSplits];
+#pragma unroll
+        for (int k = 0; k < IPT; k++) {
+            const int it = min(tid + 256 * k, G * HD / 2 - 1);
+            const int g = it / (HD / 2), d2 = it % (HD / 2);
+#pragma unroll
+            for (int u = 0; u < kMergeSplits; u++) {
+                const size_t e = (size_t)(s0 + min(u, ns - 1)) * kMaxGroup + g;
+                ov[k][u] = __hip_atomic_load(po + e * (HD / 2) + d2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        {
+            // thread (g, u) = (tid / kMergeSplits, tid % kMergeSplits)
+            const int g = tid / kMergeSplits, u = tid % kMergeSplits;
+            float ms = -INFINITY, ls = 0.f;
+            if (g < G && u < ns) {
+                const unsigned long long v = __hip_atomic_load(ml + (size_t)(s0 + u) * kMaxGroup + g, __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT);
+                ms = __uint_as_float((uint32_t)v);
+                ls = __uint_as_float((uint32_t)(v >> 32));
+            }
+            // max and weighted sum over the kMergeSplits lanes of head g (a wavefront holds 64 / kMergeSplits heads)
+            float mx = ms;
+#pragma unroll
+            for (int o = kMergeSplits / 2; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            // fold into the running (M, L) of earlier rounds
+            const float Mp = s0 == 0 ? -INFINITY : fm_merge[g < kMaxGroup ? g : 0];
+            const float M = fmaxf(mx, Mp);
+            const float w = ms == -INFINITY ? 0.f : exp2f(ms - M);
+            float lw = ls * w;
+#pragma unroll
+            for (int o = kMergeSplits / 2; o >= 1; o >>= 1) lw += __shfl_xor(lw, o, 64);
+            __syncthreads();  // earlier round's weights read
+            if (g < G) {
+                wt_s[g][u] = w;
+                if (u == 0) {
+                    const float a = Mp == -INFINITY ? 0.f : exp2f(Mp - M);
+                    fa_merge[g] = a;  // rescale of the earlier rounds' sums
+                    fl_merge[g] = (s0 == 0 ? 0.f : fl_merge[g] * a) + lw;
+                    fm_merge[g] = M;
+                }
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int k = 0; k < IPT; k++) {
+            const int it = tid + 256 * k;
+            if (it >= G * HD / 2) continue;
+            const int g = it / (HD / 2);
+            float O0 = 0.f, O1 = 0.f;
+#pragma unroll
+            for (int u = 0; u < kMergeSplits; u++) {
+                if (u < ns) {
+                    const float w = wt_s[g][u];
+                    O0 = fmaf(__uint_as_float((uint32_t)ov[k][u]), w, O0);
+                    O1 = fmaf(__uint_as_float((uint32_t)(ov[k][u] >> 32)), w, O1);
+                }
+            }
+            if (s0 > 0) {
+                const float a = fa_merge[g];
+                O0 = fmaf(acc_merge[k][0], a, O0);
+                O1 = fmaf(acc_merge[k][1], a, O1);
+            }
+            acc_merge[k][0] = O0;
+            acc_merge[k][1] = O1;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < IPT; k++) {
+        const int it = tid + 256 * k;
+        if (it >= G * HD / 2) continue;
+        const int g = it / (HD / 2), d2 = it % (HD / 2);
+        float *dst = p.out + (size_t)(kvh * G + g) * HD + 2 * d2;
+        dst[0] = acc_merge[k][0] / fl_merge[g];
+        dst[1] = acc_merge[k][1] / fl_merge[g];
+    }
+    if (tid == 0) __hip_atomic_store(&p.counters[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Workgroup (split, kv head) attends over a contiguous range of positions,
@@ -428,57 +560,377 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnParams p) {
                            __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    // Arrival: every thread's partial stores (agent scope, write-through)
-    // complete before the workgroup barrier; thread 0 then releases and
-    // counts.  The last arrival of this kv head acquires and merges.
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned old = __hip_atomic_fetch_add(&p.counters[kvh], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        last_s = old == (unsigned)(nsplit - 1);
-        if (last_s) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    split_merge<HD, GG ? GG : kMaxGroup>(p, kvh, G, nsplit, &last_s);
+}
+
+// ---------------------------------------------------------------------------
+// Matrix-core variant (head_dim 64 and 128): the same grid, splits, fused
+// q/k/v epilogue, partials and last-arriver merge as attn_kernel, with the
+// position loop on v_mfma_f32_16x16x32_f16.
+//
+// A wavefront takes tiles of 32 positions (units u_begin + wave + 4 t).
+//   scores  S[pos][col] = sum_d K[pos][d] Q[d][col]: A = K rows as stored
+//           (binary16, exact), B = the query pieces: column 2g + 0 holds
+//           binary16(q_g * scale * log2 e), column 2g + 1 the binary16 of
+//           the remainder, so S[pos][2g] + S[pos][2g + 1] is the score of
+//           head g to ~2^-22 relative (products of binary16 values are exact
+//           in the f32 accumulator).  Two 16-row tiles per 32 positions,
+//           head_dim / 32 k-steps each.
+//   softmax online per column (base 2), the row pieces summed by one DPP.
+//   values  O[col][dim] += sum_pos P[col][pos] V[pos][dim]: A = the
+//           probabilities split the same way (column 2g + 0: binary16(p),
+//           2g + 1: binary16(p - hi)), laid out exactly as the scores came
+//           out of the first product; B = V rows: each lane reads 16 bytes
+//           (dims 8j .. 8j + 7) of eight rows, and product q (0..7) takes
+//           element q of each, so its output column j stands for dim 8j + q.
+//   A reduction index (k) may be assigned to (lane group, element) in any way
+//   as long as A and B agree; both products use that freedom.
+// The workgroup merges its four wavefronts through LDS (max, rescale, sum of
+// the two pieces of each head) and continues as attn_kernel does.
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// per-component select (a select of whole vector structs becomes a select of
+// their addresses, which keeps the arrays holding them out of registers)
+__device__ __forceinline__ void pick4(bool c, const uint4 &a, uint4 &dst) {
+    dst.x = c ? a.x : dst.x;
+    dst.y = c ? a.y : dst.y;
+    dst.z = c ? a.z : dst.z;
+    dst.w = c ? a.w : dst.w;
+}
+
+__device__ __forceinline__ h8v as_h8(uint4 v) {
+    h8v r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+}
+
+template <int HD, int GG>
+__global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
+    constexpr int KS = HD / 32;  // 32-dim steps of the scores, 32-dim chunks of the values
+    constexpr int TP = 32;       // positions per wavefront tile
+    constexpr int QS = HD + 8;   // padded row of the query pieces (binary16)
+    constexpr int LPR = HD / 8;  // lanes per value row (8 dims each)
+    const int split = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+    const int pos = p.position_dev ? *p.position_dev : p.position;
+    const int n_total = pos + 1 - p.window_start;
+    const int units = (n_total + TP - 1) / TP;
+    const int per = (units + p.max_splits - 1) / p.max_splits;  // tiles per split
+    const int nsplit = (units + per - 1) / per;
+    if (split >= nsplit) return;
+    const int u_begin = split * per, nu = min(per, units - u_begin);
+    const int ntw = nu > wave ? (nu - wave + 3) / 4 : 0;  // this wavefront's tiles
+    const int G = GG ? GG : p.head_count / p.head_count_kv;
+    const bool fused = p.k_new != nullptr;
+    const bool own_pos = fused && u_begin + nu == units;  // this split holds the current position
+
+    __shared__ float q_s[kMaxGroup][HD];
+    __shared__ float kn_s[HD];
+    __shared__ __align__(16) unsigned short kn_h[HD], vn_h[HD];
+    __shared__ float red16[4 * QV_MAX];
+    __shared__ float cs_s[HD / 2], sn_s[HD / 2];
+    __shared__ __align__(16) unsigned short qp_s[16][QS];
+    __shared__ float mlw_s[4][16][2];
+    __shared__ __align__(16) float o_s[4][kMaxGroup][HD];
+    __shared__ float fm_s[kMaxGroup], fl_s[kMaxGroup];
+    __shared__ int last_s;
+
+    const size_t kv_off = (size_t)kvh * HD;
+    constexpr int QV = kMaxGroup * HD / 256;
+    const int nq = G * HD;
+    float qv[QV], kx[1] = {0.f}, vx = 0.f, qnw[QV], knw[1];
+    {
+        // norm weights too (dummy reads of q when absent): see the K/V loads
+        const float *qn = p.q_norm ? p.q_norm : p.q, *kn = p.k_norm ? p.k_norm : p.q;
+#pragma unroll
+        for (int i = 0; i < QV; i++) qnw[i] = qn[(tid + 256 * i) % HD];
+        knw[0] = kn[tid & (HD - 1)];
+    }
+#pragma unroll
+    for (int i = 0; i < QV; i++) {
+        const int idx = tid + 256 * i;
+        qv[i] = 0.f;
+        if (idx < nq) {
+            qv[i] = p.q[(size_t)kvh * nq + idx];
+            if (fused && p.q_bias) qv[i] += p.q_bias[(size_t)kvh * nq + idx];
+        }
+    }
+    {
+        // unconditional for the same reason as the K/V loads below (plain
+        // mode reads q in place of the absent k / v and ignores it)
+        const float *kn = fused ? p.k_new : p.q, *vn = fused ? p.v_new : p.q;
+        kx[0] = kn[kv_off + (tid & (HD - 1))];
+        vx = vn[kv_off + (tid & (HD - 1))];
+        if (own_pos && tid < HD) {
+            if (p.k_bias) kx[0] += p.k_bias[kv_off + tid];
+            if (p.v_bias) vx += p.v_bias[kv_off + tid];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // tile t: positions p0(t) .. p0(t) + 31; K fragments [row tile][k-step]
+    // (row p0 + 16 rt + li, dims 32 ks + 8 lg .. + 7), V fragments [row e]
+    // (rows 4 lg + e and 16 + 4 lg + e - 4, dims 8 li .. 8 li + 7).  Rows
+    // past pos re-read row pos (masked below).
+    auto p0_of = [&](int t) { return p.window_start + (u_begin + wave + 4 * t) * TP; };
+    auto load_k = [&](int t, uint4 (&k)[2][KS]) {
+        const int b = p0_of(t);
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++) {
+            const __half *src = p.k_cache + (size_t)min(b + 16 * rt + li, pos) * p.kv_dim + kv_off + 8 * lg;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) k[rt][ks] = *reinterpret_cast<const uint4 *>(src + 32 * ks);
+        }
+    };
+    auto vrow = [&](int e) { return e < 4 ? 4 * lg + e : 12 + 4 * lg + e; };
+    auto load_v = [&](int t, uint4 (&v)[8]) {
+        const int b = p0_of(t);
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            v[e] = *reinterpret_cast<const uint4 *>(p.v_cache + (size_t)min(b + vrow(e), pos) * p.kv_dim + kv_off +
+                                                    8 * (li % LPR));
+    };
+    // Unconditional (clamped) loads: a load under a branch leaves the
+    // compiler's wait counting unsure of what is in flight, and the first
+    // wait for q would then cover every K/V load as well.
+    // K now, V after the q prologue: the prologue's VALU work runs while K
+    // streams in (a wavefront stalls at issue once its loads fill the queue)
+    uint4 kr[2][2][KS];
+    uint4 vr[2][8];
+    load_k(0, kr[0]);
+    load_k(1, kr[1]);
+
+    if (fused) {
+        const int n_rot = p.rope_dim < HD ? p.rope_dim : HD;
+        rope_table(n_rot, p.rope_base, pos, cs_s, sn_s);
+        norm_rope_w<HD, QV>(qv, nq, p.q_norm != nullptr, qnw, p.eps, n_rot, p.rope_style, cs_s, sn_s, &q_s[0][0],
+                            red16);
+        if (own_pos) {
+            norm_rope_w<HD, 1>(kx, HD, p.k_norm != nullptr, knw, p.eps, n_rot, p.rope_style, cs_s, sn_s, kn_s, red16);
+            if (tid < HD) {
+                const __half kh = __float2half_rn(kn_s[tid]), vh = __float2half_rn(vx);
+                if (pos < p.ctx) {
+                    const size_t idx = (size_t)pos * p.kv_dim + kv_off + tid;
+                    p.k_cache[idx] = kh;
+                    p.v_cache[idx] = vh;
+                }
+                kn_h[tid] = __half_as_ushort(kh);
+                vn_h[tid] = __half_as_ushort(vh);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < QV; i++) {
+            const int idx = tid + 256 * i;
+            if (idx < nq) q_s[idx / HD][idx % HD] = qv[i];
+        }
     }
     __syncthreads();
-    if (!last_s) return;
-
-    // Merge: item (pair of dims of one head) folds every split with an
-    // online log-sum-exp (base 2), sixteen splits' loads in flight.
-    const unsigned long long *ml = reinterpret_cast<const unsigned long long *>(p.part_ml) +
-                                   (size_t)kvh * p.max_splits * kMaxGroup;
-    const unsigned long long *po = reinterpret_cast<const unsigned long long *>(p.part_o) +
-                                   (size_t)kvh * p.max_splits * kMaxGroup * (HD / 2);
-    for (int it = tid; it < G * HD / 2; it += 256) {
-        const int g = it / (HD / 2), d2 = it % (HD / 2);
-        float M = -INFINITY, L = 0.f, O0 = 0.f, O1 = 0.f;
-        for (int s0 = 0; s0 < nsplit; s0 += 16) {
-            unsigned long long mlv[16], ov[16];
+    // query pieces, scaled to base-2 scores
+    const float sl2 = p.scale * 1.44269504088896340736f;
+    for (int it = tid; it < 16 * HD; it += 256) {
+        const int col = it / HD, d = it % HD, g = col >> 1;
+        unsigned short h = 0;
+        if (g < G) {
+            const float v = q_s[g][d] * sl2;
+            const __half hi = __float2half_rn(v);
+            h = (col & 1) ? __half_as_ushort(__float2half_rn(v - __half2float(hi))) : __half_as_ushort(hi);
+        }
+        qp_s[col][d] = h;
+    }
+    __syncthreads();
+    load_v(0, vr[0]);
+    load_v(1, vr[1]);
+    h8v qf[KS];
 #pragma unroll
-            for (int u = 0; u < 16; u++) {
-                const size_t e = (size_t)min(s0 + u, nsplit - 1) * kMaxGroup + g;
-                mlv[u] = __hip_atomic_load(ml + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ov[u] = __hip_atomic_load(po + e * (HD / 2) + d2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int ks = 0; ks < KS; ks++) qf[ks] = as_h8(*reinterpret_cast<const uint4 *>(&qp_s[li][32 * ks + 8 * lg]));
+
+    const bool col_ok = li < 2 * G;
+    float m = -INFINITY, lsum = 0.f;  // for column li
+    f4v o[8];                         // [q]: rows 4 lg + r, dims 8 li + q
+#pragma unroll
+    for (int q = 0; q < 8; q++) o[q] = f4v{0.f, 0.f, 0.f, 0.f};
+
+    for (int t0 = 0; t0 < ntw; t0 += 2) {
+        float sc[2][2][4];
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            const bool have = t0 + tt < ntw;
+            const int b = p0_of(t0 + tt);
+            if (have && own_pos && pos >= b && pos < b + TP) {
+                // this step's k and v replace the rows of pos (loaded before the store)
+#pragma unroll
+                for (int rt = 0; rt < 2; rt++) {
+                    const bool me = b + 16 * rt + li == pos;
+#pragma unroll
+                    for (int ks = 0; ks < KS; ks++) {
+                        const uint4 kn = *reinterpret_cast<const uint4 *>(&kn_h[32 * ks + 8 * lg]);
+                        pick4(me, kn, kr[tt][rt][ks]);
+                    }
+                }
+                const uint4 vn = *reinterpret_cast<const uint4 *>(&vn_h[8 * (li % LPR)]);
+#pragma unroll
+                for (int e = 0; e < 8; e++) pick4(b + vrow(e) == pos, vn, vr[tt][e]);
             }
 #pragma unroll
-            for (int u = 0; u < 16; u++) {
-                if (s0 + u < nsplit) {
-                    const float ms = __uint_as_float((uint32_t)mlv[u]), ls = __uint_as_float((uint32_t)(mlv[u] >> 32));
-                    const float o0 = __uint_as_float((uint32_t)ov[u]), o1 = __uint_as_float((uint32_t)(ov[u] >> 32));
-                    const float Mn = fmaxf(M, ms);  // every split holds a position: ms is finite
-                    const float a = exp2f(M - Mn), b = exp2f(ms - Mn);
-                    L = fmaf(L, a, ls * b);
-                    O0 = fmaf(O0, a, o0 * b);
-                    O1 = fmaf(O1, a, o1 * b);
-                    M = Mn;
+            for (int rt = 0; rt < 2; rt++) {
+                f4v acc = {0.f, 0.f, 0.f, 0.f};
+                if (have) {
+#pragma unroll
+                    for (int ks = 0; ks < KS; ks++)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kr[tt][rt][ks]), qf[ks], acc, 0, 0, 0);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    // rows 4 lg + r of the tile; the two pieces of a head sit in lanes 2g, 2g + 1
+                    float v = acc[r];
+                    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+                    const bool valid = have && col_ok && b + 16 * rt + 4 * lg + r <= pos;
+                    sc[tt][rt][r] = valid ? v : -INFINITY;
                 }
             }
         }
-        float *dst = p.out + (size_t)(kvh * G + g) * HD + 2 * d2;
-        dst[0] = O0 / L;
-        dst[1] = O1 / L;
+        if (t0 + 2 < ntw) {  // the next two tiles into the K slots just consumed
+            load_k(t0 + 2, kr[0]);
+            load_k(t0 + 3, kr[1]);
+        }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) mt = fmaxf(mt, sc[tt][rt][r]);
+        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float mn = fmaxf(m, mt);
+        const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+        m = mn;
+        float ps = 0.f;
+        h8v pf[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float s = sc[tt][e >> 2][e & 3];
+                const float pv = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - mn);
+                ps += pv;
+                const _Float16 hi = (_Float16)pv;
+                pf[tt][e] = (li & 1) ? (_Float16)(pv - (float)hi) : hi;
+            }
+        lsum = lsum * alpha + ps;
+        if (t0 > 0) {
+            // rows 4 lg + r of O are columns 4 lg + r of P: their alpha
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float a = __shfl(alpha, 4 * lg + r, 64);
+#pragma unroll
+                for (int q = 0; q < 8; q++) o[q][r] *= a;
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            if (t0 + tt >= ntw) continue;
+            // product q takes dim 8 j + q of every row: output column j stands for dim 8 j + q
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const uint32_t sel = (q & 1) ? 0x07060302u : 0x05040100u;
+                uint32_t w[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const uint4 &r = vr[tt][e];
+                    w[e] = (q >> 1) == 0 ? r.x : (q >> 1) == 1 ? r.y : (q >> 1) == 2 ? r.z : r.w;
+                }
+                uint4 bv;
+                bv.x = __builtin_amdgcn_perm(w[1], w[0], sel);
+                bv.y = __builtin_amdgcn_perm(w[3], w[2], sel);
+                bv.z = __builtin_amdgcn_perm(w[5], w[4], sel);
+                bv.w = __builtin_amdgcn_perm(w[7], w[6], sel);
+                o[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[tt], as_h8(bv), o[q], 0, 0, 0);
+            }
+        }
+        if (t0 + 2 < ntw) {
+            load_v(t0 + 2, vr[0]);
+            load_v(t0 + 3, vr[1]);
+        }
     }
-    if (tid == 0) __hip_atomic_store(&p.counters[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // ---- merge the four wavefronts ----
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    if (lg == 0) {
+        mlw_s[wave][li][0] = m;
+        mlw_s[wave][li][1] = lsum;
+    }
+    __syncthreads();
+    // rows 4 lg + 2 hh + {0, 1} are the two pieces of head 2 lg + hh (same
+    // max): summed here, scaled to the workgroup max, one row per head
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const int head = 2 * lg + hh, row = 2 * head;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, mlw_s[w][row][0]);
+        const float mw = mlw_s[wave][row][0];
+        const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
+        if (head < G && li < LPR) {
+            float4 a, b;
+            a.x = (o[0][2 * hh] + o[0][2 * hh + 1]) * f;
+            a.y = (o[1][2 * hh] + o[1][2 * hh + 1]) * f;
+            a.z = (o[2][2 * hh] + o[2][2 * hh + 1]) * f;
+            a.w = (o[3][2 * hh] + o[3][2 * hh + 1]) * f;
+            b.x = (o[4][2 * hh] + o[4][2 * hh + 1]) * f;
+            b.y = (o[5][2 * hh] + o[5][2 * hh + 1]) * f;
+            b.z = (o[6][2 * hh] + o[6][2 * hh + 1]) * f;
+            b.w = (o[7][2 * hh] + o[7][2 * hh + 1]) * f;
+            *reinterpret_cast<float4 *>(&o_s[wave][head][8 * li]) = a;
+            *reinterpret_cast<float4 *>(&o_s[wave][head][8 * li + 4]) = b;
+        }
+    }
+    if (tid < G) {
+        const int row = 2 * tid;
+        float M = -INFINITY, L = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, mlw_s[w][row][0]);
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float mw = mlw_s[w][row][0];
+            if (mw != -INFINITY) L += mlw_s[w][row][1] * exp2f(mw - M);
+        }
+        fm_s[tid] = M;
+        fl_s[tid] = L;
+    }
+    __syncthreads();
+    // pairs of dims: one 64-bit write-through store per pair
+    for (int it = tid; it < G * HD / 2; it += 256) {
+        const int g = it / (HD / 2), d = 2 * (it % (HD / 2));
+        const float2 a0 = *reinterpret_cast<const float2 *>(&o_s[0][g][d]);
+        const float2 a1 = *reinterpret_cast<const float2 *>(&o_s[1][g][d]);
+        const float2 a2 = *reinterpret_cast<const float2 *>(&o_s[2][g][d]);
+        const float2 a3 = *reinterpret_cast<const float2 *>(&o_s[3][g][d]);
+        const float x0 = (a0.x + a1.x) + (a2.x + a3.x), x1 = (a0.y + a1.y) + (a2.y + a3.y);
+        if (nsplit == 1) {
+            float *dst = p.out + (size_t)(kvh * G + g) * HD + d;
+            dst[0] = x0 / fl_s[g];
+            dst[1] = x1 / fl_s[g];
+        } else {
+            const size_t e = (((size_t)kvh * p.max_splits + split) * kMaxGroup + g) * HD + d;
+            const unsigned long long v = (unsigned long long)__float_as_uint(x0) |
+                                         ((unsigned long long)__float_as_uint(x1) << 32);
+            __hip_atomic_store(reinterpret_cast<unsigned long long *>(p.part_o + e), v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (nsplit == 1) return;
+    if (tid < G) {
+        const size_t e = ((size_t)kvh * p.max_splits + split) * kMaxGroup + tid;
+        const unsigned long long v = (unsigned long long)__float_as_uint(fm_s[tid]) |
+                                     ((unsigned long long)__float_as_uint(fl_s[tid]) << 32);
+        __hip_atomic_store(reinterpret_cast<unsigned long long *>(p.part_ml) + e, v, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    split_merge<HD, GG ? GG : kMaxGroup>(p, kvh, G, nsplit, &last_s);
 }
 
 size_t attention_scratch_floats(int head_count, int head_dim, int max_splits) {
@@ -495,6 +947,16 @@ static int attention_target_wgs() {
         return v > 0 ? v : 256;
     }();
     return t;
+}
+
+// ZIGGY_HIP_ATTN_KERNEL=valu selects the vector-ALU kernel for every head
+// size (the matrix-core kernel covers head_dim 64 and 128).
+static bool attention_valu() {
+    static const bool v = [] {
+        const char *e = getenv("ZIGGY_HIP_ATTN_KERNEL");
+        return e && strcmp(e, "valu") == 0;
+    }();
+    return v;
 }
 
 int attention_splits(int kv_heads, int max_positions) {
@@ -514,6 +976,18 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
     const int G = p.head_count / p.head_count_kv;
     auto go = [&](auto hd_tag) {
         constexpr int HD = decltype(hd_tag)::value;
+        if constexpr (HD <= 128) {
+            if (!attention_valu()) {
+                switch (G) {
+                case 1: hipLaunchKernelGGL((attn_mfma_kernel<HD, 1>), grid, dim3(256), 0, s, p); break;
+                case 2: hipLaunchKernelGGL((attn_mfma_kernel<HD, 2>), grid, dim3(256), 0, s, p); break;
+                case 4: hipLaunchKernelGGL((attn_mfma_kernel<HD, 4>), grid, dim3(256), 0, s, p); break;
+                case 8: hipLaunchKernelGGL((attn_mfma_kernel<HD, 8>), grid, dim3(256), 0, s, p); break;
+                default: hipLaunchKernelGGL((attn_mfma_kernel<HD, 0>), grid, dim3(256), 0, s, p); break;
+                }
+                return;
+            }
+        }
         switch (G) {
         case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(256), 0, s, p); break;
         case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(256), 0, s, p); break;

@@ -430,6 +430,17 @@ int ziggy_hip_session_reset(ZiggyHipSession *s, char *err, size_t err_len) {
 
 uint32_t ziggy_hip_session_position(const ZiggyHipSession *s) { return s ? s->position : 0; }
 
+int ziggy_hip_session_rewind(ZiggyHipSession *s, uint32_t position, char *err, size_t err_len) {
+    if (!s) return ZIGGY_HIP_INVALID_ARGUMENT;
+    if (position > s->position) {
+        set_err(err, err_len, "rewind to %u: past the current position %u", position, s->position);
+        return ZIGGY_HIP_INVALID_ARGUMENT;
+    }
+    s->position = position;
+    s->logits_valid = false;
+    return ZIGGY_HIP_OK;
+}
+
 // ---- per-layer contract (gpu.Session) ----
 
 int ziggy_hip_session_begin_token(ZiggyHipSession *s, const float *hidden, char *err, size_t err_len) {

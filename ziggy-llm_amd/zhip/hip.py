@@ -131,6 +131,7 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_session_destroy": [vp],
         "ziggy_hip_session_reset": [vp] + E,
         "ziggy_hip_session_position": [vp],
+        "ziggy_hip_session_rewind": [vp, u32] + E,
         "ziggy_hip_session_begin_token": [vp, vp] + E,
         "ziggy_hip_session_run_attention_block": [vp, u32, u32] + E,
         "ziggy_hip_session_run_ffn_block": [vp, u32] + E,
@@ -394,6 +395,9 @@ class Session:
 
     def reset(self):
         _call("ziggy_hip_session_reset", self.h)
+
+    def rewind(self, position: int):
+        _call("ziggy_hip_session_rewind", self.h, position)
 
     def step_greedy(self, token: int) -> int:
         nxt = ctypes.c_uint32()
