@@ -22,6 +22,8 @@
 // A[l % 16][4 (l / 16) + 0..3], B[4 (l / 16) + 0..3][l % 16], and the result
 // D[4 (l / 16) + 0..3][l % 16].  Here A = the row tile of W, B = the token
 // tile of X transposed, D[i][j] = Y[token j][row i].
+#include <cstdlib>
+
 #include "zh_internal.h"
 #include "zh_quant.h"
 
@@ -211,6 +213,16 @@ template <int F> static GemmKernel pick_grouped(int out) {
     }
 }
 
+// ZIGGY_HIP_QGEMM=0 keeps every M >= 8 product on this file's kernel (the
+// exact-code kernel of zh_qgemm.hip otherwise takes the quantized formats).
+static bool qgemm_enabled() {
+    static const bool on = [] {
+        const char *e = getenv("ZIGGY_HIP_QGEMM");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
 template <int F> static GemmKernel pick_precise(int out) {
     return out == OUT_STORE ? gemm_kernel<F, OUT_STORE, false, true> : nullptr;
 }
@@ -219,6 +231,8 @@ hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t st
                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
                        bool precise) {
     if (M < 1 || N < 1 || K < 16 || K % 16 || ldx % 4) return hipErrorInvalidValue;
+    if (!precise && qgemm_enabled() && qgemm_supported(fmt, K))
+        return launch_qgemm(fmt, w, w2, stride, x, ldx, y, ldy, M, N, K, out, argmax, s);
     GemmKernel k = nullptr;
     if (precise) {
         switch (fmt) {
@@ -255,6 +269,9 @@ hipError_t launch_gemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uin
                                const float *x, int ldx, int x_div, float *y, int ldy, int N, int K, int out,
                                const int *tiles, const int *list, const int *ntiles, int max_tiles, hipStream_t s) {
     if (N < 1 || K < 16 || K % 16 || ldx % 4 || max_tiles < 1 || x_div < 1) return hipErrorInvalidValue;
+    if (qgemm_enabled() && qgemm_supported(fmt, K))
+        return launch_qgemm_grouped(fmt, w, w2, stride, expert_stride, x, ldx, x_div, y, ldy, N, K, out, tiles, list,
+                                    ntiles, max_tiles, s);
     GemmKernel k = nullptr;
     switch (fmt) {
     case Q4_K: k = pick_grouped<Q4_K>(out); break;

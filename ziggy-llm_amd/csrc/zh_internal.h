@@ -143,6 +143,14 @@ hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int 
 hipError_t launch_gemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, uint64_t expert_stride,
                                const float *x, int ldx, int x_div, float *y, int ldy, int N, int K, int out,
                                const int *tiles, const int *list, const int *ntiles, int max_tiles, hipStream_t s);
+// Exact-code MFMA kernel (zh_qgemm.hip) for the quantized formats, K a multiple of 256.
+bool qgemm_supported(int fmt, int K);
+hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
+                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s);
+hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride,
+                                uint64_t expert_stride, const float *x, int ldx, int x_div, float *y, int ldy, int N,
+                                int K, int out, const int *tiles, const int *list, const int *ntiles, int max_tiles,
+                                hipStream_t s);
 hipError_t launch_moe_group(const uint32_t *route, int route_stride, int M, int k, int E, int *list, int *tiles,
                             int *ntiles, hipStream_t s);
 

@@ -1,0 +1,478 @@
+// zh_qgemm.hip -- M >= 8 tokens on the matrix cores with exact weight codes
+// (Q4_K, Q6_K, Q8_0, IQ4_XS, Q3_K; reduction length a multiple of 256).
+//
+//   Y[m][n] (=, +=) sum_k W[n][k] X[m][k]
+//
+// A quantized weight is w = s_b * q (+ an offset for Q4_K), with q a small
+// integer code and s_b the scale of its 16- or 32-value sub-block.  The codes
+// enter the matrix cores exactly (bf16 represents integers up to 256
+// exactly); the scales are applied per sub-block in f32 to the product's
+// result:
+//     Y[m][n] += s_{n,b} * D_b[m][n]  (- min_{n,b} * sum_{k in b} X[m][k])
+// where D_b = sum_{k in b} X[m][k] q[n][k] is one MFMA (two: the activation
+// enters as bf16 hi + lo, x = hi + lo to 2^-17 relative).  So a weight is
+// never rounded, only the activations are, at 2^-17 -- well inside the
+// 1e-4 relative-L2 bar.
+//
+// Product layout (v_mfma_f32_16x16x32_bf16 / 16x16x16_bf16, wave64):
+// A = activations (row i = token), B = codes (column j = weight row),
+// D[token][row]: lane (li = l % 16, lg = l / 16) holds A[li][8 lg .. +7]
+// (4 lg .. +3 for 16-value steps), B[8 lg .. +7][li] and D[4 lg + r][li].
+// The lane that decodes weight row li's codes therefore also holds row li's
+// results and applies row li's scales itself: no scale exchange.
+//
+// A workgroup (4 wavefronts) takes 64 weight rows (16 per wavefront) of one
+// token tile (16 tokens) over the whole reduction.  The activations go
+// through LDS in stages of up to 2048 values (128 KB of bf16 pieces for 16
+// tokens), split once per workgroup; within a stage the wavefronts run
+// without barriers, each streaming its rows' codes through a ring of four
+// 256-value chunks.
+#include "zh_internal.h"
+#include "zh_quant.h"
+
+namespace zh {
+
+typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
+typedef short s4v __attribute__((ext_vector_type(4)));
+typedef float qf4v __attribute__((ext_vector_type(4)));
+
+constexpr int kQRows = 64;    // weight rows per workgroup (16 per wavefront)
+constexpr int kQChunk = 256;  // reduction values per staged chunk
+constexpr int kQStage = 2048; // reduction values staged in LDS at once
+
+struct QGemmParams {
+    const uint8_t *w, *w2;  // W row 0 (w2: the up matrix of SWIGLU)
+    uint64_t stride;        // bytes per W row
+    const float *x;
+    float *y;
+    int M, N, K, ldx, ldy;
+    unsigned long long *argmax;
+    // grouped: token tile blockIdx.y is tiles[3 t] = {expert, first, count} of list
+    const int *tiles, *list, *ntiles;
+    int x_div;
+    uint64_t expert_stride;
+};
+
+__device__ __forceinline__ uint32_t bf16_rne(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+// bf16 bits of two small integers held as f32 (exact: the high halves)
+__device__ __forceinline__ uint32_t pack_bf(float a, float b) {
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
+__device__ __forceinline__ bf8v as_bf8(uint4 v) {
+    bf8v r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+}
+__device__ __forceinline__ s4v as_s4(uint2 v) {
+    s4v r;
+    __builtin_memcpy(&r, &v, 8);
+    return r;
+}
+// eight unsigned byte codes (bytes of a, b) -> bf16 x 8
+__device__ __forceinline__ uint4 codes_u8(uint32_t a, uint32_t b) {
+    return {pack_bf(ub(a, 0), ub(a, 1)), pack_bf(ub(a, 2), ub(a, 3)), pack_bf(ub(b, 0), ub(b, 1)),
+            pack_bf(ub(b, 2), ub(b, 3))};
+}
+__device__ __forceinline__ uint4 codes_s8(uint32_t a, uint32_t b) {
+    return {pack_bf(sb(a, 0), sb(a, 1)), pack_bf(sb(a, 2), sb(a, 3)), pack_bf(sb(b, 0), sb(b, 1)),
+            pack_bf(sb(b, 2), sb(b, 3))};
+}
+// four unsigned byte codes minus an offset -> bf16 x 4
+__device__ __forceinline__ uint2 codes_u4(uint32_t a, float off) {
+    return {pack_bf(ub(a, 0) - off, ub(a, 1) - off), pack_bf(ub(a, 2) - off, ub(a, 3) - off)};
+}
+
+// ---- per-format chunk (256 values of one row): raw words and sub-block steps ----
+//
+// load(row, c, lg): the words lane group lg needs of chunk c of `row`.
+// Steps: kSteps sub-blocks of kSub values; step(j) gives the lane's codes for
+// values kSub/4 * lg .. of sub-block j and the sub-block's scale (and min).
+
+template <int F> struct QChunk;
+
+template <> struct QChunk<Q4_K> {
+    static constexpr int kSub = 32, kSteps = 8;
+    uint4 hd;     // d, dmin, 12 scale bytes
+    uint2 q[4];   // qs[32 g + 8 lg .. + 7] of group g
+    __device__ __forceinline__ void load(const uint8_t *row, int c, int lg) {
+        const uint8_t *blk = row + (size_t)c * 144;
+        hd = ld16(blk);
+#pragma unroll
+        for (int g = 0; g < 4; g++) q[g] = ld8(blk + 16 + 32 * g + 8 * lg);
+    }
+    __device__ __forceinline__ uint32_t sbyte(int k) const {
+        const uint32_t w = k < 4 ? hd.y : k < 8 ? hd.z : hd.w;
+        return (w >> (8 * (k & 3))) & 0xFFu;
+    }
+    // getScaleMinK4 (model/loader.zig:3814-3825)
+    __device__ __forceinline__ uint4 step(int j, float &s, float &mn) const {
+        uint32_t sc, m;
+        if (j < 4) {
+            sc = sbyte(j) & 63;
+            m = sbyte(j + 4) & 63;
+        } else {
+            sc = (sbyte(j + 4) & 0x0F) | ((sbyte(j - 4) >> 6) << 4);
+            m = (sbyte(j + 4) >> 4) | ((sbyte(j) >> 6) << 4);
+        }
+        s = h2f(hd.x) * (float)sc;
+        mn = h2f(hd.x >> 16) * (float)m;
+        const uint2 w = q[j >> 1];
+        const int sh = (j & 1) ? 4 : 0;
+        return codes_u8((w.x >> sh) & 0x0F0F0F0Fu, (w.y >> sh) & 0x0F0F0F0Fu);
+    }
+};
+
+template <> struct QChunk<Q8_0> {
+    static constexpr int kSub = 32, kSteps = 8;
+    uint2 q[8];
+    uint32_t d[8];
+    __device__ __forceinline__ void load(const uint8_t *row, int c, int lg) {
+        const uint8_t *p = row + (size_t)c * 8 * 34;
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            q[b] = ld8(p + 34 * b + 2 + 8 * lg);
+            d[b] = ld2(p + 34 * b);
+        }
+    }
+    __device__ __forceinline__ uint4 step(int j, float &s, float &mn) const {
+        s = h2f(d[j]);
+        mn = 0.f;
+        return codes_s8(q[j].x, q[j].y);
+    }
+};
+
+template <> struct QChunk<IQ4_XS> {
+    static constexpr int kSub = 32, kSteps = 8;
+    uint2 hd;     // d, scales_h, scales_l[4]
+    uint2 q[8];   // qs[16 ib + 8 (lg & 1) ..]
+    int hi;       // lane groups 2, 3 take the high nibbles (values 16..31)
+    __device__ __forceinline__ void load(const uint8_t *row, int c, int lg) {
+        const uint8_t *blk = row + (size_t)c * 136;
+        hd = ld8(blk);
+#pragma unroll
+        for (int ib = 0; ib < 8; ib++) q[ib] = ld8(blk + 8 + 16 * ib + 8 * (lg & 1));
+        hi = lg >> 1;
+    }
+    // dequantizeRowIQ4XS (model/quant_extra.zig:191-246): dl = d * (ls - 32)
+    __device__ __forceinline__ uint4 step(int j, float &s, float &mn) const {
+        const uint32_t low = (hd.y >> (8 * (j >> 1) + 4 * (j & 1))) & 0x0F;
+        const uint32_t high = (hd.x >> (16 + 2 * j)) & 3;
+        s = h2f(hd.x) * (float)((int)(low | (high << 4)) - 32);
+        mn = 0.f;
+        const int sh = hi ? 4 : 0;
+        return codes_s8(iq4_lookup4((q[j].x >> sh) & 0x0F0F0F0Fu), iq4_lookup4((q[j].y >> sh) & 0x0F0F0F0Fu));
+    }
+};
+
+// 16-value sub-blocks: a step is one 16x16x16 product (four codes per lane)
+template <> struct QChunk<Q6_K> {
+    static constexpr int kSub = 16, kSteps = 16;
+    uint32_t ql[2][2][2];  // [half][16-run][ql offset 0 / 32]
+    uint32_t qh[2][2];     // [half][16-run]
+    uint4 sc;              // 16 int8 scales
+    uint32_t d;
+    __device__ __forceinline__ void load(const uint8_t *row, int c, int lg) {
+        const uint8_t *blk = row + (size_t)c * 210;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                ql[h][r][0] = ld4(blk + 64 * h + 16 * r + 4 * lg);
+                ql[h][r][1] = ld4(blk + 64 * h + 32 + 16 * r + 4 * lg);
+                qh[h][r] = ld4(blk + 128 + 32 * h + 16 * r + 4 * lg);
+            }
+        sc = ld16(blk + 192);
+        d = ld2(blk + 208);
+    }
+    // dequantizeRowQ6K (model/loader.zig:3728-3761): sub-block j = (half, quarter, 16-run)
+    __device__ __forceinline__ uint2 step(int j, float &s) const {
+        const int h = j >> 3, qt = (j >> 1) & 3, r = j & 1;
+        const uint32_t w = ql[h][r][qt & 1];
+        const uint32_t nib = ((qt & 2) ? (w >> 4) : w) & 0x0F0F0F0Fu;
+        const uint32_t code = nib | (((qh[h][r] >> (2 * qt)) & 0x03030303u) << 4);
+        const int si = 8 * h + r + 2 * qt;
+        const uint32_t sw = si < 4 ? sc.x : si < 8 ? sc.y : si < 12 ? sc.z : sc.w;
+        s = h2f(d) * sb(sw, si & 3);
+        return codes_u4(code, 32.f);
+    }
+};
+
+template <> struct QChunk<Q3_K> {
+    static constexpr int kSub = 16, kSteps = 16;
+    uint32_t qs[2][2];  // [half h][16-run]: qs[32 h + 16 r + 4 lg ..]
+    uint32_t hm[2];     // [16-run]: hmask[16 r + 4 lg ..]
+    uint32_t raw[3];    // 12 packed scale bytes
+    uint32_t d;
+    __device__ __forceinline__ void load(const uint8_t *row, int c, int lg) {
+        const uint8_t *blk = row + (size_t)c * 110;
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            hm[r] = ld4(blk + 16 * r + 4 * lg);
+#pragma unroll
+            for (int h = 0; h < 2; h++) qs[h][r] = ld4(blk + 32 + 32 * h + 16 * r + 4 * lg);
+        }
+        raw[0] = ld4(blk + 96);
+        raw[1] = ld4(blk + 100);
+        raw[2] = ld4(blk + 104);
+        d = ld2(blk + 108);
+    }
+    // dequantizeRowQ3K / expandQ3KScales (model/quant_extra.zig:45-126, 248-279):
+    // sub-block si = 8 h + 2 j + half16; q = low 2 bits - (hmask bit ? 0 : 4)
+    __device__ __forceinline__ uint2 step(int si, float &s) const {
+        const int h = si >> 3, j = (si >> 1) & 3, r = si & 1;
+        const uint32_t code = ((qs[h][r] >> (2 * j)) & 0x03030303u) | (((hm[r] >> (4 * h + j)) & 0x01010101u) << 2);
+        const int qd = si & 3, grp = si >> 2;
+        const uint32_t lw = raw[grp & 1], hw = raw[2];
+        const uint32_t low4 = (lw >> (8 * qd + 4 * (grp >> 1))) & 0xF;
+        const uint32_t hi2 = (hw >> (8 * qd + 2 * grp)) & 3;
+        s = h2f(d) * (float)((int)(low4 | (hi2 << 4)) - 32);
+        return codes_u4(code, 4.f);
+    }
+};
+
+__device__ __forceinline__ uint32_t ordered_bits_q(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+template <int F, int OUT, bool GROUPED, int R>
+__global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
+    constexpr bool kPair = OUT == OUT_SWIGLU;
+    constexpr int kSub = QChunk<F>::kSub;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
+    int m0 = blockIdx.y * 16, M = p.M;
+    const int *ids = nullptr;
+    const uint8_t *w = p.w, *w2 = p.w2;
+    if (GROUPED) {
+        if ((int)blockIdx.y >= *p.ntiles) return;
+        const int *gt = p.tiles + 3 * blockIdx.y;
+        w += (uint64_t)gt[0] * p.expert_stride;
+        if (kPair) w2 += (uint64_t)gt[0] * p.expert_stride;
+        ids = p.list + gt[1];
+        m0 = 0;
+        M = gt[2];
+    }
+    const int n0 = blockIdx.x * kQRows + 16 * wave;
+    const int n = min(n0 + li, p.N - 1);  // this lane's weight row (clamped; dropped at the store)
+    const uint8_t *wrow = w + (uint64_t)n * p.stride;
+    const uint8_t *wrow2 = kPair ? w2 + (uint64_t)n * p.stride : nullptr;
+
+    // The activations of a stage (up to kQStage values of all 16 tokens) sit in
+    // LDS as bf16 hi / lo pieces; thread (token tt, part) stages values
+    // 16 part + 256 i of its token.
+    __shared__ __align__(16) unsigned short xs_s[2][16][kQStage + 8];  // [hi / lo][token][k]
+    __shared__ __align__(16) float xsum_s[kQStage / 32][16];          // [32-value sub-block][token]
+    const int tt = tid >> 4, part = tid & 15;
+    const bool tok_ok = m0 + tt < M;
+    const float *xrow;
+    {
+        const int m = min(m0 + tt, M - 1);
+        xrow = p.x + (size_t)(GROUPED ? ids[m] / p.x_div : m) * p.ldx + 16 * part;
+    }
+    auto stage = [&](int kb, int nv) {
+        for (int c = 0; c < nv / kQChunk; c++) {
+            const float4 *src = reinterpret_cast<const float4 *>(xrow + kb + c * kQChunk);
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 q = src[i];
+                v[4 * i] = q.x, v[4 * i + 1] = q.y, v[4 * i + 2] = q.z, v[4 * i + 3] = q.w;
+            }
+            uint32_t hw[8], lw[8];
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) {
+                const float a = tok_ok ? v[i] : 0.f, b = tok_ok ? v[i + 1] : 0.f;
+                const uint32_t ha = bf16_rne(a), hb = bf16_rne(b);
+                const float ra = a - __uint_as_float(ha << 16), rb = b - __uint_as_float(hb << 16);
+                const uint32_t la = bf16_rne(ra), lb = bf16_rne(rb);
+                hw[i / 2] = ha | (hb << 16);
+                lw[i / 2] = la | (lb << 16);
+                sum += (__uint_as_float(ha << 16) + __uint_as_float(la << 16)) +
+                       (__uint_as_float(hb << 16) + __uint_as_float(lb << 16));
+            }
+            uint4 *dh = reinterpret_cast<uint4 *>(&xs_s[0][tt][c * kQChunk + 16 * part]);
+            uint4 *dl = reinterpret_cast<uint4 *>(&xs_s[1][tt][c * kQChunk + 16 * part]);
+            dh[0] = {hw[0], hw[1], hw[2], hw[3]};
+            dh[1] = {hw[4], hw[5], hw[6], hw[7]};
+            dl[0] = {lw[0], lw[1], lw[2], lw[3]};
+            dl[1] = {lw[4], lw[5], lw[6], lw[7]};
+            if (F == Q4_K) {
+                sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
+                if (!(part & 1)) xsum_s[c * 8 + (part >> 1)][tt] = sum;
+            }
+        }
+    };
+
+    qf4v acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+    // chunk cs of the stage (offset 256 cs in LDS)
+    auto compute = [&](const QChunk<F> &r, const QChunk<F> &r2, int cs, float live) {
+#pragma unroll
+        for (int j = 0; j < QChunk<F>::kSteps; j++) {
+            const qf4v zero = {0.f, 0.f, 0.f, 0.f};
+            float s, mn = 0.f, s2 = 0.f, mn2 = 0.f;
+            qf4v dv, dv2 = zero;
+            const int kx = cs * kQChunk + kSub * j;
+            if constexpr (kSub == 32) {
+                const bf8v ah = as_bf8(*reinterpret_cast<const uint4 *>(&xs_s[0][li][kx + 8 * lg]));
+                const bf8v al = as_bf8(*reinterpret_cast<const uint4 *>(&xs_s[1][li][kx + 8 * lg]));
+                const bf8v b = as_bf8(r.step(j, s, mn));
+                dv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, zero, 0, 0, 0);
+                dv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, dv, 0, 0, 0);
+                if (kPair) {
+                    const bf8v b2 = as_bf8(r2.step(j, s2, mn2));
+                    dv2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b2, zero, 0, 0, 0);
+                    dv2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b2, dv2, 0, 0, 0);
+                }
+            } else {
+                const s4v ah = as_s4(*reinterpret_cast<const uint2 *>(&xs_s[0][li][kx + 4 * lg]));
+                const s4v al = as_s4(*reinterpret_cast<const uint2 *>(&xs_s[1][li][kx + 4 * lg]));
+                const s4v b = as_s4(r.step(j, s));
+                dv = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, b, zero, 0, 0, 0);
+                dv = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, b, dv, 0, 0, 0);
+                if (kPair) {
+                    const s4v b2 = as_s4(r2.step(j, s2));
+                    dv2 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, b2, zero, 0, 0, 0);
+                    dv2 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, b2, dv2, 0, 0, 0);
+                }
+            }
+            s *= live;
+            s2 *= live;
+            if (F == Q4_K) {
+                const float4 xsm = *reinterpret_cast<const float4 *>(&xsum_s[cs * 8 + j][4 * lg]);
+                const float xm[4] = {xsm.x, xsm.y, xsm.z, xsm.w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    acc[q] = fmaf(s, dv[q], fmaf(-mn * live, xm[q], acc[q]));
+                    if (kPair) acc2[q] = fmaf(s2, dv2[q], fmaf(-mn2 * live, xm[q], acc2[q]));
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    acc[q] = fmaf(s, dv[q], acc[q]);
+                    if (kPair) acc2[q] = fmaf(s2, dv2[q], acc2[q]);
+                }
+            }
+        }
+    };
+
+    // Stages of up to kQStage values; within a stage a ring of R chunks of
+    // codes, each slot refilled in place with the chunk R ahead.  Loads are
+    // unconditional (clamped to the stage's last chunk): a load under a branch
+    // makes the compiler's wait counting wait for everything in flight.  A
+    // chunk past the end runs with its scales zeroed (live = 0).
+    QChunk<F> rs[R], rs2[R];
+    for (int kb = 0; kb < p.K; kb += kQStage) {
+        const int nv = min(kQStage, p.K - kb), nst = nv / kQChunk, c0 = kb / kQChunk;
+        if (kb > 0) __syncthreads();  // every wavefront is done with the previous stage
+#pragma unroll
+        for (int q = 0; q < R; q++) {
+            rs[q].load(wrow, c0 + min(q, nst - 1), lg);
+            if (kPair) rs2[q].load(wrow2, c0 + min(q, nst - 1), lg);
+        }
+        stage(kb, nv);
+        __syncthreads();
+        for (int c = 0; c < nst; c += R) {
+#pragma unroll
+            for (int q = 0; q < R; q++) {
+                compute(rs[q], rs2[q], min(c + q, nst - 1), c + q < nst ? 1.f : 0.f);
+                rs[q].load(wrow, c0 + min(c + q + R, nst - 1), lg);
+                if (kPair) rs2[q].load(wrow2, c0 + min(c + q + R, nst - 1), lg);
+            }
+        }
+    }
+
+    // D[token 4 lg + r][row li]
+    const int nn = n0 + li;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int j = m0 + 4 * lg + r;  // token of result r
+        if (j >= M || nn >= p.N) continue;
+        const int jrow = GROUPED ? ids[4 * lg + r] : j;
+        float *dst = p.y ? p.y + (size_t)jrow * p.ldy + nn : nullptr;
+        const float v = acc[r];
+        if (OUT == OUT_STORE) {
+            *dst = v;
+        } else if (OUT == OUT_ADD) {
+            *dst = *dst + v;
+        } else if (OUT == OUT_SWIGLU) {
+            *dst = (v / (1.0f + expf(-v))) * acc2[r];
+        }
+    }
+    if (OUT == OUT_ARGMAX) {
+        // token 4 lg + r: the largest value over the 16 rows of lanes li, then the lowest row
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int j = m0 + 4 * lg + r;
+            const float v = acc[r];
+            if (p.y && j < M && nn < p.N) p.y[(size_t)j * p.ldy + nn] = v;
+            unsigned long long key = (j < M && nn < p.N)
+                                         ? ((unsigned long long)ordered_bits_q(v) << 32) |
+                                               (unsigned long long)(0xFFFFFFFFu - (uint32_t)nn)
+                                         : 0ull;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const unsigned long long k2 = __shfl_xor(key, o, 64);
+                key = k2 > key ? k2 : key;
+            }
+            if (li == 0 && key) atomicMax(p.argmax + j, key);
+        }
+    }
+}
+
+typedef void (*QGemmKernel)(QGemmParams);
+
+template <int F, bool G, int R> static QGemmKernel pick_q(int out) {
+    switch (out) {
+    case OUT_STORE: return qgemm_kernel<F, OUT_STORE, G, R>;
+    case OUT_SWIGLU: return qgemm_kernel<F, OUT_SWIGLU, G, R>;
+    case OUT_ADD: return G ? nullptr : qgemm_kernel<F, OUT_ADD, G, R>;
+    case OUT_ARGMAX: return G ? nullptr : qgemm_kernel<F, OUT_ARGMAX, G, R>;
+    default: return nullptr;
+    }
+}
+
+// ring depth: 4 chunks, or 2 when a stage holds only two (K = 512)
+template <bool G> static QGemmKernel pick_qf(int fmt, int out, int K) {
+    const bool r2 = K / kQChunk <= 2;
+    switch (fmt) {
+    case Q4_K: return r2 ? pick_q<Q4_K, G, 2>(out) : pick_q<Q4_K, G, 4>(out);
+    case Q6_K: return r2 ? pick_q<Q6_K, G, 2>(out) : pick_q<Q6_K, G, 4>(out);
+    case Q8_0: return r2 ? pick_q<Q8_0, G, 2>(out) : pick_q<Q8_0, G, 4>(out);
+    case IQ4_XS: return r2 ? pick_q<IQ4_XS, G, 2>(out) : pick_q<IQ4_XS, G, 4>(out);
+    case Q3_K: return r2 ? pick_q<Q3_K, G, 2>(out) : pick_q<Q3_K, G, 4>(out);
+    default: return nullptr;
+    }
+}
+
+bool qgemm_supported(int fmt, int K) {
+    return (fmt == Q4_K || fmt == Q6_K || fmt == Q8_0 || fmt == IQ4_XS || fmt == Q3_K) && K >= kQChunk &&
+           K % kQChunk == 0;
+}
+
+hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
+                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s) {
+    if (M < 1 || N < 1 || !qgemm_supported(fmt, K) || ldx % 4) return hipErrorInvalidValue;
+    QGemmKernel k = pick_qf<false>(fmt, out, K);
+    if (!k) return hipErrorInvalidValue;
+    QGemmParams p{w, w2, stride, x, y, M, N, K, ldx, ldy, argmax, nullptr, nullptr, nullptr, 1, 0};
+    hipLaunchKernelGGL(k, dim3((N + kQRows - 1) / kQRows, (M + 15) / 16), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride,
+                                uint64_t expert_stride, const float *x, int ldx, int x_div, float *y, int ldy, int N,
+                                int K, int out, const int *tiles, const int *list, const int *ntiles, int max_tiles,
+                                hipStream_t s) {
+    if (N < 1 || !qgemm_supported(fmt, K) || ldx % 4 || max_tiles < 1 || x_div < 1) return hipErrorInvalidValue;
+    QGemmKernel k = pick_qf<true>(fmt, out, K);
+    if (!k) return hipErrorInvalidValue;
+    QGemmParams p{w, w2, stride, x, y, 16, N, K, ldx, ldy, nullptr, tiles, list, ntiles, x_div, expert_stride};
+    hipLaunchKernelGGL(k, dim3((N + kQRows - 1) / kQRows, max_tiles), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+}  // namespace zh
