@@ -7,22 +7,46 @@ namespace zh {
 
 // Rows per team so that the grid has at most target_wgs workgroups, or one
 // row per team when the matrix is too small to fill them.
+// Rows per team of each segment for an even byte budget per team: segment i
+// takes rpt_i = max(1, W / row_bytes_i) rows per team, with W the smallest
+// budget whose grid fits in target_wgs workgroups.  (A grid one workgroup
+// over the CU count runs a second round on one CU and doubles the launch;
+// equal row counts across a Q4_K and a Q6_K segment leave the Q6_K
+// workgroups 1.46x the bytes.)
 void plan_matvec(MvParams &p, int target_wgs) {
     p.slots = p.cols / 64;
     p.team = team_width(p.cols);
     const int teams = kThreads / p.team;
-    int team_rows = 0;
-    for (int i = 0; i < p.nseg; i++) team_rows += (p.seg[i].rows + teams - 1) / teams;
     if (target_wgs < 1) target_wgs = 1;
-    int rpt = (team_rows + target_wgs - 1) / target_wgs;
-    if (rpt < 1) rpt = 1;
-    p.rows_per_team = rpt;
-    int wg = 0;
+    auto rpt_of = [&](int i, uint64_t W) {
+        const uint64_t rb = p.seg[i].stride ? p.seg[i].stride : 1;
+        const uint64_t r = W / rb;
+        return (int)(r < 1 ? 1 : r > (1u << 20) ? (1u << 20) : r);
+    };
+    auto wgs_of = [&](uint64_t W) {
+        int64_t g = 0;
+        for (int i = 0; i < p.nseg; i++) {
+            const int per = teams * rpt_of(i, W);
+            g += (p.seg[i].rows + per - 1) / per;
+        }
+        return g;
+    };
+    uint64_t lo = 1, hi = 1;
+    for (int i = 0; i < p.nseg; i++) hi += (uint64_t)p.seg[i].rows * (p.seg[i].stride ? p.seg[i].stride : 1);
+    while (lo < hi) {  // smallest W with wgs_of(W) <= target (wgs_of never grows with W)
+        const uint64_t mid = lo + (hi - lo) / 2;
+        if (wgs_of(mid) <= target_wgs) hi = mid;
+        else lo = mid + 1;
+    }
+    int wg = 0, rmax = 1;
     for (int i = 0; i < p.nseg; i++) {
+        const int rpt = rpt_of(i, lo);
+        rmax = rpt > rmax ? rpt : rmax;
         p.seg[i].rows_per_wg = teams * rpt;
         p.seg[i].wg_begin = wg;
         wg += (p.seg[i].rows + teams * rpt - 1) / (teams * rpt);
     }
+    p.rows_per_team = rmax;
     for (int i = p.nseg; i < kMaxSeg; i++) p.seg[i].wg_begin = 0x7fffffff;
 }
 

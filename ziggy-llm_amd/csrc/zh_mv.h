@@ -290,7 +290,7 @@ __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int 
     }
     const int r_begin = wg_in_seg * sg.rows_per_wg;
     const int r_end = min(r_begin + sg.rows_per_wg, sg.rows);
-    const int n = p.rows_per_team;
+    const int n = sg.rows_per_wg / teams;  // rows per team of this segment
     const int r0 = r_begin + team;
     // row `it` of this team, clamped to the workgroup's last row (loads only)
     auto row_of = [&](int it) { return min(r0 + it * teams, r_end - 1); };
@@ -398,7 +398,7 @@ __device__ __forceinline__ void mv_body_fast(const MvParams &p, const MvSeg &sg,
     }
     const int r_begin = wg_in_seg * sg.rows_per_wg;
     const int r_end = min(r_begin + sg.rows_per_wg, sg.rows);
-    const int n = p.rows_per_team;
+    const int n = sg.rows_per_wg / teams;  // rows per team of this segment
     const int r0 = r_begin + team;
     auto row_of = [&](int it) { return min(r0 + it * teams, r_end - 1); };
 
