@@ -191,18 +191,19 @@ struct XRun {
     float4 a[4], b[4];
 };
 
+// Loads are unconditional (threads past the runs re-read the last run; their
+// values are zeroed in coop_finish): a load under a branch makes the
+// register allocator copy its destination at the join, and the copy waits
+// for the load before anything after it (the weight loads) can issue.
 template <int IN>
 __device__ __forceinline__ void coop_load(XRun &r, int nruns, const MvParams &p, const float *x) {
-    const int t = threadIdx.x;
+    const int t = min((int)threadIdx.x, nruns - 1);
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        r.a[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-        r.b[c] = r.a[c];
-        if (t < nruns) {
-            r.a[c] = *reinterpret_cast<const float4 *>(x + 16 * t + 4 * c);
-            if (IN == IN_NORM) r.b[c] = *reinterpret_cast<const float4 *>(p.norm_w + 16 * t + 4 * c);
-            if (IN == IN_SILU) r.b[c] = *reinterpret_cast<const float4 *>(p.x2 + 16 * t + 4 * c);
-        }
+        r.a[c] = *reinterpret_cast<const float4 *>(x + 16 * t + 4 * c);
+        r.b[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (IN == IN_NORM) r.b[c] = *reinterpret_cast<const float4 *>(p.norm_w + 16 * t + 4 * c);
+        if (IN == IN_SILU) r.b[c] = *reinterpret_cast<const float4 *>(p.x2 + 16 * t + 4 * c);
     }
 }
 
@@ -211,10 +212,12 @@ __device__ __forceinline__ void coop_finish(XDig &xs, const XRun &r, int nruns, 
                                             const MvParams &p) {
     __shared__ CoopLds L;
     const int t = threadIdx.x, wave = t >> 6;
+    const bool own = t < nruns;  // threads past the runs hold a re-read run: zeros
     float v[16], aux[16];
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-        v[4 * c] = r.a[c].x, v[4 * c + 1] = r.a[c].y, v[4 * c + 2] = r.a[c].z, v[4 * c + 3] = r.a[c].w;
+        v[4 * c] = own ? r.a[c].x : 0.f, v[4 * c + 1] = own ? r.a[c].y : 0.f;
+        v[4 * c + 2] = own ? r.a[c].z : 0.f, v[4 * c + 3] = own ? r.a[c].w : 0.f;
         aux[4 * c] = r.b[c].x, aux[4 * c + 1] = r.b[c].y, aux[4 * c + 2] = r.b[c].z, aux[4 * c + 3] = r.b[c].w;
     }
     if (IN == IN_NORM) {
