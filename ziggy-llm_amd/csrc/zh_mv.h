@@ -111,20 +111,21 @@ struct XRaw {
 };
 
 template <int F, int IN>
+// Unconditional loads (an inactive lane re-reads the last slot and
+// stage_finish zeroes its values): a load under a branch makes the register
+// allocator copy its destination at the join, and that copy waits for the
+// load before the weight loads after it can issue.
 __device__ __forceinline__ void stage_load(XRaw &r, int s, bool active, const MvParams &p, const float *x) {
-    const int base = Geom<F>::x_base(s);
+    const int base = Geom<F>::x_base(active ? s : p.slots - 1);
 #pragma unroll
     for (int w = 0; w < 4; w++) {
         const int o = base + w * Geom<F>::kXStride;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            r.a[4 * w + c] = make_float4(0.f, 0.f, 0.f, 0.f);
-            r.b[4 * w + c] = r.a[4 * w + c];
-            if (active) {
-                r.a[4 * w + c] = *reinterpret_cast<const float4 *>(x + o + 4 * c);
-                if (IN == IN_NORM) r.b[4 * w + c] = *reinterpret_cast<const float4 *>(p.norm_w + o + 4 * c);
-                if (IN == IN_SILU) r.b[4 * w + c] = *reinterpret_cast<const float4 *>(p.x2 + o + 4 * c);
-            }
+            r.a[4 * w + c] = *reinterpret_cast<const float4 *>(x + o + 4 * c);
+            r.b[4 * w + c] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (IN == IN_NORM) r.b[4 * w + c] = *reinterpret_cast<const float4 *>(p.norm_w + o + 4 * c);
+            if (IN == IN_SILU) r.b[4 * w + c] = *reinterpret_cast<const float4 *>(p.x2 + o + 4 * c);
         }
     }
 }
@@ -132,11 +133,13 @@ __device__ __forceinline__ void stage_load(XRaw &r, int s, bool active, const Mv
 // Applies the input prologue to the loaded slot and converts it to the slot
 // representation of format F.
 template <int F, int IN>
-__device__ __forceinline__ void stage_finish(XOf_t<F> &xs, const XRaw &r, const MvParams &p, int T, float *lds) {
+__device__ __forceinline__ void stage_finish(XOf_t<F> &xs, const XRaw &r, const MvParams &p, int T, float *lds,
+                                             bool active) {
     float v[64], aux[64];
 #pragma unroll
     for (int k = 0; k < 16; k++) {
-        v[4 * k] = r.a[k].x, v[4 * k + 1] = r.a[k].y, v[4 * k + 2] = r.a[k].z, v[4 * k + 3] = r.a[k].w;
+        v[4 * k] = active ? r.a[k].x : 0.f, v[4 * k + 1] = active ? r.a[k].y : 0.f;
+        v[4 * k + 2] = active ? r.a[k].z : 0.f, v[4 * k + 3] = active ? r.a[k].w : 0.f;
         aux[4 * k] = r.b[k].x, aux[4 * k + 1] = r.b[k].y, aux[4 * k + 2] = r.b[k].z, aux[4 * k + 3] = r.b[k].w;
     }
     if (IN == IN_NORM) {
@@ -165,7 +168,7 @@ __device__ __forceinline__ void stage_x(XOf_t<F> &xs, int s, bool active, const 
                                         float *lds) {
     XRaw r;
     stage_load<F, IN>(r, s, active, p, x);
-    stage_finish<F, IN>(xs, r, p, T, lds);
+    stage_finish<F, IN>(xs, r, p, T, lds, active);
 }
 
 // Workgroup-cooperative staging for teams of 64 lanes (up to 64 slots; four
@@ -437,7 +440,7 @@ __device__ __forceinline__ void mv_body_fast(const MvParams &p, const MvSeg &sg,
     if constexpr (kCoop)
         coop_finish<F, IN>(xs, xrun, nruns, p.slots, lane, p);
     else
-        stage_finish<F, IN>(xs, xr, p, TT, lds);
+        stage_finish<F, IN>(xs, xr, p, TT, lds, active);
 
     float best_v = -INFINITY;
     int best_r = 0x7fffffff;
