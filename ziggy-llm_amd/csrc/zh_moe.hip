@@ -133,6 +133,93 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const float *__restrict_
     }
 }
 
+// One wavefront, up to 256 experts (four per lane): the same routing as
+// moe_route_kernel with wavefront reductions only (no barriers).
+__global__ void __launch_bounds__(64) moe_route_wave_kernel(const float *__restrict__ logits, int E, int k,
+                                                           int gating, int weights_norm, float weights_scale,
+                                                           int has_shared_gate, uint32_t *__restrict__ route,
+                                                           int logits_stride) {
+    logits += (size_t)blockIdx.x * logits_stride;
+    route += (size_t)blockIdx.x * (2 * k + 2);
+    const int l = threadIdx.x;
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pr[i] = l + 64 * i < E ? logits[l + 64 * i] : -INFINITY;
+    if (gating == 1 || gating == 2) {
+        // softmaxInPlace (model/loader.zig:4160-4170): max, exp(v - max), / sum
+        float m = fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3]));
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            pr[i] = l + 64 * i < E ? expf(pr[i] - m) : 0.f;
+            s += pr[i];
+        }
+        for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+#pragma unroll
+        for (int i = 0; i < 4; i++) pr[i] = l + 64 * i < E ? pr[i] / s : -INFINITY;
+    }
+    // k rounds of a wavefront argmax over the values not yet taken (the
+    // largest value first; equal values: the lower index first)
+    uint32_t sel[kMoeMaxK];
+    unsigned taken = 0;  // bit i: expert l + 64 i taken
+    for (int r = 0; r < k; r++) {
+        unsigned long long best = 0ull;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int idx = l + 64 * i;
+            if (idx >= E || (taken >> i & 1)) continue;
+            const unsigned long long key =
+                ((unsigned long long)ordered_bits_moe(pr[i]) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
+            best = key > best ? key : best;
+        }
+        for (int o = 32; o >= 1; o >>= 1) {
+            const unsigned long long v = __shfl_xor(best, o, 64);
+            best = v > best ? v : best;
+        }
+        const uint32_t idx = 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull);
+        sel[r] = idx;
+        if ((int)(idx & 63) == l) taken |= 1u << (idx >> 6);
+    }
+    // the selected probabilities: from the lane that holds each
+    float w[kMoeMaxK];
+    for (int r = 0; r < k; r++) {
+        const int src = sel[r] & 63, i = sel[r] >> 6;
+        const float mine = i == 0 ? pr[0] : i == 1 ? pr[1] : i == 2 ? pr[2] : pr[3];
+        w[r] = __shfl(mine, src, 64);
+    }
+    if (l == 0) {
+        if (weights_norm) {
+            float sum = 0.f;
+            for (int r = 0; r < k; r++)
+                if (isfinite(w[r]) && w[r] > 0.f) sum += w[r];
+            if (sum <= 0.f) {
+                for (int r = 0; r < k; r++) w[r] = 0.f;
+            } else {
+                const float inv = 1.0f / sum;
+                for (int r = 0; r < k; r++) w[r] = (isfinite(w[r]) && w[r] > 0.f) ? w[r] * inv : 0.f;
+            }
+        }
+        if (weights_scale != 1.0f)
+            for (int r = 0; r < k; r++) w[r] *= weights_scale;
+        for (int r = 0; r < k; r++) {
+            route[2 * r] = sel[r];
+            route[2 * r + 1] = __float_as_uint(w[r]);
+        }
+        float g = 1.0f;
+        if (has_shared_gate) {
+            const float v = logits[E];
+            if (v >= 0.f) {
+                g = 1.0f / (1.0f + expf(-v));
+            } else {
+                const float e = expf(v);
+                g = e / (1.0f + e);
+            }
+        }
+        route[2 * k] = __float_as_uint(g);
+    }
+}
+
 __global__ void moe_combine_kernel(float *__restrict__ hidden, const float *__restrict__ tmp,
                                    const uint32_t *__restrict__ route, int H, int k, int has_shared,
                                    const float *__restrict__ sh_tmp) {
@@ -159,8 +246,12 @@ __global__ void moe_combine_kernel(float *__restrict__ hidden, const float *__re
 hipError_t launch_moe_route(const float *logits, int E, int k, int gating, int weights_norm, float weights_scale,
                             int has_shared_gate, uint32_t *route, hipStream_t s, int tokens, int logits_stride) {
     if (E < 1 || E > kMoeMaxExperts || k < 1 || k > kMoeMaxK || k > E || tokens < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(moe_route_kernel, dim3(tokens), dim3(256), 0, s, logits, E, k, gating, weights_norm,
-                       weights_scale, has_shared_gate, route, logits_stride);
+    if (E <= 256)
+        hipLaunchKernelGGL(moe_route_wave_kernel, dim3(tokens), dim3(64), 0, s, logits, E, k, gating, weights_norm,
+                           weights_scale, has_shared_gate, route, logits_stride);
+    else
+        hipLaunchKernelGGL(moe_route_kernel, dim3(tokens), dim3(256), 0, s, logits, E, k, gating, weights_norm,
+                           weights_scale, has_shared_gate, route, logits_stride);
     return hipGetLastError();
 }
 

@@ -553,9 +553,12 @@ __global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
 
 // Team width of a row of `cols` values: next power of two of the slot count,
 // at most one workgroup.
+// Rows of 1024 .. 4032 values take a whole wavefront (16 .. 63 active lanes):
+// the fast path serves teams of 64 and 256 lanes only.
 inline int team_width(int cols) {
     int t = 1;
     while (t < cols / 64) t <<= 1;
+    if (cols >= 1024 && t < 64) t = 64;
     return t > kThreads ? kThreads : t;
 }
 
