@@ -51,6 +51,7 @@ struct QGemmParams {
     const int *tiles, *list, *ntiles;
     int x_div;
     uint64_t expert_stride;
+    int ksplit;  // blockIdx.z takes reduction values [z K / ksplit, (z + 1) K / ksplit); results add atomically
 };
 
 __device__ __forceinline__ uint32_t bf16_rne(float v) {
@@ -272,13 +273,25 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
         const int m = min(m0 + tt, M - 1);
         xrow = p.x + (size_t)(GROUPED ? ids[m] / p.x_div : m) * p.ldx + 16 * part;
     }
+    // chunks in batches of four: all loads of a batch in flight before the first LDS write
     auto stage = [&](int kb, int nv) {
-        for (int c = 0; c < nv / kQChunk; c++) {
-            const float4 *src = reinterpret_cast<const float4 *>(xrow + kb + c * kQChunk);
+        const int nc = nv / kQChunk;
+        for (int c0 = 0; c0 < nc; c0 += 4) {
+            float4 ld[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float4 *src = reinterpret_cast<const float4 *>(xrow + kb + min(c0 + u, nc - 1) * kQChunk);
+#pragma unroll
+                for (int i = 0; i < 4; i++) ld[u][i] = src[i];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+            const int c = c0 + u;
+            if (c >= nc) break;
             float v[16];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float4 q = src[i];
+                const float4 q = ld[u][i];
                 v[4 * i] = q.x, v[4 * i + 1] = q.y, v[4 * i + 2] = q.z, v[4 * i + 3] = q.w;
             }
             uint32_t hw[8], lw[8];
@@ -303,6 +316,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
             if (F == Q4_K) {
                 sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
                 if (!(part & 1)) xsum_s[c * 8 + (part >> 1)][tt] = sum;
+            }
             }
         }
     };
@@ -365,9 +379,10 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     // makes the compiler's wait counting wait for everything in flight.  A
     // chunk past the end runs with its scales zeroed (live = 0).
     QChunk<F> rs[R], rs2[R];
-    for (int kb = 0; kb < p.K; kb += kQStage) {
-        const int nv = min(kQStage, p.K - kb), nst = nv / kQChunk, c0 = kb / kQChunk;
-        if (kb > 0) __syncthreads();  // every wavefront is done with the previous stage
+    const int kspan = p.K / p.ksplit, kbeg = blockIdx.z * kspan;
+    for (int kb = kbeg; kb < kbeg + kspan; kb += kQStage) {
+        const int nv = min(kQStage, kbeg + kspan - kb), nst = nv / kQChunk, c0 = kb / kQChunk;
+        if (kb > kbeg) __syncthreads();  // every wavefront is done with the previous stage
 #pragma unroll
         for (int q = 0; q < R; q++) {
             rs[q].load(wrow, c0 + min(q, nst - 1), lg);
@@ -394,7 +409,9 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
         const int jrow = GROUPED ? ids[4 * lg + r] : j;
         float *dst = p.y ? p.y + (size_t)jrow * p.ldy + nn : nullptr;
         const float v = acc[r];
-        if (OUT == OUT_STORE) {
+        if ((OUT == OUT_STORE || OUT == OUT_ADD) && p.ksplit > 1) {
+            atomicAdd(dst, v);  // partial sum of this workgroup's reduction range (STORE rows zeroed first)
+        } else if (OUT == OUT_STORE) {
             *dst = v;
         } else if (OUT == OUT_ADD) {
             *dst = *dst + v;
@@ -453,13 +470,41 @@ bool qgemm_supported(int fmt, int K) {
            K % kQChunk == 0;
 }
 
+__global__ void zero_rows_kernel(float *y, int ldy, int M, int N) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < M * N) y[(size_t)(i / N) * ldy + i % N] = 0.f;
+}
+
+// Workgroups wanted for one product: every CU streams weights.
+static int qgemm_target_wgs() {
+    static int t = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        return n;
+    }();
+    return t;
+}
+
 hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                         float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s) {
     if (M < 1 || N < 1 || !qgemm_supported(fmt, K) || ldx % 4) return hipErrorInvalidValue;
-    QGemmKernel k = pick_qf<false>(fmt, out, K);
+    const int groups = (N + kQRows - 1) / kQRows, tiles = (M + 15) / 16;
+    // split the reduction over workgroups (results added atomically) when the
+    // row groups alone leave CUs idle; plain stores and adds only
+    int ks = 1;
+    if (out == OUT_STORE || out == OUT_ADD)
+        while (groups * tiles * ks * 2 <= qgemm_target_wgs() && (K / kQChunk) % (ks * 2) == 0) ks *= 2;
+    QGemmKernel k = pick_qf<false>(fmt, out, K / ks);
     if (!k) return hipErrorInvalidValue;
-    QGemmParams p{w, w2, stride, x, y, M, N, K, ldx, ldy, argmax, nullptr, nullptr, nullptr, 1, 0};
-    hipLaunchKernelGGL(k, dim3((N + kQRows - 1) / kQRows, (M + 15) / 16), dim3(256), 0, s, p);
+    if (ks > 1 && out == OUT_STORE) {
+        hipLaunchKernelGGL(zero_rows_kernel, dim3((M * N + 255) / 256), dim3(256), 0, s, y, ldy, M, N);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    QGemmParams p{w, w2, stride, x, y, M, N, K, ldx, ldy, argmax, nullptr, nullptr, nullptr, 1, 0, ks};
+    hipLaunchKernelGGL(k, dim3(groups, tiles, ks), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
@@ -470,7 +515,7 @@ hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, ui
     if (N < 1 || !qgemm_supported(fmt, K) || ldx % 4 || max_tiles < 1 || x_div < 1) return hipErrorInvalidValue;
     QGemmKernel k = pick_qf<true>(fmt, out, K);
     if (!k) return hipErrorInvalidValue;
-    QGemmParams p{w, w2, stride, x, y, 16, N, K, ldx, ldy, nullptr, tiles, list, ntiles, x_div, expert_stride};
+    QGemmParams p{w, w2, stride, x, y, 16, N, K, ldx, ldy, nullptr, tiles, list, ntiles, x_div, expert_stride, 1};
     hipLaunchKernelGGL(k, dim3((N + kQRows - 1) / kQRows, max_tiles), dim3(256), 0, s, p);
     return hipGetLastError();
 }
