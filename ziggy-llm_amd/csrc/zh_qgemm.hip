@@ -273,19 +273,20 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
         const int m = min(m0 + tt, M - 1);
         xrow = p.x + (size_t)(GROUPED ? ids[m] / p.x_div : m) * p.ldx + 16 * part;
     }
-    // chunks in batches of four: all loads of a batch in flight before the first LDS write
-    auto stage = [&](int kb, int nv) {
-        const int nc = nv / kQChunk;
-        for (int c0 = 0; c0 < nc; c0 += 4) {
-            float4 ld[4][4];
+    // A stage goes in batches of four chunks: stage_load issues a batch's
+    // loads into ld, stage_store splits and writes it (waiting for them).
+    float4 ld[4][4];
+    auto stage_load = [&](int kb, int nc, int c0) {
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const float4 *src = reinterpret_cast<const float4 *>(xrow + kb + min(c0 + u, nc - 1) * kQChunk);
+        for (int u = 0; u < 4; u++) {
+            const float4 *src = reinterpret_cast<const float4 *>(xrow + kb + min(c0 + u, nc - 1) * kQChunk);
 #pragma unroll
-                for (int i = 0; i < 4; i++) ld[u][i] = src[i];
-            }
+            for (int i = 0; i < 4; i++) ld[u][i] = src[i];
+        }
+    };
+    auto stage_store = [&](int nc, int c0) {
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < 4; u++) {
             const int c = c0 + u;
             if (c >= nc) break;
             float v[16];
@@ -317,57 +318,63 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
                 sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
                 if (!(part & 1)) xsum_s[c * 8 + (part >> 1)][tt] = sum;
             }
-            }
         }
     };
 
     qf4v acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
     // chunk cs of the stage (offset 256 cs in LDS)
+    // All products of the chunk first (independent accumulators, so the
+    // matrix core pipelines them), then the scales.
     auto compute = [&](const QChunk<F> &r, const QChunk<F> &r2, int cs, float live) {
+        constexpr int S = QChunk<F>::kSteps;
+        const qf4v zero = {0.f, 0.f, 0.f, 0.f};
+        qf4v dv[S], dv2[S];
+        float sv[S], mv[S], sv2[S], mv2[S];
 #pragma unroll
-        for (int j = 0; j < QChunk<F>::kSteps; j++) {
-            const qf4v zero = {0.f, 0.f, 0.f, 0.f};
-            float s, mn = 0.f, s2 = 0.f, mn2 = 0.f;
-            qf4v dv, dv2 = zero;
+        for (int j = 0; j < S; j++) {
+            mv[j] = 0.f, sv2[j] = 0.f, mv2[j] = 0.f;
+            dv2[j] = zero;
             const int kx = cs * kQChunk + kSub * j;
             if constexpr (kSub == 32) {
                 const bf8v ah = as_bf8(*reinterpret_cast<const uint4 *>(&xs_s[0][li][kx + 8 * lg]));
                 const bf8v al = as_bf8(*reinterpret_cast<const uint4 *>(&xs_s[1][li][kx + 8 * lg]));
-                const bf8v b = as_bf8(r.step(j, s, mn));
-                dv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, zero, 0, 0, 0);
-                dv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, dv, 0, 0, 0);
+                const bf8v b = as_bf8(r.step(j, sv[j], mv[j]));
+                dv[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, zero, 0, 0, 0);
+                dv[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, dv[j], 0, 0, 0);
                 if (kPair) {
-                    const bf8v b2 = as_bf8(r2.step(j, s2, mn2));
-                    dv2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b2, zero, 0, 0, 0);
-                    dv2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b2, dv2, 0, 0, 0);
+                    const bf8v b2 = as_bf8(r2.step(j, sv2[j], mv2[j]));
+                    dv2[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b2, zero, 0, 0, 0);
+                    dv2[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b2, dv2[j], 0, 0, 0);
                 }
             } else {
                 const s4v ah = as_s4(*reinterpret_cast<const uint2 *>(&xs_s[0][li][kx + 4 * lg]));
                 const s4v al = as_s4(*reinterpret_cast<const uint2 *>(&xs_s[1][li][kx + 4 * lg]));
-                const s4v b = as_s4(r.step(j, s));
-                dv = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, b, zero, 0, 0, 0);
-                dv = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, b, dv, 0, 0, 0);
+                const s4v b = as_s4(r.step(j, sv[j]));
+                dv[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, b, zero, 0, 0, 0);
+                dv[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, b, dv[j], 0, 0, 0);
                 if (kPair) {
-                    const s4v b2 = as_s4(r2.step(j, s2));
-                    dv2 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, b2, zero, 0, 0, 0);
-                    dv2 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, b2, dv2, 0, 0, 0);
+                    const s4v b2 = as_s4(r2.step(j, sv2[j]));
+                    dv2[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, b2, zero, 0, 0, 0);
+                    dv2[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, b2, dv2[j], 0, 0, 0);
                 }
             }
-            s *= live;
-            s2 *= live;
+        }
+#pragma unroll
+        for (int j = 0; j < S; j++) {
+            const float s = sv[j] * live, s2 = sv2[j] * live;
             if (F == Q4_K) {
                 const float4 xsm = *reinterpret_cast<const float4 *>(&xsum_s[cs * 8 + j][4 * lg]);
                 const float xm[4] = {xsm.x, xsm.y, xsm.z, xsm.w};
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    acc[q] = fmaf(s, dv[q], fmaf(-mn * live, xm[q], acc[q]));
-                    if (kPair) acc2[q] = fmaf(s2, dv2[q], fmaf(-mn2 * live, xm[q], acc2[q]));
+                    acc[q] = fmaf(s, dv[j][q], fmaf(-mv[j] * live, xm[q], acc[q]));
+                    if (kPair) acc2[q] = fmaf(s2, dv2[j][q], fmaf(-mv2[j] * live, xm[q], acc2[q]));
                 }
             } else {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    acc[q] = fmaf(s, dv[q], acc[q]);
-                    if (kPair) acc2[q] = fmaf(s2, dv2[q], acc2[q]);
+                    acc[q] = fmaf(s, dv[j][q], acc[q]);
+                    if (kPair) acc2[q] = fmaf(s2, dv2[j][q], acc2[q]);
                 }
             }
         }
@@ -383,12 +390,20 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     for (int kb = kbeg; kb < kbeg + kspan; kb += kQStage) {
         const int nv = min(kQStage, kbeg + kspan - kb), nst = nv / kQChunk, c0 = kb / kQChunk;
         if (kb > kbeg) __syncthreads();  // every wavefront is done with the previous stage
+        // the first batch of activations, then the ring's codes, then the
+        // LDS writes: the wait for the activations does not cover the codes
+        // (loads complete in order), and the codes stream during staging
+        stage_load(kb, nst, 0);
 #pragma unroll
         for (int q = 0; q < R; q++) {
             rs[q].load(wrow, c0 + min(q, nst - 1), lg);
             if (kPair) rs2[q].load(wrow2, c0 + min(q, nst - 1), lg);
         }
-        stage(kb, nv);
+        stage_store(nst, 0);
+        for (int b = 4; b < nst; b += 4) {
+            stage_load(kb, nst, b);
+            stage_store(nst, b);
+        }
         __syncthreads();
         for (int c = 0; c < nst; c += R) {
 #pragma unroll
