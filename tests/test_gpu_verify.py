@@ -54,6 +54,36 @@ def test_verify_accepts_the_greedy_stream(hip_ctx, name):
     s.close()
 
 
+LONG = {
+    # query heads per kv head 1, 4 and 8: 8, 2 and 1 queries per attention workgroup
+    "g1-hd64": dict(arch="llama", n_head=4, n_kv=4, context=512),
+    "g4-hd128-qknorm": dict(arch="qwen3", qk_norm=True, hidden=512, ffn=1024, n_head=4, n_kv=1, head_dim=128,
+                            default_type=Q8_0, attn_v_type=Q8_0, output_type=Q8_0, embd_type=Q8_0, context=512,
+                            rope_theta=1000000.0),
+    "g8-hd64": dict(arch="llama", hidden=512, n_head=8, n_kv=1, context=512),
+}
+
+
+@pytest.mark.parametrize("name", list(LONG))
+def test_verify_over_a_long_context(hip_ctx, name):
+    # 300 positions: several attention splits per query group, so the
+    # multi-query launch merges partials; the rows it stores feed the decode after
+    say(f"verify long {name}")
+    spec = synth.small_spec(**LONG[name])
+    img = synth.build(spec, seed=37)
+    prompt = synth.prompt_tokens(9, 300, spec.vocab)
+    want, _ = zo.Session(zo.Model(img.buf), context=spec.context, kv_f16=True).generate(prompt, 30)
+    want = [int(t) for t in want]
+    s = hip.Session(hip_ctx, img, context=spec.context)
+    _, st = s.generate(prompt, 0)
+    assert st.next_token == want[0]
+    pred, n = s.verify(want[0], want[1:12])
+    assert n == 12 and list(pred) == want[1:13]
+    got, _ = s.generate(np.array([want[12]], np.uint32), 8)
+    assert [int(t) for t in got] == want[13:21]
+    s.close()
+
+
 def test_verify_rejects_at_the_first_wrong_draft(hip_ctx):
     spec = synth.small_spec(**SMALL["llama-q4km"])
     img = synth.build(spec, seed=29)

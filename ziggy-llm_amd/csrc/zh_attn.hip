@@ -147,10 +147,12 @@ __device__ __forceinline__ float half_sum32(float v) {
     return v + __shfl_xor(v, 16, 64);
 }
 
-// Arrival of a split and, in the last workgroup of a kv head to arrive, the
-// merge of every split (partials stored with agent-scope write-through).
-template <int HD, int KG>
-__device__ __forceinline__ void split_merge(const AttnParams &p, int kvh, int G, int nsplit, int *last_ptr) {
+// Arrival of a split and, in the last workgroup of a kv head (partials slot)
+// to arrive, the merge of every split (partials stored with agent-scope
+// write-through); out_of(g) is head g's output row.
+template <int HD, int KG, class OutOf>
+__device__ __forceinline__ void split_merge(const AttnParams &p, int kvh, int G, int nsplit, int *last_ptr,
+                                            OutOf out_of) {
     const int tid = threadIdx.x;
     int &last_s = *last_ptr;
     constexpr int IPTM = (KG * HD / 2 + 255) / 256;
@@ -255,7 +257,7 @@ __device__ __forceinline__ void split_merge(const AttnParams &p, int kvh, int G,
         const int it = tid + 256 * k;
         if (it >= G * HD / 2) continue;
         const int g = it / (HD / 2), d2 = it % (HD / 2);
-        float *dst = p.out + (size_t)(kvh * G + g) * HD + 2 * d2;
+        float *dst = out_of(g) + 2 * d2;
         dst[0] = acc_merge[k][0] / fl_merge[g];
         dst[1] = acc_merge[k][1] / fl_merge[g];
     }
@@ -560,7 +562,8 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnParams p) {
                            __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    split_merge<HD, GG ? GG : kMaxGroup>(p, kvh, G, nsplit, &last_s);
+    split_merge<HD, GG ? GG : kMaxGroup>(p, kvh, G, nsplit, &last_s,
+                                         [&](int g) { return p.out + (size_t)(kvh * G + g) * HD; });
 }
 
 // ---------------------------------------------------------------------------
@@ -605,7 +608,12 @@ __device__ __forceinline__ h8v as_h8(uint4 v) {
     return r;
 }
 
-template <int HD, int GG>
+// MQ: several queries at consecutive positions (plain mode, q already
+// normed and rotated, their K/V rows already in the cache).  Workgroup z takes
+// queries qbase .. qbase + nqw - 1 (8 / Gq of them): query head g of query j
+// becomes column pair ("virtual head") j Gq + g, whose causal range ends at
+// its own position; splits cover the range of the last query.
+template <int HD, int GG, bool MQ>
 __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     constexpr int KS = HD / 32;  // 32-dim steps of the scores, 32-dim chunks of the values
     constexpr int TP = 32;       // positions per wavefront tile
@@ -613,7 +621,13 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     constexpr int LPR = HD / 8;  // lanes per value row (8 dims each)
     const int split = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-    const int pos = p.position_dev ? *p.position_dev : p.position;
+    const int Gq = GG ? GG : p.head_count / p.head_count_kv;  // query heads per kv head
+    const int qpw = MQ ? kMaxGroup / Gq : 1, qbase = MQ ? blockIdx.z * qpw : 0;
+    const int nqw = MQ ? min(qpw, p.n_query - qbase) : 1;
+    const int slot = MQ ? kvh + p.head_count_kv * blockIdx.z : kvh;  // partials / arrival counter
+    const int pos0 = p.position_dev ? *p.position_dev : p.position;
+    const int pos = pos0 + qbase + nqw - 1;  // the last query's position
+    const int pos_col = MQ ? pos0 + qbase + (li >> 1) / Gq : pos;  // causal end of column li
     const int n_total = pos + 1 - p.window_start;
     const int units = (n_total + TP - 1) / TP;
     const int per = (units + p.max_splits - 1) / p.max_splits;  // tiles per split
@@ -621,8 +635,8 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     if (split >= nsplit) return;
     const int u_begin = split * per, nu = min(per, units - u_begin);
     const int ntw = nu > wave ? (nu - wave + 3) / 4 : 0;  // this wavefront's tiles
-    const int G = GG ? GG : p.head_count / p.head_count_kv;
-    const bool fused = p.k_new != nullptr;
+    const int G = MQ ? nqw * Gq : Gq;                         // (virtual) heads of the workgroup
+    const bool fused = !MQ && p.k_new != nullptr;
     const bool own_pos = fused && u_begin + nu == units;  // this split holds the current position
 
     __shared__ float q_s[kMaxGroup][HD];
@@ -652,8 +666,13 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
         const int idx = tid + 256 * i;
         qv[i] = 0.f;
         if (idx < nq) {
-            qv[i] = p.q[(size_t)kvh * nq + idx];
-            if (fused && p.q_bias) qv[i] += p.q_bias[(size_t)kvh * nq + idx];
+            if (MQ) {
+                const int gv = idx / HD, j = gv / Gq;
+                qv[i] = p.q[(size_t)(qbase + j) * p.q_stride + (size_t)(kvh * Gq + gv - j * Gq) * HD + idx % HD];
+            } else {
+                qv[i] = p.q[(size_t)kvh * nq + idx];
+                if (fused && p.q_bias) qv[i] += p.q_bias[(size_t)kvh * nq + idx];
+            }
         }
     }
     {
@@ -786,7 +805,7 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
                     // rows 4 lg + r of the tile; the two pieces of a head sit in lanes 2g, 2g + 1
                     float v = acc[r];
                     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
-                    const bool valid = have && col_ok && b + 16 * rt + 4 * lg + r <= pos;
+                    const bool valid = have && col_ok && b + 16 * rt + 4 * lg + r <= pos_col;
                     sc[tt][rt][r] = valid ? v : -INFINITY;
                 }
             }
@@ -902,6 +921,13 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
         fl_s[tid] = L;
     }
     __syncthreads();
+    auto out_of = [&](int g) {
+        if (MQ) {
+            const int j = g / Gq;
+            return p.out + (size_t)(qbase + j) * p.out_stride + (size_t)(kvh * Gq + g - j * Gq) * HD;
+        }
+        return p.out + (size_t)(kvh * G + g) * HD;
+    };
     // pairs of dims: one 64-bit write-through store per pair
     for (int it = tid; it < G * HD / 2; it += 256) {
         const int g = it / (HD / 2), d = 2 * (it % (HD / 2));
@@ -911,11 +937,11 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
         const float2 a3 = *reinterpret_cast<const float2 *>(&o_s[3][g][d]);
         const float x0 = (a0.x + a1.x) + (a2.x + a3.x), x1 = (a0.y + a1.y) + (a2.y + a3.y);
         if (nsplit == 1) {
-            float *dst = p.out + (size_t)(kvh * G + g) * HD + d;
+            float *dst = out_of(g) + d;
             dst[0] = x0 / fl_s[g];
             dst[1] = x1 / fl_s[g];
         } else {
-            const size_t e = (((size_t)kvh * p.max_splits + split) * kMaxGroup + g) * HD + d;
+            const size_t e = (((size_t)slot * p.max_splits + split) * kMaxGroup + g) * HD + d;
             const unsigned long long v = (unsigned long long)__float_as_uint(x0) |
                                          ((unsigned long long)__float_as_uint(x1) << 32);
             __hip_atomic_store(reinterpret_cast<unsigned long long *>(p.part_o + e), v, __ATOMIC_RELAXED,
@@ -924,13 +950,13 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     }
     if (nsplit == 1) return;
     if (tid < G) {
-        const size_t e = ((size_t)kvh * p.max_splits + split) * kMaxGroup + tid;
+        const size_t e = ((size_t)slot * p.max_splits + split) * kMaxGroup + tid;
         const unsigned long long v = (unsigned long long)__float_as_uint(fm_s[tid]) |
                                      ((unsigned long long)__float_as_uint(fl_s[tid]) << 32);
         __hip_atomic_store(reinterpret_cast<unsigned long long *>(p.part_ml) + e, v, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
-    split_merge<HD, GG ? GG : kMaxGroup>(p, kvh, G, nsplit, &last_s);
+    split_merge<HD, (GG && !MQ) ? GG : kMaxGroup>(p, slot, G, nsplit, &last_s, out_of);  // MQ: up to 8 virtual heads
 }
 
 size_t attention_scratch_floats(int head_count, int head_dim, int max_splits) {
@@ -968,22 +994,109 @@ int attention_splits(int kv_heads, int max_positions) {
     return s < chunks ? s : chunks;
 }
 
+// The q/k/v epilogue of n_query tokens at positions position .. ahead of a
+// multi-query attention launch: workgroup (token m, kv head) adds the biases,
+// runs the per-head RMSNorm and RoPE of the group's q heads (written to
+// q_out, which may be q itself) and of k, and stores k and v as binary16 at
+// position + m -- the arithmetic of the fused single-query kernel, in the
+// same order and thread layout.
+template <int HD>
+__global__ void __launch_bounds__(256) attn_prep_kernel(AttnParams p, float *q_out) {
+    constexpr int QV = kMaxGroup * HD / 256;
+    const int m = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const int G = p.head_count / p.head_count_kv, nq = G * HD, pos = p.position + m;
+    __shared__ float q_s[kMaxGroup * HD];
+    __shared__ float kn_s[HD];
+    __shared__ float red16[4 * QV_MAX];
+    __shared__ float cs_s[HD / 2], sn_s[HD / 2];
+    const float *qrow = p.q + (size_t)m * p.q_stride + (size_t)kvh * nq;
+    const size_t kv_off = (size_t)m * p.kv_dim + (size_t)kvh * HD;
+    float qv[QV], kx[1];
+#pragma unroll
+    for (int i = 0; i < QV; i++) {
+        const int idx = tid + 256 * i;
+        qv[i] = 0.f;
+        if (idx < nq) {
+            qv[i] = qrow[idx];
+            if (p.q_bias) qv[i] += p.q_bias[(size_t)kvh * nq + idx];
+        }
+    }
+    kx[0] = p.k_new[kv_off + (tid & (HD - 1))];
+    float vx = p.v_new[kv_off + (tid & (HD - 1))];
+    if (tid < HD) {
+        if (p.k_bias) kx[0] += p.k_bias[(size_t)kvh * HD + tid];
+        if (p.v_bias) vx += p.v_bias[(size_t)kvh * HD + tid];
+    }
+    const int n_rot = p.rope_dim < HD ? p.rope_dim : HD;
+    rope_table(n_rot, p.rope_base, pos, cs_s, sn_s);
+    norm_rope<HD, QV>(qv, nq, p.q_norm, p.eps, n_rot, p.rope_style, cs_s, sn_s, q_s, red16);
+    norm_rope<HD, 1>(kx, HD, p.k_norm, p.eps, n_rot, p.rope_style, cs_s, sn_s, kn_s, red16);
+    float *qo = q_out + (size_t)m * p.q_stride + (size_t)kvh * nq;
+    for (int idx = tid; idx < nq; idx += 256) qo[idx] = q_s[idx];
+    if (tid < HD && pos < p.ctx) {
+        const size_t idx = (size_t)pos * p.kv_dim + (size_t)kvh * HD + tid;
+        p.k_cache[idx] = __float2half_rn(kn_s[tid]);
+        p.v_cache[idx] = __float2half_rn(vx);
+    }
+}
+
+hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t s) {
+    if (p.head_count_kv <= 0 || p.head_count % p.head_count_kv || p.head_count / p.head_count_kv > kMaxGroup ||
+        p.n_query < 1 || !p.q || !p.k_new || !p.v_new || !q_out || p.q_stride < p.head_count * p.head_dim)
+        return hipErrorInvalidValue;
+    const dim3 grid(p.n_query, p.head_count_kv);
+    switch (p.head_dim) {
+    case 64: hipLaunchKernelGGL(attn_prep_kernel<64>, grid, dim3(256), 0, s, p, q_out); break;
+    case 128: hipLaunchKernelGGL(attn_prep_kernel<128>, grid, dim3(256), 0, s, p, q_out); break;
+    case 256: hipLaunchKernelGGL(attn_prep_kernel<256>, grid, dim3(256), 0, s, p, q_out); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+bool attention_multi_supported(int head_dim) { return (head_dim == 64 || head_dim == 128) && !attention_valu(); }
+
+int attention_query_groups(int head_count, int head_count_kv, int n_query) {
+    const int G = head_count_kv > 0 ? head_count / head_count_kv : 1, qpw = G > 0 && G <= kMaxGroup ? kMaxGroup / G : 1;
+    return (n_query + qpw - 1) / qpw;
+}
+
 hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
     if (p.head_count_kv <= 0 || p.head_count % p.head_count_kv || p.head_count / p.head_count_kv > kMaxGroup ||
         p.max_splits < 1 || !p.counters)
         return hipErrorInvalidValue;
-    const dim3 grid(p.max_splits, p.head_count_kv);
     const int G = p.head_count / p.head_count_kv;
+    if (p.n_query > 1) {
+        // several queries: plain mode on the matrix-core kernel only
+        if (p.k_new || !attention_multi_supported(p.head_dim) || p.position_dev ||
+            p.q_stride < p.head_count * p.head_dim || p.out_stride < p.head_count * p.head_dim)
+            return hipErrorInvalidValue;
+        const dim3 grid(p.max_splits, p.head_count_kv, attention_query_groups(p.head_count, p.head_count_kv, p.n_query));
+        auto go = [&](auto hd_tag) {
+            constexpr int HD = decltype(hd_tag)::value;
+            switch (G) {
+            case 1: hipLaunchKernelGGL((attn_mfma_kernel<HD, 1, true>), grid, dim3(256), 0, s, p); break;
+            case 2: hipLaunchKernelGGL((attn_mfma_kernel<HD, 2, true>), grid, dim3(256), 0, s, p); break;
+            case 4: hipLaunchKernelGGL((attn_mfma_kernel<HD, 4, true>), grid, dim3(256), 0, s, p); break;
+            case 8: hipLaunchKernelGGL((attn_mfma_kernel<HD, 8, true>), grid, dim3(256), 0, s, p); break;
+            default: hipLaunchKernelGGL((attn_mfma_kernel<HD, 0, true>), grid, dim3(256), 0, s, p); break;
+            }
+        };
+        if (p.head_dim == 64) go(std::integral_constant<int, 64>{});
+        else go(std::integral_constant<int, 128>{});
+        return hipGetLastError();
+    }
+    const dim3 grid(p.max_splits, p.head_count_kv);
     auto go = [&](auto hd_tag) {
         constexpr int HD = decltype(hd_tag)::value;
         if constexpr (HD <= 128) {
             if (!attention_valu()) {
                 switch (G) {
-                case 1: hipLaunchKernelGGL((attn_mfma_kernel<HD, 1>), grid, dim3(256), 0, s, p); break;
-                case 2: hipLaunchKernelGGL((attn_mfma_kernel<HD, 2>), grid, dim3(256), 0, s, p); break;
-                case 4: hipLaunchKernelGGL((attn_mfma_kernel<HD, 4>), grid, dim3(256), 0, s, p); break;
-                case 8: hipLaunchKernelGGL((attn_mfma_kernel<HD, 8>), grid, dim3(256), 0, s, p); break;
-                default: hipLaunchKernelGGL((attn_mfma_kernel<HD, 0>), grid, dim3(256), 0, s, p); break;
+                case 1: hipLaunchKernelGGL((attn_mfma_kernel<HD, 1, false>), grid, dim3(256), 0, s, p); break;
+                case 2: hipLaunchKernelGGL((attn_mfma_kernel<HD, 2, false>), grid, dim3(256), 0, s, p); break;
+                case 4: hipLaunchKernelGGL((attn_mfma_kernel<HD, 4, false>), grid, dim3(256), 0, s, p); break;
+                case 8: hipLaunchKernelGGL((attn_mfma_kernel<HD, 8, false>), grid, dim3(256), 0, s, p); break;
+                default: hipLaunchKernelGGL((attn_mfma_kernel<HD, 0, false>), grid, dim3(256), 0, s, p); break;
                 }
                 return;
             }

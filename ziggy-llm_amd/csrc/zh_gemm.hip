@@ -231,7 +231,7 @@ hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t st
                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
                        bool precise) {
     if (M < 1 || N < 1 || K < 16 || K % 16 || ldx % 4) return hipErrorInvalidValue;
-    if (!precise && qgemm_enabled() && qgemm_supported(fmt, K))
+    if (!precise && qgemm_enabled() && qgemm_supported(fmt, K, w, w2, stride, 0))
         return launch_qgemm(fmt, w, w2, stride, x, ldx, y, ldy, M, N, K, out, argmax, s);
     GemmKernel k = nullptr;
     if (precise) {
@@ -269,7 +269,7 @@ hipError_t launch_gemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uin
                                const float *x, int ldx, int x_div, float *y, int ldy, int N, int K, int out,
                                const int *tiles, const int *list, const int *ntiles, int max_tiles, hipStream_t s) {
     if (N < 1 || K < 16 || K % 16 || ldx % 4 || max_tiles < 1 || x_div < 1) return hipErrorInvalidValue;
-    if (qgemm_enabled() && qgemm_supported(fmt, K))
+    if (qgemm_enabled() && qgemm_supported(fmt, K, w, w2, stride, expert_stride))
         return launch_qgemm_grouped(fmt, w, w2, stride, expert_stride, x, ldx, x_div, y, ldy, N, K, out, tiles, list,
                                     ntiles, max_tiles, s);
     GemmKernel k = nullptr;

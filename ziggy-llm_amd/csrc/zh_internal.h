@@ -144,7 +144,7 @@ hipError_t launch_gemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uin
                                const float *x, int ldx, int x_div, float *y, int ldy, int N, int K, int out,
                                const int *tiles, const int *list, const int *ntiles, int max_tiles, hipStream_t s);
 // Exact-code MFMA kernel (zh_qgemm.hip) for the quantized formats, K a multiple of 256.
-bool qgemm_supported(int fmt, int K);
+bool qgemm_supported(int fmt, int K, const void *w, const void *w2, uint64_t stride, uint64_t expert_stride);
 hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                         float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s);
 hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride,
@@ -185,8 +185,18 @@ struct AttnParams {
     float eps, rope_base;
     int rope_dim, rope_style;
     int ctx;                   // cache capacity in positions (no store at or past it)
+    // several queries (plain mode, matrix-core kernel): queries at positions
+    // position .. position + n_query - 1, rows q_stride / out_stride floats apart
+    int n_query, q_stride, out_stride;
 };
 hipError_t launch_attention(const AttnParams &p, hipStream_t s);
+// q/k/v epilogue of n_query tokens (rows q_stride / kv_dim apart): roped q to
+// q_out (may be q), k and v stored to the cache at position + m.
+hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t s);
+bool attention_multi_supported(int head_dim);
+// workgroups along the query axis of a multi-query launch (its partials and
+// arrival counters: head_count_kv * groups slots)
+int attention_query_groups(int head_count, int head_count_kv, int n_query);
 // Splits of the attention grid for kv_heads heads and up to max_positions keys.
 int attention_splits(int kv_heads, int max_positions);
 size_t attention_scratch_floats(int head_count, int head_dim, int max_splits);

@@ -22,11 +22,15 @@
 // results and applies row li's scales itself: no scale exchange.
 //
 // A workgroup (4 wavefronts) takes 64 weight rows (16 per wavefront) of one
-// token tile (16 tokens) over the whole reduction.  The activations go
+// token tile (16 tokens) over its reduction range.  The activations go
 // through LDS in stages of up to 2048 values (128 KB of bf16 pieces for 16
-// tokens), split once per workgroup; within a stage the wavefronts run
-// without barriers, each streaming its rows' codes through a ring of four
-// 256-value chunks.
+// tokens), split once per workgroup.  Each wavefront streams its 16 rows'
+// codes chunk by chunk (256 values): the chunk bytes of a row are loaded as
+// whole 16-byte windows (consecutive lanes, consecutive windows: every load
+// instruction reads a few rows' bytes contiguously) into a ring of R chunks in
+// registers, then copied into the wavefront's own LDS image of the 16 rows,
+// from which each lane reads the fields of its row in the product layout.  No
+// workgroup barrier inside a stage; the ring runs across stages.
 #include "zh_internal.h"
 #include "zh_quant.h"
 
@@ -35,10 +39,10 @@ namespace zh {
 typedef __bf16 bf8v __attribute__((ext_vector_type(8)));
 typedef short s4v __attribute__((ext_vector_type(4)));
 typedef float qf4v __attribute__((ext_vector_type(4)));
+typedef uint32_t qu4v __attribute__((ext_vector_type(4)));
 
 constexpr int kQRows = 64;    // weight rows per workgroup (16 per wavefront)
 constexpr int kQChunk = 256;  // reduction values per staged chunk
-constexpr int kQStage = 2048; // reduction values staged in LDS at once
 
 struct QGemmParams {
     const uint8_t *w, *w2;  // W row 0 (w2: the up matrix of SWIGLU)
@@ -86,23 +90,40 @@ __device__ __forceinline__ uint2 codes_u4(uint32_t a, float off) {
     return {pack_bf(ub(a, 0) - off, ub(a, 1) - off), pack_bf(ub(a, 2) - off, ub(a, 3) - off)};
 }
 
-// ---- per-format chunk (256 values of one row): raw words and sub-block steps ----
+// ---- per-format chunk (256 values of one row): fields and sub-block steps ----
 //
-// load(row, c, lg): the words lane group lg needs of chunk c of `row`.
-// Steps: kSteps sub-blocks of kSub values; step(j) gives the lane's codes for
-// values kSub/4 * lg .. of sub-block j and the sub-block's scale (and min).
+// kCB: bytes of a chunk row; kShm: the bits its address can have below 16
+// when the matrix starts 16-byte aligned (row and chunk sizes are multiples of
+// 16, 8 or 2).  A staged chunk row sits in LDS at byte offset sh (its address
+// mod 16): load(r, sh, lg) reads the words lane group lg needs from the row
+// image r.  Steps: kSteps sub-blocks of kSub values; step(j) gives the lane's
+// codes for values kSub/4 * lg .. of sub-block j and the sub-block's scale
+// (and min).
+
+// bytes o .. o + 3 of a staged row image (o even)
+template <int SHM> __device__ __forceinline__ uint32_t rw4(const uint32_t *r, int o) {
+    const uint32_t lo = r[o >> 2];
+    if constexpr ((SHM & 3) == 0) {
+        // sh has no bits below 4: o & 3 is a compile-time constant here
+        return (o & 3) ? __builtin_amdgcn_alignbyte(r[(o >> 2) + 1], lo, o & 3) : lo;
+    } else {
+        return __builtin_amdgcn_alignbyte(r[(o >> 2) + 1], lo, o & 3);
+    }
+}
+// bytes o, o + 1 (o even)
+__device__ __forceinline__ uint32_t rw2(const uint32_t *r, int o) { return (r[o >> 2] >> (8 * (o & 2))) & 0xFFFFu; }
 
 template <int F> struct QChunk;
 
 template <> struct QChunk<Q4_K> {
-    static constexpr int kSub = 32, kSteps = 8;
+    static constexpr int kSub = 32, kSteps = 8, kCB = 144, kShm = 0;
     uint4 hd;     // d, dmin, 12 scale bytes
     uint2 q[4];   // qs[32 g + 8 lg .. + 7] of group g
-    __device__ __forceinline__ void load(const uint8_t *row, int c, int lg) {
-        const uint8_t *blk = row + (size_t)c * 144;
-        hd = ld16(blk);
+    __device__ __forceinline__ void load(const uint32_t *r, int sh, int lg) {
+        hd = {rw4<kShm>(r, sh), rw4<kShm>(r, sh + 4), rw4<kShm>(r, sh + 8), rw4<kShm>(r, sh + 12)};
 #pragma unroll
-        for (int g = 0; g < 4; g++) q[g] = ld8(blk + 16 + 32 * g + 8 * lg);
+        for (int g = 0; g < 4; g++)
+            q[g] = {rw4<kShm>(r, sh + 16 + 32 * g + 8 * lg), rw4<kShm>(r, sh + 20 + 32 * g + 8 * lg)};
     }
     __device__ __forceinline__ uint32_t sbyte(int k) const {
         const uint32_t w = k < 4 ? hd.y : k < 8 ? hd.z : hd.w;
@@ -127,15 +148,14 @@ template <> struct QChunk<Q4_K> {
 };
 
 template <> struct QChunk<Q8_0> {
-    static constexpr int kSub = 32, kSteps = 8;
+    static constexpr int kSub = 32, kSteps = 8, kCB = 272, kShm = 0;
     uint2 q[8];
     uint32_t d[8];
-    __device__ __forceinline__ void load(const uint8_t *row, int c, int lg) {
-        const uint8_t *p = row + (size_t)c * 8 * 34;
+    __device__ __forceinline__ void load(const uint32_t *r, int sh, int lg) {
 #pragma unroll
         for (int b = 0; b < 8; b++) {
-            q[b] = ld8(p + 34 * b + 2 + 8 * lg);
-            d[b] = ld2(p + 34 * b);
+            q[b] = {rw4<kShm>(r, sh + 34 * b + 2 + 8 * lg), rw4<kShm>(r, sh + 34 * b + 6 + 8 * lg)};
+            d[b] = rw2(r, sh + 34 * b);
         }
     }
     __device__ __forceinline__ uint4 step(int j, float &s, float &mn) const {
@@ -146,15 +166,17 @@ template <> struct QChunk<Q8_0> {
 };
 
 template <> struct QChunk<IQ4_XS> {
-    static constexpr int kSub = 32, kSteps = 8;
+    static constexpr int kSub = 32, kSteps = 8, kCB = 136, kShm = 8;
     uint2 hd;     // d, scales_h, scales_l[4]
     uint2 q[8];   // qs[16 ib + 8 (lg & 1) ..]
     int hi;       // lane groups 2, 3 take the high nibbles (values 16..31)
-    __device__ __forceinline__ void load(const uint8_t *row, int c, int lg) {
-        const uint8_t *blk = row + (size_t)c * 136;
-        hd = ld8(blk);
+    __device__ __forceinline__ void load(const uint32_t *r, int sh, int lg) {
+        hd = {rw4<kShm>(r, sh), rw4<kShm>(r, sh + 4)};
 #pragma unroll
-        for (int ib = 0; ib < 8; ib++) q[ib] = ld8(blk + 8 + 16 * ib + 8 * (lg & 1));
+        for (int ib = 0; ib < 8; ib++) {
+            const int o = sh + 8 + 16 * ib + 8 * (lg & 1);
+            q[ib] = {rw4<kShm>(r, o), rw4<kShm>(r, o + 4)};
+        }
         hi = lg >> 1;
     }
     // dequantizeRowIQ4XS (model/quant_extra.zig:191-246): dl = d * (ls - 32)
@@ -170,23 +192,22 @@ template <> struct QChunk<IQ4_XS> {
 
 // 16-value sub-blocks: a step is one 16x16x16 product (four codes per lane)
 template <> struct QChunk<Q6_K> {
-    static constexpr int kSub = 16, kSteps = 16;
+    static constexpr int kSub = 16, kSteps = 16, kCB = 210, kShm = 14;
     uint32_t ql[2][2][2];  // [half][16-run][ql offset 0 / 32]
     uint32_t qh[2][2];     // [half][16-run]
     uint4 sc;              // 16 int8 scales
     uint32_t d;
-    __device__ __forceinline__ void load(const uint8_t *row, int c, int lg) {
-        const uint8_t *blk = row + (size_t)c * 210;
+    __device__ __forceinline__ void load(const uint32_t *rw, int sh, int lg) {
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
             for (int r = 0; r < 2; r++) {
-                ql[h][r][0] = ld4(blk + 64 * h + 16 * r + 4 * lg);
-                ql[h][r][1] = ld4(blk + 64 * h + 32 + 16 * r + 4 * lg);
-                qh[h][r] = ld4(blk + 128 + 32 * h + 16 * r + 4 * lg);
+                ql[h][r][0] = rw4<kShm>(rw, sh + 64 * h + 16 * r + 4 * lg);
+                ql[h][r][1] = rw4<kShm>(rw, sh + 64 * h + 32 + 16 * r + 4 * lg);
+                qh[h][r] = rw4<kShm>(rw, sh + 128 + 32 * h + 16 * r + 4 * lg);
             }
-        sc = ld16(blk + 192);
-        d = ld2(blk + 208);
+        sc = {rw4<kShm>(rw, sh + 192), rw4<kShm>(rw, sh + 196), rw4<kShm>(rw, sh + 200), rw4<kShm>(rw, sh + 204)};
+        d = rw2(rw, sh + 208);
     }
     // dequantizeRowQ6K (model/loader.zig:3728-3761): sub-block j = (half, quarter, 16-run)
     __device__ __forceinline__ uint2 step(int j, float &s) const {
@@ -202,23 +223,22 @@ template <> struct QChunk<Q6_K> {
 };
 
 template <> struct QChunk<Q3_K> {
-    static constexpr int kSub = 16, kSteps = 16;
+    static constexpr int kSub = 16, kSteps = 16, kCB = 110, kShm = 14;
     uint32_t qs[2][2];  // [half h][16-run]: qs[32 h + 16 r + 4 lg ..]
     uint32_t hm[2];     // [16-run]: hmask[16 r + 4 lg ..]
     uint32_t raw[3];    // 12 packed scale bytes
     uint32_t d;
-    __device__ __forceinline__ void load(const uint8_t *row, int c, int lg) {
-        const uint8_t *blk = row + (size_t)c * 110;
+    __device__ __forceinline__ void load(const uint32_t *rw, int sh, int lg) {
 #pragma unroll
         for (int r = 0; r < 2; r++) {
-            hm[r] = ld4(blk + 16 * r + 4 * lg);
+            hm[r] = rw4<kShm>(rw, sh + 16 * r + 4 * lg);
 #pragma unroll
-            for (int h = 0; h < 2; h++) qs[h][r] = ld4(blk + 32 + 32 * h + 16 * r + 4 * lg);
+            for (int h = 0; h < 2; h++) qs[h][r] = rw4<kShm>(rw, sh + 32 + 32 * h + 16 * r + 4 * lg);
         }
-        raw[0] = ld4(blk + 96);
-        raw[1] = ld4(blk + 100);
-        raw[2] = ld4(blk + 104);
-        d = ld2(blk + 108);
+        raw[0] = rw4<kShm>(rw, sh + 96);
+        raw[1] = rw4<kShm>(rw, sh + 100);
+        raw[2] = rw4<kShm>(rw, sh + 104);
+        d = rw2(rw, sh + 108);
     }
     // dequantizeRowQ3K / expandQ3KScales (model/quant_extra.zig:45-126, 248-279):
     // sub-block si = 8 h + 2 j + half16; q = low 2 bits - (hmask bit ? 0 : 4)
@@ -242,7 +262,22 @@ __device__ __forceinline__ uint32_t ordered_bits_q(float v) {
 template <int F, int OUT, bool GROUPED, int R>
 __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     constexpr bool kPair = OUT == OUT_SWIGLU;
-    constexpr int kSub = QChunk<F>::kSub;
+    constexpr int kMats = kPair ? 2 : 1;
+    using QC = QChunk<F>;
+    constexpr int kSub = QC::kSub, kCB = QC::kCB, kShm = QC::kShm;
+    // A chunk row at any offset kShm allows lies in kWin 16-byte windows.  Its
+    // LDS image has one spare window (a word read past the last byte) and an
+    // odd window count, so the 16 rows' words fall in distinct banks.
+    constexpr int kWin = (kCB + kShm + 15) / 16;
+    constexpr int kRowW = 4 * ((kWin + 1) | 1);
+    constexpr int kPieces = 16 * kWin, kP = (kPieces + 63) / 64;  // windows per wavefront chunk, per lane
+    constexpr bool kXsum = F == Q4_K;
+    constexpr int kCodeBytes = 4 * kMats * 16 * kRowW * 4;
+    constexpr int kStage =
+        (2 * 16 * (2048 + 8) * 2 + (kXsum ? 2048 / 32 * 16 * 4 : 64) + kCodeBytes <= 160 * 1024) ? 2048 : 1024;
+    constexpr int kStageChunks = kStage / kQChunk;
+    static_assert(kStageChunks % R == 0, "stages hold whole rings");
+
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
     int m0 = blockIdx.y * 16, M = p.M;
     const int *ids = nullptr;
@@ -258,14 +293,16 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     }
     const int n0 = blockIdx.x * kQRows + 16 * wave;
     const int n = min(n0 + li, p.N - 1);  // this lane's weight row (clamped; dropped at the store)
-    const uint8_t *wrow = w + (uint64_t)n * p.stride;
-    const uint8_t *wrow2 = kPair ? w2 + (uint64_t)n * p.stride : nullptr;
+    const uint8_t *wrow[kMats];
+    wrow[0] = w + (uint64_t)n * p.stride;
+    if (kPair) wrow[kMats - 1] = w2 + (uint64_t)n * p.stride;
 
-    // The activations of a stage (up to kQStage values of all 16 tokens) sit in
+    // The activations of a stage (up to kStage values of all 16 tokens) sit in
     // LDS as bf16 hi / lo pieces; thread (token tt, part) stages values
     // 16 part + 256 i of its token.
-    __shared__ __align__(16) unsigned short xs_s[2][16][kQStage + 8];  // [hi / lo][token][k]
-    __shared__ __align__(16) float xsum_s[kQStage / 32][16];          // [32-value sub-block][token]
+    __shared__ __align__(16) unsigned short xs_s[2][16][kStage + 8];  // [hi / lo][token][k]
+    __shared__ __align__(16) float xsum_s[kXsum ? kStage / 32 : 1][16];  // [32-value sub-block][token]
+    __shared__ __align__(16) uint32_t code_s[4][kMats][16 * kRowW];   // [wavefront][matrix][row image]
     const int tt = tid >> 4, part = tid & 15;
     const bool tok_ok = m0 + tt < M;
     const float *xrow;
@@ -273,22 +310,21 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
         const int m = min(m0 + tt, M - 1);
         xrow = p.x + (size_t)(GROUPED ? ids[m] / p.x_div : m) * p.ldx + 16 * part;
     }
-    // A stage goes in batches of four chunks: stage_load issues a batch's
-    // loads into ld, stage_store splits and writes it (waiting for them).
-    float4 ld[4][4];
-    auto stage_load = [&](int kb, int nc, int c0) {
+    // stage_load issues the whole stage's activation loads (clamped to its
+    // last chunk: unconditional, so the compiler's wait counting stays exact)
+    // into ld; stage_store splits every chunk and writes those of the stage.
+    float4 ld[kStageChunks][4];
+    auto stage_load = [&](int kb, int nc) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const float4 *src = reinterpret_cast<const float4 *>(xrow + kb + min(c0 + u, nc - 1) * kQChunk);
+        for (int u = 0; u < kStageChunks; u++) {
+            const float4 *src = reinterpret_cast<const float4 *>(xrow + kb + min(u, nc - 1) * kQChunk);
 #pragma unroll
             for (int i = 0; i < 4; i++) ld[u][i] = src[i];
         }
     };
-    auto stage_store = [&](int nc, int c0) {
+    auto stage_store = [&](int nc) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int c = c0 + u;
-            if (c >= nc) break;
+        for (int u = 0; u < kStageChunks; u++) {
             float v[16];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -308,15 +344,15 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
                 sum += (__uint_as_float(ha << 16) + __uint_as_float(la << 16)) +
                        (__uint_as_float(hb << 16) + __uint_as_float(lb << 16));
             }
-            uint4 *dh = reinterpret_cast<uint4 *>(&xs_s[0][tt][c * kQChunk + 16 * part]);
-            uint4 *dl = reinterpret_cast<uint4 *>(&xs_s[1][tt][c * kQChunk + 16 * part]);
-            dh[0] = {hw[0], hw[1], hw[2], hw[3]};
-            dh[1] = {hw[4], hw[5], hw[6], hw[7]};
-            dl[0] = {lw[0], lw[1], lw[2], lw[3]};
-            dl[1] = {lw[4], lw[5], lw[6], lw[7]};
-            if (F == Q4_K) {
-                sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
-                if (!(part & 1)) xsum_s[c * 8 + (part >> 1)][tt] = sum;
+            if (kXsum) sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
+            if (u < nc) {
+                uint4 *dh = reinterpret_cast<uint4 *>(&xs_s[0][tt][u * kQChunk + 16 * part]);
+                uint4 *dl = reinterpret_cast<uint4 *>(&xs_s[1][tt][u * kQChunk + 16 * part]);
+                dh[0] = {hw[0], hw[1], hw[2], hw[3]};
+                dh[1] = {hw[4], hw[5], hw[6], hw[7]};
+                dl[0] = {lw[0], lw[1], lw[2], lw[3]};
+                dl[1] = {lw[4], lw[5], lw[6], lw[7]};
+                if (kXsum && !(part & 1)) xsum_s[u * 8 + (part >> 1)][tt] = sum;
             }
         }
     };
@@ -325,8 +361,8 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     // chunk cs of the stage (offset 256 cs in LDS)
     // All products of the chunk first (independent accumulators, so the
     // matrix core pipelines them), then the scales.
-    auto compute = [&](const QChunk<F> &r, const QChunk<F> &r2, int cs, float live) {
-        constexpr int S = QChunk<F>::kSteps;
+    auto compute = [&](const QC &r, const QC &r2, int cs, float live) {
+        constexpr int S = QC::kSteps;
         const qf4v zero = {0.f, 0.f, 0.f, 0.f};
         qf4v dv[S], dv2[S];
         float sv[S], mv[S], sv2[S], mv2[S];
@@ -362,7 +398,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
 #pragma unroll
         for (int j = 0; j < S; j++) {
             const float s = sv[j] * live, s2 = sv2[j] * live;
-            if (F == Q4_K) {
+            if (kXsum) {
                 const float4 xsm = *reinterpret_cast<const float4 *>(&xsum_s[cs * 8 + j][4 * lg]);
                 const float xm[4] = {xsm.x, xsm.y, xsm.z, xsm.w};
 #pragma unroll
@@ -380,39 +416,95 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
         }
     };
 
-    // Stages of up to kQStage values; within a stage a ring of R chunks of
-    // codes, each slot refilled in place with the chunk R ahead.  Loads are
-    // unconditional (clamped to the stage's last chunk): a load under a branch
-    // makes the compiler's wait counting wait for everything in flight.  A
-    // chunk past the end runs with its scales zeroed (live = 0).
-    QChunk<F> rs[R], rs2[R];
-    const int kspan = p.K / p.ksplit, kbeg = blockIdx.z * kspan;
-    for (int kb = kbeg; kb < kbeg + kspan; kb += kQStage) {
-        const int nv = min(kQStage, kbeg + kspan - kb), nst = nv / kQChunk, c0 = kb / kQChunk;
-        if (kb > kbeg) __syncthreads();  // every wavefront is done with the previous stage
-        // the first batch of activations, then the ring's codes, then the
-        // LDS writes: the wait for the activations does not cover the codes
-        // (loads complete in order), and the codes stream during staging
-        stage_load(kb, nst, 0);
+    // The wavefront's chunk windows: window i = lane + 64 j of the 16 rows
+    // (row i / kWin, window i % kWin).  Lanes past the last window repeat it
+    // and skip the LDS write.
+    const uint8_t *pw[kMats][kP];
+    int pwin[kP], pslot[kP];
+    bool pv[kP];
 #pragma unroll
-        for (int q = 0; q < R; q++) {
-            rs[q].load(wrow, c0 + min(q, nst - 1), lg);
-            if (kPair) rs2[q].load(wrow2, c0 + min(q, nst - 1), lg);
-        }
-        stage_store(nst, 0);
-        for (int b = 4; b < nst; b += 4) {
-            stage_load(kb, nst, b);
-            stage_store(nst, b);
-        }
-        __syncthreads();
+    for (int j = 0; j < kP; j++) {
+        const int i = lane + 64 * j, ic = min(i, kPieces - 1), prow = ic / kWin;
+        pwin[j] = ic - prow * kWin;
+        pslot[j] = prow * kRowW + 4 * pwin[j];
+        pv[j] = i < kPieces;
+        const uint64_t off = (uint64_t)min(n0 + prow, p.N - 1) * p.stride;
+        pw[0][j] = w + off;
+        if (kPair) pw[kMats - 1][j] = w2 + off;
+    }
+    const int kspan = p.K / p.ksplit, kbeg = blockIdx.z * kspan;
+    const int nspan = kspan / kQChunk, cb = kbeg / kQChunk;
+    // Ring of R chunks in registers, slot q refilled in place with the chunk R
+    // ahead.  Loads are unconditional (clamped to the range's last chunk): a
+    // load under a branch makes the compiler's wait counting wait for
+    // everything in flight.  A window is an aligned 16-byte block holding at
+    // least one byte of its chunk row, so it never leaves the row's memory page.
+    qu4v raw[R][kMats][kP];  // native vectors: the ring stays in registers
+    auto ring_load = [&](int q, int c) {
+        const int ca = cb + min(c, nspan - 1);
+#pragma unroll
+        for (int m = 0; m < kMats; m++)
+#pragma unroll
+            for (int j = 0; j < kP; j++) {
+                const uint8_t *st = pw[m][j] + (size_t)ca * kCB;
+                const int sh = (int)((uintptr_t)st & kShm);
+                const int wn = (sh + kCB + 15) >> 4;
+                raw[q][m][j] = *reinterpret_cast<const qu4v *>(
+                    __builtin_assume_aligned(st - sh + 16 * min(pwin[j], wn - 1), 16));
+            }
+    };
+    // Slot q's windows into the wavefront's row images.  Lanes read what other
+    // lanes wrote: the fences keep the compiler from moving the reads of the
+    // previous chunk past these writes, or the reads of this one before them
+    // (a wavefront's LDS accesses execute in program order).
+    auto ring_put = [&](int q) {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+        for (int m = 0; m < kMats; m++)
+#pragma unroll
+            for (int j = 0; j < kP; j++)
+                if (pv[j]) *reinterpret_cast<qu4v *>(&code_s[wave][m][pslot[j]]) = raw[q][m][j];
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    };
+
+    QC f[kMats];
+    // the chunks of a staged stage; chunk s0 + c + q is in slot q (s0 and c
+    // are multiples of R)
+    auto run_stage = [&](int s0, int nst) {
         for (int c = 0; c < nst; c += R) {
 #pragma unroll
             for (int q = 0; q < R; q++) {
-                compute(rs[q], rs2[q], min(c + q, nst - 1), c + q < nst ? 1.f : 0.f);
-                rs[q].load(wrow, c0 + min(c + q + R, nst - 1), lg);
-                if (kPair) rs2[q].load(wrow2, c0 + min(c + q + R, nst - 1), lg);
+                const int cc = s0 + c + q, ca = cb + min(cc, nspan - 1);
+                ring_put(q);
+                ring_load(q, cc + R);
+#pragma unroll
+                for (int m = 0; m < kMats; m++)
+                    f[m].load(&code_s[wave][m][li * kRowW], (int)((uintptr_t)(wrow[m] + (size_t)ca * kCB) & kShm),
+                              lg);
+                compute(f[0], f[kMats - 1], min(c + q, nst - 1), c + q < nst ? 1.f : 0.f);
             }
         }
+    };
+    // First stage: the activations, then the ring's first chunks, then the
+    // LDS writes -- the wait for the activations does not cover the codes
+    // (loads complete in order), which stream during staging.  Later stages
+    // wait for the ring's loads ahead of their activations.
+    {
+        const int nst = min(kStageChunks, nspan);
+        stage_load(kbeg, nst);
+#pragma unroll
+        for (int q = 0; q < R; q++) ring_load(q, q);
+        stage_store(nst);
+        __syncthreads();
+        run_stage(0, nst);
+    }
+    for (int s0 = kStageChunks; s0 < nspan; s0 += kStageChunks) {
+        const int nst = min(kStageChunks, nspan - s0);
+        __syncthreads();  // every wavefront is done with the previous stage
+        stage_load(kbeg + s0 * kQChunk, nst);
+        stage_store(nst);
+        __syncthreads();
+        run_stage(s0, nst);
     }
 
     // D[token 4 lg + r][row li]
@@ -460,16 +552,19 @@ typedef void (*QGemmKernel)(QGemmParams);
 template <int F, bool G, int R> static QGemmKernel pick_q(int out) {
     switch (out) {
     case OUT_STORE: return qgemm_kernel<F, OUT_STORE, G, R>;
-    case OUT_SWIGLU: return qgemm_kernel<F, OUT_SWIGLU, G, R>;
+    case OUT_SWIGLU:
+        if constexpr (R == 2) return qgemm_kernel<F, OUT_SWIGLU, G, R>;  // deeper rings spill
+        return nullptr;
     case OUT_ADD: return G ? nullptr : qgemm_kernel<F, OUT_ADD, G, R>;
     case OUT_ARGMAX: return G ? nullptr : qgemm_kernel<F, OUT_ARGMAX, G, R>;
     default: return nullptr;
     }
 }
 
-// ring depth: 4 chunks, or 2 when a stage holds only two (K = 512)
+// ring depth: 4 chunks, or 2 for the two matrices of SWIGLU (the same bytes in
+// flight) and for reduction ranges of two chunks
 template <bool G> static QGemmKernel pick_qf(int fmt, int out, int K) {
-    const bool r2 = K / kQChunk <= 2;
+    const bool r2 = K / kQChunk <= 2 || out == OUT_SWIGLU;
     switch (fmt) {
     case Q4_K: return r2 ? pick_q<Q4_K, G, 2>(out) : pick_q<Q4_K, G, 4>(out);
     case Q6_K: return r2 ? pick_q<Q6_K, G, 2>(out) : pick_q<Q6_K, G, 4>(out);
@@ -480,9 +575,20 @@ template <bool G> static QGemmKernel pick_qf(int fmt, int out, int K) {
     }
 }
 
-bool qgemm_supported(int fmt, int K) {
-    return (fmt == Q4_K || fmt == Q6_K || fmt == Q8_0 || fmt == IQ4_XS || fmt == Q3_K) && K >= kQChunk &&
-           K % kQChunk == 0;
+// The chunk windows assume a 16-byte aligned matrix (and expert slices) whose
+// row stride keeps chunk addresses within the format's offsets below 16.
+bool qgemm_supported(int fmt, int K, const void *w, const void *w2, uint64_t stride, uint64_t expert_stride) {
+    int shm;
+    switch (fmt) {
+    case Q4_K: shm = QChunk<Q4_K>::kShm; break;
+    case Q8_0: shm = QChunk<Q8_0>::kShm; break;
+    case IQ4_XS: shm = QChunk<IQ4_XS>::kShm; break;
+    case Q6_K: shm = QChunk<Q6_K>::kShm; break;
+    case Q3_K: shm = QChunk<Q3_K>::kShm; break;
+    default: return false;
+    }
+    const uintptr_t base = (uintptr_t)w | (uintptr_t)w2 | (uintptr_t)expert_stride;
+    return K >= kQChunk && K % kQChunk == 0 && base % 16 == 0 && (stride & 15 & ~(uint64_t)shm) == 0;
 }
 
 __global__ void zero_rows_kernel(float *y, int ldy, int M, int N) {
@@ -504,7 +610,7 @@ static int qgemm_target_wgs() {
 
 hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                         float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s) {
-    if (M < 1 || N < 1 || !qgemm_supported(fmt, K) || ldx % 4) return hipErrorInvalidValue;
+    if (M < 1 || N < 1 || !qgemm_supported(fmt, K, w, w2, stride, 0) || ldx % 4) return hipErrorInvalidValue;
     const int groups = (N + kQRows - 1) / kQRows, tiles = (M + 15) / 16;
     // split the reduction over workgroups (results added atomically) when the
     // row groups alone leave CUs idle; plain stores and adds only
@@ -527,7 +633,8 @@ hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, ui
                                 uint64_t expert_stride, const float *x, int ldx, int x_div, float *y, int ldy, int N,
                                 int K, int out, const int *tiles, const int *list, const int *ntiles, int max_tiles,
                                 hipStream_t s) {
-    if (N < 1 || !qgemm_supported(fmt, K) || ldx % 4 || max_tiles < 1 || x_div < 1) return hipErrorInvalidValue;
+    if (N < 1 || !qgemm_supported(fmt, K, w, w2, stride, expert_stride) || ldx % 4 || max_tiles < 1 || x_div < 1)
+        return hipErrorInvalidValue;
     QGemmKernel k = pick_qf<true>(fmt, out, K);
     if (!k) return hipErrorInvalidValue;
     QGemmParams p{w, w2, stride, x, y, 16, N, K, ldx, ldy, nullptr, tiles, list, ntiles, x_div, expert_stride, 1};

@@ -62,6 +62,10 @@ struct ZiggyHipSession {
     float *b_attn = nullptr, *b_act = nullptr, *b_up = nullptr;
     uint32_t *b_tokens = nullptr;
     unsigned long long *b_argmax = nullptr;
+    // multi-query attention of a verify pass: partials and arrival counters
+    // of head_count_kv * query-group slots
+    float *b_part_o = nullptr, *b_part_ml = nullptr;
+    unsigned *b_counters = nullptr;
     uint32_t position = 0;
     bool logits_valid = false;
     std::vector<void *> allocs;
@@ -652,13 +656,29 @@ static hipError_t verify_alloc(ZiggyHipSession *s) {
         if (e != hipSuccess) return e;
         s->allocs.push_back(*r.p);
     }
+    if (attention_multi_supported((int)s->md.head_dim)) {
+        const size_t slots = (size_t)s->md.head_count_kv *
+                             attention_query_groups((int)s->md.head_count, (int)s->md.head_count_kv, (int)M);
+        const size_t po = slots * s->max_splits * 8 * s->md.head_dim, pml = slots * s->max_splits * 8 * 2;
+        hipError_t e = hipMalloc((void **)&s->b_part_o, (po + pml) * 4);
+        if (e != hipSuccess) return e;
+        s->allocs.push_back(s->b_part_o);
+        s->b_part_ml = s->b_part_o + po;
+        e = hipMalloc((void **)&s->b_counters, slots * sizeof(unsigned));
+        if (e != hipSuccess) return e;
+        s->allocs.push_back(s->b_counters);
+        e = hipMemsetAsync(s->b_counters, 0, slots * sizeof(unsigned), s->ctx->stream);  // the merge resets them
+        if (e != hipSuccess) return e;
+    }
     return hipSuccess;
 }
 
 // One batched pass of M tokens at positions pos .. pos + M - 1: embedding,
-// per layer per-token RMSNorm + q/k/v GEMMs, attention query by query (each
-// stores its K/V row, in order), o_proj / gate-up / down GEMMs with the
-// residual adds, final norm and the output GEMM fused with a per-token argmax.
+// per layer per-token RMSNorm + q/k/v GEMMs, the q/k epilogue and K/V stores
+// of all M tokens then one multi-query attention launch (or, for head sizes
+// the matrix-core kernel lacks, attention query by query, each storing its
+// K/V row in order), o_proj / gate-up / down GEMMs with the residual adds,
+// final norm and the output GEMM fused with a per-token argmax.
 static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t st) {
     const ZiggyHipModelDesc &md = s->md;
     const int H = (int)md.embedding_length, F = (int)md.feed_forward_length, Q = s->q_size, KV = s->kv_size;
@@ -677,7 +697,44 @@ static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t
         gemm(L.k, nullptr, s->b_normed, H, s->b_k, KV, OUT_STORE);
         gemm(L.v, nullptr, s->b_normed, H, s->b_v, KV, OUT_STORE);
         const size_t layer_base = (size_t)l * md.context_length * s->kv_size;
-        for (int m = 0; m < M && e == hipSuccess; m++) {
+        if (s->b_counters && e == hipSuccess) {
+            AttnParams a{};
+            a.q = s->b_q;
+            a.k_new = s->b_k;
+            a.v_new = s->b_v;
+            a.q_bias = L.q_bias.present ? (const float *)L.q_bias.p : nullptr;
+            a.k_bias = L.k_bias.present ? (const float *)L.k_bias.p : nullptr;
+            a.v_bias = L.v_bias.present ? (const float *)L.v_bias.p : nullptr;
+            a.q_norm = L.q_norm.present ? (const float *)L.q_norm.p : nullptr;
+            a.k_norm = L.k_norm.present ? (const float *)L.k_norm.p : nullptr;
+            a.k_cache = s->kc + layer_base;
+            a.v_cache = s->vc + layer_base;
+            a.head_count = (int)md.head_count;
+            a.head_count_kv = (int)md.head_count_kv;
+            a.head_dim = (int)md.head_dim;
+            a.kv_dim = s->kv_size;
+            a.position = pos;
+            a.eps = eps;
+            a.rope_base = md.rope_freq_base;
+            a.rope_dim = (int)md.rope_dim;
+            a.rope_style = (int)md.rope_style;
+            a.ctx = (int)md.context_length;
+            a.n_query = M;
+            a.q_stride = Q;
+            a.out_stride = Q;
+            e = launch_attention_prep(a, s->b_q, st);
+            // plain mode over the stored rows
+            a.k_new = a.v_new = nullptr;
+            a.out = s->b_attn;
+            a.part_o = s->b_part_o;
+            a.part_ml = s->b_part_ml;
+            a.counters = s->b_counters;
+            a.window_start = 0;
+            a.scale = 1.0f / sqrtf((float)md.head_dim);
+            a.max_splits = s->max_splits;
+            if (e == hipSuccess) e = launch_attention(a, st);
+        }
+        for (int m = 0; m < M && e == hipSuccess && !s->b_counters; m++) {
             AttnParams a{};
             a.q = s->b_q + (size_t)m * Q;
             a.k_new = s->b_k + (size_t)m * KV;
