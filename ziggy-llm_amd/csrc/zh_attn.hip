@@ -1071,15 +1071,21 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
         if (p.k_new || !attention_multi_supported(p.head_dim) || p.position_dev ||
             p.q_stride < p.head_count * p.head_dim || p.out_stride < p.head_count * p.head_dim)
             return hipErrorInvalidValue;
-        const dim3 grid(p.max_splits, p.head_count_kv, attention_query_groups(p.head_count, p.head_count_kv, p.n_query));
+        // the query groups multiply the workgroups: fewer splits each, about
+        // the decode grid's size in all (part_o keeps its max_splits layout)
+        const int groups = attention_query_groups(p.head_count, p.head_count_kv, p.n_query);
+        AttnParams q = p;
+        q.max_splits = attention_target_wgs() / (p.head_count_kv * groups);
+        q.max_splits = q.max_splits < 1 ? 1 : q.max_splits > p.max_splits ? p.max_splits : q.max_splits;
+        const dim3 grid(q.max_splits, p.head_count_kv, groups);
         auto go = [&](auto hd_tag) {
             constexpr int HD = decltype(hd_tag)::value;
             switch (G) {
-            case 1: hipLaunchKernelGGL((attn_mfma_kernel<HD, 1, true>), grid, dim3(256), 0, s, p); break;
-            case 2: hipLaunchKernelGGL((attn_mfma_kernel<HD, 2, true>), grid, dim3(256), 0, s, p); break;
-            case 4: hipLaunchKernelGGL((attn_mfma_kernel<HD, 4, true>), grid, dim3(256), 0, s, p); break;
-            case 8: hipLaunchKernelGGL((attn_mfma_kernel<HD, 8, true>), grid, dim3(256), 0, s, p); break;
-            default: hipLaunchKernelGGL((attn_mfma_kernel<HD, 0, true>), grid, dim3(256), 0, s, p); break;
+            case 1: hipLaunchKernelGGL((attn_mfma_kernel<HD, 1, true>), grid, dim3(256), 0, s, q); break;
+            case 2: hipLaunchKernelGGL((attn_mfma_kernel<HD, 2, true>), grid, dim3(256), 0, s, q); break;
+            case 4: hipLaunchKernelGGL((attn_mfma_kernel<HD, 4, true>), grid, dim3(256), 0, s, q); break;
+            case 8: hipLaunchKernelGGL((attn_mfma_kernel<HD, 8, true>), grid, dim3(256), 0, s, q); break;
+            default: hipLaunchKernelGGL((attn_mfma_kernel<HD, 0, true>), grid, dim3(256), 0, s, q); break;
             }
         };
         if (p.head_dim == 64) go(std::integral_constant<int, 64>{});

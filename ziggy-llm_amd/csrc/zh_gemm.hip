@@ -357,26 +357,66 @@ hipError_t launch_moe_group(const uint32_t *route, int route_stride, int M, int 
 }
 
 // Per-token RMSNorm of M rows (rmsNorm, model/loader.zig:3404-3426, for each
-// token): out[m] = (scale_m * x[m]) * w; one workgroup per token.
+// token): out[m] = (scale_m * x[m]) * w; one workgroup per token.  V: rows of
+// up to 8192 values (multiples of 4, 16-byte aligned) held in registers, every
+// load in flight at once.  The workgroups also clear up to three float ranges
+// (outputs that products then accumulate onto).
+struct NormClear {
+    float *p[3];
+    size_t n[3];
+};
+template <bool V>
 __global__ void __launch_bounds__(256) rms_norm_rows_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                            float *__restrict__ out, int n, float eps) {
+                                                            float *__restrict__ out, int n, float eps, NormClear cl) {
+    const int tid = threadIdx.x;
     const float *xr = x + (size_t)blockIdx.x * n;
     float *orow = out + (size_t)blockIdx.x * n;
     __shared__ float red[4];
     float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    float4 v[8], wv[8];
+    const int n4 = n / 4;
+    if (V) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(xr), *w4 = reinterpret_cast<const float4 *>(w);
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = x4[min(tid + 256 * j, n4 - 1)];
+#pragma unroll
+        for (int j = 0; j < 8; j++) wv[j] = w4[min(tid + 256 * j, n4 - 1)];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (tid + 256 * j < n4)
+                ss = fmaf(v[j].w, v[j].w, fmaf(v[j].z, v[j].z, fmaf(v[j].y, v[j].y, fmaf(v[j].x, v[j].x, ss))));
+    } else {
+        for (int i = tid; i < n; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    }
     for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
     __syncthreads();
     const float tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float scale = 1.0f / sqrtf(tot / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += 256) orow[i] = (scale * xr[i]) * w[i];
+    if (V) {
+        float4 *o4 = reinterpret_cast<float4 *>(orow);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (tid + 256 * j < n4)
+                o4[tid + 256 * j] = {(scale * v[j].x) * wv[j].x, (scale * v[j].y) * wv[j].y,
+                                     (scale * v[j].z) * wv[j].z, (scale * v[j].w) * wv[j].w};
+    } else {
+        for (int i = tid; i < n; i += 256) orow[i] = (scale * xr[i]) * w[i];
+    }
+#pragma unroll
+    for (int r = 0; r < 3; r++)
+        for (size_t i = (size_t)blockIdx.x * 256 + tid; i < cl.n[r]; i += (size_t)gridDim.x * 256) cl.p[r][i] = 0.f;
 }
 
-hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps,
-                                hipStream_t s) {
-    if (rows < 1 || n < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rms_norm_rows_kernel, dim3(rows), dim3(256), 0, s, x, w, out, n, eps);
+hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps, hipStream_t s,
+                                float *clear0, size_t n0, float *clear1, size_t n1, float *clear2, size_t n2) {
+    if (rows < 1 || n < 1 || (n0 && !clear0) || (n1 && !clear1) || (n2 && !clear2)) return hipErrorInvalidValue;
+    const NormClear cl{{clear0, clear1, clear2}, {n0, n1, n2}};
+    const bool v = n % 4 == 0 && n <= 8 * 256 * 4 && ((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) % 16 == 0;
+    if (v)
+        hipLaunchKernelGGL(rms_norm_rows_kernel<true>, dim3(rows), dim3(256), 0, s, x, w, out, n, eps, cl);
+    else
+        hipLaunchKernelGGL(rms_norm_rows_kernel<false>, dim3(rows), dim3(256), 0, s, x, w, out, n, eps, cl);
     return hipGetLastError();
 }
 

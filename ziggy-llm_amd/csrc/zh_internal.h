@@ -136,8 +136,9 @@ hipError_t launch_fill_u64(unsigned long long *p, unsigned long long v, int n, h
 hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
                        bool precise = false);
-hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps,
-                                hipStream_t s);
+hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps, hipStream_t s,
+                                float *clear0 = nullptr, size_t n0 = 0, float *clear1 = nullptr, size_t n1 = 0,
+                                float *clear2 = nullptr, size_t n2 = 0);
 // Grouped by expert (MoE prefill): token tiles from launch_moe_group; W of expert e
 // starts expert_stride bytes after W of expert e - 1; x row = id / x_div, y row = id.
 hipError_t launch_gemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, uint64_t expert_stride,

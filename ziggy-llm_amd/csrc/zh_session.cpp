@@ -692,10 +692,12 @@ static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t
     };
     for (int l = 0; l < (int)md.block_count && e == hipSuccess; l++) {
         const LayerW &L = s->layers[l];
-        e = launch_rms_norm_rows(s->b_hidden, (const float *)L.attn_norm.p, s->b_normed, M, H, eps, st);
-        gemm(L.q, nullptr, s->b_normed, H, s->b_q, Q, OUT_STORE);
-        gemm(L.k, nullptr, s->b_normed, H, s->b_k, KV, OUT_STORE);
-        gemm(L.v, nullptr, s->b_normed, H, s->b_v, KV, OUT_STORE);
+        // the norm clears the q/k/v rows, which the products then accumulate onto
+        e = launch_rms_norm_rows(s->b_hidden, (const float *)L.attn_norm.p, s->b_normed, M, H, eps, st, s->b_q,
+                                 (size_t)M * Q, s->b_k, (size_t)M * KV, s->b_v, (size_t)M * KV);
+        gemm(L.q, nullptr, s->b_normed, H, s->b_q, Q, OUT_ADD);
+        gemm(L.k, nullptr, s->b_normed, H, s->b_k, KV, OUT_ADD);
+        gemm(L.v, nullptr, s->b_normed, H, s->b_v, KV, OUT_ADD);
         const size_t layer_base = (size_t)l * md.context_length * s->kv_size;
         if (s->b_counters && e == hipSuccess) {
             AttnParams a{};
@@ -776,8 +778,10 @@ static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t
         }
         gemm(L.down, nullptr, s->b_act, F, s->b_hidden, H, OUT_ADD);
     }
-    if (e == hipSuccess) e = launch_rms_norm_rows(s->b_hidden, (const float *)s->out_norm.p, s->b_normed, M, H, eps, st);
-    if (e == hipSuccess) e = launch_fill_u64(s->b_argmax, 0ull, M, st);
+    // the final norm also clears the argmax keys
+    if (e == hipSuccess)
+        e = launch_rms_norm_rows(s->b_hidden, (const float *)s->out_norm.p, s->b_normed, M, H, eps, st,
+                                 reinterpret_cast<float *>(s->b_argmax), (size_t)M * 2);
     gemm(s->out, nullptr, s->b_normed, H, nullptr, 0, OUT_ARGMAX);
     return e;
 }
