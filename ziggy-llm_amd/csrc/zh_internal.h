@@ -130,6 +130,9 @@ hipError_t launch_weighted_sum_topk(float *dst, const float *src, const void *en
 hipError_t launch_sigmoid_scale_add(float *dst, const float *src, const float *scalar, int n, hipStream_t s);
 hipError_t launch_argmax_finalize(const unsigned long long *slot, uint32_t *state, hipStream_t s);
 hipError_t launch_fill_u64(unsigned long long *p, unsigned long long v, int n, hipStream_t s);
+// per-row argmax keys (value, then the lowest index) of rows x n values, ld
+// apart, max-ed into slots[row] (zero beforehand)
+hipError_t launch_argmax_rows(const float *x, int rows, int n, int ld, unsigned long long *slots, hipStream_t s);
 
 // MFMA GEMM for M >= 8 tokens (zh_gemm.hip): Y[m][n] (=, +=) sum_k W[n][k] X[m][k]
 // (OUT_STORE / OUT_ADD / OUT_SWIGLU with w2 / OUT_ARGMAX into argmax[M]).

@@ -114,6 +114,27 @@ __global__ void argmax_kernel(const float *__restrict__ x, int n, unsigned long 
     if (threadIdx.x == 0 && keys[0]) atomicMax(slot, keys[0]);
 }
 
+// The same over `rows` rows of n values (ld apart): blockIdx.y is the row,
+// slots[row] its packed (value, lowest index) key; slots start at zero.
+__global__ void argmax_rows_kernel(const float *__restrict__ x, int n, int ld, unsigned long long *slots) {
+    __shared__ unsigned long long keys[256];
+    const float *xr = x + (size_t)blockIdx.y * ld;
+    unsigned long long best = 0ull;
+#pragma unroll 4
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const unsigned long long k =
+            ((unsigned long long)ordered_bits_ops(xr[i]) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
+        best = k > best ? k : best;
+    }
+    keys[threadIdx.x] = best;
+    __syncthreads();
+    for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s && keys[threadIdx.x + s] > keys[threadIdx.x]) keys[threadIdx.x] = keys[threadIdx.x + s];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0 && keys[0]) atomicMax(slots + blockIdx.y, keys[0]);
+}
+
 // Writes the token of a packed argmax slot (and the reference's {bits, token}
 // state pair when state_pair != 0).
 __global__ void argmax_finalize_kernel(const unsigned long long *slot, uint32_t *out, int state_pair) {
@@ -267,6 +288,13 @@ hipError_t launch_argmax(const float *x, int n, uint32_t *out_token, unsigned lo
     if (grid < 1) grid = 1;
     hipLaunchKernelGGL(argmax_kernel, dim3(grid), dim3(256), 0, s, x, n, tmp);
     hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(1), 0, s, tmp, out_token, 0);
+    return hipGetLastError();
+}
+hipError_t launch_argmax_rows(const float *x, int rows, int n, int ld, unsigned long long *slots, hipStream_t s) {
+    if (rows < 1 || n < 1 || ld < n) return hipErrorInvalidValue;
+    int grid = cdiv(n, 256 * 16);
+    if (grid > 1024) grid = 1024;
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(grid, rows), dim3(256), 0, s, x, n, ld, slots);
     return hipGetLastError();
 }
 hipError_t launch_argmax_finalize(const unsigned long long *slot, uint32_t *state, hipStream_t s) {

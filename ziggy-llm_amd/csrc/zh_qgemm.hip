@@ -31,6 +31,8 @@
 // registers, then copied into the wavefront's own LDS image of the 16 rows,
 // from which each lane reads the fields of its row in the product layout.  No
 // workgroup barrier inside a stage; the ring runs across stages.
+#include <cstdlib>
+
 #include "zh_internal.h"
 #include "zh_quant.h"
 
@@ -58,9 +60,14 @@ struct QGemmParams {
     int ksplit;  // blockIdx.z takes reduction values [z K / ksplit, (z + 1) K / ksplit); results add atomically
 };
 
-__device__ __forceinline__ uint32_t bf16_rne(float v) {
-    const uint32_t b = __float_as_uint(v);
-    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+typedef float qf2v __attribute__((ext_vector_type(2)));
+typedef __bf16 qb2v __attribute__((ext_vector_type(2)));
+// two floats -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    const qb2v h = __builtin_convertvector((qf2v){a, b}, qb2v);
+    uint32_t u;
+    __builtin_memcpy(&u, &h, 4);
+    return u;
 }
 // bf16 bits of two small integers held as f32 (exact: the high halves)
 __device__ __forceinline__ uint32_t pack_bf(float a, float b) {
@@ -254,6 +261,23 @@ template <> struct QChunk<Q3_K> {
     }
 };
 
+// Geometry of the kernel for format F (two matrices for SWIGLU).  A chunk row
+// at any offset kShm allows lies in kWin 16-byte windows; its LDS image has
+// one spare window (a word read past the last byte) and an odd window count,
+// so the 16 rows' words fall in distinct banks.  The activation stage is as
+// long as LDS allows next to the code images (2048 or 1024 values).
+template <int F, bool kPair> struct QGeom {
+    static constexpr int kMats = kPair ? 2 : 1;
+    static constexpr int kWin = (QChunk<F>::kCB + QChunk<F>::kShm + 15) / 16;
+    static constexpr int kRowW = 4 * ((kWin + 1) | 1);
+    static constexpr int kPieces = 16 * kWin, kP = (kPieces + 63) / 64;  // windows per wavefront chunk, per lane
+    static constexpr bool kXsum = F == Q4_K;
+    static constexpr int kCodeBytes = 4 * kMats * 16 * kRowW * 4;
+    static constexpr int kStage =
+        (2 * 16 * (2048 + 8) * 2 + (kXsum ? 2048 / 32 * 16 * 4 : 64) + kCodeBytes <= 160 * 1024) ? 2048 : 1024;
+    static constexpr int kStageChunks = kStage / kQChunk;
+};
+
 __device__ __forceinline__ uint32_t ordered_bits_q(float v) {
     const uint32_t b = __float_as_uint(v);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
@@ -262,21 +286,13 @@ __device__ __forceinline__ uint32_t ordered_bits_q(float v) {
 template <int F, int OUT, bool GROUPED, int R>
 __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     constexpr bool kPair = OUT == OUT_SWIGLU;
-    constexpr int kMats = kPair ? 2 : 1;
     using QC = QChunk<F>;
+    using G = QGeom<F, kPair>;
     constexpr int kSub = QC::kSub, kCB = QC::kCB, kShm = QC::kShm;
-    // A chunk row at any offset kShm allows lies in kWin 16-byte windows.  Its
-    // LDS image has one spare window (a word read past the last byte) and an
-    // odd window count, so the 16 rows' words fall in distinct banks.
-    constexpr int kWin = (kCB + kShm + 15) / 16;
-    constexpr int kRowW = 4 * ((kWin + 1) | 1);
-    constexpr int kPieces = 16 * kWin, kP = (kPieces + 63) / 64;  // windows per wavefront chunk, per lane
-    constexpr bool kXsum = F == Q4_K;
-    constexpr int kCodeBytes = 4 * kMats * 16 * kRowW * 4;
-    constexpr int kStage =
-        (2 * 16 * (2048 + 8) * 2 + (kXsum ? 2048 / 32 * 16 * 4 : 64) + kCodeBytes <= 160 * 1024) ? 2048 : 1024;
-    constexpr int kStageChunks = kStage / kQChunk;
-    static_assert(kStageChunks % R == 0, "stages hold whole rings");
+    constexpr int kMats = G::kMats, kWin = G::kWin, kRowW = G::kRowW, kPieces = G::kPieces, kP = G::kP;
+    constexpr bool kXsum = G::kXsum;
+    constexpr int kStage = G::kStage, kStageChunks = G::kStageChunks;
+    static_assert(kStageChunks % R == 0 && R % 2 == 0, "stages hold whole rings of an even depth");
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
     int m0 = blockIdx.y * 16, M = p.M;
@@ -291,11 +307,25 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
         m0 = 0;
         M = gt[2];
     }
-    const int n0 = blockIdx.x * kQRows + 16 * wave;
-    const int n = min(n0 + li, p.N - 1);  // this lane's weight row (clamped; dropped at the store)
-    const uint8_t *wrow[kMats];
-    wrow[0] = w + (uint64_t)n * p.stride;
-    if (kPair) wrow[kMats - 1] = w2 + (uint64_t)n * p.stride;
+    const uint8_t *wm[kMats];
+    wm[0] = w;
+    if (kPair) wm[kMats - 1] = w2;
+    // Row groups of 64 rows (16 per wavefront): this workgroup takes groups
+    // blockIdx.x, blockIdx.x + gridDim.x, ... -- several only when its
+    // reduction range is one stage, whose activations then serve them all.
+    // Work items (group, chunk) run group by group; the code ring runs across
+    // groups.
+    const int groups = (p.N + kQRows - 1) / kQRows;
+    const int ng = (groups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
+    const int kspan = p.K / p.ksplit, kbeg = blockIdx.z * kspan;
+    const int nspan = kspan / kQChunk, cb = kbeg / kQChunk;
+    const int nitems = ng * nspan;
+    // first row of this wavefront in item t's group (t clamped), its chunk
+    auto item = [&](int t, int &row0, int &ca) {
+        const int tc = min(t, nitems - 1), gi = tc / nspan;
+        row0 = ((int)blockIdx.x + gi * (int)gridDim.x) * kQRows + 16 * wave;
+        ca = cb + tc - gi * nspan;
+    };
 
     // The activations of a stage (up to kStage values of all 16 tokens) sit in
     // LDS as bf16 hi / lo pieces; thread (token tt, part) stages values
@@ -325,27 +355,29 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     auto stage_store = [&](int nc) {
 #pragma unroll
         for (int u = 0; u < kStageChunks; u++) {
-            float v[16];
+            if (u >= nc) {
+                // past the range: the loads still land -- consumed here, so the
+                // compiler's wait counting sees them complete on every path
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 q = ld[u][i];
-                v[4 * i] = q.x, v[4 * i + 1] = q.y, v[4 * i + 2] = q.z, v[4 * i + 3] = q.w;
+                for (int i = 0; i < 4; i++)
+                    __asm__ volatile("" ::"v"(ld[u][i].x), "v"(ld[u][i].y), "v"(ld[u][i].z), "v"(ld[u][i].w));
+                continue;
             }
             uint32_t hw[8], lw[8];
             float sum = 0.f;
 #pragma unroll
-            for (int i = 0; i < 16; i += 2) {
-                const float a = tok_ok ? v[i] : 0.f, b = tok_ok ? v[i + 1] : 0.f;
-                const uint32_t ha = bf16_rne(a), hb = bf16_rne(b);
-                const float ra = a - __uint_as_float(ha << 16), rb = b - __uint_as_float(hb << 16);
-                const uint32_t la = bf16_rne(ra), lb = bf16_rne(rb);
-                hw[i / 2] = ha | (hb << 16);
-                lw[i / 2] = la | (lb << 16);
-                sum += (__uint_as_float(ha << 16) + __uint_as_float(la << 16)) +
-                       (__uint_as_float(hb << 16) + __uint_as_float(lb << 16));
+            for (int i = 0; i < 8; i++) {
+                const float4 q = ld[u][i >> 1];
+                const float a = tok_ok ? ((i & 1) ? q.z : q.x) : 0.f, b = tok_ok ? ((i & 1) ? q.w : q.y) : 0.f;
+                const uint32_t h = pk_bf16(a, b);
+                const float ha = __uint_as_float(h << 16), hb = __uint_as_float(h & 0xFFFF0000u);
+                const uint32_t l = pk_bf16(a - ha, b - hb);
+                hw[i] = h;
+                lw[i] = l;
+                if (kXsum) sum += (ha + __uint_as_float(l << 16)) + (hb + __uint_as_float(l & 0xFFFF0000u));
             }
             if (kXsum) sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
-            if (u < nc) {
+            {
                 uint4 *dh = reinterpret_cast<uint4 *>(&xs_s[0][tt][u * kQChunk + 16 * part]);
                 uint4 *dl = reinterpret_cast<uint4 *>(&xs_s[1][tt][u * kQChunk + 16 * part]);
                 dh[0] = {hw[0], hw[1], hw[2], hw[3]};
@@ -419,34 +451,32 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     // The wavefront's chunk windows: window i = lane + 64 j of the 16 rows
     // (row i / kWin, window i % kWin).  Lanes past the last window repeat it
     // and skip the LDS write.
-    const uint8_t *pw[kMats][kP];
-    int pwin[kP], pslot[kP];
+    int prow[kP], pwin[kP], pslot[kP];
     bool pv[kP];
 #pragma unroll
     for (int j = 0; j < kP; j++) {
-        const int i = lane + 64 * j, ic = min(i, kPieces - 1), prow = ic / kWin;
-        pwin[j] = ic - prow * kWin;
-        pslot[j] = prow * kRowW + 4 * pwin[j];
+        const int i = lane + 64 * j, ic = min(i, kPieces - 1);
+        prow[j] = ic / kWin;
+        pwin[j] = ic - prow[j] * kWin;
+        pslot[j] = prow[j] * kRowW + 4 * pwin[j];
         pv[j] = i < kPieces;
-        const uint64_t off = (uint64_t)min(n0 + prow, p.N - 1) * p.stride;
-        pw[0][j] = w + off;
-        if (kPair) pw[kMats - 1][j] = w2 + off;
     }
-    const int kspan = p.K / p.ksplit, kbeg = blockIdx.z * kspan;
-    const int nspan = kspan / kQChunk, cb = kbeg / kQChunk;
-    // Ring of R chunks in registers, slot q refilled in place with the chunk R
-    // ahead.  Loads are unconditional (clamped to the range's last chunk): a
-    // load under a branch makes the compiler's wait counting wait for
-    // everything in flight.  A window is an aligned 16-byte block holding at
-    // least one byte of its chunk row, so it never leaves the row's memory page.
+    // Ring of R items in registers, slot q refilled in place with the item R
+    // ahead.  Loads are unconditional (clamped to the last item): a load
+    // under a branch makes the compiler's wait counting wait for everything
+    // in flight.  A window is an aligned 16-byte block holding at least one
+    // byte of its chunk row, so it never leaves the row's memory page.  Rows
+    // past N re-read row N - 1 (dropped at the store).
     qu4v raw[R][kMats][kP];  // native vectors: the ring stays in registers
-    auto ring_load = [&](int q, int c) {
-        const int ca = cb + min(c, nspan - 1);
+    auto ring_load = [&](int q, int t) {
+        int row0, ca;
+        item(t, row0, ca);
 #pragma unroll
         for (int m = 0; m < kMats; m++)
 #pragma unroll
             for (int j = 0; j < kP; j++) {
-                const uint8_t *st = pw[m][j] + (size_t)ca * kCB;
+                const uint8_t *st =
+                    wm[m] + (uint64_t)min(row0 + prow[j], p.N - 1) * p.stride + (size_t)ca * kCB;
                 const int sh = (int)((uintptr_t)st & kShm);
                 const int wn = (sh + kCB + 15) >> 4;
                 raw[q][m][j] = *reinterpret_cast<const qu4v *>(
@@ -467,35 +497,119 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     };
 
-    QC f[kMats];
+    // Item t (in ring slot t % R) into the row images, its slot refilled
+    // with item t + R, and its fields read into ff.
+    auto fetch = [&](int q, int t, QC (&ff)[kMats]) {
+        int row0, ca;
+        item(t, row0, ca);
+        ring_put(q);
+        ring_load(q, t + R);
+        const uint64_t off = (uint64_t)min(row0 + li, p.N - 1) * p.stride + (size_t)ca * kCB;
+#pragma unroll
+        for (int m = 0; m < kMats; m++)
+            ff[m].load(&code_s[wave][m][li * kRowW], (int)((uintptr_t)(wm[m] + off) & kShm), lg);
+    };
+    // Two field sets: the next chunk's fields are read while the current one
+    // computes (chunk cc uses fa when cc is even; R is even).
+    QC fa[kMats], fb[kMats];
     // the chunks of a staged stage; chunk s0 + c + q is in slot q (s0 and c
     // are multiples of R)
     auto run_stage = [&](int s0, int nst) {
         for (int c = 0; c < nst; c += R) {
 #pragma unroll
             for (int q = 0; q < R; q++) {
-                const int cc = s0 + c + q, ca = cb + min(cc, nspan - 1);
-                ring_put(q);
-                ring_load(q, cc + R);
-#pragma unroll
-                for (int m = 0; m < kMats; m++)
-                    f[m].load(&code_s[wave][m][li * kRowW], (int)((uintptr_t)(wrow[m] + (size_t)ca * kCB) & kShm),
-                              lg);
-                compute(f[0], f[kMats - 1], min(c + q, nst - 1), c + q < nst ? 1.f : 0.f);
+                const int cc = s0 + c + q;
+                if (q & 1) {
+                    fetch((q + 1) % R, cc + 1, fa);
+                    compute(fb[0], fb[kMats - 1], min(c + q, nst - 1), c + q < nst ? 1.f : 0.f);
+                } else {
+                    fetch((q + 1) % R, cc + 1, fb);
+                    compute(fa[0], fa[kMats - 1], min(c + q, nst - 1), c + q < nst ? 1.f : 0.f);
+                }
             }
         }
     };
-    // First stage: the activations, then the ring's first chunks, then the
-    // LDS writes -- the wait for the activations does not cover the codes
-    // (loads complete in order), which stream during staging.  Later stages
-    // wait for the ring's loads ahead of their activations.
+    // The results of group g: D[token 4 lg + r][row li]; acc cleared after.
+    auto epilogue = [&](int g) {
+        const int nn = g * kQRows + 16 * wave + li;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int j = m0 + 4 * lg + r;  // token of result r
+            if (j >= M || nn >= p.N) continue;
+            const int jrow = GROUPED ? ids[4 * lg + r] : j;
+            float *dst = p.y ? p.y + (size_t)jrow * p.ldy + nn : nullptr;
+            const float v = acc[r];
+            if ((OUT == OUT_STORE || OUT == OUT_ADD) && p.ksplit > 1) {
+                atomicAdd(dst, v);  // partial sum of this workgroup's reduction range (STORE rows zeroed first)
+            } else if (OUT == OUT_STORE) {
+                *dst = v;
+            } else if (OUT == OUT_ADD) {
+                *dst = *dst + v;
+            } else if (OUT == OUT_SWIGLU) {
+                *dst = (v / (1.0f + expf(-v))) * acc2[r];
+            }
+        }
+        if (OUT == OUT_ARGMAX) {
+            // token 4 lg + r: the largest value over the 16 rows of lanes li, then the lowest row
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int j = m0 + 4 * lg + r;
+                const float v = acc[r];
+                if (p.y && j < M && nn < p.N) p.y[(size_t)j * p.ldy + nn] = v;
+                unsigned long long key = (j < M && nn < p.N)
+                                             ? ((unsigned long long)ordered_bits_q(v) << 32) |
+                                                   (unsigned long long)(0xFFFFFFFFu - (uint32_t)nn)
+                                             : 0ull;
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) {
+                    const unsigned long long k2 = __shfl_xor(key, o, 64);
+                    key = k2 > key ? k2 : key;
+                }
+                if (li == 0 && key) atomicMax(p.argmax + j, key);
+            }
+        }
+        acc = qf4v{0.f, 0.f, 0.f, 0.f};
+        acc2 = qf4v{0.f, 0.f, 0.f, 0.f};
+    };
+
+    if (nspan <= kStageChunks) {
+        // One stage: the activations, then the ring's first items, then the
+        // LDS writes -- the wait for the activations does not cover the codes
+        // (loads complete in order), which stream during staging.  Then every
+        // item of every group against the staged activations.
+        stage_load(kbeg, nspan);
+#pragma unroll
+        for (int q = 0; q < R; q++) ring_load(q, q);
+        stage_store(nspan);
+        __syncthreads();
+        fetch(0, 0, fa);
+        for (int t0 = 0; t0 < nitems; t0 += R) {
+#pragma unroll
+            for (int q = 0; q < R; q++) {
+                const int t = t0 + q, gi = t / nspan, c = t - gi * nspan;
+                const float live = t < nitems ? 1.f : 0.f;
+                if (q & 1) {
+                    fetch((q + 1) % R, t + 1, fa);
+                    compute(fb[0], fb[kMats - 1], c, live);
+                } else {
+                    fetch((q + 1) % R, t + 1, fb);
+                    compute(fa[0], fa[kMats - 1], c, live);
+                }
+                if (c == nspan - 1 && t < nitems) epilogue((int)blockIdx.x + gi * (int)gridDim.x);
+            }
+        }
+        return;
+    }
+    // Several stages (one group per workgroup): the first stage as above,
+    // later stages wait for the ring's loads ahead of their activations.
     {
-        const int nst = min(kStageChunks, nspan);
+        const int nst = kStageChunks;
         stage_load(kbeg, nst);
 #pragma unroll
         for (int q = 0; q < R; q++) ring_load(q, q);
         stage_store(nst);
         __syncthreads();
+        fetch(0, 0, fa);
         run_stage(0, nst);
     }
     for (int s0 = kStageChunks; s0 < nspan; s0 += kStageChunks) {
@@ -506,45 +620,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
         __syncthreads();
         run_stage(s0, nst);
     }
-
-    // D[token 4 lg + r][row li]
-    const int nn = n0 + li;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int j = m0 + 4 * lg + r;  // token of result r
-        if (j >= M || nn >= p.N) continue;
-        const int jrow = GROUPED ? ids[4 * lg + r] : j;
-        float *dst = p.y ? p.y + (size_t)jrow * p.ldy + nn : nullptr;
-        const float v = acc[r];
-        if ((OUT == OUT_STORE || OUT == OUT_ADD) && p.ksplit > 1) {
-            atomicAdd(dst, v);  // partial sum of this workgroup's reduction range (STORE rows zeroed first)
-        } else if (OUT == OUT_STORE) {
-            *dst = v;
-        } else if (OUT == OUT_ADD) {
-            *dst = *dst + v;
-        } else if (OUT == OUT_SWIGLU) {
-            *dst = (v / (1.0f + expf(-v))) * acc2[r];
-        }
-    }
-    if (OUT == OUT_ARGMAX) {
-        // token 4 lg + r: the largest value over the 16 rows of lanes li, then the lowest row
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int j = m0 + 4 * lg + r;
-            const float v = acc[r];
-            if (p.y && j < M && nn < p.N) p.y[(size_t)j * p.ldy + nn] = v;
-            unsigned long long key = (j < M && nn < p.N)
-                                         ? ((unsigned long long)ordered_bits_q(v) << 32) |
-                                               (unsigned long long)(0xFFFFFFFFu - (uint32_t)nn)
-                                         : 0ull;
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) {
-                const unsigned long long k2 = __shfl_xor(key, o, 64);
-                key = k2 > key ? k2 : key;
-            }
-            if (li == 0 && key) atomicMax(p.argmax + j, key);
-        }
-    }
+    epilogue(blockIdx.x);
 }
 
 typedef void (*QGemmKernel)(QGemmParams);
@@ -577,6 +653,17 @@ template <bool G> static QGemmKernel pick_qf(int fmt, int out, int K) {
 
 // The chunk windows assume a 16-byte aligned matrix (and expert slices) whose
 // row stride keeps chunk addresses within the format's offsets below 16.
+template <bool P> static int stage_chunks_of(int fmt) {
+    switch (fmt) {
+    case Q4_K: return QGeom<Q4_K, P>::kStageChunks;
+    case Q8_0: return QGeom<Q8_0, P>::kStageChunks;
+    case IQ4_XS: return QGeom<IQ4_XS, P>::kStageChunks;
+    case Q6_K: return QGeom<Q6_K, P>::kStageChunks;
+    case Q3_K: return QGeom<Q3_K, P>::kStageChunks;
+    default: return 0;
+    }
+}
+
 bool qgemm_supported(int fmt, int K, const void *w, const void *w2, uint64_t stride, uint64_t expert_stride) {
     int shm;
     switch (fmt) {
@@ -608,15 +695,45 @@ static int qgemm_target_wgs() {
     return t;
 }
 
+// Weight of the activation staging against the chunk work of one workgroup
+// (ZIGGY_HIP_QGEMM_STAGE_W overrides it; a tuning knob).
+static double qgemm_stage_weight() {
+    static const double w = [] {
+        const char *e = getenv("ZIGGY_HIP_QGEMM_STAGE_W");
+        return e ? atof(e) : 0.5;
+    }();
+    return w;
+}
+
 hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                         float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s) {
     if (M < 1 || N < 1 || !qgemm_supported(fmt, K, w, w2, stride, 0) || ldx % 4) return hipErrorInvalidValue;
-    const int groups = (N + kQRows - 1) / kQRows, tiles = (M + 15) / 16;
-    // split the reduction over workgroups (results added atomically) when the
-    // row groups alone leave CUs idle; plain stores and adds only
-    int ks = 1;
-    if (out == OUT_STORE || out == OUT_ADD)
-        while (groups * tiles * ks * 2 <= qgemm_target_wgs() && (K / kQChunk) % (ks * 2) == 0) ks *= 2;
+    const int groups = (N + kQRows - 1) / kQRows, tiles = (M + 15) / 16, chunks = K / kQChunk;
+    const int target = qgemm_target_wgs();
+    const int stage = out == OUT_SWIGLU ? stage_chunks_of<true>(fmt) : stage_chunks_of<false>(fmt);
+    // Reduction split ks (a power of two; results added atomically, plain
+    // stores and adds only) and workgroups per split pg, each taking every
+    // pg-th row group.  Several groups per workgroup need a one-stage range:
+    // the candidate with the shortest critical path (chunks of the busiest
+    // workgroup, plus its staging) wins, the smaller split on ties.
+    int ks = 0, pg = groups;
+    double best = 0.0;
+    const bool can_split = out == OUT_STORE || out == OUT_ADD;
+    for (int k = 1; k <= chunks && (k == 1 || can_split); k *= 2) {
+        if (chunks % k) break;
+        const int nspan = chunks / k;
+        if (nspan > stage || (k > 1 && nspan < 2)) continue;
+        int g = target / (tiles * k);
+        g = g < 1 ? 1 : g > groups ? groups : g;
+        const double cost = (double)((groups + g - 1) / g) * nspan + qgemm_stage_weight() * nspan;
+        if (ks == 0 || cost < best) ks = k, pg = g, best = cost;
+    }
+    if (ks == 0) {
+        // several stages: one group per workgroup, split while row groups leave CUs idle
+        ks = 1, pg = groups;
+        if (can_split)
+            while (groups * tiles * ks * 2 <= target && chunks % (ks * 2) == 0) ks *= 2;
+    }
     QGemmKernel k = pick_qf<false>(fmt, out, K / ks);
     if (!k) return hipErrorInvalidValue;
     if (ks > 1 && out == OUT_STORE) {
@@ -625,7 +742,7 @@ hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t s
         if (e != hipSuccess) return e;
     }
     QGemmParams p{w, w2, stride, x, y, M, N, K, ldx, ldy, argmax, nullptr, nullptr, nullptr, 1, 0, ks};
-    hipLaunchKernelGGL(k, dim3(groups, tiles, ks), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(k, dim3(pg, tiles, ks), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 

@@ -59,7 +59,7 @@ struct ZiggyHipSession {
     hipGraphExec_t graph = nullptr;
     // batched verify (allocated on first use): [kVerifyMax] rows each
     float *b_hidden = nullptr, *b_normed = nullptr, *b_q = nullptr, *b_k = nullptr, *b_v = nullptr;
-    float *b_attn = nullptr, *b_act = nullptr, *b_up = nullptr;
+    float *b_attn = nullptr, *b_act = nullptr, *b_up = nullptr, *b_logits = nullptr;
     uint32_t *b_tokens = nullptr;
     unsigned long long *b_argmax = nullptr;
     // multi-query attention of a verify pass: partials and arrival counters
@@ -650,7 +650,7 @@ static hipError_t verify_alloc(ZiggyHipSession *s) {
     } reqs[] = {{(void **)&s->b_hidden, M * H * 4}, {(void **)&s->b_normed, M * H * 4}, {(void **)&s->b_q, M * Q * 4},
                 {(void **)&s->b_k, M * KV * 4},      {(void **)&s->b_v, M * KV * 4},      {(void **)&s->b_attn, M * Q * 4},
                 {(void **)&s->b_act, M * F * 4},     {(void **)&s->b_up, M * F * 4},      {(void **)&s->b_tokens, M * 4},
-                {(void **)&s->b_argmax, M * 8}};
+                {(void **)&s->b_argmax, M * 8},     {(void **)&s->b_logits, M * s->md.vocab_size * 4}};
     for (auto &r : reqs) {
         hipError_t e = hipMalloc(r.p, r.bytes);
         if (e != hipSuccess) return e;
@@ -679,8 +679,19 @@ static hipError_t verify_alloc(ZiggyHipSession *s) {
 // the matrix-core kernel lacks, attention query by query, each storing its
 // K/V row in order), o_proj / gate-up / down GEMMs with the residual adds,
 // final norm and the output GEMM fused with a per-token argmax.
+// ZIGGY_HIP_VERIFY_SWIGLU=fused keeps gate/up as one SWIGLU product (its
+// reduction never splits); by default they are two products and SiLU * up.
+static bool verify_fused_swiglu() {
+    static const bool f = [] {
+        const char *e = getenv("ZIGGY_HIP_VERIFY_SWIGLU");
+        return e && strcmp(e, "fused") == 0;
+    }();
+    return f;
+}
+
 static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t st) {
     const ZiggyHipModelDesc &md = s->md;
+    const bool fused_swiglu = verify_fused_swiglu();
     const int H = (int)md.embedding_length, F = (int)md.feed_forward_length, Q = s->q_size, KV = s->kv_size;
     const float eps = md.rms_norm_eps;
     hipError_t e = launch_embed_rows(s->b_tokens, M, s->embd.p, s->embd.stride, (int)s->embd.rows, s->embd.type, H,
@@ -768,21 +779,30 @@ static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t
             e = launch_attention(a, st);
         }
         gemm(L.o, nullptr, s->b_attn, Q, s->b_hidden, H, OUT_ADD);
-        if (e == hipSuccess) e = launch_rms_norm_rows(s->b_hidden, (const float *)L.ffn_norm.p, s->b_normed, M, H, eps, st);
-        if (L.gate.type == L.up.type) {
+        if (fused_swiglu && L.gate.type == L.up.type) {
+            if (e == hipSuccess)
+                e = launch_rms_norm_rows(s->b_hidden, (const float *)L.ffn_norm.p, s->b_normed, M, H, eps, st);
             gemm(L.gate, &L.up, s->b_normed, H, s->b_act, F, OUT_SWIGLU);
         } else {
-            gemm(L.gate, nullptr, s->b_normed, H, s->b_act, F, OUT_STORE);
-            gemm(L.up, nullptr, s->b_normed, H, s->b_up, F, OUT_STORE);
+            // gate and up accumulate onto rows the norm clears (each product
+            // may split its reduction), then SiLU(gate) * up
+            if (e == hipSuccess)
+                e = launch_rms_norm_rows(s->b_hidden, (const float *)L.ffn_norm.p, s->b_normed, M, H, eps, st,
+                                         s->b_act, (size_t)M * F, s->b_up, (size_t)M * F);
+            gemm(L.gate, nullptr, s->b_normed, H, s->b_act, F, OUT_ADD);
+            gemm(L.up, nullptr, s->b_normed, H, s->b_up, F, OUT_ADD);
             if (e == hipSuccess) e = launch_silu_mul(s->b_act, s->b_up, M * F, st);
         }
         gemm(L.down, nullptr, s->b_act, F, s->b_hidden, H, OUT_ADD);
     }
-    // the final norm also clears the argmax keys
+    // the final norm also clears the argmax keys; the output product stores
+    // the logits (its reduction may split), then a per-token argmax
     if (e == hipSuccess)
         e = launch_rms_norm_rows(s->b_hidden, (const float *)s->out_norm.p, s->b_normed, M, H, eps, st,
                                  reinterpret_cast<float *>(s->b_argmax), (size_t)M * 2);
-    gemm(s->out, nullptr, s->b_normed, H, nullptr, 0, OUT_ARGMAX);
+    const int V = (int)md.vocab_size;
+    gemm(s->out, nullptr, s->b_normed, H, s->b_logits, V, OUT_STORE);
+    if (e == hipSuccess) e = launch_argmax_rows(s->b_logits, M, (int)s->out.rows, V, s->b_argmax, st);
     return e;
 }
 
