@@ -139,6 +139,12 @@ hipError_t launch_argmax_rows(const float *x, int rows, int n, int ld, unsigned 
 hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
                        bool precise = false);
+// Up to three matrices of one format, row stride and reduction length against
+// one input (stores or adds): one launch on the exact-code kernel, else one
+// product each.
+hipError_t launch_gemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
+                             const int *N, uint64_t stride, const float *x, int ldx, int M, int K, int out,
+                             hipStream_t s);
 hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps, hipStream_t s,
                                 float *clear0 = nullptr, size_t n0 = 0, float *clear1 = nullptr, size_t n1 = 0,
                                 float *clear2 = nullptr, size_t n2 = 0);
@@ -151,6 +157,11 @@ hipError_t launch_gemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uin
 bool qgemm_supported(int fmt, int K, const void *w, const void *w2, uint64_t stride, uint64_t expert_stride);
 hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                         float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s);
+// Up to three matrices of one format, row stride and reduction length against
+// one input in one launch (matrix i: rows N[i], output y[i] with row stride ldy[i]).
+hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
+                              const int *N, const uint8_t *w2, uint64_t stride, const float *x, int ldx, int M, int K,
+                              int out, unsigned long long *argmax, hipStream_t s);
 hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride,
                                 uint64_t expert_stride, const float *x, int ldx, int x_div, float *y, int ldy, int N,
                                 int K, int out, const int *tiles, const int *list, const int *ntiles, int max_tiles,

@@ -58,6 +58,13 @@ struct QGemmParams {
     int x_div;
     uint64_t expert_stride;
     int ksplit;  // blockIdx.z takes reduction values [z K / ksplit, (z + 1) K / ksplit); results add atomically
+    // Up to three matrices of one format and reduction length in one launch
+    // (one input): matrix 0 is w / N / y / ldy, matrices 1 and 2 start at row
+    // groups gs[0], gs[1] of the launch's `groups` row groups.
+    int groups, nseg;
+    const uint8_t *ws[2];
+    float *ys[2];
+    int Ns[2], ldys[2], gs[2];
 };
 
 typedef float qf2v __attribute__((ext_vector_type(2)));
@@ -307,23 +314,36 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
         m0 = 0;
         M = gt[2];
     }
-    const uint8_t *wm[kMats];
-    wm[0] = w;
-    if (kPair) wm[kMats - 1] = w2;
     // Row groups of 64 rows (16 per wavefront): this workgroup takes groups
     // blockIdx.x, blockIdx.x + gridDim.x, ... -- several only when its
     // reduction range is one stage, whose activations then serve them all.
     // Work items (group, chunk) run group by group; the code ring runs across
-    // groups.
-    const int groups = (p.N + kQRows - 1) / kQRows;
-    const int ng = (groups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
+    // groups.  Group g belongs to matrix seg(g) (the last whose first group
+    // is at most g).
+    struct Seg {
+        const uint8_t *w;
+        float *y;
+        int N, ldy, g0;
+    };
+    auto seg_of = [&](int g) {
+        Seg r{w, p.y, p.N, p.ldy, 0};
+        if (p.nseg > 1 && g >= p.gs[0]) r = Seg{p.ws[0], p.ys[0], p.Ns[0], p.ldys[0], p.gs[0]};
+        if (p.nseg > 2 && g >= p.gs[1]) r = Seg{p.ws[1], p.ys[1], p.Ns[1], p.ldys[1], p.gs[1]};
+        return r;
+    };
+    const int ng = (p.groups - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
     const int kspan = p.K / p.ksplit, kbeg = blockIdx.z * kspan;
     const int nspan = kspan / kQChunk, cb = kbeg / kQChunk;
     const int nitems = ng * nspan;
-    // first row of this wavefront in item t's group (t clamped), its chunk
-    auto item = [&](int t, int &row0, int &ca) {
-        const int tc = min(t, nitems - 1), gi = tc / nspan;
-        row0 = ((int)blockIdx.x + gi * (int)gridDim.x) * kQRows + 16 * wave;
+    // item t (clamped): its matrices, their rows, the first row of this
+    // wavefront, the chunk
+    auto item = [&](int t, const uint8_t *(&wm)[kMats], int &nrows, int &row0, int &ca) {
+        const int tc = min(t, nitems - 1), gi = tc / nspan, g = (int)blockIdx.x + gi * (int)gridDim.x;
+        const Seg sg = seg_of(g);
+        wm[0] = sg.w;
+        if (kPair) wm[kMats - 1] = w2;
+        nrows = sg.N;
+        row0 = (g - sg.g0) * kQRows + 16 * wave;
         ca = cb + tc - gi * nspan;
     };
 
@@ -469,14 +489,15 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     // past N re-read row N - 1 (dropped at the store).
     qu4v raw[R][kMats][kP];  // native vectors: the ring stays in registers
     auto ring_load = [&](int q, int t) {
-        int row0, ca;
-        item(t, row0, ca);
+        const uint8_t *wm[kMats];
+        int nrows, row0, ca;
+        item(t, wm, nrows, row0, ca);
 #pragma unroll
         for (int m = 0; m < kMats; m++)
 #pragma unroll
             for (int j = 0; j < kP; j++) {
                 const uint8_t *st =
-                    wm[m] + (uint64_t)min(row0 + prow[j], p.N - 1) * p.stride + (size_t)ca * kCB;
+                    wm[m] + (uint64_t)min(row0 + prow[j], nrows - 1) * p.stride + (size_t)ca * kCB;
                 const int sh = (int)((uintptr_t)st & kShm);
                 const int wn = (sh + kCB + 15) >> 4;
                 raw[q][m][j] = *reinterpret_cast<const qu4v *>(
@@ -500,11 +521,12 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     // Item t (in ring slot t % R) into the row images, its slot refilled
     // with item t + R, and its fields read into ff.
     auto fetch = [&](int q, int t, QC (&ff)[kMats]) {
-        int row0, ca;
-        item(t, row0, ca);
+        const uint8_t *wm[kMats];
+        int nrows, row0, ca;
+        item(t, wm, nrows, row0, ca);
         ring_put(q);
         ring_load(q, t + R);
-        const uint64_t off = (uint64_t)min(row0 + li, p.N - 1) * p.stride + (size_t)ca * kCB;
+        const uint64_t off = (uint64_t)min(row0 + li, nrows - 1) * p.stride + (size_t)ca * kCB;
 #pragma unroll
         for (int m = 0; m < kMats; m++)
             ff[m].load(&code_s[wave][m][li * kRowW], (int)((uintptr_t)(wm[m] + off) & kShm), lg);
@@ -531,13 +553,14 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     };
     // The results of group g: D[token 4 lg + r][row li]; acc cleared after.
     auto epilogue = [&](int g) {
-        const int nn = g * kQRows + 16 * wave + li;
+        const Seg sg = seg_of(g);
+        const int nn = (g - sg.g0) * kQRows + 16 * wave + li;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int j = m0 + 4 * lg + r;  // token of result r
-            if (j >= M || nn >= p.N) continue;
+            if (j >= M || nn >= sg.N) continue;
             const int jrow = GROUPED ? ids[4 * lg + r] : j;
-            float *dst = p.y ? p.y + (size_t)jrow * p.ldy + nn : nullptr;
+            float *dst = sg.y ? sg.y + (size_t)jrow * sg.ldy + nn : nullptr;
             const float v = acc[r];
             if ((OUT == OUT_STORE || OUT == OUT_ADD) && p.ksplit > 1) {
                 atomicAdd(dst, v);  // partial sum of this workgroup's reduction range (STORE rows zeroed first)
@@ -555,8 +578,8 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
             for (int r = 0; r < 4; r++) {
                 const int j = m0 + 4 * lg + r;
                 const float v = acc[r];
-                if (p.y && j < M && nn < p.N) p.y[(size_t)j * p.ldy + nn] = v;
-                unsigned long long key = (j < M && nn < p.N)
+                if (sg.y && j < M && nn < sg.N) sg.y[(size_t)j * sg.ldy + nn] = v;
+                unsigned long long key = (j < M && nn < sg.N)
                                              ? ((unsigned long long)ordered_bits_q(v) << 32) |
                                                    (unsigned long long)(0xFFFFFFFFu - (uint32_t)nn)
                                              : 0ull;
@@ -705,10 +728,27 @@ static double qgemm_stage_weight() {
     return w;
 }
 
-hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
-                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s) {
-    if (M < 1 || N < 1 || !qgemm_supported(fmt, K, w, w2, stride, 0) || ldx % 4) return hipErrorInvalidValue;
-    const int groups = (N + kQRows - 1) / kQRows, tiles = (M + 15) / 16, chunks = K / kQChunk;
+hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
+                              const int *N, const uint8_t *w2, uint64_t stride, const float *x, int ldx, int M, int K,
+                              int out, unsigned long long *argmax, hipStream_t s) {
+    if (nseg < 1 || nseg > 3 || M < 1 || ldx % 4 || (nseg > 1 && (out == OUT_SWIGLU || out == OUT_ARGMAX)))
+        return hipErrorInvalidValue;
+    QGemmParams p{w[0], w2, stride, x, y[0], M, N[0], K, ldx, ldy[0], argmax, nullptr, nullptr, nullptr, 1, 0, 1};
+    int groups = 0;
+    for (int i = 0; i < nseg; i++) {
+        if (N[i] < 1 || !qgemm_supported(fmt, K, w[i], w2, stride, 0)) return hipErrorInvalidValue;
+        if (i > 0) {
+            p.ws[i - 1] = w[i];
+            p.ys[i - 1] = y[i];
+            p.Ns[i - 1] = N[i];
+            p.ldys[i - 1] = ldy[i];
+            p.gs[i - 1] = groups;
+        }
+        groups += (N[i] + kQRows - 1) / kQRows;
+    }
+    p.groups = groups;
+    p.nseg = nseg;
+    const int tiles = (M + 15) / 16, chunks = K / kQChunk;
     const int target = qgemm_target_wgs();
     const int stage = out == OUT_SWIGLU ? stage_chunks_of<true>(fmt) : stage_chunks_of<false>(fmt);
     // Reduction split ks (a power of two; results added atomically, plain
@@ -734,16 +774,23 @@ hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t s
         if (can_split)
             while (groups * tiles * ks * 2 <= target && chunks % (ks * 2) == 0) ks *= 2;
     }
+    p.ksplit = ks;
     QGemmKernel k = pick_qf<false>(fmt, out, K / ks);
     if (!k) return hipErrorInvalidValue;
     if (ks > 1 && out == OUT_STORE) {
-        hipLaunchKernelGGL(zero_rows_kernel, dim3((M * N + 255) / 256), dim3(256), 0, s, y, ldy, M, N);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+        for (int i = 0; i < nseg; i++) {
+            hipLaunchKernelGGL(zero_rows_kernel, dim3((M * N[i] + 255) / 256), dim3(256), 0, s, y[i], ldy[i], M, N[i]);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
     }
-    QGemmParams p{w, w2, stride, x, y, M, N, K, ldx, ldy, argmax, nullptr, nullptr, nullptr, 1, 0, ks};
     hipLaunchKernelGGL(k, dim3(pg, tiles, ks), dim3(256), 0, s, p);
     return hipGetLastError();
+}
+
+hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
+                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s) {
+    return launch_qgemm_multi(fmt, 1, &w, &y, &ldy, &N, w2, stride, x, ldx, M, K, out, argmax, s);
 }
 
 hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride,
@@ -755,7 +802,9 @@ hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, ui
     QGemmKernel k = pick_qf<true>(fmt, out, K);
     if (!k) return hipErrorInvalidValue;
     QGemmParams p{w, w2, stride, x, y, 16, N, K, ldx, ldy, nullptr, tiles, list, ntiles, x_div, expert_stride, 1};
-    hipLaunchKernelGGL(k, dim3((N + kQRows - 1) / kQRows, max_tiles), dim3(256), 0, s, p);
+    p.groups = (N + kQRows - 1) / kQRows;
+    p.nseg = 1;
+    hipLaunchKernelGGL(k, dim3(p.groups, max_tiles), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 

@@ -701,14 +701,33 @@ static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t
         e = launch_gemm(w.type, w.p, w2 ? w2->p : nullptr, w.stride, x, ldx, y, ldy, M, (int)w.rows, (int)w.cols,
                         out, s->b_argmax, st);
     };
+    // products of the normed rows that accumulate (OUT_ADD) onto cleared
+    // outputs: one launch for the matrices that share a format and row size
+    auto multi3 = [&](const DT &a, float *ya, int lda, const DT &b, float *yb, int ldb, const DT *c, float *yc,
+                      int ldc) {
+        if (e != hipSuccess) return;
+        const DT *d[3] = {&a, &b, c};
+        float *ys[3] = {ya, yb, yc};
+        const int lds[3] = {lda, ldb, ldc};
+        const int n = c ? 3 : 2;
+        int i = 0;
+        while (i < n && e == hipSuccess) {
+            int j = i + 1;  // a run of matrices of one type and row size
+            while (j < n && d[j]->type == d[i]->type && d[j]->stride == d[i]->stride && d[j]->cols == d[i]->cols) j++;
+            const uint8_t *ws[3];
+            int Ns[3];
+            for (int k = i; k < j; k++) ws[k - i] = d[k]->p, Ns[k - i] = (int)d[k]->rows;
+            e = launch_gemm_multi(d[i]->type, j - i, ws, ys + i, lds + i, Ns, d[i]->stride, s->b_normed, H, M,
+                                  (int)d[i]->cols, OUT_ADD, st);
+            i = j;
+        }
+    };
     for (int l = 0; l < (int)md.block_count && e == hipSuccess; l++) {
         const LayerW &L = s->layers[l];
         // the norm clears the q/k/v rows, which the products then accumulate onto
         e = launch_rms_norm_rows(s->b_hidden, (const float *)L.attn_norm.p, s->b_normed, M, H, eps, st, s->b_q,
                                  (size_t)M * Q, s->b_k, (size_t)M * KV, s->b_v, (size_t)M * KV);
-        gemm(L.q, nullptr, s->b_normed, H, s->b_q, Q, OUT_ADD);
-        gemm(L.k, nullptr, s->b_normed, H, s->b_k, KV, OUT_ADD);
-        gemm(L.v, nullptr, s->b_normed, H, s->b_v, KV, OUT_ADD);
+        multi3(L.q, s->b_q, Q, L.k, s->b_k, KV, &L.v, s->b_v, KV);
         const size_t layer_base = (size_t)l * md.context_length * s->kv_size;
         if (s->b_counters && e == hipSuccess) {
             AttnParams a{};
@@ -789,8 +808,7 @@ static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t
             if (e == hipSuccess)
                 e = launch_rms_norm_rows(s->b_hidden, (const float *)L.ffn_norm.p, s->b_normed, M, H, eps, st,
                                          s->b_act, (size_t)M * F, s->b_up, (size_t)M * F);
-            gemm(L.gate, nullptr, s->b_normed, H, s->b_act, F, OUT_ADD);
-            gemm(L.up, nullptr, s->b_normed, H, s->b_up, F, OUT_ADD);
+            multi3(L.gate, s->b_act, F, L.up, s->b_up, F, nullptr, nullptr, 0);
             if (e == hipSuccess) e = launch_silu_mul(s->b_act, s->b_up, M * F, st);
         }
         gemm(L.down, nullptr, s->b_act, F, s->b_hidden, H, OUT_ADD);
