@@ -804,7 +804,16 @@ hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, ui
     QGemmParams p{w, w2, stride, x, y, 16, N, K, ldx, ldy, nullptr, tiles, list, ntiles, x_div, expert_stride, 1};
     p.groups = (N + kQRows - 1) / kQRows;
     p.nseg = 1;
-    hipLaunchKernelGGL(k, dim3(p.groups, max_tiles), dim3(256), 0, s, p);
+    // A one-stage reduction lets a workgroup take several row groups of its
+    // token tile against one staging: about four workgroups per CU at the
+    // largest tile count (the launch's bound; unused tiles exit at once).
+    const int stage = out == OUT_SWIGLU ? stage_chunks_of<true>(fmt) : stage_chunks_of<false>(fmt);
+    int pg = p.groups;
+    if (K / kQChunk <= stage) {
+        pg = 4 * qgemm_target_wgs() / max_tiles;
+        pg = pg < 1 ? 1 : pg > p.groups ? p.groups : pg;
+    }
+    hipLaunchKernelGGL(k, dim3(pg, max_tiles), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
