@@ -131,7 +131,8 @@ def main():
     if args.model == "llama8b":
         from zhip import pmc
         traffic = pmc.read_traffic(os.path.join(REPO, "profiles", "gate_up_llama8b_hbm_traffic.md"))
-    roofline = {"bound": "hbm", "kernel": "gate_up (fused RMSNorm + Q4_K gate/up + SwiGLU)",
+    gate_fmt = {"llama8b": "Q4_K", "tinyllama": "Q4_K", "qwen3": "Q8_0"}.get(args.model, "quantized")
+    roofline = {"bound": "hbm", "kernel": f"gate_up (fused RMSNorm + {gate_fmt} gate/up + SwiGLU)",
                 "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "bytes_per_launch": dom["bytes"], "avg_launch_us": dom["avg_us"]}
