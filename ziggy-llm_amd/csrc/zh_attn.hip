@@ -619,6 +619,7 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     constexpr int TP = 32;       // positions per wavefront tile
     constexpr int QS = HD + 8;   // padded row of the query pieces (binary16)
     constexpr int LPR = HD / 8;  // lanes per value row (8 dims each)
+    touch_params(p);
     const int split = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
     const int Gq = GG ? GG : p.head_count / p.head_count_kv;  // query heads per kv head

@@ -72,6 +72,20 @@ inline bool buf_ok(const ZiggyHipBuffer *b, size_t need) { return b && b->ptr &&
 enum InMode : int { IN_PLAIN = 0, IN_NORM = 1, IN_SILU = 2 };
 enum OutMode : int { OUT_STORE = 0, OUT_ADD = 1, OUT_SWIGLU = 2, OUT_ARGMAX = 3, OUT_WADD = 4 };
 
+// One batch of scalar loads touching every 64-byte line of a kernel's
+// parameter block (up to 12 lines): the kernel's later reads of any field hit
+// the scalar cache instead of paying a memory round trip each along their
+// dependent chains (segment search, then the segment's fields, then the
+// addresses of the first loads).
+template <class P> __device__ __forceinline__ void touch_params(const P &p) {
+    static_assert(sizeof(P) <= 12 * 64, "up to 12 parameter lines");
+    constexpr int L = (int)((sizeof(P) + 63) / 64) - 1;  // last line
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(&p);
+    auto at = [&](int line) { return w[16 * (line < L ? line : L)]; };
+    __asm__ volatile("" ::"s"(at(0)), "s"(at(1)), "s"(at(2)), "s"(at(3)), "s"(at(4)), "s"(at(5)), "s"(at(6)),
+                     "s"(at(7)), "s"(at(8)), "s"(at(9)), "s"(at(10)), "s"(at(11)));
+}
+
 struct MvSeg {
     const uint8_t *w;       // first row of the segment
     uint64_t stride;        // bytes per row
@@ -103,7 +117,7 @@ struct MvParams {
     int rows_per_expert;
     int expert_limit;                 // expert ids >= this are ignored (no rows are read)
     float weight_scale;               // WADD: y += scale * dot (scale from entries if expert set)
-    const int *gate_flag;             // optional device flag: kernel exits if *gate_flag == 0
+    const int *gate_flag;             // optional device flag (argmax output only): kernel exits if *gate_flag == 0
 };
 
 // Builds the launch plan (team size, rows per team, workgroup ranges) and launches.

@@ -538,13 +538,18 @@ __device__ __forceinline__ void mv_dispatch(const MvParams &p, const MvSeg &sg, 
 template <int F1, int F2, int IN, int OUT, int TT, int NB>
 __global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
     __shared__ float lds[36];
-    if (p.gate_flag && *p.gate_flag == 0) return;
+    touch_params(p);  // the segment search, the segment's fields, the inputs' addresses
+    // only the output head is gated (prompt steps skip it): the other
+    // kernels do not wait for the flag's loads before issuing their own
+    if (OUT == OUT_ARGMAX && p.gate_flag && *p.gate_flag == 0) return;
     const int wg = blockIdx.x;
     int si = 0;
 #pragma unroll
     for (int i = 1; i < kMaxSeg; i++)
         if (i < p.nseg && wg >= p.seg[i].wg_begin) si = i;
-    const MvSeg &sg = p.seg[si];
+    // a copy: every field of the segment is read in one batch of scalar
+    // loads, not one dependent round trip per use
+    const MvSeg sg = p.seg[si];
     if (F1 == F2 || sg.fmt == F1)
         mv_dispatch<F1, IN, OUT, TT, NB>(p, sg, wg - sg.wg_begin, lds);
     else

@@ -301,6 +301,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     constexpr int kStage = G::kStage, kStageChunks = G::kStageChunks;
     static_assert(kStageChunks % R == 0 && R % 2 == 0, "stages hold whole rings of an even depth");
 
+    touch_params(p);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
     int m0 = blockIdx.y * 16, M = p.M;
     const int *ids = nullptr;
