@@ -399,6 +399,42 @@ int ziggy_hip_session_verify(ZiggyHipSession *session, uint32_t current_token, c
 int ziggy_hip_session_read_logits(ZiggyHipSession *session, float *out, char *error_message,
                                   size_t error_message_len);
 
+/* ---- stochastic decoding: device shortlist, host sampler ---- */
+
+/* ShortlistEntry (runtime/gpu/types.zig:114-117). */
+typedef struct {
+    uint32_t token_id;
+    float logit;
+} ZiggyHipShortlistEntry;
+/* The sampling fields of GenerationOptions (runtime/types.zig:171-185). */
+typedef struct {
+    float temperature;
+    float repeat_penalty;
+    uint32_t top_k; /* 0: no limit */
+    float top_p;
+    float min_p;
+} ZiggyHipSamplingOptions;
+/* One decode step of `token` whose output is the top-`count` shortlist of the
+ * logits: count <= 64 (max_shortlist_len, runtime/gpu/types.zig:119), the
+ * highest logit first, ties to the lower token id (replaces
+ * Session.runOutputShortlist, runtime/gpu/session.zig:789-828, which
+ * model/loader.zig:1047 calls for the shortlist sampler).  The logits stay
+ * readable with session_read_logits; the position advances by one. */
+int ziggy_hip_session_step_shortlist(ZiggyHipSession *session, uint32_t token, uint32_t count,
+                                     ZiggyHipShortlistEntry *out, char *error_message, size_t error_message_len);
+/* shortlistLenFor (sampling.zig:47-52): the shortlist a step should return. */
+uint32_t ziggy_hip_shortlist_len(const ZiggyHipSamplingOptions *options, uint32_t vocab_size);
+/* The reference's CPU sampler, on the host: sampleShortlist
+ * (sampling.zig:31-45, policy :54-110) over a shortlist, and sampleToken
+ * (sampling.zig:11-29) over full logits.  recent: the tokens so far (repeat
+ * penalty); uniform: the value random.float(f64) gives the reference, in
+ * [0, 1).  Host code only: no device work. */
+int ziggy_hip_sample_shortlist(const ZiggyHipShortlistEntry *entries, uint32_t count, const uint32_t *recent,
+                               uint32_t recent_count, const ZiggyHipSamplingOptions *options, double uniform,
+                               uint32_t *out_token);
+int ziggy_hip_sample_logits(const float *logits, uint32_t count, const uint32_t *recent, uint32_t recent_count,
+                            const ZiggyHipSamplingOptions *options, double uniform, uint32_t *out_token);
+
 /* Times one kernel of the decode step (no counterpart in the reference; its
  * Metal profiler times host-side encode, runtime/metal_profile.zig:80-315):
  * one warm-up launch, then `iterations` back-to-back launches at the

@@ -138,6 +138,12 @@ hipError_t launch_silu_mul(float *gate, const float *up, int n, hipStream_t s);
 hipError_t launch_add(float *dst, const float *src, int n, hipStream_t s);
 hipError_t launch_argmax(const float *x, int n, uint32_t *out_token, unsigned long long *tmp, hipStream_t s);
 hipError_t launch_topk(const float *x, int n, int k, void *entries, hipStream_t s);
+// Output shortlist (zh_sample.hip): the top k (<= 64) of n (<= 262144) values
+// as entries {u32 id, f32 value}, highest first, ties to the lower id; keys:
+// shortlist_scratch_keys(n) packed keys of device scratch.
+size_t shortlist_scratch_keys(int n);
+hipError_t launch_shortlist(const float *x, int n, int k, unsigned long long *keys, uint32_t *entries,
+                            hipStream_t s);
 hipError_t launch_normalize_topk(void *entries, int k, int softmax, int normalize, float scale, hipStream_t s);
 hipError_t launch_weighted_sum_topk(float *dst, const float *src, const void *entries, int n, int slot,
                                     hipStream_t s);

@@ -640,7 +640,16 @@ int ziggy_hip_argmax_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *in, ZiggyHi
 int ziggy_hip_topk_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *in, ZiggyHipBuffer *entries, uint32_t n,
                        uint32_t k, char *err, size_t err_len) {
     ZH_N_CHECK(ctx && n > 0 && k > 0 && k <= 64 && k <= n && buf_ok(in, (size_t)n * 4) && buf_ok(entries, (size_t)k * 8));
-    // entries are produced in the context scratch (k slots + per-value flags) then copied out
+    if (n <= 262144) {
+        // two-stage shortlist (per-slice top k, then the top k of those); packed keys in the context scratch
+        ZH_N_CHECK(shortlist_scratch_keys((int)n) * 8 <= ctx->scratch_len);
+        ZH_TRY(launch_shortlist((const float *)in->ptr, (int)n, (int)k, (unsigned long long *)ctx->scratch,
+                                (uint32_t *)entries->ptr, ctx->stream),
+               "topk");
+        return finish_op(ctx, "topk", err, err_len);
+    }
+    // longer inputs: k rounds of a workgroup argmax; entries in the context
+    // scratch (k slots + per-value flags), then copied out
     ZH_N_CHECK(64 * 8 + (size_t)n <= ctx->scratch_len);
     ZH_TRY(launch_topk((const float *)in->ptr, (int)n, (int)k, ctx->scratch, ctx->stream), "topk");
     ZH_TRY(hipMemcpyAsync(entries->ptr, ctx->scratch, (size_t)k * 8, hipMemcpyDeviceToDevice, ctx->stream), "topk");

@@ -60,6 +60,9 @@ struct ZiggyHipSession {
     // batched verify (allocated on first use): [kVerifyMax] rows each
     float *b_hidden = nullptr, *b_normed = nullptr, *b_q = nullptr, *b_k = nullptr, *b_v = nullptr;
     float *b_attn = nullptr, *b_act = nullptr, *b_up = nullptr, *b_logits = nullptr;
+    // output shortlist (allocated on first use): packed keys, entries
+    unsigned long long *sl_keys = nullptr;
+    uint32_t *sl_entries = nullptr;
     uint32_t *b_tokens = nullptr;
     unsigned long long *b_argmax = nullptr;
     // multi-query attention of a verify pass: partials and arrival counters
@@ -564,6 +567,30 @@ int ziggy_hip_session_step_greedy(ZiggyHipSession *s, uint32_t token, uint32_t *
 int ziggy_hip_session_step_no_output(ZiggyHipSession *s, uint32_t token, char *err, size_t err_len) {
     if (!s) return ZIGGY_HIP_INVALID_ARGUMENT;
     return host_step(s, token, false, nullptr, err, err_len);
+}
+
+int ziggy_hip_session_step_shortlist(ZiggyHipSession *s, uint32_t token, uint32_t count,
+                                     ZiggyHipShortlistEntry *out, char *err, size_t err_len) {
+    if (!s || !out) return ZIGGY_HIP_INVALID_ARGUMENT;
+    const int V = (int)s->md.vocab_size;
+    if (count == 0 || count > 64 || (int)count > V)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "shortlist length must be 1..64 and at most the vocabulary");
+    if (V > 262144) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "vocabulary too large for the shortlist");
+    if (!s->sl_keys) {
+        ZH_TRY(hipMalloc((void **)&s->sl_keys, shortlist_scratch_keys(V) * 8), "shortlist buffers");
+        s->allocs.push_back(s->sl_keys);
+        ZH_TRY(hipMalloc((void **)&s->sl_entries, 64 * 8), "shortlist buffers");
+        s->allocs.push_back(s->sl_entries);
+    }
+    const int st = host_step(s, token, false, nullptr, err, err_len);
+    if (st != ZIGGY_HIP_OK) return st;
+    hipStream_t sm = s->ctx->stream;
+    ZH_TRY(enqueue_output_logits(s, sm), "shortlist output");
+    ZH_TRY(launch_shortlist(s->logits, V, (int)count, s->sl_keys, s->sl_entries, sm), "shortlist");
+    ZH_TRY(hipMemcpyAsync(out, s->sl_entries, (size_t)count * 8, hipMemcpyDeviceToHost, sm), "shortlist readback");
+    ZH_TRY(hipStreamSynchronize(sm), "shortlist");
+    s->logits_valid = true;
+    return ZIGGY_HIP_OK;
 }
 
 int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint32_t prompt_len, uint32_t steps,

@@ -67,6 +67,19 @@ MOE_LAYER_FIELDS = ["ffn_norm", "router", "gate_exps", "up_exps", "down_exps", "
                     "down_shexp", "gate_inp_shexp"]
 
 
+class ShortlistEntry(ctypes.Structure):
+    _fields_ = [("token_id", ctypes.c_uint32), ("logit", ctypes.c_float)]
+
+
+class SamplingOptions(ctypes.Structure):
+    """The sampling fields of GenerationOptions (runtime/types.zig:171-185)."""
+    _fields_ = [("temperature", ctypes.c_float), ("repeat_penalty", ctypes.c_float), ("top_k", ctypes.c_uint32),
+                ("top_p", ctypes.c_float), ("min_p", ctypes.c_float)]
+
+    def __init__(self, temperature=0.0, repeat_penalty=1.0, top_k=0, top_p=1.0, min_p=0.0):
+        super().__init__(temperature, repeat_penalty, top_k, top_p, min_p)
+
+
 class MoeLayerDesc(ctypes.Structure):
     _fields_ = [(n, TensorDesc) for n in MOE_LAYER_FIELDS]
 
@@ -145,6 +158,12 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_session_generate": [vp, vp, u32, u32, vp, ctypes.POINTER(GenerateStats)] + E,
         "ziggy_hip_session_read_logits": [vp, vp] + E,
         "ziggy_hip_session_verify": [vp, u32, vp, u32, vp, ctypes.POINTER(u32)] + E,
+        "ziggy_hip_session_step_shortlist": [vp, u32, u32, vp] + E,
+        "ziggy_hip_shortlist_len": [ctypes.POINTER(SamplingOptions), u32],
+        "ziggy_hip_sample_shortlist": [vp, u32, vp, u32, ctypes.POINTER(SamplingOptions), ctypes.c_double,
+                                       ctypes.POINTER(u32)],
+        "ziggy_hip_sample_logits": [vp, u32, vp, u32, ctypes.POINTER(SamplingOptions), ctypes.c_double,
+                                    ctypes.POINTER(u32)],
         "ziggy_hip_session_time_kernel": [vp, u32, u32, ctypes.POINTER(ctypes.c_uint64),
                                           ctypes.POINTER(ctypes.c_uint64)] + E,
         "ziggy_hip_moe_stack_create": [vp, ctypes.POINTER(MoeDesc), ctypes.POINTER(MoeLayerDesc), u32,
@@ -158,7 +177,8 @@ def lib() -> ctypes.CDLL:
     }
     restypes = {"ziggy_hip_destroy_context": None, "ziggy_hip_destroy_buffer": None,
                 "ziggy_hip_session_destroy": None, "ziggy_hip_moe_stack_destroy": None, "ziggy_hip_buffer_length": sz,
-                "ziggy_hip_session_position": u32, "ziggy_hip_version": ctypes.c_char_p}
+                "ziggy_hip_session_position": u32, "ziggy_hip_version": ctypes.c_char_p,
+                "ziggy_hip_shortlist_len": u32}
     for name, args in sigs.items():
         fn = getattr(L, name)
         fn.argtypes = args
@@ -415,6 +435,12 @@ class Session:
               ctypes.byref(st))
         return out[:steps].copy(), st
 
+    def step_shortlist(self, token: int, count: int):
+        """One decode step of `token`; the top-`count` logits as (token ids, logits), highest first."""
+        out = (ShortlistEntry * count)()
+        _call("ziggy_hip_session_step_shortlist", self.h, token, count, ctypes.cast(out, ctypes.c_void_p))
+        return (np.array([e.token_id for e in out], np.uint32), np.array([e.logit for e in out], np.float32))
+
     def verify(self, current: int, drafts):
         """(predicted tokens [len(drafts) + 1], emitted count) of one batched verify pass."""
         drafts = np.ascontiguousarray(drafts, dtype=np.uint32)
@@ -551,3 +577,41 @@ class MoeStack:
         if getattr(self, "h", None):
             lib().ziggy_hip_moe_stack_destroy(self.h)
             self.h = None
+
+
+def _sample_status(st: int, name: str):
+    if st != 0:
+        raise HipError(st, f"{name}: invalid arguments")
+
+
+def shortlist_len(options: SamplingOptions, vocab: int) -> int:
+    """shortlistLenFor (sampling.zig:47-52)."""
+    return int(lib().ziggy_hip_shortlist_len(ctypes.byref(options), vocab))
+
+
+def sample_shortlist(ids, logits, recent, options: SamplingOptions, uniform: float) -> int:
+    """sampleShortlist (sampling.zig:31-45) on the host; uniform: the draw random.float(f64) would give."""
+    n = len(ids)
+    ents = (ShortlistEntry * max(n, 1))()
+    for k in range(n):
+        ents[k].token_id = int(ids[k])
+        ents[k].logit = float(logits[k])
+    rec = np.ascontiguousarray(recent, np.uint32)
+    tok = ctypes.c_uint32()
+    _sample_status(lib().ziggy_hip_sample_shortlist(ctypes.cast(ents, ctypes.c_void_p), n,
+                                                      rec.ctypes.data if rec.size else None, rec.size,
+                                                      ctypes.byref(options), uniform, ctypes.byref(tok)),
+                   "sample_shortlist")
+    return int(tok.value)
+
+
+def sample_logits(logits, recent, options: SamplingOptions, uniform: float) -> int:
+    """sampleToken (sampling.zig:11-29) on the host over full logits."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    rec = np.ascontiguousarray(recent, np.uint32)
+    tok = ctypes.c_uint32()
+    _sample_status(lib().ziggy_hip_sample_logits(lg.ctypes.data, lg.size, rec.ctypes.data if rec.size else None,
+                                                   rec.size, ctypes.byref(options), uniform, ctypes.byref(tok)),
+                   "sample_logits")
+    return int(tok.value)
+
