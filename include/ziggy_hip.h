@@ -395,6 +395,18 @@ int ziggy_hip_session_generate(ZiggyHipSession *session, const uint32_t *prompt,
 int ziggy_hip_session_verify(ZiggyHipSession *session, uint32_t current_token, const uint32_t *drafts,
                              uint32_t draft_count, uint32_t *out_predicted, uint32_t *out_count,
                              char *error_message, size_t error_message_len);
+/* Prompt prefill reusing the cached prefix (replaces the prefix reuse of
+ * generateLoadedStreamingCached, model/loader.zig:2281-2336).  The session
+ * records the token of every K/V row its token steps wrote.  The longest
+ * common prefix of those and `prompt` is kept (the position moves back to it;
+ * the reference instead resets unless all of its cache is a prefix of the
+ * prompt), then the rest of the prompt is fed; the last prompt token is always
+ * fed again, for its logits.  *out_reused: the prefix kept; *out_next: the
+ * greedy token after the prompt.  Rows written by the block-level calls
+ * (run_attention_block) are not reused. */
+int ziggy_hip_session_prefill_cached(ZiggyHipSession *session, const uint32_t *prompt, uint32_t prompt_len,
+                                     uint32_t *out_reused, uint32_t *out_next, char *error_message,
+                                     size_t error_message_len);
 /* Logits of the most recent step that ran the output head (f32, vocab_size). */
 int ziggy_hip_session_read_logits(ZiggyHipSession *session, float *out, char *error_message,
                                   size_t error_message_len);

@@ -134,3 +134,43 @@ def test_rewind_then_verify_accepts_the_decoded_drafts(hip_ctx):
     with pytest.raises(hip.HipError):
         s.rewind(s.position + 1)
     s.close()
+
+
+def test_prefill_cached_reuses_the_common_prefix(hip_ctx):
+    # the stream after a prompt fed through prefill_cached equals a fresh session's, and the
+    # reused prefix is the common prefix of the rows the session holds and the prompt
+    spec = synth.small_spec(**SMALL["qwen3-q8"])
+    img = synth.build(spec, seed=47)
+    first = [int(t) for t in synth.prompt_tokens(12, 20, spec.vocab)]
+    s = hip.Session(hip_ctx, img, context=spec.context)
+    reused, nxt = s.prefill_cached(first)
+    assert reused == 0 and s.position == 20
+    gen, _ = s.generate(np.array([nxt], np.uint32), 6)  # rows: first, nxt, the 6 generated
+    held = first + [nxt] + [int(t) for t in gen]
+    assert s.position == len(held)
+
+    def fresh(prompt):
+        f = hip.Session(hip_ctx, img, context=spec.context)
+        _, st = f.generate(np.array(prompt, np.uint32), 0)
+        out, _ = f.generate(np.array([st.next_token], np.uint32), 8)
+        f.close()
+        return st.next_token, [int(t) for t in out]
+
+    cases = [
+        held + [7, 8, 9],            # extends every cached row (the reference's reuse case)
+        first[:11] + [3, 4, 5, 6],   # diverges inside the cache: rows up to 11 kept
+        held,                        # the cached rows themselves: the last token fed again
+        [5, 6] + first,              # nothing in common
+    ]
+    for prompt in cases:
+        common = 0
+        while common < min(len(held), len(prompt)) and held[common] == prompt[common]:
+            common += 1
+        reused, nxt = s.prefill_cached(prompt)
+        assert reused == min(common, len(prompt) - 1)
+        want_next, want_stream = fresh(prompt)
+        assert nxt == want_next
+        out, _ = s.generate(np.array([nxt], np.uint32), 8)
+        assert [int(t) for t in out] == want_stream
+        held = list(prompt) + [nxt] + [int(t) for t in out]
+    s.close()

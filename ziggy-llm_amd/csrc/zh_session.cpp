@@ -70,6 +70,11 @@ struct ZiggyHipSession {
     float *b_part_o = nullptr, *b_part_ml = nullptr;
     unsigned *b_counters = nullptr;
     uint32_t position = 0;
+    // the token whose K/V rows sit at each position below `position`, while
+    // every row came from a token step (prefix reuse); block-level calls,
+    // which write rows from hidden states, clear fed_ok
+    std::vector<uint32_t> fed;
+    bool fed_ok = true;
     bool logits_valid = false;
     std::vector<void *> allocs;
 };
@@ -431,6 +436,8 @@ int ziggy_hip_session_reset(ZiggyHipSession *s, char *err, size_t err_len) {
     ZH_TRY(hipMemsetAsync(s->vc, 0, cache_bytes, s->ctx->stream), "reset");
     ZH_TRY(hipStreamSynchronize(s->ctx->stream), "reset");
     s->position = 0;
+    s->fed.clear();
+    s->fed_ok = true;
     s->logits_valid = false;
     return ZIGGY_HIP_OK;
 }
@@ -444,6 +451,7 @@ int ziggy_hip_session_rewind(ZiggyHipSession *s, uint32_t position, char *err, s
         return ZIGGY_HIP_INVALID_ARGUMENT;
     }
     s->position = position;
+    if (s->fed.size() > position) s->fed.resize(position);
     s->logits_valid = false;
     return ZIGGY_HIP_OK;
 }
@@ -463,6 +471,7 @@ int ziggy_hip_session_run_attention_block(ZiggyHipSession *s, uint32_t layer, ui
                                           size_t err_len) {
     if (!s || layer >= s->md.block_count) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "bad layer");
     if (position >= s->md.context_length) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "context overflow");
+    s->fed_ok = false;  // a K/V row from a hidden state, not from a token step
     ZH_TRY(enqueue_attention_block(s, (int)layer, nullptr, (int)position, s->ctx->stream), "attention block");
     return finish_op(s->ctx, "attention block", err, err_len);
 }
@@ -551,6 +560,8 @@ static int host_step(ZiggyHipSession *s, uint32_t token, bool output, uint32_t *
     ZH_TRY(launch_step(s, st), "step graph");
     if (output) ZH_TRY(hipMemcpyAsync(h, s->st, sizeof(StepState), hipMemcpyDeviceToHost, st), "step readback");
     ZH_TRY(hipStreamSynchronize(st), "step");
+    s->fed.resize(s->position);
+    s->fed.push_back(token);
     s->position++;
     if (output) {
         s->logits_valid = true;
@@ -567,6 +578,28 @@ int ziggy_hip_session_step_greedy(ZiggyHipSession *s, uint32_t token, uint32_t *
 int ziggy_hip_session_step_no_output(ZiggyHipSession *s, uint32_t token, char *err, size_t err_len) {
     if (!s) return ZIGGY_HIP_INVALID_ARGUMENT;
     return host_step(s, token, false, nullptr, err, err_len);
+}
+
+int ziggy_hip_session_prefill_cached(ZiggyHipSession *s, const uint32_t *prompt, uint32_t prompt_len,
+                                     uint32_t *out_reused, uint32_t *out_next, char *err, size_t err_len) {
+    if (!s || !prompt || prompt_len == 0 || !out_reused || !out_next)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "invalid prefill_cached arguments");
+    if (prompt_len > s->md.context_length) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "context overflow");
+    // commonPrefixLen of the cached tokens and the prompt (model/loader.zig:2310-2313); the
+    // last prompt token is always fed again, for its logits
+    uint32_t common = 0;
+    if (s->fed_ok && s->fed.size() == s->position)
+        while (common < s->position && common < prompt_len && s->fed[common] == prompt[common]) common++;
+    if (common >= prompt_len) common = prompt_len - 1;
+    s->position = common;
+    s->fed.resize(common);
+    if (common == 0) s->fed_ok = true;  // every row from here on comes from token steps
+    ZiggyHipGenerateStats st{};
+    const int r = ziggy_hip_session_generate(s, prompt + common, prompt_len - common, 0, nullptr, &st, err, err_len);
+    if (r != ZIGGY_HIP_OK) return r;
+    *out_reused = common;
+    *out_next = st.next_token;
+    return ZIGGY_HIP_OK;
 }
 
 int ziggy_hip_session_step_shortlist(ZiggyHipSession *s, uint32_t token, uint32_t count,
@@ -650,6 +683,10 @@ int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint3
     if (steps) ZH_TRY(hipMemcpy(out_tokens, s->history, (size_t)steps * 4, hipMemcpyDeviceToHost), "history");
     ZH_TRY(hipMemcpy(h, s->st, sizeof(StepState), hipMemcpyDeviceToHost), "state readback");
     if (h->error) return fail(err, err_len, ZIGGY_HIP_EXECUTION_FAILED, "a generated token was out of range");
+    // rows of the prompt, then of each generated token but the last (still pending)
+    s->fed.resize(s->position);
+    s->fed.insert(s->fed.end(), prompt, prompt + prompt_len);
+    s->fed.insert(s->fed.end(), out_tokens, out_tokens + steps);
     s->position += (uint32_t)total;
     s->logits_valid = true;
     if (stats) {
@@ -879,6 +916,8 @@ int ziggy_hip_session_verify(ZiggyHipSession *s, uint32_t current_token, const u
         if (i < draft_count && out_predicted[i] != drafts[i]) break;
     }
     *out_count = n;
+    s->fed.resize(s->position);
+    s->fed.insert(s->fed.end(), toks, toks + n);  // the current token and the accepted drafts
     s->position += n;
     s->logits_valid = false;
     return ZIGGY_HIP_OK;

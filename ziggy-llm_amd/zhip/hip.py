@@ -159,6 +159,7 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_session_read_logits": [vp, vp] + E,
         "ziggy_hip_session_verify": [vp, u32, vp, u32, vp, ctypes.POINTER(u32)] + E,
         "ziggy_hip_session_step_shortlist": [vp, u32, u32, vp] + E,
+        "ziggy_hip_session_prefill_cached": [vp, vp, u32, ctypes.POINTER(u32), ctypes.POINTER(u32)] + E,
         "ziggy_hip_shortlist_len": [ctypes.POINTER(SamplingOptions), u32],
         "ziggy_hip_sample_shortlist": [vp, u32, vp, u32, ctypes.POINTER(SamplingOptions), ctypes.c_double,
                                        ctypes.POINTER(u32)],
@@ -434,6 +435,14 @@ class Session:
         _call("ziggy_hip_session_generate", self.h, prompt.ctypes.data, prompt.size, steps, out.ctypes.data,
               ctypes.byref(st))
         return out[:steps].copy(), st
+
+    def prefill_cached(self, prompt):
+        """Feeds `prompt` reusing the cached common prefix; returns (tokens reused, greedy next token)."""
+        p = np.ascontiguousarray(prompt, np.uint32)
+        reused, nxt = ctypes.c_uint32(), ctypes.c_uint32()
+        _call("ziggy_hip_session_prefill_cached", self.h, p.ctypes.data, p.size, ctypes.byref(reused),
+              ctypes.byref(nxt))
+        return int(reused.value), int(nxt.value)
 
     def step_shortlist(self, token: int, count: int):
         """One decode step of `token`; the top-`count` logits as (token ids, logits), highest first."""
