@@ -149,14 +149,17 @@ __device__ __forceinline__ float half_sum32(float v) {
 
 // Arrival of a split and, in the last workgroup of a kv head (partials slot)
 // to arrive, the merge of every split (partials stored with agent-scope
-// write-through); out_of(g) is head g's output row.
-template <int HD, int KG, class OutOf>
+// write-through); out_of(g) is head g's output row.  A partials slot holds VS
+// heads per split; the merge folds MS splits per round of loads (VS x MS =
+// 256: one thread per (head, split) pair).
+template <int HD, int KG, class OutOf, int VS = kMaxGroup, int MS = kMergeSplits>
 __device__ __forceinline__ void split_merge(const AttnParams &p, int kvh, int G, int nsplit, int *last_ptr,
                                             OutOf out_of) {
+    static_assert(VS * MS == 256, "one thread per (head, split) pair");
     const int tid = threadIdx.x;
     int &last_s = *last_ptr;
     constexpr int IPTM = (KG * HD / 2 + 255) / 256;
-    __shared__ float fm_merge[kMaxGroup], fl_merge[kMaxGroup], fa_merge[kMaxGroup];
+    __shared__ float fm_merge[VS], fl_merge[VS], fa_merge[VS];
     float acc_merge[IPTM][2];
     // Every thread's partial stores (agent scope, write-through)
     // complete before the workgroup barrier; thread 0 then releases and
@@ -177,46 +180,46 @@ __device__ __forceinline__ void split_merge(const AttnParams &p, int kvh, int G,
     // thread) and, for each item (pair of dims of one head), every split's
     // partial, all in flight together; the weights exp2(m_s - M) / L go
     // through LDS.
-    __shared__ float wt_s[kMaxGroup][kMergeSplits];
+    __shared__ float wt_s[VS][MS];
     const unsigned long long *ml = reinterpret_cast<const unsigned long long *>(p.part_ml) +
-                                   (size_t)kvh * p.max_splits * kMaxGroup;
+                                   (size_t)kvh * p.max_splits * VS;
     const unsigned long long *po = reinterpret_cast<const unsigned long long *>(p.part_o) +
-                                   (size_t)kvh * p.max_splits * kMaxGroup * (HD / 2);
+                                   (size_t)kvh * p.max_splits * VS * (HD / 2);
     constexpr int IPT = IPTM;  // items per thread at most
-    for (int s0 = 0; s0 < nsplit; s0 += kMergeSplits) {
-        const int ns = min(kMergeSplits, nsplit - s0);
-        unsigned long long ov[IPT][kMergeSplits];
+    for (int s0 = 0; s0 < nsplit; s0 += MS) {
+        const int ns = min(MS, nsplit - s0);
+        unsigned long long ov[IPT][MS];
 #pragma unroll
         for (int k = 0; k < IPT; k++) {
             const int it = min(tid + 256 * k, G * HD / 2 - 1);
             const int g = it / (HD / 2), d2 = it % (HD / 2);
 #pragma unroll
-            for (int u = 0; u < kMergeSplits; u++) {
-                const size_t e = (size_t)(s0 + min(u, ns - 1)) * kMaxGroup + g;
+            for (int u = 0; u < MS; u++) {
+                const size_t e = (size_t)(s0 + min(u, ns - 1)) * VS + g;
                 ov[k][u] = __hip_atomic_load(po + e * (HD / 2) + d2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         {
-            // thread (g, u) = (tid / kMergeSplits, tid % kMergeSplits)
-            const int g = tid / kMergeSplits, u = tid % kMergeSplits;
+            // thread (g, u) = (tid / MS, tid % MS)
+            const int g = tid / MS, u = tid % MS;
             float ms = -INFINITY, ls = 0.f;
             if (g < G && u < ns) {
-                const unsigned long long v = __hip_atomic_load(ml + (size_t)(s0 + u) * kMaxGroup + g, __ATOMIC_RELAXED,
+                const unsigned long long v = __hip_atomic_load(ml + (size_t)(s0 + u) * VS + g, __ATOMIC_RELAXED,
                                                                __HIP_MEMORY_SCOPE_AGENT);
                 ms = __uint_as_float((uint32_t)v);
                 ls = __uint_as_float((uint32_t)(v >> 32));
             }
-            // max and weighted sum over the kMergeSplits lanes of head g (a wavefront holds 64 / kMergeSplits heads)
+            // max and weighted sum over the MS lanes of head g (a wavefront holds 64 / MS heads)
             float mx = ms;
 #pragma unroll
-            for (int o = kMergeSplits / 2; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            for (int o = MS / 2; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
             // fold into the running (M, L) of earlier rounds
-            const float Mp = s0 == 0 ? -INFINITY : fm_merge[g < kMaxGroup ? g : 0];
+            const float Mp = s0 == 0 ? -INFINITY : fm_merge[g < VS ? g : 0];
             const float M = fmaxf(mx, Mp);
             const float w = ms == -INFINITY ? 0.f : exp2f(ms - M);
             float lw = ls * w;
 #pragma unroll
-            for (int o = kMergeSplits / 2; o >= 1; o >>= 1) lw += __shfl_xor(lw, o, 64);
+            for (int o = MS / 2; o >= 1; o >>= 1) lw += __shfl_xor(lw, o, 64);
             __syncthreads();  // earlier round's weights read
             if (g < G) {
                 wt_s[g][u] = w;
@@ -236,7 +239,7 @@ __device__ __forceinline__ void split_merge(const AttnParams &p, int kvh, int G,
             const int g = it / (HD / 2);
             float O0 = 0.f, O1 = 0.f;
 #pragma unroll
-            for (int u = 0; u < kMergeSplits; u++) {
+            for (int u = 0; u < MS; u++) {
                 if (u < ns) {
                     const float w = wt_s[g][u];
                     O0 = fmaf(__uint_as_float((uint32_t)ov[k][u]), w, O0);
@@ -610,25 +613,32 @@ __device__ __forceinline__ h8v as_h8(uint4 v) {
 
 // MQ: several queries at consecutive positions (plain mode, q already
 // normed and rotated, their K/V rows already in the cache).  Workgroup z takes
-// queries qbase .. qbase + nqw - 1 (8 / Gq of them): query head g of query j
+// queries qbase .. qbase + nqw - 1 (16 / Gq of them): query head g of query j
 // becomes column pair ("virtual head") j Gq + g, whose causal range ends at
-// its own position; splits cover the range of the last query.
+// its own position; splits cover the range of the last query.  A wavefront
+// holds two 16-column query tiles (virtual heads 0-7 and 8-15) against the
+// same K/V registers, so the K/V range is read once per 16 virtual heads.
 template <int HD, int GG, bool MQ>
 __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     constexpr int KS = HD / 32;  // 32-dim steps of the scores, 32-dim chunks of the values
     constexpr int TP = 32;       // positions per wavefront tile
     constexpr int QS = HD + 8;   // padded row of the query pieces (binary16)
     constexpr int LPR = HD / 8;  // lanes per value row (8 dims each)
+    constexpr int NT = MQ ? 2 : 1;      // 16-column query tiles per wavefront
+    constexpr int VG = kMaxGroup * NT;  // (virtual) heads per workgroup at most
+    static_assert(!MQ || VG == kMultiHeads, "multi-query partials are sized by kMultiHeads");
     touch_params(p);
     const int split = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
     const int Gq = GG ? GG : p.head_count / p.head_count_kv;  // query heads per kv head
-    const int qpw = MQ ? kMaxGroup / Gq : 1, qbase = MQ ? blockIdx.z * qpw : 0;
+    const int qpw = MQ ? VG / Gq : 1, qbase = MQ ? blockIdx.z * qpw : 0;
     const int nqw = MQ ? min(qpw, p.n_query - qbase) : 1;
     const int slot = MQ ? kvh + p.head_count_kv * blockIdx.z : kvh;  // partials / arrival counter
     const int pos0 = p.position_dev ? *p.position_dev : p.position;
     const int pos = pos0 + qbase + nqw - 1;  // the last query's position
-    const int pos_col = MQ ? pos0 + qbase + (li >> 1) / Gq : pos;  // causal end of column li
+    int pos_col[NT];                         // causal end of column li of tile nt
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) pos_col[nt] = MQ ? pos0 + qbase + ((li >> 1) + 8 * nt) / Gq : pos;
     const int n_total = pos + 1 - p.window_start;
     const int units = (n_total + TP - 1) / TP;
     const int per = (units + p.max_splits - 1) / p.max_splits;  // tiles per split
@@ -637,22 +647,23 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     const int u_begin = split * per, nu = min(per, units - u_begin);
     const int ntw = nu > wave ? (nu - wave + 3) / 4 : 0;  // this wavefront's tiles
     const int G = MQ ? nqw * Gq : Gq;                         // (virtual) heads of the workgroup
+    const bool two = NT > 1 && G > kMaxGroup;                 // the second query tile is in use
     const bool fused = !MQ && p.k_new != nullptr;
     const bool own_pos = fused && u_begin + nu == units;  // this split holds the current position
 
-    __shared__ float q_s[kMaxGroup][HD];
+    __shared__ float q_s[VG][HD];
     __shared__ float kn_s[HD];
     __shared__ __align__(16) unsigned short kn_h[HD], vn_h[HD];
     __shared__ float red16[4 * QV_MAX];
     __shared__ float cs_s[HD / 2], sn_s[HD / 2];
-    __shared__ __align__(16) unsigned short qp_s[16][QS];
-    __shared__ float mlw_s[4][16][2];
-    __shared__ __align__(16) float o_s[4][kMaxGroup][HD];
-    __shared__ float fm_s[kMaxGroup], fl_s[kMaxGroup];
+    __shared__ __align__(16) unsigned short qp_s[16 * NT][QS];
+    __shared__ float mlw_s[4][16 * NT][2];
+    __shared__ __align__(16) float o_s[4][VG][HD];
+    __shared__ float fm_s[VG], fl_s[VG];
     __shared__ int last_s;
 
     const size_t kv_off = (size_t)kvh * HD;
-    constexpr int QV = kMaxGroup * HD / 256;
+    constexpr int QV = VG * HD / 256;
     const int nq = G * HD;
     float qv[QV], kx[1] = {0.f}, vx = 0.f, qnw[QV], knw[1];
     {
@@ -749,7 +760,7 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     __syncthreads();
     // query pieces, scaled to base-2 scores
     const float sl2 = p.scale * 1.44269504088896340736f;
-    for (int it = tid; it < 16 * HD; it += 256) {
+    for (int it = tid; it < 16 * NT * HD; it += 256) {
         const int col = it / HD, d = it % HD, g = col >> 1;
         unsigned short h = 0;
         if (g < G) {
@@ -762,18 +773,24 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     __syncthreads();
     load_v(0, vr[0]);
     load_v(1, vr[1]);
-    h8v qf[KS];
+    h8v qf[NT][KS];
+    bool col_ok[NT];
+    float m[NT], lsum[NT];  // for column li of tile nt
+    f4v o[NT][8];           // [nt][q]: rows 4 lg + r, dims 8 li + q
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++) qf[ks] = as_h8(*reinterpret_cast<const uint4 *>(&qp_s[li][32 * ks + 8 * lg]));
-
-    const bool col_ok = li < 2 * G;
-    float m = -INFINITY, lsum = 0.f;  // for column li
-    f4v o[8];                         // [q]: rows 4 lg + r, dims 8 li + q
+    for (int nt = 0; nt < NT; nt++) {
 #pragma unroll
-    for (int q = 0; q < 8; q++) o[q] = f4v{0.f, 0.f, 0.f, 0.f};
+        for (int ks = 0; ks < KS; ks++)
+            qf[nt][ks] = as_h8(*reinterpret_cast<const uint4 *>(&qp_s[16 * nt + li][32 * ks + 8 * lg]));
+        col_ok[nt] = 16 * nt + li < 2 * G;
+        m[nt] = -INFINITY;
+        lsum[nt] = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) o[nt][q] = f4v{0.f, 0.f, 0.f, 0.f};
+    }
 
     for (int t0 = 0; t0 < ntw; t0 += 2) {
-        float sc[2][2][4];
+        float sc[NT][2][2][4];
 #pragma unroll
         for (int tt = 0; tt < 2; tt++) {
             const bool have = t0 + tt < ntw;
@@ -794,59 +811,65 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
                 for (int e = 0; e < 8; e++) pick4(b + vrow(e) == pos, vn, vr[tt][e]);
             }
 #pragma unroll
-            for (int rt = 0; rt < 2; rt++) {
-                f4v acc = {0.f, 0.f, 0.f, 0.f};
-                if (have) {
+            for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-                    for (int ks = 0; ks < KS; ks++)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kr[tt][rt][ks]), qf[ks], acc, 0, 0, 0);
-                }
+                for (int nt = 0; nt < NT; nt++) {
+                    f4v acc = {0.f, 0.f, 0.f, 0.f};
+                    if (have && (nt == 0 || two)) {
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    // rows 4 lg + r of the tile; the two pieces of a head sit in lanes 2g, 2g + 1
-                    float v = acc[r];
-                    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
-                    const bool valid = have && col_ok && b + 16 * rt + 4 * lg + r <= pos_col;
-                    sc[tt][rt][r] = valid ? v : -INFINITY;
+                        for (int ks = 0; ks < KS; ks++)
+                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kr[tt][rt][ks]), qf[nt][ks], acc, 0, 0,
+                                                                         0);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        // rows 4 lg + r of the tile; the two pieces of a head sit in lanes 2g, 2g + 1
+                        float v = acc[r];
+                        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+                        const bool valid = have && col_ok[nt] && b + 16 * rt + 4 * lg + r <= pos_col[nt];
+                        sc[nt][tt][rt][r] = valid ? v : -INFINITY;
+                    }
                 }
-            }
         }
         if (t0 + 2 < ntw) {  // the next two tiles into the K slots just consumed
             load_k(t0 + 2, kr[0]);
             load_k(t0 + 3, kr[1]);
         }
-        float mt = -INFINITY;
+        h8v pf[NT][2];
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++)
+        for (int nt = 0; nt < NT; nt++) {
+            float mt = -INFINITY;
 #pragma unroll
-            for (int rt = 0; rt < 2; rt++)
+            for (int tt = 0; tt < 2; tt++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) mt = fmaxf(mt, sc[tt][rt][r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        const float mn = fmaxf(m, mt);
-        const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
-        m = mn;
-        float ps = 0.f;
-        h8v pf[2];
+                for (int rt = 0; rt < 2; rt++)
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++)
+                    for (int r = 0; r < 4; r++) mt = fmaxf(mt, sc[nt][tt][rt][r]);
+            mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+            const float mn = fmaxf(m[nt], mt);
+            const float alpha = m[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[nt] - mn);
+            m[nt] = mn;
+            float ps = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float s = sc[tt][e >> 2][e & 3];
-                const float pv = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - mn);
-                ps += pv;
-                const _Float16 hi = (_Float16)pv;
-                pf[tt][e] = (li & 1) ? (_Float16)(pv - (float)hi) : hi;
-            }
-        lsum = lsum * alpha + ps;
-        if (t0 > 0) {
-            // rows 4 lg + r of O are columns 4 lg + r of P: their alpha
+            for (int tt = 0; tt < 2; tt++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float a = __shfl(alpha, 4 * lg + r, 64);
+                for (int e = 0; e < 8; e++) {
+                    const float s = sc[nt][tt][e >> 2][e & 3];
+                    const float pv = s == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - mn);
+                    ps += pv;
+                    const _Float16 hi = (_Float16)pv;
+                    pf[nt][tt][e] = (li & 1) ? (_Float16)(pv - (float)hi) : hi;
+                }
+            lsum[nt] = lsum[nt] * alpha + ps;
+            if (t0 > 0) {
+                // rows 4 lg + r of O are columns 4 lg + r of P: their alpha
 #pragma unroll
-                for (int q = 0; q < 8; q++) o[q][r] *= a;
+                for (int r = 0; r < 4; r++) {
+                    const float a = __shfl(alpha, 4 * lg + r, 64);
+#pragma unroll
+                    for (int q = 0; q < 8; q++) o[nt][q][r] *= a;
+                }
             }
         }
 #pragma unroll
@@ -867,7 +890,10 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
                 bv.y = __builtin_amdgcn_perm(w[3], w[2], sel);
                 bv.z = __builtin_amdgcn_perm(w[5], w[4], sel);
                 bv.w = __builtin_amdgcn_perm(w[7], w[6], sel);
-                o[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[tt], as_h8(bv), o[q], 0, 0, 0);
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    if (nt == 0 || two)
+                        o[nt][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pf[nt][tt], as_h8(bv), o[nt][q], 0, 0, 0);
             }
         }
         if (t0 + 2 < ntw) {
@@ -877,37 +903,45 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     }
 
     // ---- merge the four wavefronts ----
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
-    if (lg == 0) {
-        mlw_s[wave][li][0] = m;
-        mlw_s[wave][li][1] = lsum;
-    }
-    __syncthreads();
-    // rows 4 lg + 2 hh + {0, 1} are the two pieces of head 2 lg + hh (same
-    // max): summed here, scaled to the workgroup max, one row per head
 #pragma unroll
-    for (int hh = 0; hh < 2; hh++) {
-        const int head = 2 * lg + hh, row = 2 * head;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < 4; w++) M = fmaxf(M, mlw_s[w][row][0]);
-        const float mw = mlw_s[wave][row][0];
-        const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
-        if (head < G && li < LPR) {
-            float4 a, b;
-            a.x = (o[0][2 * hh] + o[0][2 * hh + 1]) * f;
-            a.y = (o[1][2 * hh] + o[1][2 * hh + 1]) * f;
-            a.z = (o[2][2 * hh] + o[2][2 * hh + 1]) * f;
-            a.w = (o[3][2 * hh] + o[3][2 * hh + 1]) * f;
-            b.x = (o[4][2 * hh] + o[4][2 * hh + 1]) * f;
-            b.y = (o[5][2 * hh] + o[5][2 * hh + 1]) * f;
-            b.z = (o[6][2 * hh] + o[6][2 * hh + 1]) * f;
-            b.w = (o[7][2 * hh] + o[7][2 * hh + 1]) * f;
-            *reinterpret_cast<float4 *>(&o_s[wave][head][8 * li]) = a;
-            *reinterpret_cast<float4 *>(&o_s[wave][head][8 * li + 4]) = b;
+    for (int nt = 0; nt < NT; nt++) {
+        float l = lsum[nt];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        if (lg == 0) {
+            mlw_s[wave][16 * nt + li][0] = m[nt];
+            mlw_s[wave][16 * nt + li][1] = l;
         }
     }
+    __syncthreads();
+    // rows 4 lg + 2 hh + {0, 1} of tile nt are the two pieces of head
+    // 8 nt + 2 lg + hh (same max): summed here, scaled to the workgroup max,
+    // one row per head
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int head = 8 * nt + 2 * lg + hh, row = 2 * head;
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < 4; w++) M = fmaxf(M, mlw_s[w][row][0]);
+            const float mw = mlw_s[wave][row][0];
+            const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
+            if (head < G && li < LPR) {
+                const f4v *on = o[nt];
+                float4 a, b;
+                a.x = (on[0][2 * hh] + on[0][2 * hh + 1]) * f;
+                a.y = (on[1][2 * hh] + on[1][2 * hh + 1]) * f;
+                a.z = (on[2][2 * hh] + on[2][2 * hh + 1]) * f;
+                a.w = (on[3][2 * hh] + on[3][2 * hh + 1]) * f;
+                b.x = (on[4][2 * hh] + on[4][2 * hh + 1]) * f;
+                b.y = (on[5][2 * hh] + on[5][2 * hh + 1]) * f;
+                b.z = (on[6][2 * hh] + on[6][2 * hh + 1]) * f;
+                b.w = (on[7][2 * hh] + on[7][2 * hh + 1]) * f;
+                *reinterpret_cast<float4 *>(&o_s[wave][head][8 * li]) = a;
+                *reinterpret_cast<float4 *>(&o_s[wave][head][8 * li + 4]) = b;
+            }
+        }
     if (tid < G) {
         const int row = 2 * tid;
         float M = -INFINITY, L = 0.f;
@@ -942,7 +976,7 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
             dst[0] = x0 / fl_s[g];
             dst[1] = x1 / fl_s[g];
         } else {
-            const size_t e = (((size_t)slot * p.max_splits + split) * kMaxGroup + g) * HD + d;
+            const size_t e = (((size_t)slot * p.max_splits + split) * VG + g) * HD + d;
             const unsigned long long v = (unsigned long long)__float_as_uint(x0) |
                                          ((unsigned long long)__float_as_uint(x1) << 32);
             __hip_atomic_store(reinterpret_cast<unsigned long long *>(p.part_o + e), v, __ATOMIC_RELAXED,
@@ -951,13 +985,14 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     }
     if (nsplit == 1) return;
     if (tid < G) {
-        const size_t e = ((size_t)slot * p.max_splits + split) * kMaxGroup + tid;
+        const size_t e = ((size_t)slot * p.max_splits + split) * VG + tid;
         const unsigned long long v = (unsigned long long)__float_as_uint(fm_s[tid]) |
                                      ((unsigned long long)__float_as_uint(fl_s[tid]) << 32);
         __hip_atomic_store(reinterpret_cast<unsigned long long *>(p.part_ml) + e, v, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
-    split_merge<HD, (GG && !MQ) ? GG : kMaxGroup>(p, slot, G, nsplit, &last_s, out_of);  // MQ: up to 8 virtual heads
+    // MQ: up to 16 virtual heads, 16 splits per round of the merge
+    split_merge<HD, (GG && !MQ) ? GG : VG, decltype(out_of), VG, 256 / VG>(p, slot, G, nsplit, &last_s, out_of);
 }
 
 size_t attention_scratch_floats(int head_count, int head_dim, int max_splits) {
@@ -1058,7 +1093,8 @@ hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t 
 bool attention_multi_supported(int head_dim) { return (head_dim == 64 || head_dim == 128) && !attention_valu(); }
 
 int attention_query_groups(int head_count, int head_count_kv, int n_query) {
-    const int G = head_count_kv > 0 ? head_count / head_count_kv : 1, qpw = G > 0 && G <= kMaxGroup ? kMaxGroup / G : 1;
+    const int G = head_count_kv > 0 ? head_count / head_count_kv : 1;
+    const int qpw = G > 0 && G <= kMaxGroup ? kMultiHeads / G : 1;
     return (n_query + qpw - 1) / qpw;
 }
 

@@ -230,8 +230,9 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t s);
 hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t s);
 bool attention_multi_supported(int head_dim);
 // workgroups along the query axis of a multi-query launch (its partials and
-// arrival counters: head_count_kv * groups slots)
+// arrival counters: head_count_kv * groups slots of kMultiHeads heads each)
 int attention_query_groups(int head_count, int head_count_kv, int n_query);
+constexpr int kMultiHeads = 16;  // (query, head) pairs per multi-query workgroup
 // Splits of the attention grid for kv_heads heads and up to max_positions keys.
 int attention_splits(int kv_heads, int max_positions);
 size_t attention_scratch_floats(int head_count, int head_dim, int max_splits);

@@ -723,7 +723,8 @@ static hipError_t verify_alloc(ZiggyHipSession *s) {
     if (attention_multi_supported((int)s->md.head_dim)) {
         const size_t slots = (size_t)s->md.head_count_kv *
                              attention_query_groups((int)s->md.head_count, (int)s->md.head_count_kv, (int)M);
-        const size_t po = slots * s->max_splits * 8 * s->md.head_dim, pml = slots * s->max_splits * 8 * 2;
+        const size_t po = slots * s->max_splits * kMultiHeads * s->md.head_dim,
+                     pml = slots * s->max_splits * kMultiHeads * 2;
         hipError_t e = hipMalloc((void **)&s->b_part_o, (po + pml) * 4);
         if (e != hipSuccess) return e;
         s->allocs.push_back(s->b_part_o);
