@@ -84,6 +84,30 @@ def test_verify_over_a_long_context(hip_ctx, name):
     s.close()
 
 
+MANY_SPLITS = {
+    # 1500 positions, up to 32 splits per query group: more splits than one
+    # round of the multi-query merge folds (16), so it folds in two rounds
+    "g1-hd64": dict(arch="llama", n_head=4, n_kv=4, context=2048),
+    "g8-hd64": dict(arch="llama", hidden=512, n_head=8, n_kv=1, context=2048),
+}
+
+
+@pytest.mark.parametrize("name", list(MANY_SPLITS))
+def test_verify_merges_more_splits_than_one_round(hip_ctx, name):
+    say(f"verify many splits {name}")
+    spec = synth.small_spec(**MANY_SPLITS[name])
+    img = synth.build(spec, seed=41)
+    prompt = synth.prompt_tokens(11, 1500, spec.vocab)
+    want, _ = zo.Session(zo.Model(img.buf), context=spec.context, kv_f16=True).generate(prompt, 16)
+    want = [int(t) for t in want]
+    s = hip.Session(hip_ctx, img, context=spec.context)
+    _, st = s.generate(prompt, 0)
+    assert st.next_token == want[0]
+    pred, n = s.verify(want[0], want[1:12])
+    assert n == 12 and list(pred) == want[1:13]
+    s.close()
+
+
 def test_verify_rejects_at_the_first_wrong_draft(hip_ctx):
     spec = synth.small_spec(**SMALL["llama-q4km"])
     img = synth.build(spec, seed=29)
