@@ -137,14 +137,14 @@ __device__ __forceinline__ float half_max32(float v) {
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
-    return fmaxf(v, __shfl_xor(v, 16, 64));
+    return xmax<16>(v);
 }
 __device__ __forceinline__ float half_sum32(float v) {
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
-    return v + __shfl_xor(v, 16, 64);
+    return xsum<16>(v);
 }
 
 // Arrival of a split and, in the last workgroup of a kv head (partials slot)
@@ -845,8 +845,7 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
                 for (int rt = 0; rt < 2; rt++)
 #pragma unroll
                     for (int r = 0; r < 4; r++) mt = fmaxf(mt, sc[nt][tt][rt][r]);
-            mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+            mt = xmax<32>(xmax<16>(mt));
             const float mn = fmaxf(m[nt], mt);
             const float alpha = m[nt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[nt] - mn);
             m[nt] = mn;
@@ -906,8 +905,7 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         float l = lsum[nt];
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
+        l = xsum<32>(xsum<16>(l));
         if (lg == 0) {
             mlw_s[wave][16 * nt + li][0] = m[nt];
             mlw_s[wave][16 * nt + li][1] = l;

@@ -10,6 +10,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "ziggy_hip.h"
 
 struct ZiggyHipContext {
@@ -84,6 +86,71 @@ template <class P> __device__ __forceinline__ void touch_params(const P &p) {
     auto at = [&](int line) { return w[16 * (line < L ? line : L)]; };
     __asm__ volatile("" ::"s"(at(0)), "s"(at(1)), "s"(at(2)), "s"(at(3)), "s"(at(4)), "s"(at(5)), "s"(at(6)),
                      "s"(at(7)), "s"(at(8)), "s"(at(9)), "s"(at(10)), "s"(at(11)));
+}
+
+// Exchanges with the lane 16 or 32 apart on the vector ALU
+// (v_permlane16_swap / v_permlane32_swap of gfx950) instead of an LDS-path
+// bpermute.  Called with one value in both operands, the swap returns this
+// lane's value and its partner's (in an order that depends on the lane), so
+// a commutative op of the two is op(own, partner) in every lane: the same
+// bits as `op(v, __shfl_xor(v, 16 or 32))`.
+template <int D> __device__ __forceinline__ void lane_pair(uint32_t v, uint32_t &a, uint32_t &b) {
+    static_assert(D == 16 || D == 32, "lane distance 16 or 32");
+    if constexpr (D == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        a = r[0];
+        b = r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        a = r[0];
+        b = r[1];
+    }
+}
+template <int D> __device__ __forceinline__ float xsum(float v) {
+    uint32_t a, b;
+    lane_pair<D>(__float_as_uint(v), a, b);
+    return __uint_as_float(a) + __uint_as_float(b);
+}
+template <int D> __device__ __forceinline__ float xmax(float v) {
+    uint32_t a, b;
+    lane_pair<D>(__float_as_uint(v), a, b);
+    return fmaxf(__uint_as_float(a), __uint_as_float(b));
+}
+template <int D> __device__ __forceinline__ unsigned long long xmax_u64(unsigned long long v) {
+    uint32_t a0, b0, a1, b1;
+    lane_pair<D>((uint32_t)v, a0, b0);
+    lane_pair<D>((uint32_t)(v >> 32), a1, b1);
+    const unsigned long long a = ((unsigned long long)a1 << 32) | a0, b = ((unsigned long long)b1 << 32) | b0;
+    return a > b ? a : b;
+}
+template <int CTRL> __device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+    return ((unsigned long long)hi << 32) | lo;
+}
+// Wavefront maximum of a 64-bit key, valid in every lane: DPP within each
+// 16-lane row (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror),
+// then the two lane swaps across rows.  Every lane must be active.
+__device__ __forceinline__ unsigned long long wave_max_key(unsigned long long v) {
+    auto mx = [](unsigned long long a, unsigned long long b) { return a > b ? a : b; };
+    v = mx(v, dpp_u64<0xB1>(v));
+    v = mx(v, dpp_u64<0x4E>(v));
+    v = mx(v, dpp_u64<0x141>(v));
+    v = mx(v, dpp_u64<0x140>(v));
+    v = xmax_u64<16>(v);
+    return xmax_u64<32>(v);
+}
+// The same for a float (max is exact in any order).
+__device__ __forceinline__ float wave_max_f32(float v) {
+    auto mov = [](float x, auto ctrl) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xF, 0xF, false));
+    };
+    v = fmaxf(v, mov(v, std::integral_constant<int, 0xB1>{}));
+    v = fmaxf(v, mov(v, std::integral_constant<int, 0x4E>{}));
+    v = fmaxf(v, mov(v, std::integral_constant<int, 0x141>{}));
+    v = fmaxf(v, mov(v, std::integral_constant<int, 0x140>{}));
+    v = xmax<16>(v);
+    return xmax<32>(v);
 }
 
 struct MvSeg {

@@ -57,7 +57,7 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const float *__restrict_
         // softmaxInPlace (model/loader.zig:4160-4170): max, exp(v - max), / sum
         float m = -INFINITY;
         for (int i = t; i < E; i += 256) m = fmaxf(m, pr[i]);
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        m = wave_max_f32(m);
         if (lane == 0) red[wave] = m;
         __syncthreads();
         m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -84,10 +84,7 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const float *__restrict_
                 ((unsigned long long)ordered_bits_moe(pr[i]) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
             best = key > best ? key : best;
         }
-        for (int o = 32; o >= 1; o >>= 1) {
-            const unsigned long long v = __shfl_xor(best, o, 64);
-            best = v > best ? v : best;
-        }
+        best = wave_max_key(best);
         if (lane == 0) keys[wave] = best;
         __syncthreads();
         if (t == 0) {
@@ -148,7 +145,7 @@ __global__ void __launch_bounds__(64) moe_route_wave_kernel(const float *__restr
     if (gating == 1 || gating == 2) {
         // softmaxInPlace (model/loader.zig:4160-4170): max, exp(v - max), / sum
         float m = fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3]));
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        m = wave_max_f32(m);
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -173,10 +170,7 @@ __global__ void __launch_bounds__(64) moe_route_wave_kernel(const float *__restr
                 ((unsigned long long)ordered_bits_moe(pr[i]) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
             best = key > best ? key : best;
         }
-        for (int o = 32; o >= 1; o >>= 1) {
-            const unsigned long long v = __shfl_xor(best, o, 64);
-            best = v > best ? v : best;
-        }
+        best = wave_max_key(best);
         const uint32_t idx = 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull);
         sel[r] = idx;
         if ((int)(idx & 63) == l) taken |= 1u << (idx >> 6);

@@ -93,9 +93,8 @@ __device__ __forceinline__ float reduce4_wave(float v0, float v1, float v2, floa
     float c = (b1 ? b : a) + dpp_mov<0x4E>(b1 ? a : b);            // lane ^ 2
     c += dpp_mov<0x124>(c);                                       // row_ror:4
     c += dpp_mov<0x128>(c);                                       // row_ror:8
-    c += __shfl_xor(c, 16, 64);
-    c += __shfl_xor(c, 32, 64);
-    return c;
+    c = xsum<16>(c);
+    return xsum<32>(c);
 }
 
 __device__ __forceinline__ uint32_t ordered_bits(float v) {

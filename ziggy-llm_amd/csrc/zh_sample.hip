@@ -24,14 +24,6 @@ __device__ __forceinline__ unsigned long long short_key(float v, uint32_t id) {
     const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - id);
 }
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const unsigned long long w = __shfl_xor(v, o, 64);
-        v = w > v ? w : v;
-    }
-    return v;
-}
 
 // The top k of the N keys each lane holds (k rounds; a taken key becomes 0,
 // which no real key equals); round r's winner goes to out(r) from lane 0.
@@ -42,7 +34,7 @@ __device__ __forceinline__ void wave_topk(unsigned long long (&key)[N], int k, O
         unsigned long long best = 0ull;
 #pragma unroll
         for (int i = 0; i < N; i++) best = key[i] > best ? key[i] : best;
-        best = wave_max_u64(best);
+        best = wave_max_key(best);
 #pragma unroll
         for (int i = 0; i < N; i++)
             if (key[i] == best) key[i] = 0ull;
