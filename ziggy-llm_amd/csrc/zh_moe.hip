@@ -3,10 +3,13 @@
 // (model/loader.zig:1718-1749) as the reference's Metal session runs it
 // (runMoeFfnBlock, runtime/gpu/session.zig:515-613).
 //
-// One layer is five launches, captured once into a HIP graph for the stack:
+// One layer is four launches (five above 256 experts), captured once into a
+// HIP graph for the stack:
 //   router   fused RMSNorm (ffn_norm) + router matvec, and the shared
 //            expert's gate row when present, into logits[E (+1)]
-//   route    softmax over all experts (expert_gating_func 1, 2), top-k with
+//   route    (in the gate/up launch's prologue up to 256 experts, see
+//            zh_route.h; a launch of its own above that)
+//            softmax over all experts (expert_gating_func 1, 2), top-k with
 //            ties to the lower index (selectTopK, :3953-3975),
 //            normalizePositiveWeights (:3977-3990) when expert_weights_norm,
 //            x expert_weights_scale; sigmoid of the shared gate
@@ -24,6 +27,7 @@
 
 #include "zh_internal.h"
 #include "zh_quant.h"
+#include "zh_route.h"
 
 namespace zh {
 
@@ -138,80 +142,8 @@ __global__ void __launch_bounds__(64) moe_route_wave_kernel(const float *__restr
                                                            int logits_stride) {
     logits += (size_t)blockIdx.x * logits_stride;
     route += (size_t)blockIdx.x * (2 * k + 2);
-    const int l = threadIdx.x;
-    float pr[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) pr[i] = l + 64 * i < E ? logits[l + 64 * i] : -INFINITY;
-    if (gating == 1 || gating == 2) {
-        // softmaxInPlace (model/loader.zig:4160-4170): max, exp(v - max), / sum
-        float m = fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3]));
-        m = wave_max_f32(m);
-        float s = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            pr[i] = l + 64 * i < E ? expf(pr[i] - m) : 0.f;
-            s += pr[i];
-        }
-        for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
-#pragma unroll
-        for (int i = 0; i < 4; i++) pr[i] = l + 64 * i < E ? pr[i] / s : -INFINITY;
-    }
-    // k rounds of a wavefront argmax over the values not yet taken (the
-    // largest value first; equal values: the lower index first)
-    uint32_t sel[kMoeMaxK];
-    unsigned taken = 0;  // bit i: expert l + 64 i taken
-    for (int r = 0; r < k; r++) {
-        unsigned long long best = 0ull;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int idx = l + 64 * i;
-            if (idx >= E || (taken >> i & 1)) continue;
-            const unsigned long long key =
-                ((unsigned long long)ordered_bits_moe(pr[i]) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
-            best = key > best ? key : best;
-        }
-        best = wave_max_key(best);
-        const uint32_t idx = 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull);
-        sel[r] = idx;
-        if ((int)(idx & 63) == l) taken |= 1u << (idx >> 6);
-    }
-    // the selected probabilities: from the lane that holds each
-    float w[kMoeMaxK];
-    for (int r = 0; r < k; r++) {
-        const int src = sel[r] & 63, i = sel[r] >> 6;
-        const float mine = i == 0 ? pr[0] : i == 1 ? pr[1] : i == 2 ? pr[2] : pr[3];
-        w[r] = __shfl(mine, src, 64);
-    }
-    if (l == 0) {
-        if (weights_norm) {
-            float sum = 0.f;
-            for (int r = 0; r < k; r++)
-                if (isfinite(w[r]) && w[r] > 0.f) sum += w[r];
-            if (sum <= 0.f) {
-                for (int r = 0; r < k; r++) w[r] = 0.f;
-            } else {
-                const float inv = 1.0f / sum;
-                for (int r = 0; r < k; r++) w[r] = (isfinite(w[r]) && w[r] > 0.f) ? w[r] * inv : 0.f;
-            }
-        }
-        if (weights_scale != 1.0f)
-            for (int r = 0; r < k; r++) w[r] *= weights_scale;
-        for (int r = 0; r < k; r++) {
-            route[2 * r] = sel[r];
-            route[2 * r + 1] = __float_as_uint(w[r]);
-        }
-        float g = 1.0f;
-        if (has_shared_gate) {
-            const float v = logits[E];
-            if (v >= 0.f) {
-                g = 1.0f / (1.0f + expf(-v));
-            } else {
-                const float e = expf(v);
-                g = e / (1.0f + e);
-            }
-        }
-        route[2 * k] = __float_as_uint(g);
-    }
+    route_wave(logits, E, k, gating, weights_norm, weights_scale, has_shared_gate,
+               [&](int i, uint32_t v) { route[i] = v; });
 }
 
 __global__ void moe_combine_kernel(float *__restrict__ hidden, const float *__restrict__ tmp,

@@ -6,6 +6,7 @@
 
 #include "zh_arena.h"
 #include "zh_internal.h"
+#include "zh_route.h"
 
 using namespace zh;
 
@@ -87,9 +88,16 @@ hipError_t enqueue_layer(ZiggyHipMoeStack *s, int l, hipStream_t st) {
         hipError_t e = launch_matvec(p, IN_NORM, OUT_STORE, st);
         if (e != hipSuccess) return e;
     }
-    hipError_t e = launch_moe_route(s->logits, E, K, (int)d.gating_func, (int)d.weights_norm, d.weights_scale,
-                                    s->shared_gate ? 1 : 0, route, st);
-    if (e != hipSuccess) return e;
+    // up to 256 experts: the gate/up launch routes the token itself (each
+    // routed workgroup, one wavefront) and writes the route for the launches
+    // after it; more experts take the routing kernel
+    const bool route_in_gate_up = E <= kRouteWaveExperts && K <= kRouteMaxK && d.gating_func <= 15;
+    hipError_t e = hipSuccess;
+    if (!route_in_gate_up) {
+        e = launch_moe_route(s->logits, E, K, (int)d.gating_func, (int)d.weights_norm, d.weights_scale,
+                             s->shared_gate ? 1 : 0, route, st);
+        if (e != hipSuccess) return e;
+    }
     // routed experts' gate/up (+ shared), SiLU(gate) * up
     {
         MvParams p{};
@@ -109,9 +117,17 @@ hipError_t enqueue_layer(ZiggyHipMoeStack *s, int l, hipStream_t st) {
         p.x = s->hidden;
         p.norm_w = (const float *)L.norm.p;
         p.eps = d.rms_norm_eps;
-        p.expert = route;
         p.rows_per_expert = FF;
         p.expert_limit = E;
+        if (route_in_gate_up) {
+            p.route_logits = s->logits;
+            p.route_out = route;
+            p.route_cfg = (uint32_t)E | (uint32_t)K << 16 | d.gating_func << 20 | (d.weights_norm ? 1u : 0u) << 24 |
+                          (s->shared_gate ? 1u : 0u) << 25;
+            p.route_scale = d.weights_scale;
+        } else {
+            p.expert = route;
+        }
         e = launch_matvec(p, IN_NORM, OUT_SWIGLU, st);
         if (e != hipSuccess) return e;
     }

@@ -29,6 +29,7 @@
 
 #include "zh_internal.h"
 #include "zh_quant.h"
+#include "zh_route.h"
 
 namespace zh {
 
@@ -548,7 +549,29 @@ __global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
         if (i < p.nseg && wg >= p.seg[i].wg_begin) si = i;
     // a copy: every field of the segment is read in one batch of scalar
     // loads, not one dependent round trip per use
-    const MvSeg sg = p.seg[si];
+    MvSeg sg = p.seg[si];
+    if constexpr (OUT == OUT_SWIGLU) {
+        if (p.route_logits && (sg.expert_slot >= 0 || wg == 0)) {  // uniform over the workgroup
+            __shared__ uint32_t route_s[2 * kRouteMaxK + 2];
+            if (threadIdx.x < 64) {
+                const uint32_t c = p.route_cfg;
+                route_wave(p.route_logits, (int)(c & 0xFFFF), (int)(c >> 16 & 0xF), (int)(c >> 20 & 0xF),
+                           (int)(c >> 24 & 1), p.route_scale, (int)(c >> 25 & 1), [&](int i, uint32_t v) {
+                               route_s[i] = v;
+                               if (wg == 0) p.route_out[i] = v;
+                           });
+            }
+            __syncthreads();
+            if (sg.expert_slot >= 0) {
+                const uint32_t e = (uint32_t)__builtin_amdgcn_readfirstlane((int)route_s[2 * sg.expert_slot]);
+                if (e >= (uint32_t)p.expert_limit) return;  // uniform over the segment: no rows are read
+                const uint64_t off = (uint64_t)e * (uint64_t)p.rows_per_expert * sg.stride;
+                sg.w += off;
+                if (sg.w2) sg.w2 += off;
+                sg.expert_slot = -1;
+            }
+        }
+    }
     if (F1 == F2 || sg.fmt == F1)
         mv_dispatch<F1, IN, OUT, TT, NB>(p, sg, wg - sg.wg_begin, lds);
     else
