@@ -185,15 +185,22 @@ struct MvParams {
     int expert_limit;                 // expert ids >= this are ignored (no rows are read)
     float weight_scale;               // WADD: y += scale * dot (scale from entries if expert set)
     const int *gate_flag;             // optional device flag (argmax output only): kernel exits if *gate_flag == 0
-    // SWIGLU of an MoE layer: when set, each workgroup of a routed segment
-    // (and workgroup 0) routes the token itself from the router logits
-    // (route_wave, one wavefront) and offsets its segment by the id it finds;
-    // workgroup 0 writes the route to route_out for the down projection and
-    // the combine.  `expert` is then unused.
-    const float *route_logits;
-    uint32_t *route_out;
-    uint32_t route_cfg;  // E | k << 16 | gating << 20 | weights_norm << 24 | shared_gate << 25
-    float route_scale;
+    // Fused prologues of the MoE decode launches (pro_in null: none).
+    //   SWIGLU  the routing: each workgroup of a routed segment (and
+    //           workgroup 0) routes the token from the router logits pro_in
+    //           (route_wave, one wavefront) and offsets its segment by the id
+    //           it finds; workgroup 0 writes the route (uint32 entries) to
+    //           pro_out.  pro_cfg = E | k << 16 | gating << 20 |
+    //           weights_norm << 24 | shared_gate << 25, pro_scale = weights
+    //           scale; `expert` is unused.
+    //   NORM    (f32 router) the previous layer's combine: the input is
+    //           x + combine(pro_in rows, route at `expert`), computed per
+    //           workgroup into LDS (cols <= kCombineMaxCols); workgroup 0
+    //           writes it to pro_out (f32, not x).  pro_cfg = k | shared << 4.
+    const float *pro_in;
+    void *pro_out;
+    uint32_t pro_cfg;
+    float pro_scale;
 };
 
 // Builds the launch plan (team size, rows per team, workgroup ranges) and launches.

@@ -157,16 +157,7 @@ __global__ void moe_combine_kernel(float *__restrict__ hidden, const float *__re
     route += (size_t)t * (2 * k + 2);
     tmp += (size_t)t * k * H;
     const float *sh = sh_tmp ? sh_tmp + (size_t)t * H : tmp + (size_t)k * H;
-    float out = 0.f;
-    for (int s = 0; s < k; s++) {
-        const float w = __uint_as_float(route[2 * s + 1]), d = tmp[(size_t)s * H + r];
-        out = w == 1.0f ? out + d : fmaf(d, w, out);
-    }
-    if (has_shared) {
-        const float g = __uint_as_float(route[2 * k]), d = sh[r];
-        out = g == 1.0f ? out + d : fmaf(d, g, out);
-    }
-    hidden[r] = hidden[r] + out;
+    hidden[r] = combine_value(hidden, tmp, route, H, k, has_shared != 0, sh, r);
 }
 
 hipError_t launch_moe_route(const float *logits, int E, int k, int gating, int weights_norm, float weights_scale,

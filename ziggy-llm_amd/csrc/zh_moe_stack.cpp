@@ -24,6 +24,12 @@ struct ZiggyHipMoeStack {
     std::vector<MoeLayerW> layers;
     uint8_t *arena = nullptr;
     float *hidden = nullptr, *logits = nullptr, *act = nullptr, *tmp = nullptr;
+    // fuse_combine: layer l > 0's router launch runs layer l - 1's combine,
+    // from the hidden state of layer l - 1 into the other of two buffers
+    // (hidden, hidden2); the buffers alternate so that the last layer's is
+    // `hidden`, where its own combine kernel runs in place
+    float *hidden2 = nullptr;
+    bool fuse_combine = false;
     uint32_t *route = nullptr;  // [layers][2k + 2]
     int act_stride = 0, route_stride = 0;
     bool shared = false, shared_gate = false;
@@ -66,13 +72,21 @@ MvSeg seg_of(const DT &t, float *y) {
     return g;
 }
 
-// One layer's five launches (see zh_moe.hip).
+// The hidden state layer l reads (and its gate/up normalises).
+float *hidden_of(const ZiggyHipMoeStack *s, int l) {
+    if (!s->fuse_combine) return s->hidden;
+    return ((int)s->layers.size() - 1 - l) % 2 == 0 ? s->hidden : s->hidden2;
+}
+
+// One layer's launches (see zh_moe.hip).
 hipError_t enqueue_layer(ZiggyHipMoeStack *s, int l, hipStream_t st) {
     const MoeLayerW &L = s->layers[l];
     const ZiggyHipMoeDesc &d = s->d;
     const int H = (int)d.hidden, E = (int)d.expert_count, K = (int)d.expert_used_count, FF = (int)d.expert_ff_length;
     uint32_t *route = s->route + (size_t)l * s->route_stride;
-    // router (+ the shared expert's gate row) on the normed hidden state
+    float *hidden = hidden_of(s, l);
+    // router (+ the shared expert's gate row) on the normed hidden state;
+    // with fuse_combine, layer l - 1's combine first (its result to `hidden`)
     {
         MvParams p{};
         p.nseg = 1;
@@ -82,7 +96,14 @@ hipError_t enqueue_layer(ZiggyHipMoeStack *s, int l, hipStream_t st) {
             p.nseg = 2;
         }
         p.cols = H;
-        p.x = s->hidden;
+        p.x = hidden;
+        if (s->fuse_combine && l > 0) {
+            p.x = hidden_of(s, l - 1);
+            p.pro_in = s->tmp;
+            p.pro_out = hidden;
+            p.expert = s->route + (size_t)(l - 1) * s->route_stride;
+            p.pro_cfg = (uint32_t)K | (s->shared ? 1u : 0u) << 4;
+        }
         p.norm_w = (const float *)L.norm.p;
         p.eps = d.rms_norm_eps;
         hipError_t e = launch_matvec(p, IN_NORM, OUT_STORE, st);
@@ -114,17 +135,17 @@ hipError_t enqueue_layer(ZiggyHipMoeStack *s, int l, hipStream_t st) {
             p.nseg = K + 1;
         }
         p.cols = H;
-        p.x = s->hidden;
+        p.x = hidden;
         p.norm_w = (const float *)L.norm.p;
         p.eps = d.rms_norm_eps;
         p.rows_per_expert = FF;
         p.expert_limit = E;
         if (route_in_gate_up) {
-            p.route_logits = s->logits;
-            p.route_out = route;
-            p.route_cfg = (uint32_t)E | (uint32_t)K << 16 | d.gating_func << 20 | (d.weights_norm ? 1u : 0u) << 24 |
-                          (s->shared_gate ? 1u : 0u) << 25;
-            p.route_scale = d.weights_scale;
+            p.pro_in = s->logits;
+            p.pro_out = route;
+            p.pro_cfg = (uint32_t)E | (uint32_t)K << 16 | d.gating_func << 20 | (d.weights_norm ? 1u : 0u) << 24 |
+                        (s->shared_gate ? 1u : 0u) << 25;
+            p.pro_scale = d.weights_scale;
         } else {
             p.expert = route;
         }
@@ -163,7 +184,9 @@ hipError_t enqueue_layer(ZiggyHipMoeStack *s, int l, hipStream_t st) {
             if (e != hipSuccess) return e;
         }
     }
-    return launch_moe_combine(s->hidden, s->tmp, route, H, K, s->shared ? 1 : 0, st);
+    // the next layer's router runs this combine when fused
+    if (s->fuse_combine && l + 1 < (int)s->layers.size()) return hipSuccess;
+    return launch_moe_combine(hidden, s->tmp, route, H, K, s->shared ? 1 : 0, st);
 }
 
 // One layer over M token rows (prefill): the rows are independent, so each
@@ -343,6 +366,7 @@ int ziggy_hip_moe_stack_create(ZiggyHipContext *ctx, const ZiggyHipMoeDesc *desc
         size_t bytes;
     } reqs[] = {
         {(void **)&s->hidden, H * 4},
+        {(void **)&s->hidden2, H * 4},
         {(void **)&s->logits, (E + 1) * 4},
         {(void **)&s->act, (K + 1) * (size_t)s->act_stride * 4},
         {(void **)&s->tmp, (K + 1) * H * 4},
@@ -362,6 +386,12 @@ int ziggy_hip_moe_stack_create(ZiggyHipContext *ctx, const ZiggyHipMoeDesc *desc
         free_stack(s);
         return hip_fail(e, "MoE upload", err, err_len);
     }
+    // the combine fuses into the next router launch when that launch is the
+    // f32 matvec (the kernel holds the combined row in LDS)
+    s->fuse_combine = layer_count > 1 && H <= (size_t)kCombineMaxCols && H % 4 == 0;
+    for (const MoeLayerW &L : s->layers)
+        if (L.router.type != ZIGGY_HIP_TYPE_F32 || (s->shared_gate && L.gate_inp_sh.type != ZIGGY_HIP_TYPE_F32))
+            s->fuse_combine = false;
     // capture every layer once; each forward replays the graph
     hipStream_t st = ctx->stream;
     hipGraph_t g = nullptr;
@@ -388,7 +418,7 @@ int ziggy_hip_moe_stack_forward(ZiggyHipMoeStack *s, const float *hidden_in, flo
     if (!s || !hidden_in || !hidden_out) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "null argument");
     hipStream_t st = s->ctx->stream;
     const size_t H = s->d.hidden, K = s->d.expert_used_count, NL = s->layers.size();
-    ZH_TRY(hipMemcpyAsync(s->hidden, hidden_in, H * 4, hipMemcpyHostToDevice, st), "MoE input");
+    ZH_TRY(hipMemcpyAsync(hidden_of(s, 0), hidden_in, H * 4, hipMemcpyHostToDevice, st), "MoE input");
     ZH_TRY(hipGraphLaunch(s->graph, st), "MoE stack");
     ZH_TRY(hipMemcpyAsync(hidden_out, s->hidden, H * 4, hipMemcpyDeviceToHost, st), "MoE output");
     std::vector<uint32_t> r;

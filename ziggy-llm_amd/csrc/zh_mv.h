@@ -275,6 +275,54 @@ __device__ __forceinline__ void coop_finish(XDig &xs, const XRun &r, int nruns, 
     xs.scale = me.scale;
 }
 
+// The fused combine of the previous MoE layer (MvParams::pro_in, NORM): CPT
+// float4 chunks of the row per thread, every load (hidden, the k routed rows,
+// the shared row) in flight before any arithmetic, then combine_value's
+// operations in its order per element; the row goes to LDS (and from the
+// writer workgroup to pro_out).  Loads past the row re-read its last chunk.
+template <int CPT>
+__device__ __forceinline__ void combine_prologue(const MvParams &p, float *xc, bool writer) {
+    const int H = p.cols, k = (int)(p.pro_cfg & 0xF);
+    const bool shared = p.pro_cfg >> 4 & 1;
+    float4 hv[CPT], tv[CPT][kRouteMaxK], sv[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; c++) {
+        const int i4 = min((int)threadIdx.x + c * kThreads, H / 4 - 1);
+        hv[c] = *reinterpret_cast<const float4 *>(p.x + 4 * i4);
+#pragma unroll
+        for (int s = 0; s < kRouteMaxK; s++)
+            tv[c][s] = *reinterpret_cast<const float4 *>(p.pro_in + (size_t)min(s, k - 1) * H + 4 * i4);
+        sv[c] = *reinterpret_cast<const float4 *>(p.pro_in + (size_t)k * H + 4 * i4);
+    }
+    float w[kRouteMaxK];
+#pragma unroll
+    for (int s = 0; s < kRouteMaxK; s++) w[s] = __uint_as_float(p.expert[2 * min(s, k - 1) + 1]);
+    const float g = __uint_as_float(p.expert[2 * k]);
+    float *out = static_cast<float *>(p.pro_out);
+#pragma unroll
+    for (int c = 0; c < CPT; c++) {
+        const int i4 = (int)threadIdx.x + c * kThreads;
+        if (i4 >= H / 4) continue;
+        float hs[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w}, ss[4] = {sv[c].x, sv[c].y, sv[c].z, sv[c].w}, r[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            // combine_value (zh_route.h), operation for operation
+            float o = 0.f;
+#pragma unroll
+            for (int s = 0; s < kRouteMaxK; s++) {
+                if (s >= k) break;
+                const float d = e == 0 ? tv[c][s].x : e == 1 ? tv[c][s].y : e == 2 ? tv[c][s].z : tv[c][s].w;
+                o = w[s] == 1.0f ? o + d : fmaf(d, w[s], o);
+            }
+            if (shared) o = g == 1.0f ? o + ss[e] : fmaf(ss[e], g, o);
+            r[e] = hs[e] + o;
+        }
+        const float4 v = make_float4(r[0], r[1], r[2], r[3]);
+        *reinterpret_cast<float4 *>(xc + 4 * i4) = v;
+        if (writer) *reinterpret_cast<float4 *>(out + 4 * i4) = v;
+    }
+}
+
 template <int F, int IN, int OUT>
 __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int wg_in_seg, float *lds) {
     constexpr int D = ring_depth<F, OUT>();
@@ -551,14 +599,15 @@ __global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
     // loads, not one dependent round trip per use
     MvSeg sg = p.seg[si];
     if constexpr (OUT == OUT_SWIGLU) {
-        if (p.route_logits && (sg.expert_slot >= 0 || wg == 0)) {  // uniform over the workgroup
+        if (p.pro_in && (sg.expert_slot >= 0 || wg == 0)) {  // uniform over the workgroup
             __shared__ uint32_t route_s[2 * kRouteMaxK + 2];
             if (threadIdx.x < 64) {
-                const uint32_t c = p.route_cfg;
-                route_wave(p.route_logits, (int)(c & 0xFFFF), (int)(c >> 16 & 0xF), (int)(c >> 20 & 0xF),
-                           (int)(c >> 24 & 1), p.route_scale, (int)(c >> 25 & 1), [&](int i, uint32_t v) {
+                const uint32_t c = p.pro_cfg;
+                uint32_t *out = static_cast<uint32_t *>(p.pro_out);
+                route_wave(p.pro_in, (int)(c & 0xFFFF), (int)(c >> 16 & 0xF), (int)(c >> 20 & 0xF),
+                           (int)(c >> 24 & 1), p.pro_scale, (int)(c >> 25 & 1), [&](int i, uint32_t v) {
                                route_s[i] = v;
-                               if (wg == 0) p.route_out[i] = v;
+                               if (wg == 0) out[i] = v;
                            });
             }
             __syncthreads();
@@ -570,6 +619,17 @@ __global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
                 if (sg.w2) sg.w2 += off;
                 sg.expert_slot = -1;
             }
+        }
+    }
+    if constexpr (IN == IN_NORM && OUT == OUT_STORE && F1 == F32 && F2 == F32) {
+        if (p.pro_in) {  // the previous MoE layer's combine, then the norm as usual
+            __shared__ __align__(16) float xc[kCombineMaxCols];
+            if (p.cols <= 2 * 4 * kThreads)
+                combine_prologue<2>(p, xc, wg == 0);
+            else
+                combine_prologue<kCombineMaxCols / (4 * kThreads)>(p, xc, wg == 0);
+            __syncthreads();
+            sg.x = xc;
         }
     }
     if (F1 == F2 || sg.fmt == F1)

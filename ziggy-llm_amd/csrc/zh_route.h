@@ -101,4 +101,25 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
     }
 }
 
+// One element of the MoE combine: out = sum over slots of w_s * down_s in slot
+// order (addScaledInPlace: an exact weight of 1 adds without a product),
+// + g * shared, then hidden + out (addInPlace) -- the reference's order.
+// Used by the combine kernel and by the fused combine of the next layer's
+// router launch.
+__device__ __forceinline__ float combine_value(const float *hidden, const float *tmp, const uint32_t *route, int H,
+                                               int k, bool has_shared, const float *sh, int r) {
+    float out = 0.f;
+    for (int s = 0; s < k; s++) {
+        const float w = __uint_as_float(route[2 * s + 1]), d = tmp[(size_t)s * H + r];
+        out = w == 1.0f ? out + d : fmaf(d, w, out);
+    }
+    if (has_shared) {
+        const float g = __uint_as_float(route[2 * k]), d = sh[r];
+        out = g == 1.0f ? out + d : fmaf(d, g, out);
+    }
+    return hidden[r] + out;
+}
+
+constexpr int kCombineMaxCols = 4096;  // hidden size of the fused combine at most
+
 }  // namespace zh
