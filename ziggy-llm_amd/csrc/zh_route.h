@@ -22,6 +22,24 @@ __device__ __forceinline__ uint32_t route_ordered_bits(float v) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// The wavefront sum of `for (o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o)`,
+// operand for operand, without LDS-path bpermutes: lane swaps for 32 and 16,
+// row_ror:8 for 8, row_shl:4 / row_shr:4 by lane for 4, quad permutations
+// for 2 and 1 (each step adds the partner lane's value, as the shuffle does).
+__device__ __forceinline__ float wave_sum_xor(float v) {
+    auto mov = [](float x, auto ctrl) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xF, 0xF, false));
+    };
+    v = xsum<32>(v);
+    v = xsum<16>(v);
+    v += mov(v, std::integral_constant<int, 0x128>{});  // row_ror:8 = lane ^ 8
+    const float up = mov(v, std::integral_constant<int, 0x104>{}), dn = mov(v, std::integral_constant<int, 0x114>{});
+    v += (threadIdx.x & 4) ? dn : up;                   // row_shr:4 / row_shl:4 = lane ^ 4
+    v += mov(v, std::integral_constant<int, 0x4E>{});   // lane ^ 2
+    v += mov(v, std::integral_constant<int, 0xB1>{});   // lane ^ 1
+    return v;
+}
+
 template <class Put>
 __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int E, int k, int gating,
                                            int weights_norm, float weights_scale, int has_shared_gate, Put put) {
@@ -39,7 +57,7 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
             pr[i] = l + 64 * i < E ? expf(pr[i] - m) : 0.f;
             s += pr[i];
         }
-        for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+        s = wave_sum_xor(s);
 #pragma unroll
         for (int i = 0; i < 4; i++) pr[i] = l + 64 * i < E ? pr[i] / s : -INFINITY;
     }
@@ -65,9 +83,9 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
     // the selected probabilities: from the lane that holds each
     float w[kRouteMaxK];
     for (int r = 0; r < k; r++) {
-        const int src = sel[r] & 63, i = sel[r] >> 6;
+        const int e = __builtin_amdgcn_readfirstlane((int)sel[r]), src = e & 63, i = e >> 6;
         const float mine = i == 0 ? pr[0] : i == 1 ? pr[1] : i == 2 ? pr[2] : pr[3];
-        w[r] = __shfl(mine, src, 64);
+        w[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), src));
     }
     if (l == 0) {
         if (weights_norm) {
