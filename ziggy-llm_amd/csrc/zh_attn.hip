@@ -641,7 +641,11 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     for (int nt = 0; nt < NT; nt++) pos_col[nt] = MQ ? pos0 + qbase + ((li >> 1) + 8 * nt) / Gq : pos;
     const int n_total = pos + 1 - p.window_start;
     const int units = (n_total + TP - 1) / TP;
-    const int per = (units + p.max_splits - 1) / p.max_splits;  // tiles per split
+    // tiles per split; a single query takes at least kMinTiles per split
+    // (fewer partials to merge: 12.8 -> 12.4 us at 4k positions, the same
+    // grid at 16k, where every split holds more)
+    constexpr int kMinTiles = MQ ? 1 : 6;
+    const int per = max((units + p.max_splits - 1) / p.max_splits, kMinTiles);
     const int nsplit = (units + per - 1) / per;
     if (split >= nsplit) return;
     const int u_begin = split * per, nu = min(per, units - u_begin);
