@@ -39,8 +39,27 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_TFLOPS = 2500.0  # dense bf16 matrix-core peak
 
 
+CPU_MAX_STEPS = 64  # upper bound on the CPU baseline's decode steps
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def context_length(model, prompt, warmup, steps):
+    """KV rows the run needs.  The GPU decode uses prompt + warmup rows, then 1 + steps more (the pending
+    token and the timed steps); time_kernel needs one free row after that; the CPU baseline fills its cache
+    to pos0 = prompt + warmup + 1 and then decodes up to CPU_MAX_STEPS steps; config 4's verify adds three
+    passes of 9 rows (drafts decoded, the position rewound, then verified)."""
+    rows = prompt + warmup + 1 + max(steps + 1, CPU_MAX_STEPS)
+    if model == "qwen3":
+        rows += 3 * 9
+    return rows + 8
+
+
+def cpu_step_budget(ctx_len, pos0):
+    """CPU baseline steps that fit the cache after pos0 (a step at position p needs p < ctx_len)."""
+    return max(0, min(CPU_MAX_STEPS, ctx_len - pos0))
 
 
 def main():
@@ -70,7 +89,7 @@ def main():
     if args.model == "moe":
         return bench_moe(args)
 
-    ctx_len = args.prompt + args.warmup + args.steps + 8 + (64 if args.model == "qwen3" else 0)
+    ctx_len = context_length(args.model, args.prompt, args.warmup, args.steps)
     spec = {"llama8b": synth.llama8b_spec, "tinyllama": synth.tinyllama_spec,
             "qwen3": synth.qwen3_8b_spec}[args.model](context=ctx_len)
     t0 = time.time()
@@ -148,15 +167,16 @@ def main():
         o = zo.Session(m, context=ctx_len, kv_f16=False, threads=threads)
         o.fill_kv_pattern(pos0, seed=1)
         tok = int(toks[0])
+        budget = cpu_step_budget(ctx_len, pos0)
         n, t_cpu = 0, 0.0
-        while t_cpu < args.cpu_seconds or n < 2:
+        while n < budget and (t_cpu < args.cpu_seconds or n < 2):
             t1 = time.perf_counter()
             tok = o.step_greedy(tok)
             t_cpu += time.perf_counter() - t1
             n += 1
-            if n >= 64:
-                break
-        cpu = {"value": round(n / t_cpu, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+        o.close()
+        cpu = {"value": round(n / t_cpu, 4), "unit": "tok/s", "cores": threads, "host_cores": ncpu,
+               "kind": "port",
                "sample": f"{n} greedy decode steps of the same {spec.name} model from position {pos0} "
                          f"(KV cache filled with a fixed pattern; decode cost does not depend on its values), "
                          f"C restatement of the reference CPU path, {threads} threads of {ncpu} host cores"}
