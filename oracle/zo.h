@@ -27,7 +27,11 @@
  *     tolerance only.
  * Everything else is pinned by the reference's known-answer tests, its
  * fixture blocks and golden text, closed forms and brute-force layouts
- * (tests/test_oracle_pins.py, tests/test_golden.py).
+ * (tests/test_oracle_pins.py, tests/test_golden.py).  The MoE composition
+ * (zo_moe_ffn: router, gating, top-k, normalisation, scale, expert row
+ * offsets, SwiGLU, slot-order combine, sigmoid-gated shared expert) is pinned
+ * against an independent float64 composition over the dequantized weights,
+ * with planted misreadings shown to fail (tests/test_moe_oracle_pin.py).
  */
 #ifndef ZIGGY_ORACLE_H
 #define ZIGGY_ORACLE_H
