@@ -248,6 +248,20 @@ int ziggy_hip_attention_fused_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *q,
                                   uint32_t context_length, uint32_t position, uint32_t layer_base,
                                   uint32_t window_start, float scale, float softcap, char *error_message,
                                   size_t error_message_len);
+/* The same attention, allocating nothing.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops that forbid it).  Its split partials and arrival
+ * counters live in a fixed per-device static array of 4 MiB (4 KiB of
+ * counters, the rest partials) instead of the context's scratch; calls whose
+ * partials (kv heads x splits x 8 x (head_dim + 2) floats) exceed it fail with
+ * ZIGGY_HIP_INVALID_ARGUMENT.  Calls on one device share the array, so calls
+ * that overlap on one device race; each call clears the counters it uses. */
+int ziggy_hip_attention_fused_f32_noalloc(ZiggyHipContext *ctx, const ZiggyHipBuffer *q,
+                                          const ZiggyHipBuffer *k_cache, const ZiggyHipBuffer *v_cache,
+                                          ZiggyHipBuffer *output, uint32_t head_count, uint32_t head_count_kv,
+                                          uint32_t head_dim, uint32_t kv_dim, uint32_t context_length,
+                                          uint32_t position, uint32_t layer_base, uint32_t window_start, float scale,
+                                          float softcap, char *error_message, size_t error_message_len);
 int ziggy_hip_silu_mul_f32(ZiggyHipContext *ctx, ZiggyHipBuffer *gate, const ZiggyHipBuffer *up, uint32_t count,
                            char *error_message, size_t error_message_len);
 int ziggy_hip_add_in_place_f32(ZiggyHipContext *ctx, ZiggyHipBuffer *dst, const ZiggyHipBuffer *src,

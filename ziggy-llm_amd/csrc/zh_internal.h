@@ -319,5 +319,14 @@ constexpr int kMultiHeads = 16;  // (query, head) pairs per multi-query workgrou
 // Splits of the attention grid for kv_heads heads and up to max_positions keys.
 int attention_splits(int kv_heads, int max_positions);
 size_t attention_scratch_floats(int head_count, int head_dim, int max_splits);
+// Validates a bridge-level attention call (ziggy_hip_attention_fused_f32's
+// arguments) and fills every field of *p but the partials and counters.
+int attention_call_params(const ZiggyHipBuffer *q, const ZiggyHipBuffer *kc, const ZiggyHipBuffer *vc,
+                          const ZiggyHipBuffer *out, uint32_t heads, uint32_t heads_kv, uint32_t hd, uint32_t kv_dim,
+                          uint32_t ctx_len, uint32_t pos, uint32_t layer_base, uint32_t window_start, float scale,
+                          float softcap, AttnParams *p, char *err, size_t err_len);
+// Per-device address of the allocation-free attention's static scratch;
+// called once per device by context creation, with that device current.
+int noalloc_init_device(int device, char *err, size_t err_len);
 
 }  // namespace zh

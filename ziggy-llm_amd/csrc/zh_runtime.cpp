@@ -67,6 +67,45 @@ int check_matvec(ZiggyHipContext *ctx, uint32_t type, const ZiggyHipBuffer *m, s
 
 }  // namespace
 
+namespace zh {
+
+int attention_call_params(const ZiggyHipBuffer *q, const ZiggyHipBuffer *kc, const ZiggyHipBuffer *vc,
+                          const ZiggyHipBuffer *out, uint32_t heads, uint32_t heads_kv, uint32_t hd, uint32_t kv_dim,
+                          uint32_t ctx_len, uint32_t pos, uint32_t layer_base, uint32_t window_start, float scale,
+                          float softcap, AttnParams *p, char *err, size_t err_len) {
+    if (heads == 0 || heads_kv == 0 || heads % heads_kv || heads / heads_kv > 8 ||
+        (hd != 64 && hd != 128 && hd != 256) || kv_dim != heads_kv * hd || pos >= ctx_len || window_start > pos) {
+        set_err(err, err_len, "unsupported attention shape");
+        return ZIGGY_HIP_INVALID_ARGUMENT;
+    }
+    if (softcap != 0.f) {
+        set_err(err, err_len, "attention softcapping is not supported on this path");
+        return ZIGGY_HIP_INVALID_ARGUMENT;
+    }
+    const size_t cache_need = ((size_t)layer_base + (size_t)ctx_len * kv_dim) * 2;
+    if (!buf_ok(q, (size_t)heads * hd * 4) || !buf_ok(kc, cache_need) || !buf_ok(vc, cache_need) ||
+        !buf_ok(out, (size_t)heads * hd * 4)) {
+        set_err(err, err_len, "attention buffers too small");
+        return ZIGGY_HIP_INVALID_ARGUMENT;
+    }
+    *p = AttnParams{};
+    p->q = (const float *)q->ptr;
+    p->k_cache = (__half *)kc->ptr + layer_base;
+    p->v_cache = (__half *)vc->ptr + layer_base;
+    p->out = (float *)out->ptr;
+    p->head_count = (int)heads;
+    p->head_count_kv = (int)heads_kv;
+    p->head_dim = (int)hd;
+    p->kv_dim = (int)kv_dim;
+    p->position = (int)pos;
+    p->window_start = (int)window_start;
+    p->scale = scale;
+    p->max_splits = attention_splits((int)heads_kv, (int)(pos + 1 - window_start));
+    return ZIGGY_HIP_OK;
+}
+
+}  // namespace zh
+
 extern "C" {
 
 const char *ziggy_hip_version(void) { return "libziggy_hip gfx950 " __DATE__; }
@@ -119,6 +158,11 @@ int ziggy_hip_create_context(int device_index, ZiggyHipContext **out_ctx, ZiggyH
         return ZIGGY_HIP_INITIALIZATION_FAILED;
     }
     ctx->scratch_len = kCtxScratch;
+    const int nst = noalloc_init_device(device_index, err, err_len);
+    if (nst != ZIGGY_HIP_OK) {
+        ziggy_hip_destroy_context(ctx);
+        return nst;
+    }
     if (out_info) *out_info = ctx->info;
     *out_ctx = ctx;
     return ZIGGY_HIP_OK;
@@ -543,34 +587,14 @@ int ziggy_hip_attention_fused_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *q,
                                   const ZiggyHipBuffer *vc, ZiggyHipBuffer *out, uint32_t heads, uint32_t heads_kv,
                                   uint32_t hd, uint32_t kv_dim, uint32_t ctx_len, uint32_t pos, uint32_t layer_base,
                                   uint32_t window_start, float scale, float softcap, char *err, size_t err_len) {
-    if (!ctx || heads == 0 || heads_kv == 0 || heads_kv > kCtxCounters || heads % heads_kv || heads / heads_kv > 8 || (hd != 64 && hd != 128 && hd != 256) ||
-        kv_dim != heads_kv * hd || pos >= ctx_len || window_start > pos) {
+    if (!ctx || heads_kv > kCtxCounters) {
         set_err(err, err_len, "unsupported attention shape");
         return ZIGGY_HIP_INVALID_ARGUMENT;
     }
-    if (softcap != 0.f) {
-        set_err(err, err_len, "attention softcapping is not supported on this path");
-        return ZIGGY_HIP_INVALID_ARGUMENT;
-    }
-    const size_t cache_need = ((size_t)layer_base + (size_t)ctx_len * kv_dim) * 2;
-    if (!buf_ok(q, (size_t)heads * hd * 4) || !buf_ok(kc, cache_need) || !buf_ok(vc, cache_need) ||
-        !buf_ok(out, (size_t)heads * hd * 4)) {
-        set_err(err, err_len, "attention buffers too small");
-        return ZIGGY_HIP_INVALID_ARGUMENT;
-    }
     AttnParams p{};
-    p.q = (const float *)q->ptr;
-    p.k_cache = (__half *)kc->ptr + layer_base;
-    p.v_cache = (__half *)vc->ptr + layer_base;
-    p.out = (float *)out->ptr;
-    p.head_count = (int)heads;
-    p.head_count_kv = (int)heads_kv;
-    p.head_dim = (int)hd;
-    p.kv_dim = (int)kv_dim;
-    p.position = (int)pos;
-    p.window_start = (int)window_start;
-    p.scale = scale;
-    p.max_splits = attention_splits((int)heads_kv, (int)(pos + 1 - window_start));
+    const int st = attention_call_params(q, kc, vc, out, heads, heads_kv, hd, kv_dim, ctx_len, pos, layer_base,
+                                         window_start, scale, softcap, &p, err, err_len);
+    if (st != ZIGGY_HIP_OK) return st;
     p.counters = ctx->counters;
     const size_t need = attention_scratch_floats((int)heads, (int)hd, p.max_splits) * 4;
     if (need > ctx->scratch_len) {

@@ -129,6 +129,8 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_apply_rope_to_dst_f32": [vp, vp, vp, sz, u32, u32, u32, u32, f, u32] + E,
         "ziggy_hip_store_kv_half": [vp, vp, vp, sz, u32] + E,
         "ziggy_hip_attention_fused_f32": [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, u32, f, f] + E,
+        "ziggy_hip_attention_fused_f32_noalloc": [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, u32, f,
+                                                  f] + E,
         "ziggy_hip_silu_mul_f32": [vp, vp, vp, u32] + E,
         "ziggy_hip_add_in_place_f32": [vp, vp, vp, u32] + E,
         "ziggy_hip_rms_norm_f32": [vp, vp, vp, vp, u32, f, f] + E,
@@ -296,6 +298,12 @@ class Context:
         scale = 1.0 / np.sqrt(hd) if scale is None else scale
         _call("ziggy_hip_attention_fused_f32", self.h, q.h, kc.h, vc.h, out.h, heads, heads_kv, hd, kv_dim, ctx_len,
               pos, layer_base, window_start, float(scale), float(softcap))
+
+    def attention_noalloc(self, q, kc, vc, out, heads, heads_kv, hd, kv_dim, ctx_len, pos, layer_base=0,
+                          window_start=0, scale=None, softcap=0.0):
+        scale = 1.0 / np.sqrt(hd) if scale is None else scale
+        _call("ziggy_hip_attention_fused_f32_noalloc", self.h, q.h, kc.h, vc.h, out.h, heads, heads_kv, hd, kv_dim,
+              ctx_len, pos, layer_base, window_start, float(scale), float(softcap))
 
     def silu_mul(self, g, u, n):
         _call("ziggy_hip_silu_mul_f32", self.h, g.h, u.h, n)
