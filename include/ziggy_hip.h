@@ -328,6 +328,7 @@ typedef struct {
     uint64_t wall_ns;          /* host clock around the decode steps */
     uint32_t next_token;       /* greedy token of the last step (not emitted) */
     uint32_t reserved;
+    uint64_t prompt_ns;        /* host clock around the prompt (batched passes and its last step) */
 } ZiggyHipGenerateStats;
 
 /* Kernels of one decode step, for ziggy_hip_session_time_kernel. */
@@ -387,7 +388,11 @@ int ziggy_hip_session_step_greedy(ZiggyHipSession *session, uint32_t token, uint
 int ziggy_hip_session_step_no_output(ZiggyHipSession *session, uint32_t token, char *error_message,
                                      size_t error_message_len);
 /* Device-resident greedy generation (generateLoadedStreaming's greedy loop,
- * model/loader.zig:2065-2279): the prompt is consumed token by token, then
+ * model/loader.zig:2065-2279): every prompt token but the last runs in
+ * batched passes of up to 64 tokens on the matrix cores (the reference's
+ * runPrompt, model/loader.zig:1016-1036, steps them one by one; head sizes
+ * without the multi-query attention, or ZIGGY_HIP_PREFILL=steps, step them
+ * too), the last one through the decode step for its logits, then
  * `steps` tokens are generated with every token fed back on the device;
  * replays of one step graph are queued back to back.  out_tokens receives
  * the generated ids.  EOS is not checked (the benchmark configurations
@@ -415,12 +420,26 @@ int ziggy_hip_session_verify(ZiggyHipSession *session, uint32_t current_token, c
  * common prefix of those and `prompt` is kept (the position moves back to it;
  * the reference instead resets unless all of its cache is a prefix of the
  * prompt), then the rest of the prompt is fed; the last prompt token is always
- * fed again, for its logits.  *out_reused: the prefix kept; *out_next: the
- * greedy token after the prompt.  Rows written by the block-level calls
- * (run_attention_block) are not reused. */
+ * fed again, for its logits.  *out_reused: commonPrefixLen of the cached
+ * tokens and the prompt, the count the reference reports as
+ * reused_prompt_token_count (model/loader.zig:2310-2313; when the prompt
+ * equals the cached tokens, one more than the rows kept, since the last
+ * prompt row is recomputed); *out_next: the greedy token after the prompt.
+ * Rows written by the block-level calls (run_attention_block) or by
+ * session_fill_kv_pattern are not reused. */
 int ziggy_hip_session_prefill_cached(ZiggyHipSession *session, const uint32_t *prompt, uint32_t prompt_len,
                                      uint32_t *out_reused, uint32_t *out_next, char *error_message,
                                      size_t error_message_len);
+/* Test and benchmark hook (no counterpart in the reference's runtime; it
+ * mirrors the CPU oracle's fill): writes a deterministic binary16-exact
+ * pattern into the K/V rows [0, position) of every layer and moves the
+ * position there, so one long-context step can be compared with a CPU session
+ * filled the same way, or timed, without a prefill.  x = seed *
+ * 0x9E3779B97F4A7C15 + 1, then per layer, position and dimension one
+ * xorshift64 step (13, 7, 17) and v = ((x >> 40 & 0x7FF) - 1024) / 1024;
+ * K = v, V = -v.  The rows are not reusable by prefill_cached. */
+int ziggy_hip_session_fill_kv_pattern(ZiggyHipSession *session, uint32_t position, uint64_t seed,
+                                      char *error_message, size_t error_message_len);
 /* Logits of the most recent step that ran the output head (f32, vocab_size). */
 int ziggy_hip_session_read_logits(ZiggyHipSession *session, float *out, char *error_message,
                                   size_t error_message_len);

@@ -145,9 +145,13 @@ int zo_session_step_no_output(zo_session *s, uint32_t token);
 int zo_session_hidden(const zo_session *s, float *out);
 int zo_session_kv(const zo_session *s, uint32_t layer, uint32_t position, float *k_out, float *v_out);
 /* Fills the K/V cache of every layer for positions [0, position) with a
- * deterministic pattern and sets the position; used only to time decode at a
- * long context without running the prefill (decode cost does not depend on
- * the cached values). */
+ * deterministic pattern and sets the position: to time decode at a long
+ * context without running the prefill (decode cost does not depend on the
+ * cached values), and to compare one long-context step with the HIP session
+ * filled the same way.  x = seed * 0x9E3779B97F4A7C15 + 1, then for each
+ * layer, position and dimension in that order one xorshift64 step (x ^= x<<13,
+ * x ^= x>>7, x ^= x<<17) and v = ((x >> 40 & 0x7FF) - 1024) / 1024 (exact in
+ * binary16); K = v, V = -v. */
 int zo_session_fill_kv_pattern(zo_session *s, uint32_t position, uint64_t seed);
 
 /* Greedy generation as generateLoadedStreaming runs it on the CPU path

@@ -691,7 +691,8 @@ int zo_session_fill_kv_pattern(zo_session *s, uint32_t pos, uint64_t seed) {
             x ^= x << 13;
             x ^= x >> 7;
             x ^= x << 17;
-            float v = (float)((int)(x >> 40 & 0xFFFF) - 32768) * (1.0f / 32768.0f);
+            /* multiples of 2^-10 in [-1, 1): exact in binary16, so both cache modes hold the same values */
+            float v = (float)((int)(x >> 40 & 0x7FF) - 1024) * (1.0f / 1024.0f);
             size_t idx = (size_t)l * s->ctx * kvs + i;
             s->kc[idx] = v;
             s->vc[idx] = -v;

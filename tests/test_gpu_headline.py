@@ -1,0 +1,202 @@
+"""GPU parity at the headline shapes: the Llama-3.1-8B-shaped Q4_K_M model and the
+Qwen3-8B-shaped Q8_0 model (config 4), both from zhip.synth with seed 1.
+
+The reference pins its GPU path by equality with its CPU path (runtime/llama_runtime.zig:237-272); here
+the HIP session is compared with the CPU oracle (binary16-KV mode, the reference GPU path's cache
+semantics):
+  * 64 greedy tokens after an 8-token prompt equal the oracle's stream (computed once by
+    tests/golden/make_headline_streams.py: the oracle needs minutes for it), and the logits after the
+    prompt match a live oracle run: the same argmax, within 2e-3 relative L2;
+  * steps at a long position over a cache both sides fill with the same binary16-exact pattern
+    (positions 4096-4097 for Llama, 16383 for Qwen3): the same argmax, logits within 1e-4 relative L2;
+  * Qwen3: one batched verify pass of the pending token and 8 drafts (M = 9 GEMMs on the matrix cores)
+    predicts the oracle's greedy continuation, after the prompt and over a 2048-row filled cache.
+
+Why 2e-3 for the logits after a prompt when each kernel is held to 1e-4 (tests/test_gpu_kernels.py),
+as are the 2-3-layer models' logits (tests/test_gpu_session.py) and the long-position steps here (one
+new cache row each): over rows that both sides computed, 32-36 random layers and a binary16 cache
+amplify any last-bit difference.  A rounding difference in a K or V value can move its binary16
+rounding by one step (2^-11 relative), and those steps propagate.  The oracle alone shows it: one ulp
+changed in one weight of layer 0's attention norm moves its own Llama-shaped logits by ~2.4e-4 relative
+L2.  The test measures that sensitivity live and prints it next to the HIP distance.
+"""
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import zo
+from zhip import hip, synth
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+FIXTURE = json.load(open(os.path.join(HERE, "golden", "headline_streams.json")))
+THREADS = 16
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def rel_l2(a, b):
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def image_digest(buf) -> str:
+    # the digest tests/golden/make_headline_streams.py records
+    h = hashlib.blake2b(digest_size=16)
+    h.update(str(buf.nbytes).encode())
+    mv = memoryview(buf)
+    for off in range(0, buf.nbytes, 1 << 20):
+        h.update(mv[off:off + 4096])
+    h.update(mv[max(0, buf.nbytes - 4096):])
+    return h.hexdigest()
+
+
+class Model:
+    def __init__(self, key, spec_fn, long_context):
+        fx = FIXTURE[key]
+        self.fx = fx
+        # the image as the fixture was made (its context_length is in the metadata); the sessions set their own
+        self.spec = spec_fn(context=fx["context"])
+        self.long_context = long_context
+        say(f"building {self.spec.name}")
+        self.img = synth.build(self.spec, seed=fx["seed"])
+        assert image_digest(self.img.buf) == fx["image_digest"], \
+            "synthetic weights changed: rerun tests/golden/make_headline_streams.py"
+        self.prompt = np.array(fx["prompt"], np.uint32)
+        self.want = [int(t) for t in fx["tokens"]]
+        self.zm = zo.Model(self.img.buf)
+
+
+@pytest.fixture(scope="module")
+def llama8b():
+    m = Model("llama8b", synth.llama8b_spec, 4160)
+    yield m
+    m.zm.close()
+
+
+@pytest.fixture(scope="module")
+def qwen3():
+    m = Model("qwen3_8b", synth.qwen3_8b_spec, 16384)
+    yield m
+    m.zm.close()
+
+
+LOGITS_BAR = 2e-3   # logits after a prompt whose rows both sides computed
+STEP_BAR = 1e-4     # logits of a step over a cache filled identically on both sides
+
+
+def oracle_prompt_logits(m, ctx_len):
+    o = zo.Session(m.zm, context=ctx_len, kv_f16=True, threads=THREADS)
+    for t in m.prompt[:-1]:
+        o.step_no_output(int(t))
+    ol = o.step(int(m.prompt[-1]))
+    o.close()
+    return ol
+
+
+def stream_and_prompt_logits(hip_ctx, m):
+    ctx_len = m.fx["context"]
+    s = hip.Session(hip_ctx, m.img, context=ctx_len)
+    got, _ = s.generate(m.prompt, 64)
+    assert [int(t) for t in got] == m.want
+    # logits after the prompt (fed token by token), against a live oracle run of the same prompt
+    s.reset()
+    for t in m.prompt[:-1]:
+        s.step_no_output(int(t))
+    nxt = s.step_greedy(int(m.prompt[-1]))
+    ol = oracle_prompt_logits(m, ctx_len)
+    # the oracle's own sensitivity: one ulp of one layer-0 attention-norm weight
+    w = m.img.tensor_view("blk.0.attn_norm.weight").view(np.float32)
+    keep = w[5]
+    w[5] = np.nextafter(keep, np.float32(2))
+    ol_ulp = oracle_prompt_logits(m, ctx_len)
+    w[5] = keep
+    d, d_ulp = rel_l2(s.logits(), ol), rel_l2(ol_ulp, ol)
+    say(f"{m.spec.name}: logits after the prompt: HIP vs oracle {d:.2e}; oracle vs itself with one "
+        f"ulp moved in layer 0: {d_ulp:.2e}")
+    assert nxt == zo.argmax(ol) == m.want[0]
+    assert d < LOGITS_BAR
+    s.close()
+
+
+def long_position_steps(hip_ctx, m, pos, steps):
+    ctx_len = m.long_context
+    o = zo.Session(m.zm, context=ctx_len, kv_f16=True, threads=THREADS)
+    s = hip.Session(hip_ctx, m.img, context=ctx_len)
+    o.fill_kv_pattern(pos, seed=5)
+    s.fill_kv_pattern(pos, seed=5)
+    tok = int(m.prompt[0])
+    for i in range(steps):
+        say(f"{m.spec.name}: step at position {pos + i}")
+        ol = o.step(tok)
+        nxt = s.step_greedy(tok)
+        assert nxt == zo.argmax(ol), (pos + i, nxt, zo.argmax(ol))
+        d = rel_l2(s.logits(), ol)
+        say(f"{m.spec.name}: logits at position {pos + i}: HIP vs oracle {d:.2e}")
+        assert d < STEP_BAR
+        tok = nxt
+    # the step's own K/V row as well
+    for layer in (0, m.spec.n_layers - 1):
+        k_g, v_g = s.kv(layer, pos)
+        k_o, v_o = o.kv(layer, pos)
+        assert rel_l2(k_g, k_o) < 1e-3 and rel_l2(v_g, v_o) < 1e-3
+    o.close()
+    s.close()
+
+
+def test_llama8b_stream_64_and_logits(hip_ctx, llama8b):
+    say("llama8b: 64-token stream")
+    stream_and_prompt_logits(hip_ctx, llama8b)
+
+
+def test_llama8b_steps_at_position_4096(hip_ctx, llama8b):
+    long_position_steps(hip_ctx, llama8b, 4096, 2)
+
+
+def test_qwen3_stream_64_and_logits(hip_ctx, qwen3):
+    say("qwen3: 64-token stream")
+    stream_and_prompt_logits(hip_ctx, qwen3)
+
+
+def test_qwen3_verify_m9_after_the_prompt(hip_ctx, qwen3):
+    say("qwen3: verify after the prompt")
+    want = qwen3.want
+    s = hip.Session(hip_ctx, qwen3.img, context=qwen3.fx["context"])
+    _, st = s.generate(qwen3.prompt, 0)
+    assert st.next_token == want[0]
+    pred, n = s.verify(want[0], want[1:9])
+    assert n == 9 and [int(t) for t in pred] == want[1:10]
+    got, _ = s.generate(np.array([want[9]], np.uint32), 8)
+    assert [int(t) for t in got] == want[10:18]
+    s.close()
+
+
+def test_qwen3_verify_m9_over_a_filled_cache(hip_ctx, qwen3):
+    # 2048 filled rows: the multi-query attention runs many splits per query group at the real shape
+    say("qwen3: verify over 2048 filled rows")
+    pos = 2048
+    o = zo.Session(qwen3.zm, context=pos + 16, kv_f16=True, threads=THREADS)
+    o.fill_kv_pattern(pos, seed=9)
+    tok = int(qwen3.prompt[0])
+    want, t = [], tok
+    for _ in range(9):
+        t = o.step_greedy(t)
+        want.append(int(t))
+    o.close()
+    s = hip.Session(hip_ctx, qwen3.img, context=pos + 16)
+    s.fill_kv_pattern(pos, seed=9)
+    pred, n = s.verify(tok, want[:8])
+    assert n == 9 and [int(x) for x in pred] == want
+    s.close()
+
+
+def test_qwen3_step_at_position_16383(hip_ctx, qwen3):
+    long_position_steps(hip_ctx, qwen3, 16383, 1)

@@ -191,7 +191,7 @@ def test_prefill_cached_reuses_the_common_prefix(hip_ctx):
         while common < min(len(held), len(prompt)) and held[common] == prompt[common]:
             common += 1
         reused, nxt = s.prefill_cached(prompt)
-        assert reused == min(common, len(prompt) - 1)
+        assert reused == common  # commonPrefixLen (model/loader.zig:2310-2313)
         want_next, want_stream = fresh(prompt)
         assert nxt == want_next
         out, _ = s.generate(np.array([nxt], np.uint32), 8)

@@ -42,11 +42,17 @@ __device__ __forceinline__ float wsum(float v) {
 // RoPE angles of one position, once per workgroup: cs[i], sn[i] for pair i
 // of the n_rot rotated dims, theta = pos / base^(2i / n_rot) (applyRoPE,
 // model/loader.zig:3827-3866).
-__device__ __forceinline__ void rope_table(int n_rot, float base, int pos, float *cs, float *sn) {
+// This thread's RoPE denominator base^(2t / n_rot) (t = threadIdx.x < n_rot / 2): the host's table when
+// given, read early so that its wait does not cover the K/V loads issued after it.
+__device__ __forceinline__ float rope_den(int n_rot, float base, const float *denom) {
+    const int t = threadIdx.x;
+    if (t >= n_rot / 2) return 1.f;
+    return denom ? denom[t] : powf(base, (float)(2 * t) / (float)n_rot);
+}
+__device__ __forceinline__ void rope_table(int n_rot, float den, int pos, float *cs, float *sn) {
     const int t = threadIdx.x;
     if (t < n_rot / 2) {
-        const float e = (float)(2 * t) / (float)n_rot;
-        const float theta = (float)pos / powf(base, e);
+        const float theta = (float)pos / den;
         float sv, cv;
         sincosf(theta, &sv, &cv);
         cs[t] = cv;
@@ -364,7 +370,7 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnParams p) {
 
     if (fused) {
         const int n_rot = p.rope_dim < HD ? p.rope_dim : HD;
-        rope_table(n_rot, p.rope_base, pos, cs_s, sn_s);
+        rope_table(n_rot, rope_den(n_rot, p.rope_base, p.rope_denom), pos, cs_s, sn_s);
         norm_rope<HD, QV>(qv, nq, p.q_norm, p.eps, n_rot, p.rope_style, cs_s, sn_s, &q_s[0][0], red16);
         if (own_pos) {
             norm_rope<HD, 1>(kx, HD, p.k_norm, p.eps, n_rot, p.rope_style, cs_s, sn_s, kn_s, red16);
@@ -670,6 +676,8 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     constexpr int QV = VG * HD / 256;
     const int nq = G * HD;
     float qv[QV], kx[1] = {0.f}, vx = 0.f, qnw[QV], knw[1];
+    const int n_rot_f = p.rope_dim < HD ? p.rope_dim : HD;
+    const float rden = fused ? rope_den(n_rot_f, p.rope_base, p.rope_denom) : 1.f;
     {
         // norm weights too (dummy reads of q when absent): see the K/V loads
         const float *qn = p.q_norm ? p.q_norm : p.q, *kn = p.k_norm ? p.k_norm : p.q;
@@ -737,8 +745,8 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     load_k(1, kr[1]);
 
     if (fused) {
-        const int n_rot = p.rope_dim < HD ? p.rope_dim : HD;
-        rope_table(n_rot, p.rope_base, pos, cs_s, sn_s);
+        const int n_rot = n_rot_f;
+        rope_table(n_rot, rden, pos, cs_s, sn_s);
         norm_rope_w<HD, QV>(qv, nq, p.q_norm != nullptr, qnw, p.eps, n_rot, p.rope_style, cs_s, sn_s, &q_s[0][0],
                             red16);
         if (own_pos) {
@@ -1066,7 +1074,7 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(AttnParams p, float *q_o
         if (p.v_bias) vx += p.v_bias[(size_t)kvh * HD + tid];
     }
     const int n_rot = p.rope_dim < HD ? p.rope_dim : HD;
-    rope_table(n_rot, p.rope_base, pos, cs_s, sn_s);
+    rope_table(n_rot, rope_den(n_rot, p.rope_base, p.rope_denom), pos, cs_s, sn_s);
     norm_rope<HD, QV>(qv, nq, p.q_norm, p.eps, n_rot, p.rope_style, cs_s, sn_s, q_s, red16);
     norm_rope<HD, 1>(kx, HD, p.k_norm, p.eps, n_rot, p.rope_style, cs_s, sn_s, kn_s, red16);
     float *qo = q_out + (size_t)m * p.q_stride + (size_t)kvh * nq;

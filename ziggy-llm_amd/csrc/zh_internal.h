@@ -25,6 +25,12 @@ struct ZiggyHipContext {
     size_t scratch_len = 0;
     // zeroed arrival counters of the attention kernel (each launch leaves them zero)
     unsigned *counters = nullptr;
+    // RoPE denominators base^(2i / n_rot) per (base, n_rot) seen, computed on the host
+    struct RopeTable {
+        float base;
+        int n_rot;
+        float *dev;
+    } rope_tables[8] = {};
 };
 
 struct ZiggyHipBuffer {
@@ -68,6 +74,17 @@ inline int finish_op(ZiggyHipContext *ctx, const char *what, char *err, size_t e
 }
 
 inline bool buf_ok(const ZiggyHipBuffer *b, size_t need) { return b && b->ptr && b->len >= need; }
+
+// RoPE denominators base^(2i / n_rot), i < n_rot / 2, with the exponent and
+// powf of the CPU path (applyRoPE, model/loader.zig:3827-3866): theta =
+// pos / denom[i].  Computed on the host so the angles are the CPU path's to
+// the bit; at positions in the thousands one ulp of a denominator moves an
+// angle by ~1e-3 rad.
+inline void rope_denominators(float base, int n_rot, float *out) {
+    for (int i = 0; i < n_rot / 2; i++) out[i] = powf(base, (float)(2 * i) / (float)n_rot);
+}
+// The context's device table of rope_denominators(base, n_rot) (made on first use).
+hipError_t ctx_rope_denom(ZiggyHipContext *ctx, float base, int n_rot, const float **out);
 
 // ---------------- kernel launchers (implemented in the .hip files) ----------------
 
@@ -214,7 +231,7 @@ hipError_t launch_dequant(int fmt, const uint8_t *w, uint64_t stride, float *out
 hipError_t launch_rms_norm(const float *x, const float *w, float *out, int n, float eps, float off, hipStream_t s);
 hipError_t launch_rms_norm_per_head(const float *x, const float *w, float *out, int heads, int hd, float eps,
                                     float off, hipStream_t s);
-hipError_t launch_rope(const float *src, float *dst, int heads, int hd, int rope_dim, int pos, float base,
+hipError_t launch_rope(const float *src, float *dst, int heads, int hd, int rope_dim, int pos, const float *denom,
                        int style, hipStream_t s);
 hipError_t launch_store_kv_half(const float *src, __half *dst, int count, hipStream_t s);
 hipError_t launch_silu_mul(float *gate, const float *up, int n, hipStream_t s);
@@ -301,6 +318,7 @@ struct AttnParams {
     const float *q_bias, *k_bias, *v_bias;   // optional
     const float *q_norm, *k_norm;            // optional per-head RMSNorm weights [head_dim]
     float eps, rope_base;
+    const float *rope_denom;   // optional [n_rot / 2]: base^(2i / n_rot) from the host's powf (else powf here)
     int rope_dim, rope_style;
     int ctx;                   // cache capacity in positions (no store at or past it)
     // several queries (plain mode, matrix-core kernel): queries at positions

@@ -48,7 +48,7 @@ __global__ void rms_norm_per_head_kernel(const float *__restrict__ x, const floa
 // style 1 (NeoX) rotates (i, i + n_rot/2); theta = pos / base^(2i / n_rot).
 // Dimensions at or beyond n_rot are copied unchanged.
 __global__ void rope_kernel(const float *__restrict__ src, float *__restrict__ dst, int heads, int hd, int n_rot,
-                            float pos, float base, int style) {
+                            float pos, const float *__restrict__ denom, int style) {
     const int half = n_rot / 2;
     const int tid = blockIdx.x * blockDim.x + threadIdx.x;
     const int per_head = hd - half;  // pairs + untouched tail entries
@@ -58,8 +58,7 @@ __global__ void rope_kernel(const float *__restrict__ src, float *__restrict__ d
     float *d = dst + (size_t)h * hd;
     if (i < half) {
         const int a = style == 0 ? 2 * i : i, b = style == 0 ? 2 * i + 1 : i + half;
-        const float e = (float)(2 * i) / (float)n_rot;
-        const float theta = pos / powf(base, e);
+        const float theta = pos / denom[i];
         const float c = cosf(theta), sn = sinf(theta);
         const float x0 = s[a], x1 = s[b];
         d[a] = fmaf(x0, c, -x1 * sn);
@@ -251,13 +250,13 @@ hipError_t launch_rms_norm_per_head(const float *x, const float *w, float *out, 
                        x, w, out, hd, eps, off);
     return hipGetLastError();
 }
-hipError_t launch_rope(const float *src, float *dst, int heads, int hd, int rope_dim, int pos, float base, int style,
-                       hipStream_t s) {
+hipError_t launch_rope(const float *src, float *dst, int heads, int hd, int rope_dim, int pos, const float *denom,
+                       int style, hipStream_t s) {
     const int n_rot = rope_dim < hd ? rope_dim : hd;
     const int per_head = hd - n_rot / 2;
     const int n = heads * per_head;
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(rope_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, src, dst, heads, hd, n_rot, (float)pos, base,
+    hipLaunchKernelGGL(rope_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, src, dst, heads, hd, n_rot, (float)pos, denom,
                        style);
     return hipGetLastError();
 }

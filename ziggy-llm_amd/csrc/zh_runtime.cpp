@@ -69,6 +69,47 @@ int check_matvec(ZiggyHipContext *ctx, uint32_t type, const ZiggyHipBuffer *m, s
 
 namespace zh {
 
+hipError_t ctx_rope_denom(ZiggyHipContext *ctx, float base, int n_rot, const float **out) {
+    for (auto &t : ctx->rope_tables)
+        if (t.dev && t.base == base && t.n_rot == n_rot) {
+            *out = t.dev;
+            return hipSuccess;
+        }
+    // a new (base, n_rot): a table of its own (never overwritten, so launches
+    // still queued on the stream keep reading theirs); the oldest is replaced
+    // once eight are held, after the stream drains
+    ZiggyHipContext::RopeTable *slot = nullptr;
+    for (auto &t : ctx->rope_tables)
+        if (!t.dev) {
+            slot = &t;
+            break;
+        }
+    if (!slot) {
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return e;
+        slot = &ctx->rope_tables[0];
+        hipFree(slot->dev);
+        for (int i = 0; i + 1 < 8; i++) ctx->rope_tables[i] = ctx->rope_tables[i + 1];
+        slot = &ctx->rope_tables[7];
+        slot->dev = nullptr;
+    }
+    float host[128];
+    const int half = n_rot / 2 > 0 ? n_rot / 2 : 1;
+    if (half > 128) return hipErrorInvalidValue;
+    rope_denominators(base, n_rot, host);
+    float *dev = nullptr;
+    hipError_t e = hipMalloc((void **)&dev, (size_t)half * 4);
+    if (e != hipSuccess) return e;
+    e = hipMemcpy(dev, host, (size_t)half * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        hipFree(dev);
+        return e;
+    }
+    *slot = {base, n_rot, dev};
+    *out = dev;
+    return hipSuccess;
+}
+
 int attention_call_params(const ZiggyHipBuffer *q, const ZiggyHipBuffer *kc, const ZiggyHipBuffer *vc,
                           const ZiggyHipBuffer *out, uint32_t heads, uint32_t heads_kv, uint32_t hd, uint32_t kv_dim,
                           uint32_t ctx_len, uint32_t pos, uint32_t layer_base, uint32_t window_start, float scale,
@@ -172,6 +213,8 @@ void ziggy_hip_destroy_context(ZiggyHipContext *ctx) {
     if (!ctx) return;
     hipSetDevice(ctx->device);
     if (ctx->stream) hipStreamSynchronize(ctx->stream);
+    for (auto &t : ctx->rope_tables)
+        if (t.dev) hipFree(t.dev);
     if (ctx->scratch) hipFree(ctx->scratch);
     if (ctx->counters) hipFree(ctx->counters);
     if (ctx->seq_begin) hipEventDestroy(ctx->seq_begin);
@@ -549,8 +592,10 @@ static int rope_common(ZiggyHipContext *ctx, const ZiggyHipBuffer *src, size_t s
         set_err(err, err_len, "invalid rope arguments");
         return ZIGGY_HIP_INVALID_ARGUMENT;
     }
+    const float *denom = nullptr;
+    ZH_TRY(ctx_rope_denom(ctx, base, (int)(rope_dim < hd ? rope_dim : hd), &denom), "rope table");
     ZH_TRY(launch_rope((const float *)((const char *)src->ptr + soff), (float *)((char *)dst->ptr + doff), (int)heads,
-                       (int)hd, (int)rope_dim, (int)pos, base, (int)style, ctx->stream),
+                       (int)hd, (int)rope_dim, (int)pos, denom, (int)style, ctx->stream),
            "apply_rope");
     return finish_op(ctx, "apply_rope", err, err_len);
 }

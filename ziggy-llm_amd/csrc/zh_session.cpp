@@ -50,6 +50,7 @@ struct ZiggyHipSession {
     int q_size = 0, kv_size = 0, max_splits = 0;
     float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *act = nullptr;
     float *logits = nullptr, *part_o = nullptr, *part_ml = nullptr;
+    float *rope_denom = nullptr;  // [rope_dim / 2] RoPE denominators from the host's powf
     unsigned *counters = nullptr;  // attention arrival counters (zero between launches)
     __half *kc = nullptr, *vc = nullptr;
     StepState *st = nullptr;
@@ -150,6 +151,7 @@ hipError_t enqueue_kernel(ZiggyHipSession *s, int id, int l, const int *pos_dev,
         a.max_splits = s->max_splits;
         a.eps = md.rms_norm_eps;
         a.rope_base = md.rope_freq_base;
+        a.rope_denom = s->rope_denom;
         a.rope_dim = (int)md.rope_dim;
         a.rope_style = (int)md.rope_style;
         a.ctx = (int)md.context_length;
@@ -396,6 +398,7 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
         {(void **)&s->attn, Q * 4}, {(void **)&s->act, F * 4}, {(void **)&s->logits, logits_len * 4},
         {(void **)&s->part_o, attn_scratch * 4}, {(void **)&s->kc, cache_elems * 2}, {(void **)&s->vc, cache_elems * 2},
         {(void **)&s->st, sizeof(StepState)}, {(void **)&s->counters, md.head_count_kv * sizeof(unsigned)},
+        {(void **)&s->rope_denom, 4 * (size_t)(md.head_dim / 2 + 1)},
     };
     for (auto &r : reqs) {
         e = hipMalloc(r.p, r.bytes);
@@ -407,6 +410,17 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
         s->allocs.push_back(*r.p);
     }
     s->part_ml = s->part_o + (size_t)md.head_count * s->max_splits * 8 * md.head_dim;
+    {
+        const int n_rot = (int)(md.rope_dim < md.head_dim ? md.rope_dim : md.head_dim);
+        std::vector<float> den((size_t)md.head_dim / 2 + 1, 1.0f);
+        rope_denominators(md.rope_freq_base, n_rot, den.data());
+        e = hipMemcpyAsync(s->rope_denom, den.data(), den.size() * 4, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            free_session(s);
+            return hip_fail(e, "rope table upload", err, err_len);
+        }
+    }
     e = hipHostMalloc((void **)&s->st_host, sizeof(StepState), hipHostMallocDefault);
     if (e != hipSuccess) {
         free_session(s);
@@ -535,6 +549,35 @@ int ziggy_hip_session_read_kv(ZiggyHipSession *s, uint32_t layer, uint32_t pos, 
     return ZIGGY_HIP_OK;
 }
 
+int ziggy_hip_session_fill_kv_pattern(ZiggyHipSession *s, uint32_t position, uint64_t seed, char *err,
+                                      size_t err_len) {
+    if (!s) return ZIGGY_HIP_INVALID_ARGUMENT;
+    if (position > s->md.context_length) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "context overflow");
+    const size_t n = (size_t)position * s->kv_size;
+    std::vector<__half> kb(n ? n : 1), vb(n ? n : 1);
+    uint64_t x = seed * 0x9E3779B97F4A7C15ull + 1;
+    for (uint32_t l = 0; l < s->md.block_count; l++) {
+        for (size_t i = 0; i < n; i++) {
+            x ^= x << 13;
+            x ^= x >> 7;
+            x ^= x << 17;
+            const float v = (float)((int)(x >> 40 & 0x7FF) - 1024) * (1.0f / 1024.0f);
+            kb[i] = __float2half(v);
+            vb[i] = __float2half(-v);
+        }
+        const size_t base = (size_t)l * s->md.context_length * s->kv_size;
+        if (n) {
+            ZH_TRY(hipMemcpy(s->kc + base, kb.data(), n * 2, hipMemcpyHostToDevice), "fill_kv_pattern");
+            ZH_TRY(hipMemcpy(s->vc + base, vb.data(), n * 2, hipMemcpyHostToDevice), "fill_kv_pattern");
+        }
+    }
+    s->position = position;
+    s->fed.clear();
+    s->fed_ok = false;  // rows not written by token steps: nothing to reuse
+    s->logits_valid = false;
+    return ZIGGY_HIP_OK;
+}
+
 int ziggy_hip_session_read_logits(ZiggyHipSession *s, float *out, char *err, size_t err_len) {
     if (!s || !out) return ZIGGY_HIP_INVALID_ARGUMENT;
     if (!s->logits_valid) return fail(err, err_len, ZIGGY_HIP_EXECUTION_FAILED, "no logits computed yet");
@@ -587,17 +630,17 @@ int ziggy_hip_session_prefill_cached(ZiggyHipSession *s, const uint32_t *prompt,
     if (prompt_len > s->md.context_length) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "context overflow");
     // commonPrefixLen of the cached tokens and the prompt (model/loader.zig:2310-2313); the
     // last prompt token is always fed again, for its logits
-    uint32_t common = 0;
+    uint32_t matched = 0;
     if (s->fed_ok && s->fed.size() == s->position)
-        while (common < s->position && common < prompt_len && s->fed[common] == prompt[common]) common++;
-    if (common >= prompt_len) common = prompt_len - 1;
+        while (matched < s->position && matched < prompt_len && s->fed[matched] == prompt[matched]) matched++;
+    const uint32_t common = matched >= prompt_len ? prompt_len - 1 : matched;
     s->position = common;
     s->fed.resize(common);
     if (common == 0) s->fed_ok = true;  // every row from here on comes from token steps
     ZiggyHipGenerateStats st{};
     const int r = ziggy_hip_session_generate(s, prompt + common, prompt_len - common, 0, nullptr, &st, err, err_len);
     if (r != ZIGGY_HIP_OK) return r;
-    *out_reused = common;
+    *out_reused = matched;  // commonPrefixLen, as the reference reports it (reused_prompt_token_count)
     *out_next = st.next_token;
     return ZIGGY_HIP_OK;
 }
@@ -625,6 +668,26 @@ int ziggy_hip_session_step_shortlist(ZiggyHipSession *s, uint32_t token, uint32_
     s->logits_valid = true;
     return ZIGGY_HIP_OK;
 }
+
+}  // extern "C"
+
+static hipError_t pass_alloc(ZiggyHipSession *s);
+static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M, int pos, bool output,
+                               hipStream_t st);
+constexpr uint32_t kPrefillChunk = 64;  // prompt rows per batched pass (the pass buffers' row count)
+
+// Prompt rows go through batched passes on the matrix cores unless the head
+// size lacks the multi-query attention or ZIGGY_HIP_PREFILL=steps asks for
+// the token-by-token path.
+static bool prefill_batched(const ZiggyHipSession *s) {
+    static const bool steps = [] {
+        const char *e = getenv("ZIGGY_HIP_PREFILL");
+        return e && strcmp(e, "steps") == 0;
+    }();
+    return !steps && attention_multi_supported((int)s->md.head_dim);
+}
+
+extern "C" {
 
 int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint32_t prompt_len, uint32_t steps,
                                uint32_t *out_tokens, ZiggyHipGenerateStats *stats, char *err, size_t err_len) {
@@ -663,17 +726,31 @@ int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint3
     int bst = build_graph(s, err, err_len);
     if (bst) return bst;
     ZH_TRY(hipMemcpyAsync(s->prompt, prompt, (size_t)prompt_len * 4, hipMemcpyHostToDevice, st), "prompt upload");
+    // every prompt row but the last in batched passes of up to kPrefillChunk
+    // tokens (GEMMs on the matrix cores, multi-query causal attention), the
+    // last one through the step graph for its logits; the reference feeds
+    // the prompt token by token (runPrompt, model/loader.zig:1016-1036)
+    const bool batched = prompt_len > 1 && prefill_batched(s);
+    const uint32_t n_batched = batched ? prompt_len - 1 : 0;
+    if (batched) ZH_TRY(pass_alloc(s), "prefill buffers");
     StepState *h = s->st_host;
     memset(h, 0, sizeof(*h));
     h->mode = 1;
     h->base_pos = (int)s->position;
+    h->step = (int)n_batched;  // the graph's first step takes prompt[n_batched]
     h->n_prompt = (int)prompt_len;
     h->n_gen = (int)steps;
     ZH_TRY(hipMemcpyAsync(s->st, h, sizeof(StepState), hipMemcpyHostToDevice, st), "step state");
     ZH_TRY(hipStreamSynchronize(st), "generate setup");
+    const uint64_t tp0 = now_ns();
+    for (uint32_t off = 0; off < n_batched; off += kPrefillChunk) {
+        const uint32_t m = std::min(kPrefillChunk, n_batched - off);
+        ZH_TRY(pass_enqueue(s, s->prompt + off, (int)m, (int)(s->position + off), false, st), "prefill pass");
+    }
     // prompt steps, then the timed decode steps (the decode_ns bracket of model/loader.zig:2135-2257)
-    for (uint32_t i = 0; i < prompt_len; i++) ZH_TRY(launch_step(s, st), "prompt step");
+    for (uint32_t i = n_batched; i < prompt_len; i++) ZH_TRY(launch_step(s, st), "prompt step");
     ZH_TRY(hipStreamSynchronize(st), "prompt");
+    const uint64_t tp1 = now_ns();
     ZH_TRY(hipEventRecord(s->ctx->seq_begin, st), "generate");
     const uint64_t t0 = now_ns();
     for (uint32_t i = 0; i < steps; i++) ZH_TRY(launch_step(s, st), "decode step");
@@ -696,6 +773,7 @@ int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint3
         stats->gpu_elapsed_ns = (uint64_t)((double)ms * 1e6);
         stats->wall_ns = t1 - t0;
         stats->next_token = 0xFFFFFFFFu - (uint32_t)(h->argmax & 0xFFFFFFFFull);
+        stats->prompt_ns = tp1 - tp0;
     }
     return ZIGGY_HIP_OK;
 }
@@ -703,18 +781,21 @@ int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint3
 // ---- speculative verify: a batch of tokens in one pass ----
 
 constexpr uint32_t kVerifyMax = 16;  // tokens of one verify pass (one MFMA token tile)
+constexpr uint32_t kPassMax = kPrefillChunk;  // token rows of one batched pass
+static_assert(kPassMax >= kVerifyMax, "a verify pass fits the pass buffers");
 
-static hipError_t verify_alloc(ZiggyHipSession *s) {
+// Row buffers of the batched passes (verify, prompt chunks), allocated on first use.
+static hipError_t pass_alloc(ZiggyHipSession *s) {
     if (s->b_hidden) return hipSuccess;
     const size_t H = s->md.embedding_length, F = s->md.feed_forward_length, Q = (size_t)s->q_size,
-                 KV = (size_t)s->kv_size, M = kVerifyMax;
+                 KV = (size_t)s->kv_size, M = kPassMax;
     struct {
         void **p;
         size_t bytes;
     } reqs[] = {{(void **)&s->b_hidden, M * H * 4}, {(void **)&s->b_normed, M * H * 4}, {(void **)&s->b_q, M * Q * 4},
                 {(void **)&s->b_k, M * KV * 4},      {(void **)&s->b_v, M * KV * 4},      {(void **)&s->b_attn, M * Q * 4},
                 {(void **)&s->b_act, M * F * 4},     {(void **)&s->b_up, M * F * 4},      {(void **)&s->b_tokens, M * 4},
-                {(void **)&s->b_argmax, M * 8},     {(void **)&s->b_logits, M * s->md.vocab_size * 4}};
+                {(void **)&s->b_argmax, M * 8},     {(void **)&s->b_logits, kVerifyMax * s->md.vocab_size * 4}};
     for (auto &r : reqs) {
         hipError_t e = hipMalloc(r.p, r.bytes);
         if (e != hipSuccess) return e;
@@ -754,12 +835,13 @@ static bool verify_fused_swiglu() {
     return f;
 }
 
-static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t st) {
+static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M, int pos, bool output,
+                               hipStream_t st) {
     const ZiggyHipModelDesc &md = s->md;
     const bool fused_swiglu = verify_fused_swiglu();
     const int H = (int)md.embedding_length, F = (int)md.feed_forward_length, Q = s->q_size, KV = s->kv_size;
     const float eps = md.rms_norm_eps;
-    hipError_t e = launch_embed_rows(s->b_tokens, M, s->embd.p, s->embd.stride, (int)s->embd.rows, s->embd.type, H,
+    hipError_t e = launch_embed_rows(tokens, M, s->embd.p, s->embd.stride, (int)s->embd.rows, s->embd.type, H,
                                      s->b_hidden, st);
     auto gemm = [&](const DT &w, const DT *w2, const float *x, int ldx, float *y, int ldy, int out) {
         if (e != hipSuccess) return;
@@ -813,6 +895,7 @@ static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t
             a.position = pos;
             a.eps = eps;
             a.rope_base = md.rope_freq_base;
+            a.rope_denom = s->rope_denom;
             a.rope_dim = (int)md.rope_dim;
             a.rope_style = (int)md.rope_style;
             a.ctx = (int)md.context_length;
@@ -857,6 +940,7 @@ static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t
             a.max_splits = s->max_splits;
             a.eps = eps;
             a.rope_base = md.rope_freq_base;
+            a.rope_denom = s->rope_denom;
             a.rope_dim = (int)md.rope_dim;
             a.rope_style = (int)md.rope_style;
             a.ctx = (int)md.context_length;
@@ -878,6 +962,7 @@ static hipError_t verify_enqueue(ZiggyHipSession *s, int M, int pos, hipStream_t
         }
         gemm(L.down, nullptr, s->b_act, F, s->b_hidden, H, OUT_ADD);
     }
+    if (!output) return e;  // a prompt chunk: K/V rows only
     // the final norm also clears the argmax keys; the output product stores
     // the logits (its reduction may split), then a per-token argmax
     if (e == hipSuccess)
@@ -902,9 +987,9 @@ int ziggy_hip_session_verify(ZiggyHipSession *s, uint32_t current_token, const u
     for (uint32_t i = 0; i < M; i++)
         if (toks[i] >= s->embd.rows) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "token id out of range");
     hipStream_t st = s->ctx->stream;
-    ZH_TRY(verify_alloc(s), "verify buffers");
+    ZH_TRY(pass_alloc(s), "verify buffers");
     ZH_TRY(hipMemcpyAsync(s->b_tokens, toks, M * 4, hipMemcpyHostToDevice, st), "verify tokens");
-    ZH_TRY(verify_enqueue(s, (int)M, (int)s->position, st), "verify");
+    ZH_TRY(pass_enqueue(s, s->b_tokens, (int)M, (int)s->position, true, st), "verify");
     unsigned long long keys[kVerifyMax];
     ZH_TRY(hipMemcpyAsync(keys, s->b_argmax, M * 8, hipMemcpyDeviceToHost, st), "verify readback");
     ZH_TRY(hipStreamSynchronize(st), "verify");

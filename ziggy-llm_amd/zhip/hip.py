@@ -60,7 +60,7 @@ class ModelDesc(ctypes.Structure):
 
 class GenerateStats(ctypes.Structure):
     _fields_ = [("steps", ctypes.c_uint64), ("gpu_elapsed_ns", ctypes.c_uint64), ("wall_ns", ctypes.c_uint64),
-                ("next_token", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+                ("next_token", ctypes.c_uint32), ("reserved", ctypes.c_uint32), ("prompt_ns", ctypes.c_uint64)]
 
 
 MOE_LAYER_FIELDS = ["ffn_norm", "router", "gate_exps", "up_exps", "down_exps", "gate_shexp", "up_shexp",
@@ -155,6 +155,7 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_session_read_hidden": [vp, vp] + E,
         "ziggy_hip_session_write_hidden": [vp, vp] + E,
         "ziggy_hip_session_read_kv": [vp, u32, u32, vp, vp] + E,
+        "ziggy_hip_session_fill_kv_pattern": [vp, u32, ctypes.c_uint64] + E,
         "ziggy_hip_session_step_greedy": [vp, u32, ctypes.POINTER(u32)] + E,
         "ziggy_hip_session_step_no_output": [vp, u32] + E,
         "ziggy_hip_session_generate": [vp, vp, u32, u32, vp, ctypes.POINTER(GenerateStats)] + E,
@@ -483,6 +484,10 @@ class Session:
         k, v = np.empty(n, np.float32), np.empty(n, np.float32)
         _call("ziggy_hip_session_read_kv", self.h, layer, pos, k.ctypes.data, v.ctypes.data)
         return k, v
+
+    def fill_kv_pattern(self, position: int, seed: int = 0):
+        """The CPU oracle's deterministic K/V fill of rows [0, position); the position moves there."""
+        _call("ziggy_hip_session_fill_kv_pattern", self.h, position, seed)
 
     # per-layer contract (gpu.Session)
     def begin_token(self, hidden: np.ndarray):
