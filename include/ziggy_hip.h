@@ -430,6 +430,19 @@ int ziggy_hip_session_verify(ZiggyHipSession *session, uint32_t current_token, c
 int ziggy_hip_session_prefill_cached(ZiggyHipSession *session, const uint32_t *prompt, uint32_t prompt_len,
                                      uint32_t *out_reused, uint32_t *out_next, char *error_message,
                                      size_t error_message_len);
+/* Paged KV cache.  The session's binary16 cache is a pool of pages of
+ * ZIGGY_HIP_KV_PAGE_POSITIONS consecutive positions per layer; a block table
+ * maps each logical page (positions 64 p .. 64 p + 63) to a pool page, shared
+ * by every layer.  The reference keeps one contiguous [layer][pos][kv_dim]
+ * cache (runtime/gpu/session.zig:106-111, 382-383); a paged table lets a
+ * cache manager place pages (and is what the bridge-level attention's
+ * layer_base addressing becomes per page).  Pages start in order.
+ * set_block_table replaces the table (a permutation of the session's
+ * kv_pages pages) on an empty cache (position 0). */
+#define ZIGGY_HIP_KV_PAGE_POSITIONS 64
+uint32_t ziggy_hip_session_kv_pages(const ZiggyHipSession *session);
+int ziggy_hip_session_set_block_table(ZiggyHipSession *session, const uint32_t *table, uint32_t count,
+                                      char *error_message, size_t error_message_len);
 /* Test and benchmark hook (no counterpart in the reference's runtime; it
  * mirrors the CPU oracle's fill): writes a deterministic binary16-exact
  * pattern into the K/V rows [0, position) of every layer and moves the

@@ -8,7 +8,8 @@ semantics):
     tests/golden/make_headline_streams.py: the oracle needs minutes for it), and the logits after the
     prompt match a live oracle run: the same argmax, within 2e-3 relative L2;
   * steps at a long position over a cache both sides fill with the same binary16-exact pattern
-    (positions 4096-4097 for Llama, 16383 for Qwen3): the same argmax, logits within 1e-4 relative L2;
+    (positions 4096-4097 for Llama, its paged cache through a shuffled block table; 16383 for Qwen3):
+    the same argmax, logits within 1e-4 relative L2;
   * Qwen3: one batched verify pass of the pending token and 8 drafts (M = 9 GEMMs on the matrix cores)
     predicts the oracle's greedy continuation, after the prompt and over a 2048-row filled cache.
 
@@ -127,10 +128,12 @@ def stream_and_prompt_logits(hip_ctx, m):
     s.close()
 
 
-def long_position_steps(hip_ctx, m, pos, steps):
+def long_position_steps(hip_ctx, m, pos, steps, shuffle=False):
     ctx_len = m.long_context
     o = zo.Session(m.zm, context=ctx_len, kv_f16=True, threads=THREADS)
     s = hip.Session(hip_ctx, m.img, context=ctx_len)
+    if shuffle:  # the paged cache through a random block table
+        s.set_block_table(np.random.default_rng(11).permutation(s.kv_pages).astype(np.uint32))
     o.fill_kv_pattern(pos, seed=5)
     s.fill_kv_pattern(pos, seed=5)
     tok = int(m.prompt[0])
@@ -158,7 +161,7 @@ def test_llama8b_stream_64_and_logits(hip_ctx, llama8b):
 
 
 def test_llama8b_steps_at_position_4096(hip_ctx, llama8b):
-    long_position_steps(hip_ctx, llama8b, 4096, 2)
+    long_position_steps(hip_ctx, llama8b, 4096, 2, shuffle=True)
 
 
 def test_qwen3_stream_64_and_logits(hip_ctx, qwen3):

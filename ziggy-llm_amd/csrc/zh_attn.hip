@@ -42,6 +42,20 @@ __device__ __forceinline__ float wsum(float v) {
 // RoPE angles of one position, once per workgroup: cs[i], sn[i] for pair i
 // of the n_rot rotated dims, theta = pos / base^(2i / n_rot) (applyRoPE,
 // model/loader.zig:3827-3866).
+// Cache row of position t, through the page table (a page is 1 << page_shift
+// consecutive positions in consecutive rows; a contiguous cache passes the
+// identity table).
+// The table is read through the constant address space: with a uniform t
+// that is a scalar load, whose wait does not cover the vector loads in flight
+// (a vector load's wait would, vmcnt completing in order).
+typedef const __attribute__((address_space(4))) uint32_t *const_u32_ptr;
+// Pages hold 1 << kKvPageShift positions (the launcher checks page_shift).
+__device__ __forceinline__ size_t kv_row(const AttnParams &p, int t) {
+    constexpr int m = (1 << kKvPageShift) - 1;
+    const uint32_t page = ((const_u32_ptr)p.page_table)[t >> kKvPageShift];
+    return ((size_t)page << kKvPageShift) + (size_t)(t & m);
+}
+
 // This thread's RoPE denominator base^(2t / n_rot) (t = threadIdx.x < n_rot / 2): the host's table when
 // given, read early so that its wait does not cover the K/V loads issued after it.
 __device__ __forceinline__ float rope_den(int n_rot, float base, const float *denom) {
@@ -345,7 +359,7 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnParams p) {
     }
     __builtin_amdgcn_sched_barrier(0);
     uint4 kr[NP][2], vr[NP][2];
-    auto row_off = [&](int i) { return (size_t)min(pos_of(min(i, npass - 1)), pos) * p.kv_dim + kv_off + 16 * sub; };
+    auto row_off = [&](int i) { return kv_row(p, min(pos_of(min(i, npass - 1)), pos)) * p.kv_dim + kv_off + 16 * sub; };
     auto load_k = [&](int i, uint4 (&k)[2]) {
         const uint4 *kp = reinterpret_cast<const uint4 *>(p.k_cache + row_off(i));
         k[0] = kp[0];
@@ -377,7 +391,7 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnParams p) {
             if (tid < HD) {
                 const __half kh = __float2half_rn(kn_s[tid]), vh = __float2half_rn(vx);
                 if (pos < p.ctx) {
-                    const size_t idx = (size_t)pos * p.kv_dim + kv_off + tid;
+                    const size_t idx = kv_row(p, pos) * p.kv_dim + kv_off + tid;
                     p.k_cache[idx] = kh;
                     p.v_cache[idx] = vh;
                 }
@@ -672,6 +686,22 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     __shared__ float fm_s[VG], fl_s[VG];
     __shared__ int last_s;
 
+    // the wavefront index as a scalar: tile positions, and the page-table
+    // reads below, are uniform, so the reads are scalar loads whose waits do
+    // not cover the vector loads in flight
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    auto p0_of = [&](int t) { return p.window_start + (u_begin + wv + 4 * t) * TP; };
+    // a tile's 32 positions lie in one page (tiles start at multiples of 32 and
+    // pages hold 64 or more): one table read per tile, rows of the page after
+    // it.  A tile past pos (its rows all clamp to pos) reads pos's entry, so
+    // the table is never read past the context.
+    auto tile_row = [&](int b) {
+        const int bb = min(b, pos);
+        return (long long)kv_row(p, bb) - bb;
+    };
+    // the first two tiles' pages, read before the q loads are issued: their
+    // scalar loads overlap that issue, and the K loads wait only for them
+    const long long tb_first[2] = {tile_row(p0_of(0)), tile_row(p0_of(1))};
     const size_t kv_off = (size_t)kvh * HD;
     constexpr int QV = VG * HD / 256;
     const int nq = G * HD;
@@ -716,12 +746,12 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     // (row p0 + 16 rt + li, dims 32 ks + 8 lg .. + 7), V fragments [row e]
     // (rows 4 lg + e and 16 + 4 lg + e - 4, dims 8 li .. 8 li + 7).  Rows
     // past pos re-read row pos (masked below).
-    auto p0_of = [&](int t) { return p.window_start + (u_begin + wave + 4 * t) * TP; };
     auto load_k = [&](int t, uint4 (&k)[2][KS]) {
         const int b = p0_of(t);
+        const long long tb = t < 2 ? tb_first[t] : tile_row(b);
 #pragma unroll
         for (int rt = 0; rt < 2; rt++) {
-            const __half *src = p.k_cache + (size_t)min(b + 16 * rt + li, pos) * p.kv_dim + kv_off + 8 * lg;
+            const __half *src = p.k_cache + (size_t)(tb + min(b + 16 * rt + li, pos)) * p.kv_dim + kv_off + 8 * lg;
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) k[rt][ks] = *reinterpret_cast<const uint4 *>(src + 32 * ks);
         }
@@ -729,10 +759,11 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     auto vrow = [&](int e) { return e < 4 ? 4 * lg + e : 12 + 4 * lg + e; };
     auto load_v = [&](int t, uint4 (&v)[8]) {
         const int b = p0_of(t);
+        const long long tb = t < 2 ? tb_first[t] : tile_row(b);
 #pragma unroll
         for (int e = 0; e < 8; e++)
-            v[e] = *reinterpret_cast<const uint4 *>(p.v_cache + (size_t)min(b + vrow(e), pos) * p.kv_dim + kv_off +
-                                                    8 * (li % LPR));
+            v[e] = *reinterpret_cast<const uint4 *>(p.v_cache + (size_t)(tb + min(b + vrow(e), pos)) * p.kv_dim +
+                                                    kv_off + 8 * (li % LPR));
     };
     // Unconditional (clamped) loads: a load under a branch leaves the
     // compiler's wait counting unsure of what is in flight, and the first
@@ -754,7 +785,7 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
             if (tid < HD) {
                 const __half kh = __float2half_rn(kn_s[tid]), vh = __float2half_rn(vx);
                 if (pos < p.ctx) {
-                    const size_t idx = (size_t)pos * p.kv_dim + kv_off + tid;
+                    const size_t idx = kv_row(p, pos) * p.kv_dim + kv_off + tid;
                     p.k_cache[idx] = kh;
                     p.v_cache[idx] = vh;
                 }
@@ -1080,13 +1111,14 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(AttnParams p, float *q_o
     float *qo = q_out + (size_t)m * p.q_stride + (size_t)kvh * nq;
     for (int idx = tid; idx < nq; idx += 256) qo[idx] = q_s[idx];
     if (tid < HD && pos < p.ctx) {
-        const size_t idx = (size_t)pos * p.kv_dim + (size_t)kvh * HD + tid;
+        const size_t idx = kv_row(p, pos) * p.kv_dim + (size_t)kvh * HD + tid;
         p.k_cache[idx] = __float2half_rn(kn_s[tid]);
         p.v_cache[idx] = __float2half_rn(vx);
     }
 }
 
 hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t s) {
+    if (!p.page_table || p.page_shift != kKvPageShift) return hipErrorInvalidValue;
     if (p.head_count_kv <= 0 || p.head_count % p.head_count_kv || p.head_count / p.head_count_kv > kMaxGroup ||
         p.n_query < 1 || !p.q || !p.k_new || !p.v_new || !q_out || p.q_stride < p.head_count * p.head_dim)
         return hipErrorInvalidValue;
@@ -1111,6 +1143,9 @@ int attention_query_groups(int head_count, int head_count_kv, int n_query) {
 hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
     if (p.head_count_kv <= 0 || p.head_count % p.head_count_kv || p.head_count / p.head_count_kv > kMaxGroup ||
         p.max_splits < 1 || !p.counters)
+        return hipErrorInvalidValue;
+    // pages of kKvPageShift (two 32-position tiles), the window on a page boundary
+    if (!p.page_table || p.page_shift != kKvPageShift || (p.window_start & ((1 << kKvPageShift) - 1)))
         return hipErrorInvalidValue;
     const int G = p.head_count / p.head_count_kv;
     if (p.n_query > 1) {

@@ -229,10 +229,10 @@ template <int F> static GemmKernel pick_precise(int out) {
 
 hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
-                       bool precise) {
+                       bool precise, int max_split) {
     if (M < 1 || N < 1 || K < 16 || K % 16 || ldx % 4) return hipErrorInvalidValue;
     if (!precise && qgemm_enabled() && qgemm_supported(fmt, K, w, w2, stride, 0))
-        return launch_qgemm(fmt, w, w2, stride, x, ldx, y, ldy, M, N, K, out, argmax, s);
+        return launch_qgemm(fmt, w, w2, stride, x, ldx, y, ldy, M, N, K, out, argmax, s, max_split);
     GemmKernel k = nullptr;
     if (precise) {
         switch (fmt) {
@@ -267,11 +267,12 @@ hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t st
 
 hipError_t launch_gemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
                              const int *N, uint64_t stride, const float *x, int ldx, int M, int K, int out,
-                             hipStream_t s) {
+                             hipStream_t s, int max_split) {
     if (nseg < 1 || nseg > 3 || (out != OUT_STORE && out != OUT_ADD)) return hipErrorInvalidValue;
     bool one = qgemm_enabled();
     for (int i = 0; i < nseg && one; i++) one = qgemm_supported(fmt, K, w[i], nullptr, stride, 0);
-    if (one) return launch_qgemm_multi(fmt, nseg, w, y, ldy, N, nullptr, stride, x, ldx, M, K, out, nullptr, s);
+    if (one)
+        return launch_qgemm_multi(fmt, nseg, w, y, ldy, N, nullptr, stride, x, ldx, M, K, out, nullptr, s, max_split);
     for (int i = 0; i < nseg; i++) {
         const hipError_t e = launch_gemm(fmt, w[i], nullptr, stride, x, ldx, y[i], ldy[i], M, N[i], K, out, nullptr, s);
         if (e != hipSuccess) return e;

@@ -25,6 +25,8 @@ struct ZiggyHipContext {
     size_t scratch_len = 0;
     // zeroed arrival counters of the attention kernel (each launch leaves them zero)
     unsigned *counters = nullptr;
+    // identity block table (kIdentityPages entries): the bridge-level attention's contiguous cache
+    uint32_t *identity_pages = nullptr;
     // RoPE denominators base^(2i / n_rot) per (base, n_rot) seen, computed on the host
     struct RopeTable {
         float base;
@@ -256,15 +258,18 @@ hipError_t launch_argmax_rows(const float *x, int rows, int n, int ld, unsigned 
 
 // MFMA GEMM for M >= 8 tokens (zh_gemm.hip): Y[m][n] (=, +=) sum_k W[n][k] X[m][k]
 // (OUT_STORE / OUT_ADD / OUT_SWIGLU with w2 / OUT_ARGMAX into argmax[M]).
+// max_split bounds the reduction split of the exact-code kernel, whose
+// partial results add atomically: 1 keeps a += product deterministic, 2 a
+// product into a cleared output (0 + a + b is the same in either order).
 hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
-                       bool precise = false);
+                       bool precise = false, int max_split = 16);
 // Up to three matrices of one format, row stride and reduction length against
 // one input (stores or adds): one launch on the exact-code kernel, else one
 // product each.
 hipError_t launch_gemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
                              const int *N, uint64_t stride, const float *x, int ldx, int M, int K, int out,
-                             hipStream_t s);
+                             hipStream_t s, int max_split = 16);
 hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps, hipStream_t s,
                                 float *clear0 = nullptr, size_t n0 = 0, float *clear1 = nullptr, size_t n1 = 0,
                                 float *clear2 = nullptr, size_t n2 = 0);
@@ -276,12 +281,13 @@ hipError_t launch_gemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uin
 // Exact-code MFMA kernel (zh_qgemm.hip) for the quantized formats, K a multiple of 256.
 bool qgemm_supported(int fmt, int K, const void *w, const void *w2, uint64_t stride, uint64_t expert_stride);
 hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
-                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s);
+                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
+                        int max_split = 16);
 // Up to three matrices of one format, row stride and reduction length against
 // one input in one launch (matrix i: rows N[i], output y[i] with row stride ldy[i]).
 hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
                               const int *N, const uint8_t *w2, uint64_t stride, const float *x, int ldx, int M, int K,
-                              int out, unsigned long long *argmax, hipStream_t s);
+                              int out, unsigned long long *argmax, hipStream_t s, int max_split = 16);
 hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride,
                                 uint64_t expert_stride, const float *x, int ldx, int x_div, float *y, int ldy, int N,
                                 int K, int out, const int *tiles, const int *list, const int *ntiles, int max_tiles,
@@ -301,8 +307,12 @@ hipError_t launch_moe_combine(float *hidden, const float *tmp, const uint32_t *r
 // attention (zh_attn.hip)
 struct AttnParams {
     const float *q;            // [head_count * head_dim]: raw projection (fused) or roped q (plain)
-    __half *k_cache;           // layer base applied: [ctx][kv_dim]
+    __half *k_cache;           // layer base applied: [rows][kv_dim], row = kv_row(position)
     __half *v_cache;
+    // paged cache: position t lives in row (page_table[t >> page_shift] << page_shift) + (t & page mask);
+    // a contiguous cache passes an identity table (kIdentityPages entries per context)
+    const uint32_t *page_table;
+    int page_shift;
     float *out;                // [head_count * head_dim]
     float *part_o;             // [kv_heads][max_splits][8][head_dim]
     float *part_ml;            // [kv_heads][max_splits][8][2]
@@ -326,6 +336,9 @@ struct AttnParams {
     int n_query, q_stride, out_stride;
 };
 hipError_t launch_attention(const AttnParams &p, hipStream_t s);
+constexpr int kKvPageShift = 6;  // a session's KV page: 64 positions (two 32-position attention tiles)
+constexpr int kIdentityPages = 65536;  // a context's identity table: contiguous caches of up to 4M positions
+hipError_t launch_iota_u32(uint32_t *p, int n, hipStream_t s);
 // q/k/v epilogue of n_query tokens (rows q_stride / kv_dim apart): roped q to
 // q_out (may be q), k and v stored to the cache at position + m.
 hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t s);

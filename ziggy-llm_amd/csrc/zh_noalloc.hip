@@ -89,6 +89,8 @@ extern "C" int ziggy_hip_attention_fused_f32_noalloc(ZiggyHipContext *ctx, const
         set_err(err, err_len, "static scratch not resolved on device %d", ctx->device);
         return ZIGGY_HIP_INITIALIZATION_FAILED;
     }
+    p.page_table = ctx->identity_pages;  // made at context creation: nothing allocated here
+    p.page_shift = kKvPageShift;
     p.counters = reinterpret_cast<unsigned *>(base);
     p.part_o = reinterpret_cast<float *>(base + kCounterBytes);
     p.part_ml = reinterpret_cast<float *>(base + kCounterBytes + part_o_bytes);

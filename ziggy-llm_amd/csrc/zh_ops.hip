@@ -147,6 +147,11 @@ __global__ void argmax_finalize_kernel(const unsigned long long *slot, uint32_t 
     }
 }
 
+__global__ void iota_u32_kernel(uint32_t *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = (uint32_t)i;
+}
+
 __global__ void fill_u64_kernel(unsigned long long *p, unsigned long long v, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -273,6 +278,10 @@ hipError_t launch_silu_mul(float *gate, const float *up, int n, hipStream_t s) {
 hipError_t launch_add(float *dst, const float *src, int n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(add_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, dst, src, n);
+    return hipGetLastError();
+}
+hipError_t launch_iota_u32(uint32_t *p, int n, hipStream_t s) {
+    hipLaunchKernelGGL(iota_u32_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, p, n);
     return hipGetLastError();
 }
 hipError_t launch_fill_u64(unsigned long long *p, unsigned long long v, int n, hipStream_t s) {

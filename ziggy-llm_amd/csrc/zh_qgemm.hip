@@ -731,7 +731,7 @@ static double qgemm_stage_weight() {
 
 hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
                               const int *N, const uint8_t *w2, uint64_t stride, const float *x, int ldx, int M, int K,
-                              int out, unsigned long long *argmax, hipStream_t s) {
+                              int out, unsigned long long *argmax, hipStream_t s, int max_split) {
     if (nseg < 1 || nseg > 3 || M < 1 || ldx % 4 || (nseg > 1 && (out == OUT_SWIGLU || out == OUT_ARGMAX)))
         return hipErrorInvalidValue;
     QGemmParams p{w[0], w2, stride, x, y[0], M, N[0], K, ldx, ldy[0], argmax, nullptr, nullptr, nullptr, 1, 0, 1};
@@ -760,7 +760,7 @@ hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float 
     int ks = 0, pg = groups;
     double best = 0.0;
     const bool can_split = out == OUT_STORE || out == OUT_ADD;
-    for (int k = 1; k <= chunks && (k == 1 || can_split); k *= 2) {
+    for (int k = 1; k <= chunks && k <= max_split && (k == 1 || can_split); k *= 2) {
         if (chunks % k) break;
         const int nspan = chunks / k;
         if (nspan > stage || (k > 1 && nspan < 2)) continue;
@@ -773,7 +773,7 @@ hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float 
         // several stages: one group per workgroup, split while row groups leave CUs idle
         ks = 1, pg = groups;
         if (can_split)
-            while (groups * tiles * ks * 2 <= target && chunks % (ks * 2) == 0) ks *= 2;
+            while (groups * tiles * ks * 2 <= target && chunks % (ks * 2) == 0 && ks * 2 <= max_split) ks *= 2;
     }
     p.ksplit = ks;
     QGemmKernel k = pick_qf<false>(fmt, out, K / ks);
@@ -790,8 +790,9 @@ hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float 
 }
 
 hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
-                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s) {
-    return launch_qgemm_multi(fmt, 1, &w, &y, &ldy, &N, w2, stride, x, ldx, M, K, out, argmax, s);
+                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
+                        int max_split) {
+    return launch_qgemm_multi(fmt, 1, &w, &y, &ldy, &N, w2, stride, x, ldx, M, K, out, argmax, s, max_split);
 }
 
 hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride,

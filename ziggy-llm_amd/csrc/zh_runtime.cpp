@@ -115,7 +115,8 @@ int attention_call_params(const ZiggyHipBuffer *q, const ZiggyHipBuffer *kc, con
                           uint32_t ctx_len, uint32_t pos, uint32_t layer_base, uint32_t window_start, float scale,
                           float softcap, AttnParams *p, char *err, size_t err_len) {
     if (heads == 0 || heads_kv == 0 || heads % heads_kv || heads / heads_kv > 8 ||
-        (hd != 64 && hd != 128 && hd != 256) || kv_dim != heads_kv * hd || pos >= ctx_len || window_start > pos) {
+        (hd != 64 && hd != 128 && hd != 256) || kv_dim != heads_kv * hd || pos >= ctx_len || window_start > pos ||
+        (uint64_t)ctx_len > ((uint64_t)kIdentityPages << kKvPageShift) || (window_start & ((1u << kKvPageShift) - 1))) {
         set_err(err, err_len, "unsupported attention shape");
         return ZIGGY_HIP_INVALID_ARGUMENT;
     }
@@ -193,7 +194,10 @@ int ziggy_hip_create_context(int device_index, ZiggyHipContext **out_ctx, ZiggyH
         hipEventCreate(&ctx->seq_begin) != hipSuccess || hipEventCreate(&ctx->seq_end) != hipSuccess ||
         hipMalloc(&ctx->scratch, kCtxScratch) != hipSuccess ||
         hipMalloc((void **)&ctx->counters, kCtxCounters * sizeof(unsigned)) != hipSuccess ||
-        hipMemset(ctx->counters, 0, kCtxCounters * sizeof(unsigned)) != hipSuccess) {
+        hipMemset(ctx->counters, 0, kCtxCounters * sizeof(unsigned)) != hipSuccess ||
+        hipMalloc((void **)&ctx->identity_pages, kIdentityPages * sizeof(uint32_t)) != hipSuccess ||
+        launch_iota_u32(ctx->identity_pages, kIdentityPages, ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
         set_err(err, err_len, "stream/event/scratch creation failed");
         ziggy_hip_destroy_context(ctx);
         return ZIGGY_HIP_INITIALIZATION_FAILED;
@@ -217,6 +221,7 @@ void ziggy_hip_destroy_context(ZiggyHipContext *ctx) {
         if (t.dev) hipFree(t.dev);
     if (ctx->scratch) hipFree(ctx->scratch);
     if (ctx->counters) hipFree(ctx->counters);
+    if (ctx->identity_pages) hipFree(ctx->identity_pages);
     if (ctx->seq_begin) hipEventDestroy(ctx->seq_begin);
     if (ctx->seq_end) hipEventDestroy(ctx->seq_end);
     if (ctx->stream) hipStreamDestroy(ctx->stream);
@@ -641,6 +646,8 @@ int ziggy_hip_attention_fused_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *q,
                                          window_start, scale, softcap, &p, err, err_len);
     if (st != ZIGGY_HIP_OK) return st;
     p.counters = ctx->counters;
+    p.page_table = ctx->identity_pages;
+    p.page_shift = kKvPageShift;
     const size_t need = attention_scratch_floats((int)heads, (int)hd, p.max_splits) * 4;
     if (need > ctx->scratch_len) {
         set_err(err, err_len, "context too long for the context scratch (%zu bytes)", need);

@@ -52,7 +52,12 @@ struct ZiggyHipSession {
     float *logits = nullptr, *part_o = nullptr, *part_ml = nullptr;
     float *rope_denom = nullptr;  // [rope_dim / 2] RoPE denominators from the host's powf
     unsigned *counters = nullptr;  // attention arrival counters (zero between launches)
+    // binary16 K/V, paged: per layer kv_pages pages of 64 positions ([page][row in page][kv_dim]);
+    // page_table[logical page] = the page's index in every layer's pool
     __half *kc = nullptr, *vc = nullptr;
+    uint32_t kv_pages = 0;
+    uint32_t *page_table = nullptr;
+    std::vector<uint32_t> pages;  // host copy of page_table
     StepState *st = nullptr;
     StepState *st_host = nullptr;  // pinned staging for the host-driven step state
     uint32_t *prompt = nullptr, *history = nullptr;
@@ -81,6 +86,14 @@ struct ZiggyHipSession {
 };
 
 namespace {
+
+// Start of layer l's pages in the K or V pool, and the row of position pos in it.
+size_t kv_layer_base(const ZiggyHipSession *s, int l) {
+    return (size_t)l * ((size_t)s->kv_pages << kKvPageShift) * s->kv_size;
+}
+size_t kv_row_host(const ZiggyHipSession *s, uint32_t pos) {
+    return ((size_t)s->pages[pos >> kKvPageShift] << kKvPageShift) + (pos & ((1u << kKvPageShift) - 1));
+}
 
 int fail(char *err, size_t err_len, int code, const char *msg) {
     set_err(err, err_len, "%s", msg);
@@ -112,7 +125,7 @@ hipError_t enqueue_kernel(ZiggyHipSession *s, int id, int l, const int *pos_dev,
     const ZiggyHipModelDesc &md = s->md;
     const int H = (int)md.embedding_length, F = (int)md.feed_forward_length;
     const LayerW &L = s->layers[l < 0 ? 0 : l];
-    const size_t layer_base = (size_t)l * md.context_length * s->kv_size;
+    const size_t layer_base = kv_layer_base(s, l < 0 ? 0 : l);
     switch (id) {
     case ZIGGY_HIP_KERNEL_QKV: {
         const DT *m[3] = {&L.q, &L.k, &L.v};
@@ -136,6 +149,8 @@ hipError_t enqueue_kernel(ZiggyHipSession *s, int id, int l, const int *pos_dev,
         a.k_norm = L.k_norm.present ? (const float *)L.k_norm.p : nullptr;
         a.k_cache = s->kc + layer_base;
         a.v_cache = s->vc + layer_base;
+        a.page_table = s->page_table;
+        a.page_shift = kKvPageShift;
         a.out = s->attn;
         a.part_o = s->part_o;
         a.part_ml = s->part_ml;
@@ -387,7 +402,8 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
     }
 
     // ---- activations, KV cache, step state ----
-    const size_t cache_elems = (size_t)md.block_count * md.context_length * KV;
+    s->kv_pages = (md.context_length + (1u << kKvPageShift) - 1) >> kKvPageShift;
+    const size_t cache_elems = (size_t)md.block_count * ((size_t)s->kv_pages << kKvPageShift) * KV;
     const size_t logits_len = md.vocab_size > F ? md.vocab_size : F;
     const size_t attn_scratch = attention_scratch_floats((int)md.head_count, (int)md.head_dim, s->max_splits);
     struct {
@@ -399,6 +415,7 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
         {(void **)&s->part_o, attn_scratch * 4}, {(void **)&s->kc, cache_elems * 2}, {(void **)&s->vc, cache_elems * 2},
         {(void **)&s->st, sizeof(StepState)}, {(void **)&s->counters, md.head_count_kv * sizeof(unsigned)},
         {(void **)&s->rope_denom, 4 * (size_t)(md.head_dim / 2 + 1)},
+        {(void **)&s->page_table, 4 * (size_t)s->kv_pages},
     };
     for (auto &r : reqs) {
         e = hipMalloc(r.p, r.bytes);
@@ -410,6 +427,17 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
         s->allocs.push_back(*r.p);
     }
     s->part_ml = s->part_o + (size_t)md.head_count * s->max_splits * 8 * md.head_dim;
+    // pages in order until the caller sets a block table
+    s->pages.resize(s->kv_pages);
+    for (uint32_t i = 0; i < s->kv_pages; i++) s->pages[i] = i;
+    // on the session stream, after the zero fill queued there above (a copy on the
+    // null stream would not be ordered after it)
+    e = hipMemcpyAsync(s->page_table, s->pages.data(), 4 * (size_t)s->kv_pages, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        free_session(s);
+        return hip_fail(e, "block table upload", err, err_len);
+    }
     {
         const int n_rot = (int)(md.rope_dim < md.head_dim ? md.rope_dim : md.head_dim);
         std::vector<float> den((size_t)md.head_dim / 2 + 1, 1.0f);
@@ -445,7 +473,7 @@ void ziggy_hip_session_destroy(ZiggyHipSession *s) { free_session(s); }
 
 int ziggy_hip_session_reset(ZiggyHipSession *s, char *err, size_t err_len) {
     if (!s) return ZIGGY_HIP_INVALID_ARGUMENT;
-    const size_t cache_bytes = (size_t)s->md.block_count * s->md.context_length * s->kv_size * 2;
+    const size_t cache_bytes = (size_t)s->md.block_count * ((size_t)s->kv_pages << kKvPageShift) * s->kv_size * 2;
     ZH_TRY(hipMemsetAsync(s->kc, 0, cache_bytes, s->ctx->stream), "reset");
     ZH_TRY(hipMemsetAsync(s->vc, 0, cache_bytes, s->ctx->stream), "reset");
     ZH_TRY(hipStreamSynchronize(s->ctx->stream), "reset");
@@ -535,7 +563,7 @@ int ziggy_hip_session_read_kv(ZiggyHipSession *s, uint32_t layer, uint32_t pos, 
     if (!s || layer >= s->md.block_count || pos >= s->md.context_length || !k_out || !v_out)
         return ZIGGY_HIP_INVALID_ARGUMENT;
     std::vector<__half> tmp(2 * (size_t)s->kv_size);
-    const size_t base = ((size_t)layer * s->md.context_length + pos) * s->kv_size;
+    const size_t base = kv_layer_base(s, (int)layer) + kv_row_host(s, pos) * s->kv_size;
     ZH_TRY(hipMemcpyAsync(tmp.data(), s->kc + base, (size_t)s->kv_size * 2, hipMemcpyDeviceToHost, s->ctx->stream),
            "read_kv");
     ZH_TRY(hipMemcpyAsync(tmp.data() + s->kv_size, s->vc + base, (size_t)s->kv_size * 2, hipMemcpyDeviceToHost,
@@ -549,12 +577,38 @@ int ziggy_hip_session_read_kv(ZiggyHipSession *s, uint32_t layer, uint32_t pos, 
     return ZIGGY_HIP_OK;
 }
 
+int ziggy_hip_session_set_block_table(ZiggyHipSession *s, const uint32_t *table, uint32_t count, char *err,
+                                      size_t err_len) {
+    if (!s || !table) return ZIGGY_HIP_INVALID_ARGUMENT;
+    if (count != s->kv_pages) {
+        set_err(err, err_len, "block table of %u pages; this session has %u", count, s->kv_pages);
+        return ZIGGY_HIP_INVALID_ARGUMENT;
+    }
+    std::vector<uint8_t> seen(count, 0);
+    for (uint32_t i = 0; i < count; i++) {
+        if (table[i] >= count || seen[table[i]]) {
+            set_err(err, err_len, "block table entry %u (page %u) out of range or repeated", i, table[i]);
+            return ZIGGY_HIP_INVALID_ARGUMENT;
+        }
+        seen[table[i]] = 1;
+    }
+    if (s->position != 0)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "the block table is set on an empty cache (position 0)");
+    ZH_TRY(hipStreamSynchronize(s->ctx->stream), "set_block_table");
+    ZH_TRY(hipMemcpy(s->page_table, table, 4 * (size_t)count, hipMemcpyHostToDevice), "set_block_table");
+    s->pages.assign(table, table + count);
+    return ZIGGY_HIP_OK;
+}
+
+uint32_t ziggy_hip_session_kv_pages(const ZiggyHipSession *s) { return s ? s->kv_pages : 0; }
+
 int ziggy_hip_session_fill_kv_pattern(ZiggyHipSession *s, uint32_t position, uint64_t seed, char *err,
                                       size_t err_len) {
     if (!s) return ZIGGY_HIP_INVALID_ARGUMENT;
     if (position > s->md.context_length) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "context overflow");
     const size_t n = (size_t)position * s->kv_size;
     std::vector<__half> kb(n ? n : 1), vb(n ? n : 1);
+    ZH_TRY(hipStreamSynchronize(s->ctx->stream), "fill_kv_pattern");  // the copies below are on the null stream
     uint64_t x = seed * 0x9E3779B97F4A7C15ull + 1;
     for (uint32_t l = 0; l < s->md.block_count; l++) {
         for (size_t i = 0; i < n; i++) {
@@ -565,10 +619,14 @@ int ziggy_hip_session_fill_kv_pattern(ZiggyHipSession *s, uint32_t position, uin
             kb[i] = __float2half(v);
             vb[i] = __float2half(-v);
         }
-        const size_t base = (size_t)l * s->md.context_length * s->kv_size;
-        if (n) {
-            ZH_TRY(hipMemcpy(s->kc + base, kb.data(), n * 2, hipMemcpyHostToDevice), "fill_kv_pattern");
-            ZH_TRY(hipMemcpy(s->vc + base, vb.data(), n * 2, hipMemcpyHostToDevice), "fill_kv_pattern");
+        const size_t base = kv_layer_base(s, (int)l);
+        // a page's positions are consecutive rows: one copy per page
+        const uint32_t P = 1u << kKvPageShift;
+        for (uint32_t p0 = 0; p0 < position; p0 += P) {
+            const size_t cnt = (size_t)std::min(P, position - p0) * s->kv_size;
+            const size_t dst = base + kv_row_host(s, p0) * s->kv_size, src = (size_t)p0 * s->kv_size;
+            ZH_TRY(hipMemcpy(s->kc + dst, kb.data() + src, cnt * 2, hipMemcpyHostToDevice), "fill_kv_pattern");
+            ZH_TRY(hipMemcpy(s->vc + dst, vb.data() + src, cnt * 2, hipMemcpyHostToDevice), "fill_kv_pattern");
         }
     }
     s->position = position;
@@ -843,10 +901,16 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
     const float eps = md.rms_norm_eps;
     hipError_t e = launch_embed_rows(tokens, M, s->embd.p, s->embd.stride, (int)s->embd.rows, s->embd.type, H,
                                      s->b_hidden, st);
+    // Prompt chunks are deterministic: no reduction split onto the residual,
+    // at most two onto cleared rows (0 + a + b is the same sum in either
+    // order); their token tiles fill the chip.  Verify passes (one token
+    // tile) keep the split for speed; their sums vary in the last bits.
+    const bool det = !output;
+    const int split_add = det ? 1 : 16, split_clear = det ? 2 : 16;
     auto gemm = [&](const DT &w, const DT *w2, const float *x, int ldx, float *y, int ldy, int out) {
         if (e != hipSuccess) return;
         e = launch_gemm(w.type, w.p, w2 ? w2->p : nullptr, w.stride, x, ldx, y, ldy, M, (int)w.rows, (int)w.cols,
-                        out, s->b_argmax, st);
+                        out, s->b_argmax, st, false, out == OUT_ADD ? split_add : split_clear);
     };
     // products of the normed rows that accumulate (OUT_ADD) onto cleared
     // outputs: one launch for the matrices that share a format and row size
@@ -865,7 +929,7 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
             int Ns[3];
             for (int k = i; k < j; k++) ws[k - i] = d[k]->p, Ns[k - i] = (int)d[k]->rows;
             e = launch_gemm_multi(d[i]->type, j - i, ws, ys + i, lds + i, Ns, d[i]->stride, s->b_normed, H, M,
-                                  (int)d[i]->cols, OUT_ADD, st);
+                                  (int)d[i]->cols, OUT_ADD, st, split_clear);  // onto rows the norm cleared
             i = j;
         }
     };
@@ -875,7 +939,7 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
         e = launch_rms_norm_rows(s->b_hidden, (const float *)L.attn_norm.p, s->b_normed, M, H, eps, st, s->b_q,
                                  (size_t)M * Q, s->b_k, (size_t)M * KV, s->b_v, (size_t)M * KV);
         multi3(L.q, s->b_q, Q, L.k, s->b_k, KV, &L.v, s->b_v, KV);
-        const size_t layer_base = (size_t)l * md.context_length * s->kv_size;
+        const size_t layer_base = kv_layer_base(s, l);
         if (s->b_counters && e == hipSuccess) {
             AttnParams a{};
             a.q = s->b_q;
@@ -888,6 +952,8 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
             a.k_norm = L.k_norm.present ? (const float *)L.k_norm.p : nullptr;
             a.k_cache = s->kc + layer_base;
             a.v_cache = s->vc + layer_base;
+            a.page_table = s->page_table;
+            a.page_shift = kKvPageShift;
             a.head_count = (int)md.head_count;
             a.head_count_kv = (int)md.head_count_kv;
             a.head_dim = (int)md.head_dim;
@@ -926,6 +992,8 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
             a.k_norm = L.k_norm.present ? (const float *)L.k_norm.p : nullptr;
             a.k_cache = s->kc + layer_base;
             a.v_cache = s->vc + layer_base;
+            a.page_table = s->page_table;
+            a.page_shift = kKvPageShift;
             a.out = s->b_attn + (size_t)m * Q;
             a.part_o = s->part_o;
             a.part_ml = s->part_ml;

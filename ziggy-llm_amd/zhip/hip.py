@@ -156,6 +156,8 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_session_write_hidden": [vp, vp] + E,
         "ziggy_hip_session_read_kv": [vp, u32, u32, vp, vp] + E,
         "ziggy_hip_session_fill_kv_pattern": [vp, u32, ctypes.c_uint64] + E,
+        "ziggy_hip_session_set_block_table": [vp, vp, u32] + E,
+        "ziggy_hip_session_kv_pages": [vp],
         "ziggy_hip_session_step_greedy": [vp, u32, ctypes.POINTER(u32)] + E,
         "ziggy_hip_session_step_no_output": [vp, u32] + E,
         "ziggy_hip_session_generate": [vp, vp, u32, u32, vp, ctypes.POINTER(GenerateStats)] + E,
@@ -182,6 +184,7 @@ def lib() -> ctypes.CDLL:
     restypes = {"ziggy_hip_destroy_context": None, "ziggy_hip_destroy_buffer": None,
                 "ziggy_hip_session_destroy": None, "ziggy_hip_moe_stack_destroy": None, "ziggy_hip_buffer_length": sz,
                 "ziggy_hip_session_position": u32, "ziggy_hip_version": ctypes.c_char_p,
+                "ziggy_hip_session_kv_pages": u32,
                 "ziggy_hip_shortlist_len": u32}
     for name, args in sigs.items():
         fn = getattr(L, name)
@@ -484,6 +487,15 @@ class Session:
         k, v = np.empty(n, np.float32), np.empty(n, np.float32)
         _call("ziggy_hip_session_read_kv", self.h, layer, pos, k.ctypes.data, v.ctypes.data)
         return k, v
+
+    @property
+    def kv_pages(self) -> int:
+        return int(lib().ziggy_hip_session_kv_pages(self.h))
+
+    def set_block_table(self, table):
+        """Maps logical KV page i to pool page table[i] (a permutation; on an empty cache)."""
+        t = np.ascontiguousarray(table, np.uint32)
+        _call("ziggy_hip_session_set_block_table", self.h, t.ctypes.data, t.size)
 
     def fill_kv_pattern(self, position: int, seed: int = 0):
         """The CPU oracle's deterministic K/V fill of rows [0, position); the position moves there."""
