@@ -2,9 +2,10 @@
 
 A "step" is one greedy decode step (one token through every layer and the
 output head).  The KV cache is first filled by a 4096-token seeded prompt
-(run through the same decode path, token by token, as the reference's
-runPrompt does), then W untimed warm-up steps run, then exactly K timed steps
-(positions ~4.1k).  tok/s = K / decode wall time, the reference's definition
+(batched passes of up to 64 tokens on the matrix cores, the last prompt token
+through the decode step; the reference's runPrompt feeds the same rows token
+by token and the K/V rows agree), then W untimed warm-up steps run, then
+exactly K timed steps (positions ~4.1k).  tok/s = K / decode wall time, the reference's definition
 (runtime/types.zig:220-223).  Weights are random N(0, 0.02) of the
 Llama-3.1-8B shape quantized by this package's own Q4_K_M mix; data is
 synthetic.
@@ -19,7 +20,7 @@ Also reported, on the same JSON line:
                    layers (weights stream from HBM), against the 8 TB/s peak;
                    `traffic` is the HBM bytes per launch from the committed
                    rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-                   (profiles/gate_up_llama8b_hbm_traffic.md), else null;
+                   (profiles/decode_kernels_llama8b_4k_hbm_traffic.md), else null;
   cpu_baseline  -- the CPU oracle (a C restatement of the reference's CPU
                    decode path, same threads policy: 1 + min(11, ncpu - 1))
                    decoding the same model at the same context on host cores.
@@ -158,7 +159,7 @@ def main():
     traffic = None
     if args.model == "llama8b":
         from zhip import pmc
-        traffic = pmc.read_traffic(os.path.join(REPO, "profiles", "gate_up_llama8b_hbm_traffic.md"))
+        traffic = pmc.read_traffic(os.path.join(REPO, "profiles", "decode_kernels_llama8b_4k_hbm_traffic.md"))
     gate_fmt = {"llama8b": "Q4_K", "tinyllama": "Q4_K", "qwen3": "Q8_0"}.get(args.model, "quantized")
     roofline = {"bound": "hbm", "kernel": f"gate_up (fused RMSNorm + {gate_fmt} gate/up + SwiGLU)",
                 "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -10,8 +10,8 @@ GB/s counts the weight bytes plus x and y (rows*cols*bytes_per_weight +
 4*(rows+cols)).
 
 Usage: python -m zhip.microbench [--iters N] [--formats q4_k,q6_k,q8_0]
-                                 [--shapes 4096x4096,14336x4096]
-Prints one JSON object per case.
+                                 [--shapes 4096x4096,14336x4096] [--out FILE.md]
+Prints one JSON object per case; --out also writes them as a markdown table.
 """
 from __future__ import annotations
 
@@ -59,13 +59,30 @@ def main():
     ap.add_argument("--formats", default="q4_k,q6_k,q8_0")
     ap.add_argument("--shapes", default=",".join(f"{r}x{c}" for r, c in SHAPES),
                     help="comma-separated ROWSxCOLS list")
+    ap.add_argument("--out", help="also write the results as a markdown table")
     args = ap.parse_args()
     shapes = [tuple(int(v) for v in s.split("x")) for s in args.shapes.split(",")]
     ctx = hip.Context(0)
+    results = []
     for f in args.formats.split(","):
         for rows, cols in shapes:
-            print(json.dumps(run(ctx, FORMATS[f], rows, cols, args.iters)), flush=True)
+            r = run(ctx, FORMATS[f], rows, cols, args.iters)
+            results.append(r)
+            print(json.dumps(r), flush=True)
     ctx.close()
+    if args.out:
+        lines = ["# Dequant-matvec microbenchmark (batch 1), one MI355X", "",
+                 "Command (from ziggy-llm_amd/):", "",
+                 f"    python3 -m zhip.microbench --iters {args.iters} --formats {args.formats} "
+                 f"--shapes {args.shapes} --out <file>", "",
+                 "Each launch streams one of >= 1 GiB of distinct weight copies from HBM and is timed with its own",
+                 "HIP events; GB/s counts the weight bytes plus x and y.", "",
+                 "| format | rows x cols | weight + x + y bytes | avg us | GB/s | % of 8 TB/s |", "|---|---|---|---|---|---|"]
+        for r in results:
+            lines.append(f"| {r['format']} | {r['rows']} x {r['cols']} | {r['bytes']} | {r['avg_us']} | {r['gbs']} | "
+                         f"{100 * r['frac_of_peak']:.1f} |")
+        with open(args.out, "w") as fh:
+            fh.write("\n".join(lines) + "\n")
 
 
 if __name__ == "__main__":
