@@ -3,7 +3,7 @@ the CPU oracle's matvec, token by token.
 
 Bar: each token's output within 1e-4 relative L2 of the oracle (the matvec
 tolerance); the bf16 hi/lo operand split keeps ~2^-16 relative error per
-product.  Ragged token counts (1, 9, 33) and row counts (not multiples of the
+product.  Ragged token counts (1, 9, 33, 47, 65, 100) and row counts (not multiples of the
 16-row tile) exercise the clamped tails.
 """
 import sys
@@ -29,7 +29,9 @@ def rel_l2(a, b):
     return float(np.linalg.norm(np.asarray(a, np.float64) - b) / max(np.linalg.norm(b), 1e-30))
 
 
-SHAPES = [(1, 16, 256), (8, 100, 256), (9, 64, 4096), (16, 4096, 4096), (33, 300, 512), (9, 1000, 14336)]
+# token counts of several 16-token tiles, ragged past them, with one- and several-stage reductions
+SHAPES = [(1, 16, 256), (8, 100, 256), (9, 64, 4096), (16, 4096, 4096), (33, 300, 512), (9, 1000, 14336),
+          (47, 200, 4096), (64, 300, 4096), (65, 130, 1024), (100, 1000, 512)]
 
 
 @pytest.mark.parametrize("ttype", [Q4_K, Q6_K, Q8_0, IQ4_XS, Q3_K, F16, F32])
@@ -51,8 +53,9 @@ def test_gemm_matches_oracle_per_token(hip_ctx, ttype, shape):
         assert rel_l2(got[t], want) < REL_L2, (t, rel_l2(got[t], want))
 
 
-def test_gemm_add_accumulates(hip_ctx):
-    tokens, rows, cols = 9, 256, 2048
+@pytest.mark.parametrize("tokens", [9, 64])
+def test_gemm_add_accumulates(hip_ctx, tokens):
+    rows, cols = 256, 2048
     q = np.zeros(row_bytes(Q4_K, cols) * rows, np.uint8)
     synth.fill_tensor(q, Q4_K, rows, cols, seed=5)
     x = np.stack([synth.normal_row(1, t, cols, 0.0, 1.0) for t in range(tokens)])
