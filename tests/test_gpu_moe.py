@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from oracle import zo
-from zhip import hip, synth
+from zhip import gguf, hip, synth
 from zhip.gguf import F32, IQ4_XS, Q3_K, Q8_0
 
 pytestmark = pytest.mark.gpu
@@ -89,6 +89,32 @@ def test_moe_stack_config5_shape(hip_ctx):
     assert np.max(np.abs(w - want_w)) < 1e-5
     assert rel_l2(got, want) < 1e-4
     assert np.array_equal(got, got2) and np.array_equal(sel, sel2)
+
+
+@pytest.mark.parametrize("name", ["small", "small-q8-router-rawlogits"])
+def test_moe_stack_router_ties(hip_ctx, name):
+    # router rows 2e + 1 copied from rows 2e: every expert's logit ties with its pair's, so each top-k
+    # round meets equal values and must take the lower index first (selectTopK, model/loader.zig:3953-3975)
+    spec = CASES[name]()
+    layers = synth.build_moe_stack(spec, seed=17)
+    for lay in layers:
+        buf, rows, cols, t = lay["router"]
+        rb = gguf.row_bytes(t, cols)
+        for e in range(0, spec.n_experts - 1, 2):
+            buf[(e + 1) * rb:(e + 2) * rb] = buf[e * rb:(e + 1) * rb]
+    x = synth.normal_row(8, 0, spec.hidden, 0.0, 1.0)
+    want, want_sel, want_w = oracle_stack(spec, layers, x)
+    st = hip.MoeStack(hip_ctx, synth.moe_desc(spec), layers)
+    got, sel, w = st.forward(x)
+    xs = np.stack([synth.normal_row(8, t, spec.hidden, 0.0, 1.0) for t in range(5)])
+    pgot, psel, pw = st.prefill(xs)
+    st.close()
+    assert np.array_equal(sel, want_sel), (sel, want_sel)
+    # pairs are taken together, lower index first
+    assert all(s[i] % 2 == 0 and s[i + 1] == s[i] + 1 for s in sel for i in range(0, spec.top_k - 1, 2))
+    assert np.max(np.abs(w - want_w)) < 1e-5
+    assert rel_l2(got, want) < 1e-4
+    check_prefill(spec, layers, xs, pgot, psel, pw)
 
 
 def test_moe_stack_rejects_bad_shapes(hip_ctx):

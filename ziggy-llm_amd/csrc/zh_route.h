@@ -40,6 +40,24 @@ __device__ __forceinline__ float wave_sum_xor(float v) {
     return v;
 }
 
+// The wavefront maximum of a 32-bit unsigned value, valid in every lane: DPP
+// within each 16-lane row, then the two lane swaps across rows (as
+// wave_max_key does for 64 bits).  Every lane must be active.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    auto mov = [](uint32_t x, auto ctrl) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, decltype(ctrl)::value, 0xF, 0xF, false);
+    };
+    v = max(v, mov(v, std::integral_constant<int, 0xB1>{}));
+    v = max(v, mov(v, std::integral_constant<int, 0x4E>{}));
+    v = max(v, mov(v, std::integral_constant<int, 0x141>{}));
+    v = max(v, mov(v, std::integral_constant<int, 0x140>{}));
+    uint32_t a, b;
+    lane_pair<16>(v, a, b);
+    v = max(a, b);
+    lane_pair<32>(v, a, b);
+    return max(a, b);
+}
+
 template <class Put>
 __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int E, int k, int gating,
                                            int weights_norm, float weights_scale, int has_shared_gate, Put put) {
@@ -47,6 +65,8 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
     float pr[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) pr[i] = l + 64 * i < E ? logits[l + 64 * i] : -INFINITY;
+    // the shared expert's gate logit, loaded with the others (not after the top-k)
+    const float gate_logit = has_shared_gate ? logits[E] : 0.f;
     if (gating == 1 || gating == 2) {
         // softmaxInPlace (model/loader.zig:4160-4170): max, exp(v - max), / sum
         float m = fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3]));
@@ -61,53 +81,71 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
 #pragma unroll
         for (int i = 0; i < 4; i++) pr[i] = l + 64 * i < E ? pr[i] / s : -INFINITY;
     }
-    // k rounds of a wavefront argmax over the values not yet taken (the
-    // largest value first; equal values: the lower index first)
+    // k rounds: the largest value not yet taken (in the total order of
+    // route_ordered_bits), then, among the entries holding it, the lowest
+    // index (ballots: entry l + 64 i, i first, then the lane).  The round's
+    // value is the selected probability itself, so no lane read follows.
+    uint32_t ob[4];
+    bool live[4];  // in range and not yet taken
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        ob[i] = route_ordered_bits(pr[i]);
+        live[i] = l + 64 * i < E;
+    }
+    // (loops over r run to the compile-time bound kRouteMaxK with a uniform
+    // r < k guard: sel and w stay in registers, indexed statically)
     uint32_t sel[kRouteMaxK];
-    unsigned taken = 0;  // bit i: expert l + 64 i taken
-    for (int r = 0; r < k; r++) {
-        unsigned long long best = 0ull;
+    float w[kRouteMaxK];
+#pragma unroll
+    for (int r = 0; r < kRouteMaxK; r++) {
+        sel[r] = 0u;
+        w[r] = 0.f;
+        if (r >= k) continue;
+        uint32_t mine = 0u;
+        bool any = false;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int idx = l + 64 * i;
-            if (idx >= E || (taken >> i & 1)) continue;
-            const unsigned long long key =
-                ((unsigned long long)route_ordered_bits(pr[i]) << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
-            best = key > best ? key : best;
+            if (live[i] && (!any || ob[i] > mine)) mine = ob[i];
+            any = any || live[i];
         }
-        best = wave_max_key(best);
-        const uint32_t idx = 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull);
-        sel[r] = idx;
-        if ((int)(idx & 63) == l) taken |= 1u << (idx >> 6);
-    }
-    // the selected probabilities: from the lane that holds each
-    float w[kRouteMaxK];
-    for (int r = 0; r < k; r++) {
-        const int e = __builtin_amdgcn_readfirstlane((int)sel[r]), src = e & 63, i = e >> 6;
-        const float mine = i == 0 ? pr[0] : i == 1 ? pr[1] : i == 2 ? pr[2] : pr[3];
-        w[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), src));
+        const uint32_t best = wave_max_u32(mine);
+        int idx = -1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const unsigned long long b = __ballot(live[i] && ob[i] == best);
+            if (idx < 0 && b) idx = 64 * i + __builtin_ctzll(b);
+        }
+        sel[r] = (uint32_t)idx;
+        w[r] = __uint_as_float((best & 0x80000000u) ? (best & 0x7FFFFFFFu) : ~best);
+        if ((idx & 63) == l) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (i == (idx >> 6)) live[i] = false;
+        }
     }
     if (l == 0) {
         if (weights_norm) {
             float sum = 0.f;
-            for (int r = 0; r < k; r++)
-                if (isfinite(w[r]) && w[r] > 0.f) sum += w[r];
-            if (sum <= 0.f) {
-                for (int r = 0; r < k; r++) w[r] = 0.f;
-            } else {
-                const float inv = 1.0f / sum;
-                for (int r = 0; r < k; r++) w[r] = (isfinite(w[r]) && w[r] > 0.f) ? w[r] * inv : 0.f;
-            }
+#pragma unroll
+            for (int r = 0; r < kRouteMaxK; r++)
+                if (r < k && isfinite(w[r]) && w[r] > 0.f) sum += w[r];
+            const float inv = sum > 0.f ? 1.0f / sum : 0.f;
+#pragma unroll
+            for (int r = 0; r < kRouteMaxK; r++) w[r] = (sum > 0.f && isfinite(w[r]) && w[r] > 0.f) ? w[r] * inv : 0.f;
         }
-        if (weights_scale != 1.0f)
-            for (int r = 0; r < k; r++) w[r] *= weights_scale;
-        for (int r = 0; r < k; r++) {
+        if (weights_scale != 1.0f) {
+#pragma unroll
+            for (int r = 0; r < kRouteMaxK; r++) w[r] *= weights_scale;
+        }
+#pragma unroll
+        for (int r = 0; r < kRouteMaxK; r++) {
+            if (r >= k) continue;
             put(2 * r, sel[r]);
             put(2 * r + 1, __float_as_uint(w[r]));
         }
         float g = 1.0f;
         if (has_shared_gate) {
-            const float v = logits[E];
+            const float v = gate_logit;
             if (v >= 0.f) {
                 g = 1.0f / (1.0f + expf(-v));
             } else {
