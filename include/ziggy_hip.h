@@ -240,8 +240,8 @@ int ziggy_hip_store_kv_half(ZiggyHipContext *ctx, const ZiggyHipBuffer *src, Zig
 /* GQA decode attention over the binary16 cache; split-K flash decoding whose
  * last split to finish merges the others (replaces
  * ziggy_metal_attention_fused_f32, bridge.h:459-477).  q is the roped query;
- * the cache already holds the current position.  softcap must be 0
- * (softcapping belongs to Gemma, outside this path). */
+ * the cache already holds the current position.  head_dim 64, 96, 128 or
+ * 256; softcap must be 0 (softcapping belongs to Gemma, outside this path). */
 int ziggy_hip_attention_fused_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *q, const ZiggyHipBuffer *k_cache,
                                   const ZiggyHipBuffer *v_cache, ZiggyHipBuffer *output, uint32_t head_count,
                                   uint32_t head_count_kv, uint32_t head_dim, uint32_t kv_dim,

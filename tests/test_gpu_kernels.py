@@ -159,7 +159,7 @@ def test_silu_down_add(hip_ctx):
 # most, (16, 16, 128) and (64, 64, 64) fold several chunks per split (online
 # softmax across chunks) from positions 1024 and 256 on.
 @pytest.mark.parametrize("heads,kv_heads,hd", [(32, 8, 128), (32, 4, 64), (3, 1, 128), (1, 1, 256), (16, 16, 128),
-                                               (64, 64, 64)])
+                                               (64, 64, 64), (3, 1, 96), (24, 8, 96)])
 @pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 200, 1000, 4095])
 def test_attention_parity(hip_ctx, heads, kv_heads, hd, pos):
     say(f"attention {heads}/{kv_heads}x{hd} pos {pos}")
@@ -174,6 +174,37 @@ def test_attention_parity(hip_ctx, heads, kv_heads, hd, pos):
     hip_ctx.attention(hip_ctx.buffer(q), hip_ctx.buffer(k), hip_ctx.buffer(v), out, heads, kv_heads, hd, kv_dim,
                       ctx_len, pos)
     assert rel_l2(out.read(), want) < REL_L2
+
+
+def test_attention_reference_case_head_dim_96(hip_ctx):
+    # runtime/metal_backend_test.zig:691-766: 3 query heads on 1 kv head of 96, 5 positions, query at 4, scale
+    # 0.125; the reference's expected values come from f32 caches, its kernel reads binary16 ones (tolerance
+    # 0.005 absolute); against the binary16 cache the result is held to the kernel bar
+    heads, kvh, hd, ctx_len, pos, scale = 3, 1, 96, 5, 4, 0.125
+    kv_dim = kvh * hd
+    i = np.arange(heads * hd)
+    q = (((i % 19) - 9) * 0.07 + 0.02).astype(np.float32)
+    j = np.arange(ctx_len * kv_dim)
+    k32 = (((j % 17) - 8) * 0.06 - 0.01).astype(np.float32)
+    v32 = (((j % 13) - 6) * 0.08 + 0.03).astype(np.float32)
+    k16, v16 = k32.astype(np.float16), v32.astype(np.float16)
+
+    def reference(kc, vc):
+        kc = kc.astype(np.float64).reshape(ctx_len, hd)[:pos + 1]
+        vc = vc.astype(np.float64).reshape(ctx_len, hd)[:pos + 1]
+        out = []
+        for h in range(heads):
+            s = kc @ q[h * hd:(h + 1) * hd].astype(np.float64) * scale
+            w = np.exp(s - s.max())
+            out.append((w / w.sum()) @ vc)
+        return np.concatenate(out)
+
+    o = hip_ctx.empty(heads * hd * 4)
+    hip_ctx.attention(hip_ctx.buffer(q), hip_ctx.buffer(k16), hip_ctx.buffer(v16), o, heads, kvh, hd, kv_dim, ctx_len,
+                      pos, scale=scale)
+    got = o.read()
+    assert np.max(np.abs(got - reference(k32, v32))) <= 0.005
+    assert rel_l2(got, reference(k16, v16)) < REL_L2
 
 
 def test_attention_layer_base(hip_ctx):
@@ -293,4 +324,4 @@ def test_invalid_arguments_are_rejected(hip_ctx):
     with pytest.raises(hip.HipError):
         hip_ctx.matvec(Q4_K, m, x, y, 1, 300)  # not a block multiple
     with pytest.raises(hip.HipError):
-        hip_ctx.attention(x, m, m, y, 32, 8, 96, 768, 10, 3)  # head_dim 96 unsupported
+        hip_ctx.attention(x, m, m, y, 32, 8, 80, 640, 10, 3)  # head_dim 80 unsupported

@@ -35,6 +35,7 @@ MODELS = {
     "qwen3-q8-g8-hd128": dict(arch="qwen3", qk_norm=True, hidden=512, ffn=1024, n_head=8, n_kv=1, head_dim=128,
                               default_type=Q8_0, attn_v_type=Q8_0, output_type=Q8_0, embd_type=Q8_0, context=512,
                               rope_theta=1000000.0),
+    "llama-hd96-g4": dict(arch="llama", hidden=768, ffn=1024, n_head=8, n_kv=2, head_dim=96, context=512),
 }
 
 

@@ -718,7 +718,7 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
         const float *qn = p.q_norm ? p.q_norm : p.q, *kn = p.k_norm ? p.k_norm : p.q;
 #pragma unroll
         for (int i = 0; i < QV; i++) qnw[i] = qn[(tid + 256 * i) % HD];
-        knw[0] = kn[tid & (HD - 1)];
+        knw[0] = kn[tid % HD];
     }
 #pragma unroll
     for (int i = 0; i < QV; i++) {
@@ -738,8 +738,8 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
         // unconditional for the same reason as the K/V loads below (plain
         // mode reads q in place of the absent k / v and ignores it)
         const float *kn = fused ? p.k_new : p.q, *vn = fused ? p.v_new : p.q;
-        kx[0] = kn[kv_off + (tid & (HD - 1))];
-        vx = vn[kv_off + (tid & (HD - 1))];
+        kx[0] = kn[kv_off + tid % HD];
+        vx = vn[kv_off + tid % HD];
         if (own_pos && tid < HD) {
             if (p.k_bias) kx[0] += p.k_bias[kv_off + tid];
             if (p.v_bias) vx += p.v_bias[kv_off + tid];
@@ -1103,8 +1103,8 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(AttnParams p, float *q_o
             if (p.q_bias) qv[i] += p.q_bias[(size_t)kvh * nq + idx];
         }
     }
-    kx[0] = p.k_new[kv_off + (tid & (HD - 1))];
-    float vx = p.v_new[kv_off + (tid & (HD - 1))];
+    kx[0] = p.k_new[kv_off + tid % HD];
+    float vx = p.v_new[kv_off + tid % HD];
     if (tid < HD) {
         if (p.k_bias) kx[0] += p.k_bias[(size_t)kvh * HD + tid];
         if (p.v_bias) vx += p.v_bias[(size_t)kvh * HD + tid];
@@ -1122,14 +1122,20 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(AttnParams p, float *q_o
     }
 }
 
+// The per-head norm reduces over whole wavefronts: heads of 64, 128 or 256
+// values (no QK-norm for head_dim 96)
+static bool norms_fit(const AttnParams &p) { return !(p.q_norm || p.k_norm) || p.head_dim % 64 == 0; }
+
 hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t s) {
     if (!p.page_table || p.page_shift != kKvPageShift) return hipErrorInvalidValue;
     if (p.head_count_kv <= 0 || p.head_count % p.head_count_kv || p.head_count / p.head_count_kv > kMaxGroup ||
         p.n_query < 1 || !p.q || !p.k_new || !p.v_new || !q_out || p.q_stride < p.head_count * p.head_dim)
         return hipErrorInvalidValue;
+    if (!norms_fit(p)) return hipErrorInvalidValue;
     const dim3 grid(p.n_query, p.head_count_kv);
     switch (p.head_dim) {
     case 64: hipLaunchKernelGGL(attn_prep_kernel<64>, grid, dim3(256), 0, s, p, q_out); break;
+    case 96: hipLaunchKernelGGL(attn_prep_kernel<96>, grid, dim3(256), 0, s, p, q_out); break;
     case 128: hipLaunchKernelGGL(attn_prep_kernel<128>, grid, dim3(256), 0, s, p, q_out); break;
     case 256: hipLaunchKernelGGL(attn_prep_kernel<256>, grid, dim3(256), 0, s, p, q_out); break;
     default: return hipErrorInvalidValue;
@@ -1137,7 +1143,11 @@ hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t 
     return hipGetLastError();
 }
 
-bool attention_multi_supported(int head_dim) { return (head_dim == 64 || head_dim == 128) && !attention_valu(); }
+// head_dim 96 has only the matrix-core kernel (the vector kernel's position
+// lanes need a power-of-two head)
+bool attention_multi_supported(int head_dim) {
+    return head_dim == 96 || ((head_dim == 64 || head_dim == 128) && !attention_valu());
+}
 
 int attention_query_groups(int head_count, int head_count_kv, int n_query) {
     const int G = head_count_kv > 0 ? head_count / head_count_kv : 1;
@@ -1147,7 +1157,7 @@ int attention_query_groups(int head_count, int head_count_kv, int n_query) {
 
 hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
     if (p.head_count_kv <= 0 || p.head_count % p.head_count_kv || p.head_count / p.head_count_kv > kMaxGroup ||
-        p.max_splits < 1 || !p.counters)
+        p.max_splits < 1 || !p.counters || !norms_fit(p))
         return hipErrorInvalidValue;
     // pages of kKvPageShift (two 32-position tiles), the window on a page boundary
     if (!p.page_table || p.page_shift != kKvPageShift || (p.window_start & ((1 << kKvPageShift) - 1)))
@@ -1176,6 +1186,7 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
             }
         };
         if (p.head_dim == 64) go(std::integral_constant<int, 64>{});
+        else if (p.head_dim == 96) go(std::integral_constant<int, 96>{});
         else go(std::integral_constant<int, 128>{});
         return hipGetLastError();
     }
@@ -1183,7 +1194,7 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
     auto go = [&](auto hd_tag) {
         constexpr int HD = decltype(hd_tag)::value;
         if constexpr (HD <= 128) {
-            if (!attention_valu()) {
+            if (!attention_valu() || HD % 64) {
                 switch (G) {
                 case 1: hipLaunchKernelGGL((attn_mfma_kernel<HD, 1, false>), grid, dim3(256), 0, s, p); break;
                 case 2: hipLaunchKernelGGL((attn_mfma_kernel<HD, 2, false>), grid, dim3(256), 0, s, p); break;
@@ -1194,16 +1205,19 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
                 return;
             }
         }
-        switch (G) {
-        case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(256), 0, s, p); break;
-        case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(256), 0, s, p); break;
-        case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(256), 0, s, p); break;
-        case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(256), 0, s, p); break;
-        default: hipLaunchKernelGGL((attn_kernel<HD, 0>), grid, dim3(256), 0, s, p); break;
+        if constexpr (HD % 64 == 0) {
+            switch (G) {
+            case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(256), 0, s, p); break;
+            case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(256), 0, s, p); break;
+            case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(256), 0, s, p); break;
+            case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(256), 0, s, p); break;
+            default: hipLaunchKernelGGL((attn_kernel<HD, 0>), grid, dim3(256), 0, s, p); break;
+            }
         }
     };
     switch (p.head_dim) {
     case 64: go(std::integral_constant<int, 64>{}); break;
+    case 96: go(std::integral_constant<int, 96>{}); break;
     case 128: go(std::integral_constant<int, 128>{}); break;
     case 256: go(std::integral_constant<int, 256>{}); break;
     default: return hipErrorInvalidValue;

@@ -328,7 +328,8 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
     const ZiggyHipModelDesc &md = *model;
     if (md.block_count == 0 || md.embedding_length == 0 || md.head_count == 0 || md.head_count_kv == 0 ||
         md.head_count % md.head_count_kv || md.head_count / md.head_count_kv > 8 ||
-        (md.head_dim != 64 && md.head_dim != 128 && md.head_dim != 256) || md.rope_dim > md.head_dim || md.rope_style > 1 ||
+        (md.head_dim != 64 && md.head_dim != 96 && md.head_dim != 128 && md.head_dim != 256) ||
+        md.rope_dim > md.head_dim || md.rope_style > 1 ||
         md.context_length == 0 || md.embedding_length % 64 || md.feed_forward_length % 64 ||
         md.embedding_length / 64 > 256 || md.feed_forward_length / 64 > 256 ||
         (md.head_count * md.head_dim) % 64)
@@ -375,6 +376,8 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
                                 (b == ZIGGY_HIP_TYPE_Q4_K || b == ZIGGY_HIP_TYPE_Q6_K) &&
                                 (c == ZIGGY_HIP_TYPE_Q4_K || c == ZIGGY_HIP_TYPE_Q6_K));
             if (!uniform && !mixed) ok = false;
+            // the per-head norm reduces over whole wavefronts (heads of 64, 128 or 256)
+            if (md.head_dim % 64 && (L.q_norm.present || L.k_norm.present)) ok = false;
         }
     }
     if (!ok) {
