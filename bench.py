@@ -106,8 +106,12 @@ def main():
     prompt = synth.prompt_tokens(args.seed, args.prompt, spec.vocab)
     t0 = time.time()
     warm_tokens, wst = sess.generate(prompt, args.warmup)
+    # the batched passes cover every prompt row but the last (which runs through the decode step)
+    pflops = spec.prompt_pass_flops(args.prompt - 1)
+    ptflops = pflops / max(wst.prompt_ns, 1) / 1e3
     prefill = {"tokens": args.prompt, "ms": round(wst.prompt_ns / 1e6, 3),
                "tok_s": round(args.prompt / max(wst.prompt_ns, 1) * 1e9, 1),
+               "tflops": round(ptflops, 2), "mfma_fraction_bf16": round(ptflops / MFMA_BF16_TFLOPS, 5),
                "path": "batched passes of up to 64 tokens (MFMA GEMMs, multi-query causal attention), "
                        "the last token through the decode step"}
     log(f"prefill {args.prompt} tokens in {wst.prompt_ns / 1e6:.1f} ms ({prefill['tok_s']} tok/s); with "
@@ -144,9 +148,12 @@ def main():
             accepted.append(int(n))
             cur = int(pred[n - 1])
         tv = sorted(times)[1]
+        # the pass reads every weight once (the output head included) for its 9 rows
+        wbytes = spec.weight_bytes_per_token()
         verify = {"tokens": 9, "drafts": 8, "ms": round(1e3 * tv, 3), "accepted": accepted,
                   "prediction_mismatches": mismatches, "tok_s_equiv": round(9 / tv, 1),
-                  "decode_ms_for_9": round(9 * ms_per_step, 3)}
+                  "decode_ms_for_9": round(9 * ms_per_step, 3),
+                  "weight_bytes": wbytes, "weights_hbm_fraction": round(wbytes / tv / (HBM_PEAK_GBS * 1e9), 4)}
         log(f"verify (1 + 8 drafts, MFMA GEMMs): {1e3 * tv:.3f} ms vs {9 * ms_per_step:.3f} ms for 9 decode steps")
 
     kernels = {}

@@ -153,6 +153,18 @@ class ModelSpec:
                 total += t.nbytes
         return total
 
+    def matmul_params_per_layer(self) -> int:
+        """Weights one token meets in a layer's projections (q, k, v, o, gate, up, down)."""
+        H, F, hd = self.hidden, self.ffn, self.head_dim
+        return H * (self.n_head * hd) * 2 + H * (self.n_kv * hd) * 2 + 3 * H * F
+
+    def prompt_pass_flops(self, tokens: int) -> int:
+        """Multiply-add flops (x2) of batched prompt passes over `tokens` rows from position 0: the layer
+        projections and the causal attention (scores and values), without the output head."""
+        proj = 2 * tokens * self.matmul_params_per_layer()
+        attn = 2 * 2 * self.n_head * self.head_dim * (tokens * (tokens + 1) // 2)
+        return self.n_layers * (proj + attn)
+
     def kv_bytes_per_token(self, position: int) -> int:
         """fp16 K+V bytes one decode step at `position` reads (pos+1 rows) and writes (one row)."""
         kv_dim = self.n_kv * self.head_dim
