@@ -112,7 +112,9 @@ int ziggy_hip_commit_sequence_timed(ZiggyHipContext *ctx, ZiggyHipCommitStats *o
 /* ---- dequant-matvec (replaces the ziggy_metal_run_matvec_{f32,q4k,q6k,q8_0,q3k}_f32
  * {,_to_dst,_add} family, bridge.h:79-292).  One typed entry point:
  *   output[output_offset_bytes/4 + r] (=|+=) dot(row r of matrix, input[0..cols))
- * matrix rows start at matrix_offset bytes; add != 0 selects the _add variant. ---- */
+ * matrix rows start at matrix_offset bytes; add != 0 selects the _add variant.
+ * cols: a multiple of 64 (and of the format's block), at most 65536; rows
+ * longer than 16384 values run as column windows whose sums add in turn. ---- */
 int ziggy_hip_run_matvec(ZiggyHipContext *ctx, uint32_t tensor_type, const ZiggyHipBuffer *matrix,
                          size_t matrix_offset, const ZiggyHipBuffer *input, ZiggyHipBuffer *output,
                          size_t output_offset_bytes, uint32_t rows, uint32_t cols, int add, char *error_message,

@@ -98,8 +98,12 @@ def test_q4k_reference_matrix(hip_ctx):
 
 # cols 64..16384 cover every team width (1..256 lanes) and both partial
 # (slots < team) and exact teams; rows cover ragged workgroup tails.
+# Rows longer than one team (16384 values) run as column windows, the first
+# stored or added as asked and the rest added: 16640 (a window of 256 after
+# a full one), 28672 (Llama-70B-sized down rows) and 40960 (three windows).
 SHAPES = [(7, 64), (33, 128), (96, 256), (50, 512), (300, 1024), (4096, 4096), (14336, 4096), (4096, 14336),
-          (1024, 2048), (4096, 12288), (129, 8192), (65, 16384), (128256, 4096)]
+          (1024, 2048), (4096, 12288), (129, 8192), (65, 16384), (128256, 4096), (70, 16640), (300, 28672),
+          (33, 40960)]
 BLOCK_VALUES = {Q4_K: 256, Q6_K: 256, Q3_K: 256, IQ4_XS: 256, Q8_0: 32, F16: 1, F32: 1}
 
 
@@ -125,6 +129,20 @@ def test_matvec_parity(hip_ctx, ttype, shape):
     got = yb2.read()
     assert np.array_equal(got[:3], base[:3])
     assert rel_l2(got[3:], base[3:] + want) < REL_L2
+
+
+def test_silu_down_add_long_rows(hip_ctx):
+    # the SiLU prologue over column windows: silu(gate) * up, both inputs offset per window
+    rows, cols = 100, 20480
+    q = random_weights(Q4_K, rows, cols, 5)
+    g = synth.normal_row(3, 0, cols, 0.0, 1.0)
+    u = synth.normal_row(4, 0, cols, 0.0, 1.0)
+    base = synth.normal_row(5, 0, rows, 0.0, 1.0)
+    act = zo.silu(g) * u
+    want = base + zo.matvec(Q4_K, q, rows, cols, act.astype(np.float32), threads=8)
+    out = hip_ctx.buffer(base)
+    hip_ctx.matvec_silu_down_add(Q4_K, hip_ctx.buffer(q), hip_ctx.buffer(g), hip_ctx.buffer(u), out, rows, cols)
+    assert rel_l2(out.read(), want) < REL_L2
 
 
 def test_q6k_output_head_argmax(hip_ctx):

@@ -45,6 +45,8 @@ SMALL = {
     "llama-hd128-g4": dict(arch="llama", hidden=512, ffn=1024, n_head=4, n_kv=1, head_dim=128, n_layers=3,
                            context=160),
     "llama-f16": dict(arch="llama", default_type=F16, attn_v_type=F16, output_type=F16, embd_type=F16),
+    # an FFN longer than one matvec team (16384): the down rows run as two column windows
+    "llama-ffn16640": dict(arch="llama", hidden=256, ffn=16640, n_layers=2, down_q6k_layers=[1]),
     # head_dim 96 (the reference's own attention test shape): the matrix-core kernel with 3 k-steps
     "llama-hd96-g4": dict(arch="llama", hidden=768, ffn=1024, n_head=8, n_kv=2, head_dim=96, n_layers=2,
                           context=160),

@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "ziggy_hip.h"
+#include "zh_internal.h"
 
 namespace zh {
 
@@ -40,7 +41,8 @@ using ArenaTodo = std::vector<std::pair<const ZiggyHipTensorDesc *, DT *>>;
 
 // Reserves arena space for tensor d (want_rows / want_cols 0 = any): a missing
 // tensor is accepted unless required; f32_only restricts the type; matvec
-// operands need cols a multiple of 64 and at most 256 slots.  The device
+// operands need cols a multiple of 64 (the session limits the rows whose
+// input is normed to one team; longer rows run as column windows).  The device
 // address is an offset until the arena exists (fixed up by the caller).
 inline bool take_tensor(const ZiggyHipTensorDesc *d, uint64_t want_rows, uint64_t want_cols, bool required,
                         bool f32_only, DT *out, size_t *arena_off, ArenaTodo &todo) {
@@ -49,7 +51,7 @@ inline bool take_tensor(const ZiggyHipTensorDesc *d, uint64_t want_rows, uint64_
     if (row_bytes(d->tensor_type, d->cols, &stride)) return false;
     if (f32_only && d->tensor_type != ZIGGY_HIP_TYPE_F32) return false;
     if ((want_rows && d->rows != want_rows) || (want_cols && d->cols != want_cols)) return false;
-    if (!f32_only && (d->cols % 64 || d->cols / 64 > 256)) return false;
+    if (!f32_only && (d->cols % 64 || d->cols > (uint64_t)kMaxMatvecRowLen)) return false;
     out->rows = d->rows;
     out->cols = d->cols;
     out->stride = stride;

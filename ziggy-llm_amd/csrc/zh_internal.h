@@ -222,6 +222,10 @@ struct MvParams {
     float pro_scale;
 };
 
+// Values of a row one team covers (256 lanes of 64); longer rows of plain or
+// SiLU inputs run as column windows (launch_matvec).
+constexpr int kMaxMatvecCols = 256 * 64;
+constexpr int kMaxMatvecRowLen = 4 * kMaxMatvecCols;  // plain / SiLU rows the windows serve
 // Builds the launch plan (team size, rows per team, workgroup ranges) and launches.
 hipError_t launch_matvec(const MvParams &p, int in_mode, int out_mode, hipStream_t s);
 void plan_matvec(MvParams &p, int target_wgs);

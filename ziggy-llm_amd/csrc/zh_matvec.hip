@@ -90,7 +90,48 @@ static float workgroups_per_cu() {
     return w;
 }
 
+// Bytes of the first c columns of a row (c a multiple of the format's block).
+static uint64_t column_bytes(int fmt, int c) {
+    auto of = [&](auto geom) { return (uint64_t)c / decltype(geom)::kValues * decltype(geom)::kBytes; };
+    switch (fmt) {
+    case Q4_K: return of(Geom<Q4_K>{});
+    case Q6_K: return of(Geom<Q6_K>{});
+    case Q3_K: return of(Geom<Q3_K>{});
+    case IQ4_XS: return of(Geom<IQ4_XS>{});
+    case Q8_0: return of(Geom<Q8_0>{});
+    case F16: return of(Geom<F16>{});
+    default: return of(Geom<F32>{});
+    }
+}
+
+static hipError_t launch_matvec_team(const MvParams &p_in, int in, int out, hipStream_t s);
+
+// A row longer than one team covers (kMaxMatvecCols values: 256 lanes of 64)
+// runs as column windows of that length, the first with the call's output
+// mode and the rest adding onto it.  Plain and SiLU inputs only (a norm needs
+// the whole row before any window); stored or added outputs only.
 hipError_t launch_matvec(const MvParams &p_in, int in, int out, hipStream_t s) {
+    if (p_in.cols <= kMaxMatvecCols) return launch_matvec_team(p_in, in, out, s);
+    if ((in != IN_PLAIN && in != IN_SILU) || (out != OUT_STORE && out != OUT_ADD) || p_in.expert || p_in.pro_in)
+        return hipErrorInvalidValue;
+    for (int c0 = 0; c0 < p_in.cols; c0 += kMaxMatvecCols) {
+        MvParams q = p_in;
+        q.cols = p_in.cols - c0 < kMaxMatvecCols ? p_in.cols - c0 : kMaxMatvecCols;
+        for (int i = 0; i < q.nseg; i++) {
+            const uint64_t off = column_bytes(q.seg[i].fmt, c0);
+            q.seg[i].w += off;
+            if (q.seg[i].w2) q.seg[i].w2 += off;
+            if (q.seg[i].x) q.seg[i].x += c0;
+        }
+        if (q.x) q.x += c0;
+        if (q.x2) q.x2 += c0;
+        const hipError_t e = launch_matvec_team(q, in, c0 == 0 ? out : OUT_ADD, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+static hipError_t launch_matvec_team(const MvParams &p_in, int in, int out, hipStream_t s) {
     MvParams p = p_in;
     int f1 = p.seg[0].fmt, f2 = f1;
     for (int i = 1; i < p.nseg; i++)

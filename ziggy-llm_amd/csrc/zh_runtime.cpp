@@ -40,7 +40,7 @@ uint64_t now_ns() {
 // Validates a matvec call: shapes, alignment of the x slot layout, buffer sizes.
 int check_matvec(ZiggyHipContext *ctx, uint32_t type, const ZiggyHipBuffer *m, size_t moff, const ZiggyHipBuffer *in,
                  const ZiggyHipBuffer *out, size_t ooff, uint32_t rows, uint32_t cols, uint64_t *stride, char *err,
-                 size_t err_len) {
+                 size_t err_len, uint32_t max_cols) {
     if (!ctx) {
         set_err(err, err_len, "null context");
         return ZIGGY_HIP_INVALID_ARGUMENT;
@@ -53,8 +53,8 @@ int check_matvec(ZiggyHipContext *ctx, uint32_t type, const ZiggyHipBuffer *m, s
         set_err(err, err_len, "row length %u must be a non-zero multiple of 64", cols);
         return ZIGGY_HIP_INVALID_ARGUMENT;
     }
-    if (cols / 64 > 256) {
-        set_err(err, err_len, "row length %u exceeds 16384", cols);
+    if (cols > max_cols) {
+        set_err(err, err_len, "row length %u exceeds %u", cols, max_cols);
         return ZIGGY_HIP_INVALID_ARGUMENT;
     }
     if (!buf_ok(m, moff + *stride * rows) || !buf_ok(in, (size_t)cols * 4) || !out ||
@@ -370,7 +370,8 @@ static int run_matvec_mode(ZiggyHipContext *ctx, uint32_t type, const ZiggyHipBu
                            uint32_t rows, uint32_t cols, int in_mode, int out_mode, const char *what, char *err,
                            size_t err_len) {
     uint64_t stride;
-    int st = check_matvec(ctx, type, m, moff, in, out, ooff, rows, cols, &stride, err, err_len);
+    // plain and SiLU inputs: rows longer than one team run as column windows
+    int st = check_matvec(ctx, type, m, moff, in, out, ooff, rows, cols, &stride, err, err_len, kMaxMatvecRowLen);
     if (st) return st;
     if (in2 && !buf_ok(in2, (size_t)cols * 4)) {
         set_err(err, err_len, "second input too small");
@@ -493,7 +494,7 @@ extern "C" int ziggy_hip_run_gemm(ZiggyHipContext *ctx, uint32_t type, const Zig
                                   const ZiggyHipBuffer *in, ZiggyHipBuffer *out, uint32_t tokens, uint32_t rows,
                                   uint32_t cols, int add, char *err, size_t err_len) {
     uint64_t stride;
-    int st = check_matvec(ctx, type, m, 0, in, out, 0, rows, cols, &stride, err, err_len);
+    int st = check_matvec(ctx, type, m, 0, in, out, 0, rows, cols, &stride, err, err_len, kMaxMatvecCols);
     if (st) return st;
     if (tokens == 0 || cols % 16 || !buf_ok(in, (size_t)tokens * cols * 4) || !buf_ok(out, (size_t)tokens * rows * 4)) {
         set_err(err, err_len, "buffers too small for a %u-token %ux%u GEMM", tokens, rows, cols);
@@ -513,7 +514,7 @@ static int indexed_common(ZiggyHipContext *ctx, uint32_t type, const ZiggyHipBuf
                           uint32_t cols, const ZiggyHipBuffer *entries, uint32_t slot, uint32_t rpe, int out_mode,
                           const char *what, char *err, size_t err_len) {
     uint64_t stride;
-    int st = check_matvec(ctx, type, ma, 0, in, outa, 0, rows, cols, &stride, err, err_len);
+    int st = check_matvec(ctx, type, ma, 0, in, outa, 0, rows, cols, &stride, err, err_len, kMaxMatvecCols);
     if (st) return st;
     if (!buf_ok(entries, (size_t)(slot + 1) * 8) || rows > rpe) {
         set_err(err, err_len, "invalid expert entries/slot");
@@ -771,7 +772,7 @@ extern "C" int ziggy_hip_time_matvec(ZiggyHipContext *ctx, uint32_t type, const 
         return ZIGGY_HIP_INVALID_ARGUMENT;
     }
     int st = check_matvec(ctx, type, m, (size_t)(copies - 1) * copy_stride, in, out, 0, rows, cols, &stride, err,
-                          err_len);
+                          err_len, kMaxMatvecCols);
     if (st) return st;
     if (copy_stride < stride * rows) {
         set_err(err, err_len, "copy stride smaller than one matrix");

@@ -331,7 +331,7 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
         (md.head_dim != 64 && md.head_dim != 96 && md.head_dim != 128 && md.head_dim != 256) ||
         md.rope_dim > md.head_dim || md.rope_style > 1 ||
         md.context_length == 0 || md.embedding_length % 64 || md.feed_forward_length % 64 ||
-        md.embedding_length / 64 > 256 || md.feed_forward_length / 64 > 256 ||
+        md.embedding_length > (uint32_t)kMaxMatvecCols || md.feed_forward_length > (uint32_t)kMaxMatvecRowLen ||
         (md.head_count * md.head_dim) % 64)
         return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "unsupported model shape");
     ZiggyHipSession *s = new (std::nothrow) ZiggyHipSession();
