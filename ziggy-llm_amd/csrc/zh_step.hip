@@ -15,27 +15,43 @@ namespace zh {
 
 // Device-side embedding lookup: hidden = dequant(token_embd[token])
 // (embeddingLookup, model/loader.zig:3391-3402); bit-exact decode.
-template <int F> __device__ void embed_row(const uint8_t *row, int cols, float *out) {
-    constexpr int V = Geom<F>::kValues, B = Geom<F>::kBytes;
-    for (int i = threadIdx.x; i < cols; i += blockDim.x) out[i] = dequant_value<F>(row + (size_t)(i / V) * B, i % V);
+// U values per thread per round, their loads issued before any store (the
+// row and the output do not alias, so the loads need not wait for the stores
+// of the round before: one memory round trip per round, not per value).
+template <int F> __device__ void embed_row(const uint8_t *__restrict__ row, int cols, float *__restrict__ out) {
+    constexpr int V = Geom<F>::kValues, B = Geom<F>::kBytes, U = 8;
+    for (int i0 = threadIdx.x; i0 < cols; i0 += blockDim.x * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = min(i0 + u * (int)blockDim.x, cols - 1);  // past the row: re-read its last value
+            v[u] = dequant_value<F>(row + (size_t)(i / V) * B, i % V);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * (int)blockDim.x;
+            if (i < cols) out[i] = v[u];
+        }
+    }
 }
 
 __global__ void step_begin_kernel(StepState *st, const uint32_t *prompt, uint32_t *history, const uint8_t *embd,
                                   uint64_t embd_stride, int embd_rows, int embd_type, int cols, float *hidden) {
     __shared__ uint32_t tok;
     if (threadIdx.x == 0) {
-        uint32_t t = st->token;
-        if (st->mode == 1) {
-            const int i = st->step;
-            if (i < st->n_prompt) {
+        // every field in one batch of loads (not one round trip per branch)
+        const StepState s = *st;
+        uint32_t t = s.token;
+        if (s.mode == 1) {
+            const int i = s.step;
+            if (i < s.n_prompt) {
                 t = prompt[i];
             } else {
-                const unsigned long long k = st->argmax;
-                t = 0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull);
-                if (i - st->n_prompt < st->n_gen) history[i - st->n_prompt] = t;
+                t = 0xFFFFFFFFu - (uint32_t)(s.argmax & 0xFFFFFFFFull);
+                if (i - s.n_prompt < s.n_gen) history[i - s.n_prompt] = t;
             }
-            st->pos = st->base_pos + i;
-            st->out_flag = (i >= st->n_prompt - 1) ? 1 : 0;
+            st->pos = s.base_pos + i;
+            st->out_flag = (i >= s.n_prompt - 1) ? 1 : 0;
             st->step = i + 1;
         }
         if (t >= (uint32_t)embd_rows) {
