@@ -2,7 +2,7 @@
 
 A "step" is one greedy decode step (one token through every layer and the
 output head).  The KV cache is first filled by a 4096-token seeded prompt
-(batched passes of up to 64 tokens on the matrix cores, the last prompt token
+(batched passes of up to 256 tokens on the matrix cores, the last prompt token
 through the decode step; the reference's runPrompt feeds the same rows token
 by token and the K/V rows agree), then W untimed warm-up steps run, then
 exactly K timed steps (positions ~4.1k).  tok/s = K / decode wall time, the reference's definition
@@ -112,7 +112,7 @@ def main():
     prefill = {"tokens": args.prompt, "ms": round(wst.prompt_ns / 1e6, 3),
                "tok_s": round(args.prompt / max(wst.prompt_ns, 1) * 1e9, 1),
                "tflops": round(ptflops, 2), "mfma_fraction_bf16": round(ptflops / MFMA_BF16_TFLOPS, 5),
-               "path": "batched passes of up to 64 tokens (MFMA GEMMs, multi-query causal attention), "
+               "path": "batched passes of up to 256 tokens (MFMA GEMMs, multi-query causal attention), "
                        "the last token through the decode step"}
     log(f"prefill {args.prompt} tokens in {wst.prompt_ns / 1e6:.1f} ms ({prefill['tok_s']} tok/s); with "
         f"{args.warmup} warm-up steps {time.time() - t0:.1f}s")

@@ -735,7 +735,17 @@ int ziggy_hip_session_step_shortlist(ZiggyHipSession *s, uint32_t token, uint32_
 static hipError_t pass_alloc(ZiggyHipSession *s);
 static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M, int pos, bool output,
                                hipStream_t st);
-constexpr uint32_t kPrefillChunk = 64;  // prompt rows per batched pass (the pass buffers' row count)
+constexpr uint32_t kPrefillMax = 256;  // prompt rows per batched pass at most (the pass buffers' row count)
+// prompt rows per batched pass (ZIGGY_HIP_PREFILL_CHUNK, 16 .. 256; a tuning knob): the whole
+// buffer by default (4096 tokens: 725 ms in passes of 64, 635 in 128, 613 in 256)
+static uint32_t prefill_chunk() {
+    static const uint32_t v = [] {
+        const char *e = getenv("ZIGGY_HIP_PREFILL_CHUNK");
+        const int c = e ? atoi(e) : (int)kPrefillMax;
+        return (uint32_t)(c < 16 ? 16 : c > (int)kPrefillMax ? (int)kPrefillMax : c);
+    }();
+    return v;
+}
 
 // Prompt rows go through batched passes on the matrix cores unless the head
 // size lacks the multi-query attention or ZIGGY_HIP_PREFILL=steps asks for
@@ -787,7 +797,7 @@ int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint3
     int bst = build_graph(s, err, err_len);
     if (bst) return bst;
     ZH_TRY(hipMemcpyAsync(s->prompt, prompt, (size_t)prompt_len * 4, hipMemcpyHostToDevice, st), "prompt upload");
-    // every prompt row but the last in batched passes of up to kPrefillChunk
+    // every prompt row but the last in batched passes of up to prefill_chunk()
     // tokens (GEMMs on the matrix cores, multi-query causal attention), the
     // last one through the step graph for its logits; the reference feeds
     // the prompt token by token (runPrompt, model/loader.zig:1016-1036)
@@ -804,8 +814,9 @@ int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint3
     ZH_TRY(hipMemcpyAsync(s->st, h, sizeof(StepState), hipMemcpyHostToDevice, st), "step state");
     ZH_TRY(hipStreamSynchronize(st), "generate setup");
     const uint64_t tp0 = now_ns();
-    for (uint32_t off = 0; off < n_batched; off += kPrefillChunk) {
-        const uint32_t m = std::min(kPrefillChunk, n_batched - off);
+    const uint32_t chunk = prefill_chunk();
+    for (uint32_t off = 0; off < n_batched; off += chunk) {
+        const uint32_t m = std::min(chunk, n_batched - off);
         ZH_TRY(pass_enqueue(s, s->prompt + off, (int)m, (int)(s->position + off), false, st), "prefill pass");
     }
     // prompt steps, then the timed decode steps (the decode_ns bracket of model/loader.zig:2135-2257)
@@ -842,7 +853,7 @@ int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint3
 // ---- speculative verify: a batch of tokens in one pass ----
 
 constexpr uint32_t kVerifyMax = 16;  // tokens of one verify pass (one MFMA token tile)
-constexpr uint32_t kPassMax = kPrefillChunk;  // token rows of one batched pass
+constexpr uint32_t kPassMax = kPrefillMax;  // token rows of one batched pass
 static_assert(kPassMax >= kVerifyMax, "a verify pass fits the pass buffers");
 
 // Row buffers of the batched passes (verify, prompt chunks), allocated on first use.
