@@ -391,7 +391,7 @@ int ziggy_hip_session_step_no_output(ZiggyHipSession *session, uint32_t token, c
                                      size_t error_message_len);
 /* Device-resident greedy generation (generateLoadedStreaming's greedy loop,
  * model/loader.zig:2065-2279): every prompt token but the last runs in
- * batched passes of up to 64 tokens on the matrix cores (the reference's
+ * batched passes of up to 256 tokens on the matrix cores (the reference's
  * runPrompt, model/loader.zig:1016-1036, steps them one by one; head sizes
  * without the multi-query attention, or ZIGGY_HIP_PREFILL=steps, step them
  * too), the last one through the decode step for its logits, then
