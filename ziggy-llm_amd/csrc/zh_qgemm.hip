@@ -12,7 +12,9 @@
 // where D_b = sum_{k in b} X[m][k] q[n][k] is one MFMA (two: the activation
 // enters as bf16 hi + lo, x = hi + lo to 2^-17 relative).  So a weight is
 // never rounded, only the activations are, at 2^-17 -- well inside the
-// 1e-4 relative-L2 bar.
+// 1e-4 relative-L2 bar.  Q4_K codes enter as 128 + c, built from their bits
+// without a conversion; the products' excess, 128 times the sub-block's
+// activation sum, goes with the minimum term.
 //
 // Product layout (v_mfma_f32_16x16x32_bf16 / 16x16x16_bf16, wave64):
 // A = activations (row i = token), B = codes (column j = weight row),
@@ -90,18 +92,25 @@ __device__ __forceinline__ s4v as_s4(uint2 v) {
     __builtin_memcpy(&r, &v, 8);
     return r;
 }
-// eight unsigned byte codes (bytes of a, b) -> bf16 x 8
-__device__ __forceinline__ uint4 codes_u8(uint32_t a, uint32_t b) {
-    return {pack_bf(ub(a, 0), ub(a, 1)), pack_bf(ub(a, 2), ub(a, 3)), pack_bf(ub(b, 0), ub(b, 1)),
-            pack_bf(ub(b, 2), ub(b, 3))};
+// four unsigned byte codes minus an offset -> bf16 x 4
+__device__ __forceinline__ uint2 codes_u4(uint32_t a, float off) {
+    return {pack_bf(ub(a, 0) - off, ub(a, 1) - off), pack_bf(ub(a, 2) - off, ub(a, 3) - off)};
 }
 __device__ __forceinline__ uint4 codes_s8(uint32_t a, uint32_t b) {
     return {pack_bf(sb(a, 0), sb(a, 1)), pack_bf(sb(a, 2), sb(a, 3)), pack_bf(sb(b, 0), sb(b, 1)),
             pack_bf(sb(b, 2), sb(b, 3))};
 }
-// four unsigned byte codes minus an offset -> bf16 x 4
-__device__ __forceinline__ uint2 codes_u4(uint32_t a, float off) {
-    return {pack_bf(ub(a, 0) - off, ub(a, 1) - off), pack_bf(ub(a, 2) - off, ub(a, 3) - off)};
+// Four byte codes c < 128 -> bf16 of 128 + c, by bits: 0x43 above a byte c
+// is the bf16 with exponent 2^7 and mantissa c, i.e. exactly 128 + c.  The
+// products then carry 128 x (the sub-block's activation sum) plus the
+// format's own offset, which the scale step takes off again (kOff).
+constexpr uint32_t kMagic43 = 0x43434343u;
+__device__ __forceinline__ uint2 codes_m4(uint32_t c) {
+    return {__builtin_amdgcn_perm(kMagic43, c, 0x04010400u), __builtin_amdgcn_perm(kMagic43, c, 0x04030402u)};
+}
+__device__ __forceinline__ uint4 codes_m8(uint32_t a, uint32_t b) {
+    const uint2 x = codes_m4(a), y = codes_m4(b);
+    return {x.x, x.y, y.x, y.y};
 }
 
 // ---- per-format chunk (256 values of one row): fields and sub-block steps ----
@@ -129,8 +138,11 @@ __device__ __forceinline__ uint32_t rw2(const uint32_t *r, int o) { return (r[o 
 
 template <int F> struct QChunk;
 
+// kOff: what the step's bf16 codes add to every weight of a sub-block (the
+// products' excess is kOff x the activation sum; 0: codes are the values).
 template <> struct QChunk<Q4_K> {
     static constexpr int kSub = 32, kSteps = 8, kCB = 144, kShm = 0;
+    static constexpr float kOff = 128.f;
     uint4 hd;     // d, dmin, 12 scale bytes
     uint2 q[4];   // qs[32 g + 8 lg .. + 7] of group g
     __device__ __forceinline__ void load(const uint32_t *r, int sh, int lg) {
@@ -157,12 +169,13 @@ template <> struct QChunk<Q4_K> {
         mn = h2f(hd.x >> 16) * (float)m;
         const uint2 w = q[j >> 1];
         const int sh = (j & 1) ? 4 : 0;
-        return codes_u8((w.x >> sh) & 0x0F0F0F0Fu, (w.y >> sh) & 0x0F0F0F0Fu);
+        return codes_m8((w.x >> sh) & 0x0F0F0F0Fu, (w.y >> sh) & 0x0F0F0F0Fu);
     }
 };
 
 template <> struct QChunk<Q8_0> {
     static constexpr int kSub = 32, kSteps = 8, kCB = 272, kShm = 0;
+    static constexpr float kOff = 0.f;
     uint2 q[8];
     uint32_t d[8];
     __device__ __forceinline__ void load(const uint32_t *r, int sh, int lg) {
@@ -181,6 +194,7 @@ template <> struct QChunk<Q8_0> {
 
 template <> struct QChunk<IQ4_XS> {
     static constexpr int kSub = 32, kSteps = 8, kCB = 136, kShm = 8;
+    static constexpr float kOff = 0.f;
     uint2 hd;     // d, scales_h, scales_l[4]
     uint2 q[8];   // qs[16 ib + 8 (lg & 1) ..]
     int hi;       // lane groups 2, 3 take the high nibbles (values 16..31)
@@ -207,6 +221,7 @@ template <> struct QChunk<IQ4_XS> {
 // 16-value sub-blocks: a step is one 16x16x16 product (four codes per lane)
 template <> struct QChunk<Q6_K> {
     static constexpr int kSub = 16, kSteps = 16, kCB = 210, kShm = 14;
+    static constexpr float kOff = 0.f;
     uint32_t ql[2][2][2];  // [half][16-run][ql offset 0 / 32]
     uint32_t qh[2][2];     // [half][16-run]
     uint4 sc;              // 16 int8 scales
@@ -238,6 +253,7 @@ template <> struct QChunk<Q6_K> {
 
 template <> struct QChunk<Q3_K> {
     static constexpr int kSub = 16, kSteps = 16, kCB = 110, kShm = 14;
+    static constexpr float kOff = 0.f;
     uint32_t qs[2][2];  // [half h][16-run]: qs[32 h + 16 r + 4 lg ..]
     uint32_t hm[2];     // [16-run]: hmask[16 r + 4 lg ..]
     uint32_t raw[3];    // 12 packed scale bytes
@@ -278,10 +294,13 @@ template <int F, bool kPair> struct QGeom {
     static constexpr int kWin = (QChunk<F>::kCB + QChunk<F>::kShm + 15) / 16;
     static constexpr int kRowW = 4 * ((kWin + 1) | 1);
     static constexpr int kPieces = 16 * kWin, kP = (kPieces + 63) / 64;  // windows per wavefront chunk, per lane
-    static constexpr bool kXsum = F == Q4_K;
+    // activation sums per sub-block: the Q4_K minimums and the code offsets
+    static constexpr bool kXsum = QChunk<F>::kOff != 0.f || F == Q4_K;
     static constexpr int kCodeBytes = 4 * kMats * 16 * kRowW * 4;
     static constexpr int kStage =
-        (2 * 16 * (2048 + 8) * 2 + (kXsum ? 2048 / 32 * 16 * 4 : 64) + kCodeBytes <= 160 * 1024) ? 2048 : 1024;
+        (2 * 16 * (2048 + 8) * 2 + (kXsum ? 2048 / QChunk<F>::kSub * 16 * 4 : 64) + kCodeBytes <= 160 * 1024)
+            ? 2048
+            : 1024;
     static constexpr int kStageChunks = kStage / kQChunk;
 };
 
@@ -352,7 +371,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     // LDS as bf16 hi / lo pieces; thread (token tt, part) stages values
     // 16 part + 256 i of its token.
     __shared__ __align__(16) unsigned short xs_s[2][16][kStage + 8];  // [hi / lo][token][k]
-    __shared__ __align__(16) float xsum_s[kXsum ? kStage / 32 : 1][16];  // [32-value sub-block][token]
+    __shared__ __align__(16) float xsum_s[kXsum ? kStage / kSub : 1][16];  // [sub-block][token]
     __shared__ __align__(16) uint32_t code_s[4][kMats][16 * kRowW];   // [wavefront][matrix][row image]
     const int tt = tid >> 4, part = tid & 15;
     const bool tok_ok = m0 + tt < M;
@@ -397,7 +416,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
                 lw[i] = l;
                 if (kXsum) sum += (ha + __uint_as_float(l << 16)) + (hb + __uint_as_float(l & 0xFFFF0000u));
             }
-            if (kXsum) sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
+            if (kXsum && kSub == 32) sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
             {
                 uint4 *dh = reinterpret_cast<uint4 *>(&xs_s[0][tt][u * kQChunk + 16 * part]);
                 uint4 *dl = reinterpret_cast<uint4 *>(&xs_s[1][tt][u * kQChunk + 16 * part]);
@@ -405,7 +424,8 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
                 dh[1] = {hw[4], hw[5], hw[6], hw[7]};
                 dl[0] = {lw[0], lw[1], lw[2], lw[3]};
                 dl[1] = {lw[4], lw[5], lw[6], lw[7]};
-                if (kXsum && !(part & 1)) xsum_s[u * 8 + (part >> 1)][tt] = sum;
+                if (kXsum && kSub == 32 && !(part & 1)) xsum_s[u * 8 + (part >> 1)][tt] = sum;
+                if (kXsum && kSub == 16) xsum_s[u * 16 + part][tt] = sum;
             }
         }
     };
@@ -452,12 +472,14 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
         for (int j = 0; j < S; j++) {
             const float s = sv[j] * live, s2 = sv2[j] * live;
             if (kXsum) {
-                const float4 xsm = *reinterpret_cast<const float4 *>(&xsum_s[cs * 8 + j][4 * lg]);
+                // s (D + kOff X) - (kOff s + min) X, X the sub-block's activation sum
+                const float4 xsm = *reinterpret_cast<const float4 *>(&xsum_s[cs * (kQChunk / kSub) + j][4 * lg]);
                 const float xm[4] = {xsm.x, xsm.y, xsm.z, xsm.w};
+                const float c = fmaf(QC::kOff, sv[j], mv[j]) * live, c2 = fmaf(QC::kOff, sv2[j], mv2[j]) * live;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    acc[q] = fmaf(s, dv[j][q], fmaf(-mv[j] * live, xm[q], acc[q]));
-                    if (kPair) acc2[q] = fmaf(s2, dv2[j][q], fmaf(-mv2[j] * live, xm[q], acc2[q]));
+                    acc[q] = fmaf(s, dv[j][q], fmaf(-c, xm[q], acc[q]));
+                    if (kPair) acc2[q] = fmaf(s2, dv2[j][q], fmaf(-c2, xm[q], acc2[q]));
                 }
             } else {
 #pragma unroll
