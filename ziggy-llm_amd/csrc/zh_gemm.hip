@@ -229,10 +229,10 @@ template <int F> static GemmKernel pick_precise(int out) {
 
 hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
-                       bool precise, int max_split) {
+                       bool precise, int max_split, const XPlanes *xp) {
     if (M < 1 || N < 1 || K < 16 || K % 16 || ldx % 4) return hipErrorInvalidValue;
     if (!precise && qgemm_enabled() && qgemm_supported(fmt, K, w, w2, stride, 0))
-        return launch_qgemm(fmt, w, w2, stride, x, ldx, y, ldy, M, N, K, out, argmax, s, max_split);
+        return launch_qgemm(fmt, w, w2, stride, x, ldx, y, ldy, M, N, K, out, argmax, s, max_split, xp);
     GemmKernel k = nullptr;
     if (precise) {
         switch (fmt) {

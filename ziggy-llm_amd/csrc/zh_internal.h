@@ -107,6 +107,36 @@ template <class P> __device__ __forceinline__ void touch_params(const P &p) {
                      "s"(at(7)), "s"(at(8)), "s"(at(9)), "s"(at(10)), "s"(at(11)));
 }
 
+// The exact-code GEMM's activation pieces (zh_qgemm.hip): x = hi + lo with
+// hi = bf16(x) and lo = bf16(x - hi), both rounded to nearest even, x = hi +
+// lo to 2^-17 relative.  One run is 16 consecutive values: eight words of
+// packed pieces each, and the sum of hi + lo over the run in one fixed order
+// (the producers and the GEMM's own staging call this same function, so the
+// sums, and hence the products, do not depend on where the split ran).
+typedef float zh_f2v __attribute__((ext_vector_type(2)));
+typedef __bf16 zh_b2v __attribute__((ext_vector_type(2)));
+// two floats -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    const zh_b2v h = __builtin_convertvector((zh_f2v){a, b}, zh_b2v);
+    uint32_t u;
+    __builtin_memcpy(&u, &h, 4);
+    return u;
+}
+__device__ __forceinline__ float split_run16(const float (&v)[16], uint32_t (&hw)[8], uint32_t (&lw)[8]) {
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float a = v[2 * i], b = v[2 * i + 1];
+        const uint32_t h = pk_bf16(a, b);
+        const float ha = __uint_as_float(h << 16), hb = __uint_as_float(h & 0xFFFF0000u);
+        const uint32_t l = pk_bf16(a - ha, b - hb);
+        hw[i] = h;
+        lw[i] = l;
+        sum += (ha + __uint_as_float(l << 16)) + (hb + __uint_as_float(l & 0xFFFF0000u));
+    }
+    return sum;
+}
+
 // Exchanges with the lane 16 or 32 apart on the vector ALU
 // (v_permlane16_swap / v_permlane32_swap of gfx950) instead of an LDS-path
 // bpermute.  Called with one value in both operands, the swap returns this
@@ -260,14 +290,29 @@ hipError_t launch_fill_u64(unsigned long long *p, unsigned long long v, int n, h
 // apart, max-ed into slots[row] (zero beforehand)
 hipError_t launch_argmax_rows(const float *x, int rows, int n, int ld, unsigned long long *slots, hipStream_t s);
 
+// Rows of activations split once for the exact-code GEMM (split_run16): row r
+// of the pieces at hi + r ld and lo + r ld, its 32-value sums at sum + r ld / 32
+// (ld a multiple of 32).  A producer writes them next to (or instead of the
+// GEMM re-splitting) its f32 rows; launch_gemm takes them as a hint.
+struct XPlanes {
+    uint16_t *hi, *lo;
+    float *sum;
+    int ld;
+};
+// rows x n values of x (row stride ldx, n a multiple of 32) into xp
+hipError_t launch_split_rows(const float *x, int ldx, int rows, int n, const XPlanes &xp, hipStream_t s);
+// gate = silu(gate) * up (as launch_silu_mul, rows x n, row stride n), also into xp
+hipError_t launch_silu_mul_split(float *gate, const float *up, int rows, int n, const XPlanes &xp, hipStream_t s);
 // MFMA GEMM for M >= 8 tokens (zh_gemm.hip): Y[m][n] (=, +=) sum_k W[n][k] X[m][k]
 // (OUT_STORE / OUT_ADD / OUT_SWIGLU with w2 / OUT_ARGMAX into argmax[M]).
 // max_split bounds the reduction split of the exact-code kernel, whose
 // partial results add atomically: 1 keeps a += product deterministic, 2 a
 // product into a cleared output (0 + a + b is the same in either order).
+// xp (optional): the same input already split (XPlanes), used when the
+// exact-code kernel runs.
 hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
-                       bool precise = false, int max_split = 16);
+                       bool precise = false, int max_split = 16, const XPlanes *xp = nullptr);
 // Up to three matrices of one format, row stride and reduction length against
 // one input (stores or adds): one launch on the exact-code kernel, else one
 // product each.
@@ -286,12 +331,13 @@ hipError_t launch_gemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uin
 bool qgemm_supported(int fmt, int K, const void *w, const void *w2, uint64_t stride, uint64_t expert_stride);
 hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                         float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
-                        int max_split = 16);
+                        int max_split = 16, const XPlanes *xp = nullptr);
 // Up to three matrices of one format, row stride and reduction length against
 // one input in one launch (matrix i: rows N[i], output y[i] with row stride ldy[i]).
 hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
                               const int *N, const uint8_t *w2, uint64_t stride, const float *x, int ldx, int M, int K,
-                              int out, unsigned long long *argmax, hipStream_t s, int max_split = 16);
+                              int out, unsigned long long *argmax, hipStream_t s, int max_split = 16,
+                              const XPlanes *xp = nullptr);
 hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride,
                                 uint64_t expert_stride, const float *x, int ldx, int x_div, float *y, int ldy, int N,
                                 int K, int out, const int *tiles, const int *list, const int *ntiles, int max_tiles,

@@ -84,6 +84,58 @@ __global__ void silu_mul_kernel(float *__restrict__ g, const float *__restrict__
     }
 }
 
+// Rows of x into the exact-code GEMM's pieces (split_run16): thread t takes
+// run t of the row-major runs (16 values; n a multiple of 32, so the two runs
+// of a 32-value sum sit in neighbouring lanes).  SILU: the values are
+// silu(x) * up first (as silu_mul_kernel), also stored back into x.
+template <bool SILU>
+__global__ void split_rows_kernel(float *__restrict__ x, const float *__restrict__ up, int ldx, int rows, int n,
+                                  XPlanes xp) {
+    const int runs = n >> 4;
+    const long long total = (long long)rows * runs;
+    const long long gi = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool ok = gi < total;
+    const long long g = ok ? gi : total - 1;  // past the end: the last run again, nothing stored
+    const int row = (int)(g / runs), r = (int)(g - (long long)row * runs);
+    float *src = x + (size_t)row * ldx + 16 * r;
+    float v[16];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const float4 q = reinterpret_cast<const float4 *>(src)[c];
+        v[4 * c] = q.x, v[4 * c + 1] = q.y, v[4 * c + 2] = q.z, v[4 * c + 3] = q.w;
+    }
+    if (SILU) {
+        const float *u = up + (size_t)row * ldx + 16 * r;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float4 q = reinterpret_cast<const float4 *>(u)[c];
+            const float uq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float g0 = v[4 * c + i];
+                v[4 * c + i] = (g0 / (1.0f + expf(-g0))) * uq[i];
+            }
+        }
+        if (ok) {
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                reinterpret_cast<float4 *>(src)[c] = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+        }
+    }
+    uint32_t hw[8], lw[8];
+    float sum = split_run16(v, hw, lw);
+    sum += __shfl_xor(sum, 1, 64);  // the other run of the 32-value sum
+    if (ok) {
+        uint4 *dh = reinterpret_cast<uint4 *>(xp.hi + (size_t)row * xp.ld + 16 * r);
+        uint4 *dl = reinterpret_cast<uint4 *>(xp.lo + (size_t)row * xp.ld + 16 * r);
+        dh[0] = {hw[0], hw[1], hw[2], hw[3]};
+        dh[1] = {hw[4], hw[5], hw[6], hw[7]};
+        dl[0] = {lw[0], lw[1], lw[2], lw[3]};
+        dl[1] = {lw[4], lw[5], lw[6], lw[7]};
+        if (!(r & 1)) xp.sum[(size_t)row * (xp.ld / 32) + (r >> 1)] = sum;
+    }
+}
+
 __global__ void add_kernel(float *__restrict__ dst, const float *__restrict__ src, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) dst[i] = dst[i] + src[i];
@@ -273,6 +325,24 @@ hipError_t launch_store_kv_half(const float *src, __half *dst, int count, hipStr
 hipError_t launch_silu_mul(float *gate, const float *up, int n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(silu_mul_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, gate, up, n);
+    return hipGetLastError();
+}
+static bool split_args_ok(int ldx, int rows, int n, const XPlanes &xp) {
+    return rows > 0 && n > 0 && n % 32 == 0 && ldx % 4 == 0 && ldx >= n && xp.hi && xp.lo && xp.sum &&
+           xp.ld % 32 == 0 && xp.ld >= n;
+}
+hipError_t launch_split_rows(const float *x, int ldx, int rows, int n, const XPlanes &xp, hipStream_t s) {
+    if (!split_args_ok(ldx, rows, n, xp)) return hipErrorInvalidValue;
+    const long long runs = (long long)rows * (n / 16);
+    hipLaunchKernelGGL(split_rows_kernel<false>, dim3((unsigned)((runs + 255) / 256)), dim3(256), 0, s,
+                       const_cast<float *>(x), nullptr, ldx, rows, n, xp);
+    return hipGetLastError();
+}
+hipError_t launch_silu_mul_split(float *gate, const float *up, int rows, int n, const XPlanes &xp, hipStream_t s) {
+    if (!split_args_ok(n, rows, n, xp) || !up) return hipErrorInvalidValue;
+    const long long runs = (long long)rows * (n / 16);
+    hipLaunchKernelGGL(split_rows_kernel<true>, dim3((unsigned)((runs + 255) / 256)), dim3(256), 0, s, gate, up, n,
+                       rows, n, xp);
     return hipGetLastError();
 }
 hipError_t launch_add(float *dst, const float *src, int n, hipStream_t s) {

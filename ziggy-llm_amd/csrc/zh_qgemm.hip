@@ -67,17 +67,13 @@ struct QGemmParams {
     const uint8_t *ws[2];
     float *ys[2];
     int Ns[2], ldys[2], gs[2];
+    // the input already split (XPlanes; the XP kernels): row r's pieces at
+    // xh / xl + r ldxs, its 32-value sums at xsum + r ldxs / 32
+    const uint16_t *xh, *xl;
+    const float *xsum;
+    int ldxs;
 };
 
-typedef float qf2v __attribute__((ext_vector_type(2)));
-typedef __bf16 qb2v __attribute__((ext_vector_type(2)));
-// two floats -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32)
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
-    const qb2v h = __builtin_convertvector((qf2v){a, b}, qb2v);
-    uint32_t u;
-    __builtin_memcpy(&u, &h, 4);
-    return u;
-}
 // bf16 bits of two small integers held as f32 (exact: the high halves)
 __device__ __forceinline__ uint32_t pack_bf(float a, float b) {
     return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
@@ -309,7 +305,7 @@ __device__ __forceinline__ uint32_t ordered_bits_q(float v) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-template <int F, int OUT, bool GROUPED, int R>
+template <int F, int OUT, bool GROUPED, int R, bool XP>
 __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     constexpr bool kPair = OUT == OUT_SWIGLU;
     using QC = QChunk<F>;
@@ -375,21 +371,44 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     __shared__ __align__(16) uint32_t code_s[4][kMats][16 * kRowW];   // [wavefront][matrix][row image]
     const int tt = tid >> 4, part = tid & 15;
     const bool tok_ok = m0 + tt < M;
+    static_assert(!XP || !kXsum || kSub == 32, "split inputs carry 32-value sums");
     const float *xrow;
+    const uint16_t *xhrow, *xlrow;
+    const float *xsrow;
     {
         const int m = min(m0 + tt, M - 1);
-        xrow = p.x + (size_t)(GROUPED ? ids[m] / p.x_div : m) * p.ldx + 16 * part;
+        const size_t r = (size_t)(GROUPED ? ids[m] / p.x_div : m);
+        xrow = p.x + r * p.ldx + 16 * part;
+        if (XP) {
+            xhrow = p.xh + r * p.ldxs + 16 * part;
+            xlrow = p.xl + r * p.ldxs + 16 * part;
+            xsrow = p.xsum + r * (p.ldxs / 32) + (part >> 1);
+        }
     }
     // stage_load issues the whole stage's activation loads (clamped to its
     // last chunk: unconditional, so the compiler's wait counting stays exact)
     // into ld; stage_store splits every chunk and writes those of the stage.
+    // XP: the pieces and sums as split by the producer (tokens past M repeat
+    // the last row; their results are never stored).
     float4 ld[kStageChunks][4];
+    float lsum[XP ? kStageChunks : 1];
     auto stage_load = [&](int kb, int nc) {
 #pragma unroll
         for (int u = 0; u < kStageChunks; u++) {
-            const float4 *src = reinterpret_cast<const float4 *>(xrow + kb + min(u, nc - 1) * kQChunk);
+            const int ko = kb + min(u, nc - 1) * kQChunk;
+            if constexpr (XP) {
+                const float4 *h = reinterpret_cast<const float4 *>(xhrow + ko);
+                const float4 *l = reinterpret_cast<const float4 *>(xlrow + ko);
+                ld[u][0] = h[0];
+                ld[u][1] = h[1];
+                ld[u][2] = l[0];
+                ld[u][3] = l[1];
+                if (kXsum) lsum[u] = xsrow[ko / 32];
+            } else {
+                const float4 *src = reinterpret_cast<const float4 *>(xrow + ko);
 #pragma unroll
-            for (int i = 0; i < 4; i++) ld[u][i] = src[i];
+                for (int i = 0; i < 4; i++) ld[u][i] = src[i];
+            }
         }
     };
     auto stage_store = [&](int nc) {
@@ -401,22 +420,28 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     __asm__ volatile("" ::"v"(ld[u][i].x), "v"(ld[u][i].y), "v"(ld[u][i].z), "v"(ld[u][i].w));
+                if (XP && kXsum) __asm__ volatile("" ::"v"(lsum[XP ? u : 0]));
                 continue;
             }
             uint32_t hw[8], lw[8];
             float sum = 0.f;
+            if constexpr (XP) {
+                // the loaded words are the pieces: hi of values 0..15, then lo
+                __builtin_memcpy(hw, &ld[u][0], 32);
+                __builtin_memcpy(lw, &ld[u][2], 32);
+                if (kXsum) sum = lsum[XP ? u : 0];
+            } else {
+                float v[16];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float4 q = ld[u][i >> 1];
-                const float a = tok_ok ? ((i & 1) ? q.z : q.x) : 0.f, b = tok_ok ? ((i & 1) ? q.w : q.y) : 0.f;
-                const uint32_t h = pk_bf16(a, b);
-                const float ha = __uint_as_float(h << 16), hb = __uint_as_float(h & 0xFFFF0000u);
-                const uint32_t l = pk_bf16(a - ha, b - hb);
-                hw[i] = h;
-                lw[i] = l;
-                if (kXsum) sum += (ha + __uint_as_float(l << 16)) + (hb + __uint_as_float(l & 0xFFFF0000u));
+                for (int i = 0; i < 4; i++) {
+                    v[4 * i] = tok_ok ? ld[u][i].x : 0.f;
+                    v[4 * i + 1] = tok_ok ? ld[u][i].y : 0.f;
+                    v[4 * i + 2] = tok_ok ? ld[u][i].z : 0.f;
+                    v[4 * i + 3] = tok_ok ? ld[u][i].w : 0.f;
+                }
+                sum = split_run16(v, hw, lw);
+                if (kXsum && kSub == 32) sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
             }
-            if (kXsum && kSub == 32) sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
             {
                 uint4 *dh = reinterpret_cast<uint4 *>(&xs_s[0][tt][u * kQChunk + 16 * part]);
                 uint4 *dl = reinterpret_cast<uint4 *>(&xs_s[1][tt][u * kQChunk + 16 * part]);
@@ -671,28 +696,35 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
 
 typedef void (*QGemmKernel)(QGemmParams);
 
-template <int F, bool G, int R> static QGemmKernel pick_q(int out) {
+template <int F, bool G, int R, bool XP> static QGemmKernel pick_q(int out) {
+    if constexpr (XP) {
+        // split inputs: the dense stores and adds (the prompt passes' o and down products)
+        if constexpr (G) return nullptr;
+        return out == OUT_STORE ? qgemm_kernel<F, OUT_STORE, G, R, XP>
+               : out == OUT_ADD ? qgemm_kernel<F, OUT_ADD, G, R, XP>
+                                : nullptr;
+    }
     switch (out) {
-    case OUT_STORE: return qgemm_kernel<F, OUT_STORE, G, R>;
+    case OUT_STORE: return qgemm_kernel<F, OUT_STORE, G, R, XP>;
     case OUT_SWIGLU:
-        if constexpr (R == 2) return qgemm_kernel<F, OUT_SWIGLU, G, R>;  // deeper rings spill
+        if constexpr (R == 2) return qgemm_kernel<F, OUT_SWIGLU, G, R, XP>;  // deeper rings spill
         return nullptr;
-    case OUT_ADD: return G ? nullptr : qgemm_kernel<F, OUT_ADD, G, R>;
-    case OUT_ARGMAX: return G ? nullptr : qgemm_kernel<F, OUT_ARGMAX, G, R>;
+    case OUT_ADD: return G ? nullptr : qgemm_kernel<F, OUT_ADD, G, R, XP>;
+    case OUT_ARGMAX: return G ? nullptr : qgemm_kernel<F, OUT_ARGMAX, G, R, XP>;
     default: return nullptr;
     }
 }
 
 // ring depth: 4 chunks, or 2 for the two matrices of SWIGLU (the same bytes in
 // flight) and for reduction ranges of two chunks
-template <bool G> static QGemmKernel pick_qf(int fmt, int out, int K) {
+template <bool G, bool XP> static QGemmKernel pick_qf(int fmt, int out, int K) {
     const bool r2 = K / kQChunk <= 2 || out == OUT_SWIGLU;
     switch (fmt) {
-    case Q4_K: return r2 ? pick_q<Q4_K, G, 2>(out) : pick_q<Q4_K, G, 4>(out);
-    case Q6_K: return r2 ? pick_q<Q6_K, G, 2>(out) : pick_q<Q6_K, G, 4>(out);
-    case Q8_0: return r2 ? pick_q<Q8_0, G, 2>(out) : pick_q<Q8_0, G, 4>(out);
-    case IQ4_XS: return r2 ? pick_q<IQ4_XS, G, 2>(out) : pick_q<IQ4_XS, G, 4>(out);
-    case Q3_K: return r2 ? pick_q<Q3_K, G, 2>(out) : pick_q<Q3_K, G, 4>(out);
+    case Q4_K: return r2 ? pick_q<Q4_K, G, 2, XP>(out) : pick_q<Q4_K, G, 4, XP>(out);
+    case Q6_K: return r2 ? pick_q<Q6_K, G, 2, XP>(out) : pick_q<Q6_K, G, 4, XP>(out);
+    case Q8_0: return r2 ? pick_q<Q8_0, G, 2, XP>(out) : pick_q<Q8_0, G, 4, XP>(out);
+    case IQ4_XS: return r2 ? pick_q<IQ4_XS, G, 2, XP>(out) : pick_q<IQ4_XS, G, 4, XP>(out);
+    case Q3_K: return r2 ? pick_q<Q3_K, G, 2, XP>(out) : pick_q<Q3_K, G, 4, XP>(out);
     default: return nullptr;
     }
 }
@@ -753,7 +785,7 @@ static double qgemm_stage_weight() {
 
 hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
                               const int *N, const uint8_t *w2, uint64_t stride, const float *x, int ldx, int M, int K,
-                              int out, unsigned long long *argmax, hipStream_t s, int max_split) {
+                              int out, unsigned long long *argmax, hipStream_t s, int max_split, const XPlanes *xp) {
     if (nseg < 1 || nseg > 3 || M < 1 || ldx % 4 || (nseg > 1 && (out == OUT_SWIGLU || out == OUT_ARGMAX)))
         return hipErrorInvalidValue;
     QGemmParams p{w[0], w2, stride, x, y[0], M, N[0], K, ldx, ldy[0], argmax, nullptr, nullptr, nullptr, 1, 0, 1};
@@ -798,7 +830,12 @@ hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float 
             while (groups * tiles * ks * 2 <= target && chunks % (ks * 2) == 0 && ks * 2 <= max_split) ks *= 2;
     }
     p.ksplit = ks;
-    QGemmKernel k = pick_qf<false>(fmt, out, K / ks);
+    QGemmKernel k = nullptr;
+    if (xp && xp->hi && xp->lo && xp->sum && xp->ld % 32 == 0 && K <= xp->ld) {
+        k = pick_qf<false, true>(fmt, out, K / ks);
+        if (k) p.xh = xp->hi, p.xl = xp->lo, p.xsum = xp->sum, p.ldxs = xp->ld;
+    }
+    if (!k) k = pick_qf<false, false>(fmt, out, K / ks);
     if (!k) return hipErrorInvalidValue;
     if (ks > 1 && out == OUT_STORE) {
         for (int i = 0; i < nseg; i++) {
@@ -813,8 +850,8 @@ hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float 
 
 hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                         float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
-                        int max_split) {
-    return launch_qgemm_multi(fmt, 1, &w, &y, &ldy, &N, w2, stride, x, ldx, M, K, out, argmax, s, max_split);
+                        int max_split, const XPlanes *xp) {
+    return launch_qgemm_multi(fmt, 1, &w, &y, &ldy, &N, w2, stride, x, ldx, M, K, out, argmax, s, max_split, xp);
 }
 
 hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride,
@@ -823,7 +860,7 @@ hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, ui
                                 hipStream_t s) {
     if (N < 1 || !qgemm_supported(fmt, K, w, w2, stride, expert_stride) || ldx % 4 || max_tiles < 1 || x_div < 1)
         return hipErrorInvalidValue;
-    QGemmKernel k = pick_qf<true>(fmt, out, K);
+    QGemmKernel k = pick_qf<true, false>(fmt, out, K);
     if (!k) return hipErrorInvalidValue;
     QGemmParams p{w, w2, stride, x, y, 16, N, K, ldx, ldy, nullptr, tiles, list, ntiles, x_div, expert_stride, 1};
     p.groups = (N + kQRows - 1) / kQRows;

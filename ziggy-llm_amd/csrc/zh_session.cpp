@@ -74,6 +74,7 @@ struct ZiggyHipSession {
     // multi-query attention of a verify pass: partials and arrival counters
     // of head_count_kv * query-group slots
     float *b_part_o = nullptr, *b_part_ml = nullptr;
+    zh::XPlanes xp{};  // the o and down products' inputs, split once per pass
     unsigned *b_counters = nullptr;
     uint32_t position = 0;
     // the token whose K/V rows sit at each position below `position`, while
@@ -873,6 +874,17 @@ static hipError_t pass_alloc(ZiggyHipSession *s) {
         if (e != hipSuccess) return e;
         s->allocs.push_back(*r.p);
     }
+    {
+        const size_t ld = (std::max(Q, F) + 31) / 32 * 32;
+        uint8_t *base = nullptr;
+        hipError_t e = hipMalloc((void **)&base, M * ld * 4 + M * (ld / 32) * 4);
+        if (e != hipSuccess) return e;
+        s->allocs.push_back(base);
+        s->xp.hi = reinterpret_cast<uint16_t *>(base);
+        s->xp.lo = s->xp.hi + M * ld;
+        s->xp.sum = reinterpret_cast<float *>(s->xp.lo + M * ld);
+        s->xp.ld = (int)ld;
+    }
     if (attention_multi_supported((int)s->md.head_dim)) {
         const size_t slots = (size_t)s->md.head_count_kv *
                              attention_query_groups((int)s->md.head_count, (int)s->md.head_count_kv, (int)M);
@@ -921,11 +933,16 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
     // tile) keep the split for speed; their sums vary in the last bits.
     const bool det = !output;
     const int split_add = det ? 1 : 16, split_clear = det ? 2 : 16;
-    auto gemm = [&](const DT &w, const DT *w2, const float *x, int ldx, float *y, int ldy, int out) {
+    auto gemm = [&](const DT &w, const DT *w2, const float *x, int ldx, float *y, int ldy, int out,
+                    const XPlanes *xp = nullptr) {
         if (e != hipSuccess) return;
         e = launch_gemm(w.type, w.p, w2 ? w2->p : nullptr, w.stride, x, ldx, y, ldy, M, (int)w.rows, (int)w.cols,
-                        out, s->b_argmax, st, false, out == OUT_ADD ? split_add : split_clear);
+                        out, s->b_argmax, st, false, out == OUT_ADD ? split_add : split_clear, xp);
     };
+    // The o and down products take their inputs as pieces split once here
+    // (one workgroup per row group: each would split the whole rows again);
+    // in a verify pass (one token tile, split reductions) o splits its own.
+    const bool split_o = det && Q % 32 == 0, split_down = F % 32 == 0;
     // products of the normed rows that accumulate (OUT_ADD) onto cleared
     // outputs: one launch for the matrices that share a format and row size
     auto multi3 = [&](const DT &a, float *ya, int lda, const DT &b, float *yb, int ldb, const DT *c, float *yc,
@@ -1028,7 +1045,9 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
             a.ctx = (int)md.context_length;
             e = launch_attention(a, st);
         }
-        gemm(L.o, nullptr, s->b_attn, Q, s->b_hidden, H, OUT_ADD);
+        if (split_o && e == hipSuccess) e = launch_split_rows(s->b_attn, Q, M, Q, s->xp, st);
+        gemm(L.o, nullptr, s->b_attn, Q, s->b_hidden, H, OUT_ADD, split_o ? &s->xp : nullptr);
+        bool down_split = false;
         if (fused_swiglu && L.gate.type == L.up.type) {
             if (e == hipSuccess)
                 e = launch_rms_norm_rows(s->b_hidden, (const float *)L.ffn_norm.p, s->b_normed, M, H, eps, st);
@@ -1040,9 +1059,12 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
                 e = launch_rms_norm_rows(s->b_hidden, (const float *)L.ffn_norm.p, s->b_normed, M, H, eps, st,
                                          s->b_act, (size_t)M * F, s->b_up, (size_t)M * F);
             multi3(L.gate, s->b_act, F, L.up, s->b_up, F, nullptr, nullptr, 0);
-            if (e == hipSuccess) e = launch_silu_mul(s->b_act, s->b_up, M * F, st);
+            down_split = split_down;
+            if (e == hipSuccess)
+                e = down_split ? launch_silu_mul_split(s->b_act, s->b_up, M, F, s->xp, st)
+                               : launch_silu_mul(s->b_act, s->b_up, M * F, st);
         }
-        gemm(L.down, nullptr, s->b_act, F, s->b_hidden, H, OUT_ADD);
+        gemm(L.down, nullptr, s->b_act, F, s->b_hidden, H, OUT_ADD, down_split ? &s->xp : nullptr);
     }
     if (!output) return e;  // a prompt chunk: K/V rows only
     // the final norm also clears the argmax keys; the output product stores
