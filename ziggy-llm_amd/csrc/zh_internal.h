@@ -318,7 +318,7 @@ hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t st
 // product each.
 hipError_t launch_gemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
                              const int *N, uint64_t stride, const float *x, int ldx, int M, int K, int out,
-                             hipStream_t s, int max_split = 16);
+                             hipStream_t s, int max_split = 16, const XPlanes *xp = nullptr);
 hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps, hipStream_t s,
                                 float *clear0 = nullptr, size_t n0 = 0, float *clear1 = nullptr, size_t n1 = 0,
                                 float *clear2 = nullptr, size_t n2 = 0);

@@ -283,9 +283,10 @@ template <> struct QChunk<Q3_K> {
 // Geometry of the kernel for format F (two matrices for SWIGLU).  A chunk row
 // at any offset kShm allows lies in kWin 16-byte windows; its LDS image has
 // one spare window (a word read past the last byte) and an odd window count,
-// so the 16 rows' words fall in distinct banks.  The activation stage is as
-// long as LDS allows next to the code images (2048 or 1024 values).
-template <int F, bool kPair> struct QGeom {
+// so the 16 rows' words fall in distinct banks.  The activation stage (TT
+// token tiles of 16) is as long as LDS allows next to the code images (2048,
+// 1024 or 512 values).
+template <int F, bool kPair, int TT = 1> struct QGeom {
     static constexpr int kMats = kPair ? 2 : 1;
     static constexpr int kWin = (QChunk<F>::kCB + QChunk<F>::kShm + 15) / 16;
     static constexpr int kRowW = 4 * ((kWin + 1) | 1);
@@ -293,10 +294,15 @@ template <int F, bool kPair> struct QGeom {
     // activation sums per sub-block: the Q4_K minimums and the code offsets
     static constexpr bool kXsum = QChunk<F>::kOff != 0.f || F == Q4_K;
     static constexpr int kCodeBytes = 4 * kMats * 16 * kRowW * 4;
-    static constexpr int kStage =
-        (2 * 16 * (2048 + 8) * 2 + (kXsum ? 2048 / QChunk<F>::kSub * 16 * 4 : 64) + kCodeBytes <= 160 * 1024)
-            ? 2048
-            : 1024;
+    static constexpr int lds_bytes(int st) {
+        return 2 * 16 * TT * (st + 8) * 2 + (kXsum ? st / QChunk<F>::kSub * 16 * TT * 4 : 64) + kCodeBytes;
+    }
+    // two token tiles: a 512-value stage where it leaves LDS for two
+    // workgroups per CU (one stages or waits while the other computes)
+    static constexpr int kStage = TT == 2 && lds_bytes(512) <= 80 * 1024 ? 512
+                                  : lds_bytes(2048) <= 160 * 1024        ? 2048
+                                  : lds_bytes(1024) <= 160 * 1024        ? 1024
+                                                                         : 512;
     static constexpr int kStageChunks = kStage / kQChunk;
 };
 
@@ -305,11 +311,14 @@ __device__ __forceinline__ uint32_t ordered_bits_q(float v) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// XP: the input comes split (XPlanes) and a workgroup takes two token tiles
+// (32 tokens): every decoded code serves both tiles' products.
 template <int F, int OUT, bool GROUPED, int R, bool XP>
 __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     constexpr bool kPair = OUT == OUT_SWIGLU;
+    constexpr int TT = XP ? 2 : 1;  // token tiles of 16 per workgroup
     using QC = QChunk<F>;
-    using G = QGeom<F, kPair>;
+    using G = QGeom<F, kPair, TT>;
     constexpr int kSub = QC::kSub, kCB = QC::kCB, kShm = QC::kShm;
     constexpr int kMats = G::kMats, kWin = G::kWin, kRowW = G::kRowW, kPieces = G::kPieces, kP = G::kP;
     constexpr bool kXsum = G::kXsum;
@@ -318,7 +327,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
 
     touch_params(p);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
-    int m0 = blockIdx.y * 16, M = p.M;
+    int m0 = blockIdx.y * 16 * TT, M = p.M;
     const int *ids = nullptr;
     const uint8_t *w = p.w, *w2 = p.w2;
     if (GROUPED) {
@@ -363,26 +372,29 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
         ca = cb + tc - gi * nspan;
     };
 
-    // The activations of a stage (up to kStage values of all 16 tokens) sit in
-    // LDS as bf16 hi / lo pieces; thread (token tt, part) stages values
-    // 16 part + 256 i of its token.
-    __shared__ __align__(16) unsigned short xs_s[2][16][kStage + 8];  // [hi / lo][token][k]
-    __shared__ __align__(16) float xsum_s[kXsum ? kStage / kSub : 1][16];  // [sub-block][token]
-    __shared__ __align__(16) uint32_t code_s[4][kMats][16 * kRowW];   // [wavefront][matrix][row image]
+    // The activations of a stage (up to kStage values of all 16 TT tokens)
+    // sit in LDS as bf16 hi / lo pieces; thread (token tt, part) stages values
+    // 16 part + 256 i of tokens tt, tt + 16, ...
+    constexpr int NT = 16 * TT;
+    __shared__ __align__(16) unsigned short xs_s[2][NT][kStage + 8];        // [hi / lo][token][k]
+    __shared__ __align__(16) float xsum_s[kXsum ? kStage / kSub : 1][NT];   // [sub-block][token]
+    __shared__ __align__(16) uint32_t code_s[4][kMats][16 * kRowW];        // [wavefront][matrix][row image]
     const int tt = tid >> 4, part = tid & 15;
-    const bool tok_ok = m0 + tt < M;
     static_assert(!XP || !kXsum || kSub == 32, "split inputs carry 32-value sums");
-    const float *xrow;
-    const uint16_t *xhrow, *xlrow;
-    const float *xsrow;
-    {
-        const int m = min(m0 + tt, M - 1);
+    bool tok_ok[TT];
+    const float *xrow[TT];
+    const uint16_t *xhrow[TT], *xlrow[TT];
+    const float *xsrow[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+        tok_ok[t] = m0 + 16 * t + tt < M;
+        const int m = min(m0 + 16 * t + tt, M - 1);
         const size_t r = (size_t)(GROUPED ? ids[m] / p.x_div : m);
-        xrow = p.x + r * p.ldx + 16 * part;
+        xrow[t] = p.x + r * p.ldx + 16 * part;
         if (XP) {
-            xhrow = p.xh + r * p.ldxs + 16 * part;
-            xlrow = p.xl + r * p.ldxs + 16 * part;
-            xsrow = p.xsum + r * (p.ldxs / 32) + (part >> 1);
+            xhrow[t] = p.xh + r * p.ldxs + 16 * part;
+            xlrow[t] = p.xl + r * p.ldxs + 16 * part;
+            xsrow[t] = p.xsum + r * (p.ldxs / 32) + (part >> 1);
         }
     }
     // stage_load issues the whole stage's activation loads (clamped to its
@@ -390,127 +402,147 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     // into ld; stage_store splits every chunk and writes those of the stage.
     // XP: the pieces and sums as split by the producer (tokens past M repeat
     // the last row; their results are never stored).
-    float4 ld[kStageChunks][4];
-    float lsum[XP ? kStageChunks : 1];
+    float4 ld[TT][kStageChunks][4];
+    float lsum[TT][XP ? kStageChunks : 1];
     auto stage_load = [&](int kb, int nc) {
 #pragma unroll
-        for (int u = 0; u < kStageChunks; u++) {
-            const int ko = kb + min(u, nc - 1) * kQChunk;
-            if constexpr (XP) {
-                const float4 *h = reinterpret_cast<const float4 *>(xhrow + ko);
-                const float4 *l = reinterpret_cast<const float4 *>(xlrow + ko);
-                ld[u][0] = h[0];
-                ld[u][1] = h[1];
-                ld[u][2] = l[0];
-                ld[u][3] = l[1];
-                if (kXsum) lsum[u] = xsrow[ko / 32];
-            } else {
-                const float4 *src = reinterpret_cast<const float4 *>(xrow + ko);
+        for (int t = 0; t < TT; t++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) ld[u][i] = src[i];
+            for (int u = 0; u < kStageChunks; u++) {
+                const int ko = kb + min(u, nc - 1) * kQChunk;
+                if constexpr (XP) {
+                    const float4 *h = reinterpret_cast<const float4 *>(xhrow[t] + ko);
+                    const float4 *l = reinterpret_cast<const float4 *>(xlrow[t] + ko);
+                    ld[t][u][0] = h[0];
+                    ld[t][u][1] = h[1];
+                    ld[t][u][2] = l[0];
+                    ld[t][u][3] = l[1];
+                    if (kXsum) lsum[t][XP ? u : 0] = xsrow[t][ko / 32];
+                } else {
+                    const float4 *src = reinterpret_cast<const float4 *>(xrow[t] + ko);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) ld[t][u][i] = src[i];
+                }
             }
-        }
     };
     auto stage_store = [&](int nc) {
 #pragma unroll
-        for (int u = 0; u < kStageChunks; u++) {
-            if (u >= nc) {
-                // past the range: the loads still land -- consumed here, so the
-                // compiler's wait counting sees them complete on every path
+        for (int t = 0; t < TT; t++)
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    __asm__ volatile("" ::"v"(ld[u][i].x), "v"(ld[u][i].y), "v"(ld[u][i].z), "v"(ld[u][i].w));
-                if (XP && kXsum) __asm__ volatile("" ::"v"(lsum[XP ? u : 0]));
-                continue;
-            }
-            uint32_t hw[8], lw[8];
-            float sum = 0.f;
-            if constexpr (XP) {
-                // the loaded words are the pieces: hi of values 0..15, then lo
-                __builtin_memcpy(hw, &ld[u][0], 32);
-                __builtin_memcpy(lw, &ld[u][2], 32);
-                if (kXsum) sum = lsum[XP ? u : 0];
-            } else {
-                float v[16];
+            for (int u = 0; u < kStageChunks; u++) {
+                if (u >= nc) {
+                    // past the range: the loads still land -- consumed here, so the
+                    // compiler's wait counting sees them complete on every path
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    v[4 * i] = tok_ok ? ld[u][i].x : 0.f;
-                    v[4 * i + 1] = tok_ok ? ld[u][i].y : 0.f;
-                    v[4 * i + 2] = tok_ok ? ld[u][i].z : 0.f;
-                    v[4 * i + 3] = tok_ok ? ld[u][i].w : 0.f;
+                    for (int i = 0; i < 4; i++)
+                        __asm__ volatile("" ::"v"(ld[t][u][i].x), "v"(ld[t][u][i].y), "v"(ld[t][u][i].z),
+                                         "v"(ld[t][u][i].w));
+                    if (XP && kXsum) __asm__ volatile("" ::"v"(lsum[t][XP ? u : 0]));
+                    continue;
                 }
-                sum = split_run16(v, hw, lw);
-                if (kXsum && kSub == 32) sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
-            }
-            {
-                uint4 *dh = reinterpret_cast<uint4 *>(&xs_s[0][tt][u * kQChunk + 16 * part]);
-                uint4 *dl = reinterpret_cast<uint4 *>(&xs_s[1][tt][u * kQChunk + 16 * part]);
+                uint32_t hw[8], lw[8];
+                float sum = 0.f;
+                if constexpr (XP) {
+                    // the loaded words are the pieces: hi of values 0..15, then lo
+                    __builtin_memcpy(hw, &ld[t][u][0], 32);
+                    __builtin_memcpy(lw, &ld[t][u][2], 32);
+                    if (kXsum) sum = lsum[t][XP ? u : 0];
+                } else {
+                    float v[16];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        v[4 * i] = tok_ok[t] ? ld[t][u][i].x : 0.f;
+                        v[4 * i + 1] = tok_ok[t] ? ld[t][u][i].y : 0.f;
+                        v[4 * i + 2] = tok_ok[t] ? ld[t][u][i].z : 0.f;
+                        v[4 * i + 3] = tok_ok[t] ? ld[t][u][i].w : 0.f;
+                    }
+                    sum = split_run16(v, hw, lw);
+                    if (kXsum && kSub == 32) sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
+                }
+                const int tk = 16 * t + tt;
+                uint4 *dh = reinterpret_cast<uint4 *>(&xs_s[0][tk][u * kQChunk + 16 * part]);
+                uint4 *dl = reinterpret_cast<uint4 *>(&xs_s[1][tk][u * kQChunk + 16 * part]);
                 dh[0] = {hw[0], hw[1], hw[2], hw[3]};
                 dh[1] = {hw[4], hw[5], hw[6], hw[7]};
                 dl[0] = {lw[0], lw[1], lw[2], lw[3]};
                 dl[1] = {lw[4], lw[5], lw[6], lw[7]};
-                if (kXsum && kSub == 32 && !(part & 1)) xsum_s[u * 8 + (part >> 1)][tt] = sum;
-                if (kXsum && kSub == 16) xsum_s[u * 16 + part][tt] = sum;
+                if (kXsum && kSub == 32 && !(part & 1)) xsum_s[u * 8 + (part >> 1)][tk] = sum;
+                if (kXsum && kSub == 16) xsum_s[u * 16 + part][tk] = sum;
             }
-        }
     };
 
-    qf4v acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+    qf4v acc[TT], acc2[TT];
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[t] = acc2[t] = qf4v{0.f, 0.f, 0.f, 0.f};
     // chunk cs of the stage (offset 256 cs in LDS)
     // All products of the chunk first (independent accumulators, so the
-    // matrix core pipelines them), then the scales.
+    // matrix core pipelines them), then the scales.  A step's codes are
+    // decoded once for the TT token tiles.
     auto compute = [&](const QC &r, const QC &r2, int cs, float live) {
         constexpr int S = QC::kSteps;
         const qf4v zero = {0.f, 0.f, 0.f, 0.f};
-        qf4v dv[S], dv2[S];
+        qf4v dv[TT][S], dv2[TT][S];
         float sv[S], mv[S], sv2[S], mv2[S];
 #pragma unroll
         for (int j = 0; j < S; j++) {
             mv[j] = 0.f, sv2[j] = 0.f, mv2[j] = 0.f;
-            dv2[j] = zero;
             const int kx = cs * kQChunk + kSub * j;
             if constexpr (kSub == 32) {
-                const bf8v ah = as_bf8(*reinterpret_cast<const uint4 *>(&xs_s[0][li][kx + 8 * lg]));
-                const bf8v al = as_bf8(*reinterpret_cast<const uint4 *>(&xs_s[1][li][kx + 8 * lg]));
                 const bf8v b = as_bf8(r.step(j, sv[j], mv[j]));
-                dv[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, zero, 0, 0, 0);
-                dv[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, dv[j], 0, 0, 0);
-                if (kPair) {
-                    const bf8v b2 = as_bf8(r2.step(j, sv2[j], mv2[j]));
-                    dv2[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b2, zero, 0, 0, 0);
-                    dv2[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b2, dv2[j], 0, 0, 0);
+                bf8v b2 = b;
+                if (kPair) b2 = as_bf8(r2.step(j, sv2[j], mv2[j]));
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    const bf8v ah = as_bf8(*reinterpret_cast<const uint4 *>(&xs_s[0][16 * t + li][kx + 8 * lg]));
+                    const bf8v al = as_bf8(*reinterpret_cast<const uint4 *>(&xs_s[1][16 * t + li][kx + 8 * lg]));
+                    dv[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, zero, 0, 0, 0);
+                    dv[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, dv[t][j], 0, 0, 0);
+                    dv2[t][j] = zero;
+                    if (kPair) {
+                        dv2[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b2, zero, 0, 0, 0);
+                        dv2[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b2, dv2[t][j], 0, 0, 0);
+                    }
                 }
             } else {
-                const s4v ah = as_s4(*reinterpret_cast<const uint2 *>(&xs_s[0][li][kx + 4 * lg]));
-                const s4v al = as_s4(*reinterpret_cast<const uint2 *>(&xs_s[1][li][kx + 4 * lg]));
                 const s4v b = as_s4(r.step(j, sv[j]));
-                dv[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, b, zero, 0, 0, 0);
-                dv[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, b, dv[j], 0, 0, 0);
-                if (kPair) {
-                    const s4v b2 = as_s4(r2.step(j, sv2[j]));
-                    dv2[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, b2, zero, 0, 0, 0);
-                    dv2[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, b2, dv2[j], 0, 0, 0);
+                s4v b2 = b;
+                if (kPair) b2 = as_s4(r2.step(j, sv2[j]));
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    const s4v ah = as_s4(*reinterpret_cast<const uint2 *>(&xs_s[0][16 * t + li][kx + 4 * lg]));
+                    const s4v al = as_s4(*reinterpret_cast<const uint2 *>(&xs_s[1][16 * t + li][kx + 4 * lg]));
+                    dv[t][j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, b, zero, 0, 0, 0);
+                    dv[t][j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, b, dv[t][j], 0, 0, 0);
+                    dv2[t][j] = zero;
+                    if (kPair) {
+                        dv2[t][j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, b2, zero, 0, 0, 0);
+                        dv2[t][j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, b2, dv2[t][j], 0, 0, 0);
+                    }
                 }
             }
         }
 #pragma unroll
         for (int j = 0; j < S; j++) {
             const float s = sv[j] * live, s2 = sv2[j] * live;
-            if (kXsum) {
-                // s (D + kOff X) - (kOff s + min) X, X the sub-block's activation sum
-                const float4 xsm = *reinterpret_cast<const float4 *>(&xsum_s[cs * (kQChunk / kSub) + j][4 * lg]);
-                const float xm[4] = {xsm.x, xsm.y, xsm.z, xsm.w};
-                const float c = fmaf(QC::kOff, sv[j], mv[j]) * live, c2 = fmaf(QC::kOff, sv2[j], mv2[j]) * live;
+            const float c = fmaf(QC::kOff, sv[j], mv[j]) * live, c2 = fmaf(QC::kOff, sv2[j], mv2[j]) * live;
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    acc[q] = fmaf(s, dv[j][q], fmaf(-c, xm[q], acc[q]));
-                    if (kPair) acc2[q] = fmaf(s2, dv2[j][q], fmaf(-c2, xm[q], acc2[q]));
-                }
-            } else {
+            for (int t = 0; t < TT; t++) {
+                if (kXsum) {
+                    // s (D + kOff X) - (kOff s + min) X, X the sub-block's activation sum
+                    const float4 xsm =
+                        *reinterpret_cast<const float4 *>(&xsum_s[cs * (kQChunk / kSub) + j][16 * t + 4 * lg]);
+                    const float xm[4] = {xsm.x, xsm.y, xsm.z, xsm.w};
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    acc[q] = fmaf(s, dv[j][q], acc[q]);
-                    if (kPair) acc2[q] = fmaf(s2, dv2[j][q], acc2[q]);
+                    for (int q = 0; q < 4; q++) {
+                        acc[t][q] = fmaf(s, dv[t][j][q], fmaf(-c, xm[q], acc[t][q]));
+                        if (kPair) acc2[t][q] = fmaf(s2, dv2[t][j][q], fmaf(-c2, xm[q], acc2[t][q]));
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        acc[t][q] = fmaf(s, dv[t][j][q], acc[t][q]);
+                        if (kPair) acc2[t][q] = fmaf(s2, dv2[t][j][q], acc2[t][q]);
+                    }
                 }
             }
         }
@@ -599,48 +631,51 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
             }
         }
     };
-    // The results of group g: D[token 4 lg + r][row li]; acc cleared after.
+    // The results of group g: D[token 16 t + 4 lg + r][row li]; acc cleared after.
     auto epilogue = [&](int g) {
         const Seg sg = seg_of(g);
         const int nn = (g - sg.g0) * kQRows + 16 * wave + li;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int j = m0 + 4 * lg + r;  // token of result r
-            if (j >= M || nn >= sg.N) continue;
-            const int jrow = GROUPED ? ids[4 * lg + r] : j;
-            float *dst = sg.y ? sg.y + (size_t)jrow * sg.ldy + nn : nullptr;
-            const float v = acc[r];
-            if ((OUT == OUT_STORE || OUT == OUT_ADD) && p.ksplit > 1) {
-                atomicAdd(dst, v);  // partial sum of this workgroup's reduction range (STORE rows zeroed first)
-            } else if (OUT == OUT_STORE) {
-                *dst = v;
-            } else if (OUT == OUT_ADD) {
-                *dst = *dst + v;
-            } else if (OUT == OUT_SWIGLU) {
-                *dst = (v / (1.0f + expf(-v))) * acc2[r];
-            }
-        }
-        if (OUT == OUT_ARGMAX) {
-            // token 4 lg + r: the largest value over the 16 rows of lanes li, then the lowest row
+        for (int t = 0; t < TT; t++) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int j = m0 + 4 * lg + r;
-                const float v = acc[r];
-                if (sg.y && j < M && nn < sg.N) sg.y[(size_t)j * sg.ldy + nn] = v;
-                unsigned long long key = (j < M && nn < sg.N)
-                                             ? ((unsigned long long)ordered_bits_q(v) << 32) |
-                                                   (unsigned long long)(0xFFFFFFFFu - (uint32_t)nn)
-                                             : 0ull;
-#pragma unroll
-                for (int o = 1; o < 16; o <<= 1) {
-                    const unsigned long long k2 = __shfl_xor(key, o, 64);
-                    key = k2 > key ? k2 : key;
+                const int j = m0 + 16 * t + 4 * lg + r;  // token of result r
+                if (j >= M || nn >= sg.N) continue;
+                const int jrow = GROUPED ? ids[16 * t + 4 * lg + r] : j;
+                float *dst = sg.y ? sg.y + (size_t)jrow * sg.ldy + nn : nullptr;
+                const float v = acc[t][r];
+                if ((OUT == OUT_STORE || OUT == OUT_ADD) && p.ksplit > 1) {
+                    atomicAdd(dst, v);  // partial sum of this workgroup's reduction range (STORE rows zeroed first)
+                } else if (OUT == OUT_STORE) {
+                    *dst = v;
+                } else if (OUT == OUT_ADD) {
+                    *dst = *dst + v;
+                } else if (OUT == OUT_SWIGLU) {
+                    *dst = (v / (1.0f + expf(-v))) * acc2[t][r];
                 }
-                if (li == 0 && key) atomicMax(p.argmax + j, key);
             }
+            if (OUT == OUT_ARGMAX) {
+                // token 4 lg + r: the largest value over the 16 rows of lanes li, then the lowest row
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int j = m0 + 16 * t + 4 * lg + r;
+                    const float v = acc[t][r];
+                    if (sg.y && j < M && nn < sg.N) sg.y[(size_t)j * sg.ldy + nn] = v;
+                    unsigned long long key = (j < M && nn < sg.N)
+                                                 ? ((unsigned long long)ordered_bits_q(v) << 32) |
+                                                       (unsigned long long)(0xFFFFFFFFu - (uint32_t)nn)
+                                                 : 0ull;
+#pragma unroll
+                    for (int o = 1; o < 16; o <<= 1) {
+                        const unsigned long long k2 = __shfl_xor(key, o, 64);
+                        key = k2 > key ? k2 : key;
+                    }
+                    if (li == 0 && key) atomicMax(p.argmax + j, key);
+                }
+            }
+            acc[t] = qf4v{0.f, 0.f, 0.f, 0.f};
+            acc2[t] = qf4v{0.f, 0.f, 0.f, 0.f};
         }
-        acc = qf4v{0.f, 0.f, 0.f, 0.f};
-        acc2 = qf4v{0.f, 0.f, 0.f, 0.f};
     };
 
     if (nspan <= kStageChunks) {
@@ -698,27 +733,31 @@ typedef void (*QGemmKernel)(QGemmParams);
 
 template <int F, bool G, int R, bool XP> static QGemmKernel pick_q(int out) {
     if constexpr (XP) {
-        // split inputs: the dense stores and adds (the prompt passes' o and down products)
-        if constexpr (G) return nullptr;
-        return out == OUT_STORE ? qgemm_kernel<F, OUT_STORE, G, R, XP>
-               : out == OUT_ADD ? qgemm_kernel<F, OUT_ADD, G, R, XP>
-                                : nullptr;
-    }
-    switch (out) {
-    case OUT_STORE: return qgemm_kernel<F, OUT_STORE, G, R, XP>;
-    case OUT_SWIGLU:
-        if constexpr (R == 2) return qgemm_kernel<F, OUT_SWIGLU, G, R, XP>;  // deeper rings spill
-        return nullptr;
-    case OUT_ADD: return G ? nullptr : qgemm_kernel<F, OUT_ADD, G, R, XP>;
-    case OUT_ARGMAX: return G ? nullptr : qgemm_kernel<F, OUT_ARGMAX, G, R, XP>;
-    default: return nullptr;
+        // split inputs, two token tiles: the dense stores and adds of the batched passes
+        if constexpr (G || R != 2)
+            return nullptr;
+        else
+            return out == OUT_STORE ? qgemm_kernel<F, OUT_STORE, G, R, XP>
+                   : out == OUT_ADD ? qgemm_kernel<F, OUT_ADD, G, R, XP>
+                                    : nullptr;
+    } else {
+        switch (out) {
+        case OUT_STORE: return qgemm_kernel<F, OUT_STORE, G, R, XP>;
+        case OUT_SWIGLU:
+            if constexpr (R == 2) return qgemm_kernel<F, OUT_SWIGLU, G, R, XP>;  // deeper rings spill
+            return nullptr;
+        case OUT_ADD: return G ? nullptr : qgemm_kernel<F, OUT_ADD, G, R, XP>;
+        case OUT_ARGMAX: return G ? nullptr : qgemm_kernel<F, OUT_ARGMAX, G, R, XP>;
+        default: return nullptr;
+        }
     }
 }
 
 // ring depth: 4 chunks, or 2 for the two matrices of SWIGLU (the same bytes in
-// flight) and for reduction ranges of two chunks
+// flight), for reduction ranges of two chunks and for two token tiles (the
+// products' registers)
 template <bool G, bool XP> static QGemmKernel pick_qf(int fmt, int out, int K) {
-    const bool r2 = K / kQChunk <= 2 || out == OUT_SWIGLU;
+    const bool r2 = K / kQChunk <= 2 || out == OUT_SWIGLU || XP;
     switch (fmt) {
     case Q4_K: return r2 ? pick_q<Q4_K, G, 2, XP>(out) : pick_q<Q4_K, G, 4, XP>(out);
     case Q6_K: return r2 ? pick_q<Q6_K, G, 2, XP>(out) : pick_q<Q6_K, G, 4, XP>(out);
@@ -731,13 +770,13 @@ template <bool G, bool XP> static QGemmKernel pick_qf(int fmt, int out, int K) {
 
 // The chunk windows assume a 16-byte aligned matrix (and expert slices) whose
 // row stride keeps chunk addresses within the format's offsets below 16.
-template <bool P> static int stage_chunks_of(int fmt) {
+template <bool P, int TT = 1> static int stage_chunks_of(int fmt) {
     switch (fmt) {
-    case Q4_K: return QGeom<Q4_K, P>::kStageChunks;
-    case Q8_0: return QGeom<Q8_0, P>::kStageChunks;
-    case IQ4_XS: return QGeom<IQ4_XS, P>::kStageChunks;
-    case Q6_K: return QGeom<Q6_K, P>::kStageChunks;
-    case Q3_K: return QGeom<Q3_K, P>::kStageChunks;
+    case Q4_K: return QGeom<Q4_K, P, TT>::kStageChunks;
+    case Q8_0: return QGeom<Q8_0, P, TT>::kStageChunks;
+    case IQ4_XS: return QGeom<IQ4_XS, P, TT>::kStageChunks;
+    case Q6_K: return QGeom<Q6_K, P, TT>::kStageChunks;
+    case Q3_K: return QGeom<Q3_K, P, TT>::kStageChunks;
     default: return 0;
     }
 }
@@ -803,9 +842,15 @@ hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float 
     }
     p.groups = groups;
     p.nseg = nseg;
-    const int tiles = (M + 15) / 16, chunks = K / kQChunk;
+    // split inputs (more than one token tile): the XP kernels, two token tiles per workgroup
+    const bool use_xp = xp && xp->hi && xp->lo && xp->sum && xp->ld % 32 == 0 && K <= xp->ld && M > 16 &&
+                        (out == OUT_STORE || out == OUT_ADD);
+    const int TT = use_xp ? 2 : 1;
+    const int tiles = (M + 16 * TT - 1) / (16 * TT), chunks = K / kQChunk;
     const int target = qgemm_target_wgs();
-    const int stage = out == OUT_SWIGLU ? stage_chunks_of<true>(fmt) : stage_chunks_of<false>(fmt);
+    const int stage = use_xp                ? stage_chunks_of<false, 2>(fmt)
+                      : out == OUT_SWIGLU ? stage_chunks_of<true>(fmt)
+                                          : stage_chunks_of<false>(fmt);
     // Reduction split ks (a power of two; results added atomically, plain
     // stores and adds only) and workgroups per split pg, each taking every
     // pg-th row group.  Several groups per workgroup need a one-stage range:
@@ -830,13 +875,9 @@ hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float 
             while (groups * tiles * ks * 2 <= target && chunks % (ks * 2) == 0 && ks * 2 <= max_split) ks *= 2;
     }
     p.ksplit = ks;
-    QGemmKernel k = nullptr;
-    if (xp && xp->hi && xp->lo && xp->sum && xp->ld % 32 == 0 && K <= xp->ld) {
-        k = pick_qf<false, true>(fmt, out, K / ks);
-        if (k) p.xh = xp->hi, p.xl = xp->lo, p.xsum = xp->sum, p.ldxs = xp->ld;
-    }
-    if (!k) k = pick_qf<false, false>(fmt, out, K / ks);
+    QGemmKernel k = use_xp ? pick_qf<false, true>(fmt, out, K / ks) : pick_qf<false, false>(fmt, out, K / ks);
     if (!k) return hipErrorInvalidValue;
+    if (use_xp) p.xh = xp->hi, p.xl = xp->lo, p.xsum = xp->sum, p.ldxs = xp->ld;
     if (ks > 1 && out == OUT_STORE) {
         for (int i = 0; i < nseg; i++) {
             hipLaunchKernelGGL(zero_rows_kernel, dim3((M * N[i] + 255) / 256), dim3(256), 0, s, y[i], ldy[i], M, N[i]);

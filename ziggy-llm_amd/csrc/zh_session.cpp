@@ -875,7 +875,7 @@ static hipError_t pass_alloc(ZiggyHipSession *s) {
         s->allocs.push_back(*r.p);
     }
     {
-        const size_t ld = (std::max(Q, F) + 31) / 32 * 32;
+        const size_t ld = (std::max(std::max(Q, F), H) + 31) / 32 * 32;
         uint8_t *base = nullptr;
         hipError_t e = hipMalloc((void **)&base, M * ld * 4 + M * (ld / 32) * 4);
         if (e != hipSuccess) return e;
@@ -939,14 +939,16 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
         e = launch_gemm(w.type, w.p, w2 ? w2->p : nullptr, w.stride, x, ldx, y, ldy, M, (int)w.rows, (int)w.cols,
                         out, s->b_argmax, st, false, out == OUT_ADD ? split_add : split_clear, xp);
     };
-    // The o and down products take their inputs as pieces split once here
-    // (one workgroup per row group: each would split the whole rows again);
-    // in a verify pass (one token tile, split reductions) o splits its own.
-    const bool split_o = det && Q % 32 == 0, split_down = F % 32 == 0;
+    // Prompt passes of more than one token tile give the products their
+    // inputs as pieces split once here: the products then take two token
+    // tiles per workgroup, and no workgroup splits the rows again.  (A verify
+    // pass, one token tile, lets the products split their own.)
+    const bool split_in = det && M > 16 && H % 32 == 0, split_o = det && M > 16 && Q % 32 == 0,
+               split_down = F % 32 == 0;
     // products of the normed rows that accumulate (OUT_ADD) onto cleared
     // outputs: one launch for the matrices that share a format and row size
     auto multi3 = [&](const DT &a, float *ya, int lda, const DT &b, float *yb, int ldb, const DT *c, float *yc,
-                      int ldc) {
+                      int ldc, const XPlanes *xp) {
         if (e != hipSuccess) return;
         const DT *d[3] = {&a, &b, c};
         float *ys[3] = {ya, yb, yc};
@@ -960,7 +962,7 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
             int Ns[3];
             for (int k = i; k < j; k++) ws[k - i] = d[k]->p, Ns[k - i] = (int)d[k]->rows;
             e = launch_gemm_multi(d[i]->type, j - i, ws, ys + i, lds + i, Ns, d[i]->stride, s->b_normed, H, M,
-                                  (int)d[i]->cols, OUT_ADD, st, split_clear);  // onto rows the norm cleared
+                                  (int)d[i]->cols, OUT_ADD, st, split_clear, xp);  // onto rows the norm cleared
             i = j;
         }
     };
@@ -969,7 +971,8 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
         // the norm clears the q/k/v rows, which the products then accumulate onto
         e = launch_rms_norm_rows(s->b_hidden, (const float *)L.attn_norm.p, s->b_normed, M, H, eps, st, s->b_q,
                                  (size_t)M * Q, s->b_k, (size_t)M * KV, s->b_v, (size_t)M * KV);
-        multi3(L.q, s->b_q, Q, L.k, s->b_k, KV, &L.v, s->b_v, KV);
+        if (split_in && e == hipSuccess) e = launch_split_rows(s->b_normed, H, M, H, s->xp, st);
+        multi3(L.q, s->b_q, Q, L.k, s->b_k, KV, &L.v, s->b_v, KV, split_in ? &s->xp : nullptr);
         const size_t layer_base = kv_layer_base(s, l);
         if (s->b_counters && e == hipSuccess) {
             AttnParams a{};
@@ -1058,7 +1061,8 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
             if (e == hipSuccess)
                 e = launch_rms_norm_rows(s->b_hidden, (const float *)L.ffn_norm.p, s->b_normed, M, H, eps, st,
                                          s->b_act, (size_t)M * F, s->b_up, (size_t)M * F);
-            multi3(L.gate, s->b_act, F, L.up, s->b_up, F, nullptr, nullptr, 0);
+            if (split_in && e == hipSuccess) e = launch_split_rows(s->b_normed, H, M, H, s->xp, st);
+            multi3(L.gate, s->b_act, F, L.up, s->b_up, F, nullptr, nullptr, 0, split_in ? &s->xp : nullptr);
             down_split = split_down;
             if (e == hipSuccess)
                 e = down_split ? launch_silu_mul_split(s->b_act, s->b_up, M, F, s->xp, st)
