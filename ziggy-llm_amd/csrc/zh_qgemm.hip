@@ -286,7 +286,7 @@ template <> struct QChunk<Q3_K> {
 // so the 16 rows' words fall in distinct banks.  The activation stage (TT
 // token tiles of 16) is as long as LDS allows next to the code images (2048,
 // 1024 or 512 values).
-template <int F, bool kPair, int TT = 1> struct QGeom {
+template <int F, bool kPair, int TT = 1, int OCC = 1> struct QGeom {
     static constexpr int kMats = kPair ? 2 : 1;
     static constexpr int kWin = (QChunk<F>::kCB + QChunk<F>::kShm + 15) / 16;
     static constexpr int kRowW = 4 * ((kWin + 1) | 1);
@@ -297,12 +297,15 @@ template <int F, bool kPair, int TT = 1> struct QGeom {
     static constexpr int lds_bytes(int st) {
         return 2 * 16 * TT * (st + 8) * 2 + (kXsum ? st / QChunk<F>::kSub * 16 * TT * 4 : 64) + kCodeBytes;
     }
-    // two token tiles: a 512-value stage where it leaves LDS for two
-    // workgroups per CU (one stages or waits while the other computes)
-    static constexpr int kStage = TT == 2 && lds_bytes(512) <= 80 * 1024 ? 512
-                                  : lds_bytes(2048) <= 160 * 1024        ? 2048
-                                  : lds_bytes(1024) <= 160 * 1024        ? 1024
-                                                                         : 512;
+    // OCC > 1: the longest stage that leaves LDS for OCC workgroups per CU
+    // (one stages or waits while another computes), where one fits
+    static constexpr int kPart = 160 * 1024 / OCC, kAll = 160 * 1024;
+    static constexpr int kStage = OCC > 1 && lds_bytes(2048) <= kPart   ? 2048
+                                  : OCC > 1 && lds_bytes(1024) <= kPart ? 1024
+                                  : OCC > 1 && lds_bytes(512) <= kPart  ? 512
+                                  : lds_bytes(2048) <= kAll             ? 2048
+                                  : lds_bytes(1024) <= kAll             ? 1024
+                                                                        : 512;
     static constexpr int kStageChunks = kStage / kQChunk;
 };
 
@@ -317,8 +320,11 @@ template <int F, int OUT, bool GROUPED, int R, bool XP>
 __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     constexpr bool kPair = OUT == OUT_SWIGLU;
     constexpr int TT = XP ? 2 : 1;  // token tiles of 16 per workgroup
+    // LDS for two workgroups per CU (the two-tile and the grouped kernels;
+    // three for the grouped single products, whose registers allow it)
+    constexpr int OCC = GROUPED && !kPair ? 3 : XP || GROUPED ? 2 : 1;
     using QC = QChunk<F>;
-    using G = QGeom<F, kPair, TT>;
+    using G = QGeom<F, kPair, TT, OCC>;
     constexpr int kSub = QC::kSub, kCB = QC::kCB, kShm = QC::kShm;
     constexpr int kMats = G::kMats, kWin = G::kWin, kRowW = G::kRowW, kPieces = G::kPieces, kP = G::kP;
     constexpr bool kXsum = G::kXsum;
@@ -740,24 +746,30 @@ template <int F, bool G, int R, bool XP> static QGemmKernel pick_q(int out) {
             return out == OUT_STORE ? qgemm_kernel<F, OUT_STORE, G, R, XP>
                    : out == OUT_ADD ? qgemm_kernel<F, OUT_ADD, G, R, XP>
                                     : nullptr;
+    } else if constexpr (G && R != 2) {
+        return nullptr;  // grouped: ring depth 2 (their stages may hold two chunks)
     } else {
         switch (out) {
         case OUT_STORE: return qgemm_kernel<F, OUT_STORE, G, R, XP>;
         case OUT_SWIGLU:
             if constexpr (R == 2) return qgemm_kernel<F, OUT_SWIGLU, G, R, XP>;  // deeper rings spill
             return nullptr;
-        case OUT_ADD: return G ? nullptr : qgemm_kernel<F, OUT_ADD, G, R, XP>;
-        case OUT_ARGMAX: return G ? nullptr : qgemm_kernel<F, OUT_ARGMAX, G, R, XP>;
+        case OUT_ADD:
+            if constexpr (G) return nullptr;
+            else return qgemm_kernel<F, OUT_ADD, G, R, XP>;
+        case OUT_ARGMAX:
+            if constexpr (G) return nullptr;
+            else return qgemm_kernel<F, OUT_ARGMAX, G, R, XP>;
         default: return nullptr;
         }
     }
 }
 
 // ring depth: 4 chunks, or 2 for the two matrices of SWIGLU (the same bytes in
-// flight), for reduction ranges of two chunks and for two token tiles (the
-// products' registers)
+// flight), for reduction ranges of two chunks, for two token tiles (the
+// products' registers) and for the grouped kernels (stages of two chunks)
 template <bool G, bool XP> static QGemmKernel pick_qf(int fmt, int out, int K) {
-    const bool r2 = K / kQChunk <= 2 || out == OUT_SWIGLU || XP;
+    const bool r2 = K / kQChunk <= 2 || out == OUT_SWIGLU || XP || G;
     switch (fmt) {
     case Q4_K: return r2 ? pick_q<Q4_K, G, 2, XP>(out) : pick_q<Q4_K, G, 4, XP>(out);
     case Q6_K: return r2 ? pick_q<Q6_K, G, 2, XP>(out) : pick_q<Q6_K, G, 4, XP>(out);
@@ -770,13 +782,13 @@ template <bool G, bool XP> static QGemmKernel pick_qf(int fmt, int out, int K) {
 
 // The chunk windows assume a 16-byte aligned matrix (and expert slices) whose
 // row stride keeps chunk addresses within the format's offsets below 16.
-template <bool P, int TT = 1> static int stage_chunks_of(int fmt) {
+template <bool P, int TT = 1, int OCC = 1> static int stage_chunks_of(int fmt) {
     switch (fmt) {
-    case Q4_K: return QGeom<Q4_K, P, TT>::kStageChunks;
-    case Q8_0: return QGeom<Q8_0, P, TT>::kStageChunks;
-    case IQ4_XS: return QGeom<IQ4_XS, P, TT>::kStageChunks;
-    case Q6_K: return QGeom<Q6_K, P, TT>::kStageChunks;
-    case Q3_K: return QGeom<Q3_K, P, TT>::kStageChunks;
+    case Q4_K: return QGeom<Q4_K, P, TT, OCC>::kStageChunks;
+    case Q8_0: return QGeom<Q8_0, P, TT, OCC>::kStageChunks;
+    case IQ4_XS: return QGeom<IQ4_XS, P, TT, OCC>::kStageChunks;
+    case Q6_K: return QGeom<Q6_K, P, TT, OCC>::kStageChunks;
+    case Q3_K: return QGeom<Q3_K, P, TT, OCC>::kStageChunks;
     default: return 0;
     }
 }
@@ -848,7 +860,7 @@ hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float 
     const int TT = use_xp ? 2 : 1;
     const int tiles = (M + 16 * TT - 1) / (16 * TT), chunks = K / kQChunk;
     const int target = qgemm_target_wgs();
-    const int stage = use_xp                ? stage_chunks_of<false, 2>(fmt)
+    const int stage = use_xp                ? stage_chunks_of<false, 2, 2>(fmt)
                       : out == OUT_SWIGLU ? stage_chunks_of<true>(fmt)
                                           : stage_chunks_of<false>(fmt);
     // Reduction split ks (a power of two; results added atomically, plain
@@ -909,7 +921,7 @@ hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, ui
     // A one-stage reduction lets a workgroup take several row groups of its
     // token tile against one staging: about four workgroups per CU at the
     // largest tile count (the launch's bound; unused tiles exit at once).
-    const int stage = out == OUT_SWIGLU ? stage_chunks_of<true>(fmt) : stage_chunks_of<false>(fmt);
+    const int stage = out == OUT_SWIGLU ? stage_chunks_of<true, 1, 2>(fmt) : stage_chunks_of<false, 1, 3>(fmt);
     int pg = p.groups;
     if (K / kQChunk <= stage) {
         pg = 4 * qgemm_target_wgs() / max_tiles;
