@@ -1,6 +1,7 @@
 // zh_moe_stack.cpp -- host side of the MoE FFN layer stack (ziggy_hip_moe_stack_*):
 // weight residency, buffers, and the per-layer launch sequence of zh_moe.hip
 // captured into one HIP graph.
+#include <algorithm>
 #include <new>
 #include <vector>
 
@@ -38,7 +39,8 @@ struct ZiggyHipMoeStack {
     // prefill (token batches of up to pre_max rows), allocated at the first call
     int pre_max = 0;
     float *p_input = nullptr, *p_hidden = nullptr, *p_normed = nullptr, *p_logits = nullptr, *p_act = nullptr,
-          *p_act_sh = nullptr, *p_tmp = nullptr, *p_sh = nullptr;
+          *p_act_sh = nullptr, *p_tmp = nullptr, *p_sh = nullptr, *p_up_sh = nullptr;
+    zh::XPlanes p_xp{};  // the shared expert's inputs, split once per layer
     uint32_t *p_route = nullptr;  // [layers][pre_max][2k + 2]
     int *p_list = nullptr, *p_tiles = nullptr, *p_ntiles = nullptr;
 };
@@ -207,10 +209,13 @@ hipError_t enqueue_prefill_layer(ZiggyHipMoeStack *s, int l, int M, hipStream_t 
               SF = (int)d.shared_ff_length;
     uint32_t *route = s->p_route + (size_t)l * s->pre_max * s->route_stride;
     hipError_t e = launch_rms_norm_rows(s->p_hidden, (const float *)L.norm.p, s->p_normed, M, H, d.rms_norm_eps, st);
+    // the shared gate row, stored right after the router's rows, is row E of one launch
+    const bool gate_row_next = s->shared_gate && L.gate_inp_sh.p == L.router.p + (uint64_t)E * L.router.stride &&
+                               L.gate_inp_sh.stride == L.router.stride;
     if (e == hipSuccess)
-        e = launch_gemm(L.router.type, L.router.p, nullptr, L.router.stride, s->p_normed, H, s->p_logits, E + 1, M, E,
-                        H, OUT_STORE, nullptr, st, true);
-    if (e == hipSuccess && s->shared_gate)
+        e = launch_gemm(L.router.type, L.router.p, nullptr, L.router.stride, s->p_normed, H, s->p_logits, E + 1, M,
+                        gate_row_next ? E + 1 : E, H, OUT_STORE, nullptr, st, true);
+    if (e == hipSuccess && s->shared_gate && !gate_row_next)
         e = launch_gemm(L.gate_inp_sh.type, L.gate_inp_sh.p, nullptr, L.gate_inp_sh.stride, s->p_normed, H,
                         s->p_logits + E, E + 1, M, 1, H, OUT_STORE, nullptr, st, true);
     if (e == hipSuccess)
@@ -223,16 +228,29 @@ hipError_t enqueue_prefill_layer(ZiggyHipMoeStack *s, int l, int M, hipStream_t 
         e = launch_gemm_grouped(L.gate.type, L.gate.p, L.up.p, L.gate.stride, (uint64_t)FF * L.gate.stride,
                                 s->p_normed, H, K, s->p_act, FF, FF, H, OUT_SWIGLU, s->p_tiles, s->p_list,
                                 s->p_ntiles, max_tiles, st);
-    if (e == hipSuccess && s->shared)
+    // the shared expert on split inputs (more than one token tile): gate and up
+    // as two stores in one launch, then SiLU * up split for down
+    const bool sh_split = s->shared && M > 16 && H % 32 == 0 && SF % 32 == 0 && s->p_xp.hi;
+    if (e == hipSuccess && sh_split) {
+        e = launch_split_rows(s->p_normed, H, M, H, s->p_xp, st);
+        const uint8_t *ws[2] = {L.gate_sh.p, L.up_sh.p};
+        float *ys[2] = {s->p_act_sh, s->p_up_sh};
+        const int lds[2] = {SF, SF}, Ns[2] = {SF, SF};
+        if (e == hipSuccess)
+            e = launch_gemm_multi(L.gate_sh.type, 2, ws, ys, lds, Ns, L.gate_sh.stride, s->p_normed, H, M, H,
+                                  OUT_STORE, st, 1, &s->p_xp);
+        if (e == hipSuccess) e = launch_silu_mul_split(s->p_act_sh, s->p_up_sh, M, SF, s->p_xp, st);
+    } else if (e == hipSuccess && s->shared) {
         e = launch_gemm(L.gate_sh.type, L.gate_sh.p, L.up_sh.p, L.gate_sh.stride, s->p_normed, H, s->p_act_sh, SF, M,
                         SF, H, OUT_SWIGLU, nullptr, st);
+    }
     if (e == hipSuccess)
         e = launch_gemm_grouped(L.down.type, L.down.p, nullptr, L.down.stride, (uint64_t)H * L.down.stride, s->p_act,
                                 FF, 1, s->p_tmp, H, H, FF, OUT_STORE, s->p_tiles, s->p_list, s->p_ntiles, max_tiles,
                                 st);
     if (e == hipSuccess && s->shared)
         e = launch_gemm(L.down_sh.type, L.down_sh.p, nullptr, L.down_sh.stride, s->p_act_sh, SF, s->p_sh, H, M, H, SF,
-                        OUT_STORE, nullptr, st);
+                        OUT_STORE, nullptr, st, false, 16, sh_split ? &s->p_xp : nullptr);
     if (e == hipSuccess)
         e = launch_moe_combine(s->p_hidden, s->p_tmp, route, H, K, s->shared ? 1 : 0, st, M,
                                s->shared ? s->p_sh : nullptr);
@@ -256,6 +274,7 @@ hipError_t prefill_alloc(ZiggyHipMoeStack *s) {
         {(void **)&s->p_logits, Mc * (E + 1) * 4},
         {(void **)&s->p_act, Mc * K * FF * 4},
         {(void **)&s->p_act_sh, Mc * (SF ? SF : 1) * 4},
+        {(void **)&s->p_up_sh, Mc * (SF ? SF : 1) * 4},
         {(void **)&s->p_tmp, Mc * K * H * 4},
         {(void **)&s->p_sh, Mc * H * 4},
         {(void **)&s->p_route, NL * Mc * s->route_stride * 4},
@@ -268,6 +287,17 @@ hipError_t prefill_alloc(ZiggyHipMoeStack *s) {
         if (e == hipSuccess) e = hipMemsetAsync(*r.p, 0, r.bytes, s->ctx->stream);
         if (e != hipSuccess) return e;
         s->allocs.push_back(*r.p);
+    }
+    {
+        const size_t ld = (std::max(H, SF) + 31) / 32 * 32;
+        uint8_t *base = nullptr;
+        hipError_t e = hipMalloc((void **)&base, Mc * ld * 4 + Mc * (ld / 32) * 4);
+        if (e != hipSuccess) return e;
+        s->allocs.push_back(base);
+        s->p_xp.hi = reinterpret_cast<uint16_t *>(base);
+        s->p_xp.lo = s->p_xp.hi + Mc * ld;
+        s->p_xp.sum = reinterpret_cast<float *>(s->p_xp.lo + Mc * ld);
+        s->p_xp.ld = (int)ld;
     }
     s->pre_max = (int)Mc;
     return hipSuccess;
@@ -315,13 +345,14 @@ int ziggy_hip_moe_stack_create(ZiggyHipContext *ctx, const ZiggyHipMoeDesc *desc
         MoeLayerW &L = s->layers[l];
         ok = take_tensor(&t.ffn_norm, 1, H, true, true, &L.norm, &off, todo) &&
              take_tensor(&t.router, E, H, true, false, &L.router, &off, todo) &&
+             // right after the router: one prefill launch takes both as E + 1 rows
+             take_tensor(&t.gate_inp_shexp, 1, H, false, false, &L.gate_inp_sh, &off, todo) &&
              take_tensor(&t.gate_exps, E * FF, H, true, false, &L.gate, &off, todo) &&
              take_tensor(&t.up_exps, E * FF, H, true, false, &L.up, &off, todo) &&
              take_tensor(&t.down_exps, E * H, FF, true, false, &L.down, &off, todo) &&
              take_tensor(&t.gate_shexp, SF, H, false, false, &L.gate_sh, &off, todo) &&
              take_tensor(&t.up_shexp, SF, H, false, false, &L.up_sh, &off, todo) &&
-             take_tensor(&t.down_shexp, H, SF, false, false, &L.down_sh, &off, todo) &&
-             take_tensor(&t.gate_inp_shexp, 1, H, false, false, &L.gate_inp_sh, &off, todo);
+             take_tensor(&t.down_shexp, H, SF, false, false, &L.down_sh, &off, todo);
         if (!ok) break;
         // the same routed / shared / router types in every layer, launched together
         const bool sh = L.gate_sh.present;
