@@ -109,6 +109,35 @@ __device__ __forceinline__ uint4 codes_m8(uint32_t a, uint32_t b) {
     return {x.x, x.y, y.x, y.y};
 }
 
+// bf16 bits of a small integer (|v| < 256, exact in bf16)
+constexpr uint32_t bf16_of_int(int v) {
+    if (v == 0) return 0u;
+    const uint32_t a = (uint32_t)(v < 0 ? -v : v);
+    int e = 0;
+    while ((a >> (e + 1)) != 0u) e++;  // the leading one
+    return (v < 0 ? 0x8000u : 0u) | (uint32_t)(e + 127) << 7 | (((a << 7) >> e) & 0x7Fu);
+}
+// byte `hi` (0 low, 1 high) of the bf16 of kvalues_iq4nl entries 4 w .. 4 w + 3
+constexpr uint32_t iq4_bf16_word(int w, int hi) {
+    uint32_t r = 0;
+    for (int i = 0; i < 4; i++) r |= ((bf16_of_int(kIq4Int[4 * w + i]) >> (8 * hi)) & 0xFFu) << (8 * i);
+    return r;
+}
+// Four IQ4_XS nibbles (one per byte of n) -> the bf16 of their kvalues_iq4nl
+// entries, two per word: the low and the high bytes of the bf16 values are
+// looked up as in iq4_lookup4 and interleaved.
+__device__ __forceinline__ uint2 iq4_bf16_lookup4(uint32_t n) {
+    constexpr uint32_t L0 = iq4_bf16_word(0, 0), L1 = iq4_bf16_word(1, 0), L2 = iq4_bf16_word(2, 0),
+                       L3 = iq4_bf16_word(3, 0), H0 = iq4_bf16_word(0, 1), H1 = iq4_bf16_word(1, 1),
+                       H2 = iq4_bf16_word(2, 1), H3 = iq4_bf16_word(3, 1);
+    const uint32_t sel = n & 0x07070707u, pick = 0x03020100u + ((n & 0x08080808u) >> 1);
+    const uint32_t lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(L3, L2, sel), __builtin_amdgcn_perm(L1, L0, sel), pick);
+    const uint32_t hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(H3, H2, sel), __builtin_amdgcn_perm(H1, H0, sel), pick);
+    return {__builtin_amdgcn_perm(hi, lo, 0x05010400u), __builtin_amdgcn_perm(hi, lo, 0x07030602u)};
+}
+static_assert(bf16_of_int(1) == 0x3F80u && bf16_of_int(113) == 0x42E2u && bf16_of_int(-127) == 0xC2FEu,
+              "bf16 bits of small integers");
+
 // ---- per-format chunk (256 values of one row): fields and sub-block steps ----
 //
 // kCB: bytes of a chunk row; kShm: the bits its address can have below 16
@@ -210,7 +239,8 @@ template <> struct QChunk<IQ4_XS> {
         s = h2f(hd.x) * (float)((int)(low | (high << 4)) - 32);
         mn = 0.f;
         const int sh = hi ? 4 : 0;
-        return codes_s8(iq4_lookup4((q[j].x >> sh) & 0x0F0F0F0Fu), iq4_lookup4((q[j].y >> sh) & 0x0F0F0F0Fu));
+        const uint2 a = iq4_bf16_lookup4((q[j].x >> sh) & 0x0F0F0F0Fu), b = iq4_bf16_lookup4((q[j].y >> sh) & 0x0F0F0F0Fu);
+        return {a.x, a.y, b.x, b.y};
     }
 };
 

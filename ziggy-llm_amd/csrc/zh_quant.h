@@ -348,12 +348,18 @@ template <> __device__ __forceinline__ float slot_dot<Q3_K>(const Raw<Q3_K> &r, 
 __device__ __constant__ static const float kIq4nl[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
                                                          1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
 
+// kvalues_iq4nl as integers (the same table as kIq4nl)
+constexpr int kIq4Int[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
 // kvalues_iq4nl as signed bytes, 4 entries per word, for register table lookups with v_perm
 #define ZH_IQ4_B(v, i) (((uint32_t)(uint8_t)(int8_t)(v)) << (8 * (i)))
-#define ZH_IQ4_T0 (ZH_IQ4_B(-127, 0) | ZH_IQ4_B(-104, 1) | ZH_IQ4_B(-83, 2) | ZH_IQ4_B(-65, 3))
-#define ZH_IQ4_T1 (ZH_IQ4_B(-49, 0) | ZH_IQ4_B(-35, 1) | ZH_IQ4_B(-22, 2) | ZH_IQ4_B(-10, 3))
-#define ZH_IQ4_T2 (ZH_IQ4_B(1, 0) | ZH_IQ4_B(13, 1) | ZH_IQ4_B(25, 2) | ZH_IQ4_B(38, 3))
-#define ZH_IQ4_T3 (ZH_IQ4_B(53, 0) | ZH_IQ4_B(69, 1) | ZH_IQ4_B(89, 2) | ZH_IQ4_B(113, 3))
+#define ZH_IQ4_W(w) \
+    (ZH_IQ4_B(kIq4Int[4 * (w)], 0) | ZH_IQ4_B(kIq4Int[4 * (w) + 1], 1) | ZH_IQ4_B(kIq4Int[4 * (w) + 2], 2) | \
+     ZH_IQ4_B(kIq4Int[4 * (w) + 3], 3))
+#define ZH_IQ4_T0 ZH_IQ4_W(0)
+#define ZH_IQ4_T1 ZH_IQ4_W(1)
+#define ZH_IQ4_T2 ZH_IQ4_W(2)
+#define ZH_IQ4_T3 ZH_IQ4_W(3)
 
 // Looks up 4 nibbles (one per byte of n, each 0..15) in kvalues_iq4nl (signed bytes).
 __device__ __forceinline__ uint32_t iq4_lookup4(uint32_t n) {
