@@ -324,8 +324,10 @@ template <int F, bool kPair, int TT = 1, int OCC = 1> struct QGeom {
     // activation sums per sub-block: the Q4_K minimums and the code offsets
     static constexpr bool kXsum = QChunk<F>::kOff != 0.f || F == Q4_K;
     static constexpr int kCodeBytes = 4 * kMats * 16 * kRowW * 4;
+    // activation rows of st + 8 values (the last without its padding), the
+    // sums, the code images
     static constexpr int lds_bytes(int st) {
-        return 2 * 16 * TT * (st + 8) * 2 + (kXsum ? st / QChunk<F>::kSub * 16 * TT * 4 : 64) + kCodeBytes;
+        return 2 * ((2 * 16 * TT - 1) * (st + 8) + st) + (kXsum ? st / QChunk<F>::kSub * 16 * TT * 4 : 4) + kCodeBytes;
     }
     // OCC > 1: the longest stage that leaves LDS for OCC workgroups per CU
     // (one stages or waits while another computes), where one fits
@@ -347,7 +349,7 @@ __device__ __forceinline__ uint32_t ordered_bits_q(float v) {
 // XP: the input comes split (XPlanes) and a workgroup takes two token tiles
 // (32 tokens): every decoded code serves both tiles' products.
 template <int F, int OUT, bool GROUPED, int R, bool XP>
-__global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
+__global__ void __launch_bounds__(256, XP || (GROUPED && OUT != OUT_SWIGLU) ? 2 : 1) qgemm_kernel(QGemmParams p) {
     constexpr bool kPair = OUT == OUT_SWIGLU;
     constexpr int TT = XP ? 2 : 1;  // token tiles of 16 per workgroup
     // LDS for two workgroups per CU (the two-tile and the grouped kernels;
@@ -412,8 +414,12 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     // sit in LDS as bf16 hi / lo pieces; thread (token tt, part) stages values
     // 16 part + 256 i of tokens tt, tt + 16, ...
     constexpr int NT = 16 * TT;
-    __shared__ __align__(16) unsigned short xs_s[2][NT][kStage + 8];        // [hi / lo][token][k]
-    __shared__ __align__(16) float xsum_s[kXsum ? kStage / kSub : 1][NT];   // [sub-block][token]
+    // [hi / lo][token][k]: rows kStage + 8 apart (the padding spreads the
+    // rows' words over the banks), the last row without its padding
+    constexpr int kXRow = kStage + 8;
+    __shared__ __align__(16) unsigned short xs_raw[(2 * NT - 1) * kXRow + kStage];
+    auto xs_at = [&](int piece, int tok, int k) -> unsigned short * { return &xs_raw[(piece * NT + tok) * kXRow + k]; };
+    __shared__ __align__(16) float xsum_s[kXsum ? kStage / kSub : 1][kXsum ? NT : 1];  // [sub-block][token]
     __shared__ __align__(16) uint32_t code_s[4][kMats][16 * kRowW];        // [wavefront][matrix][row image]
     const int tt = tid >> 4, part = tid & 15;
     static_assert(!XP || !kXsum || kSub == 32, "split inputs carry 32-value sums");
@@ -496,8 +502,8 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
                     if (kXsum && kSub == 32) sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
                 }
                 const int tk = 16 * t + tt;
-                uint4 *dh = reinterpret_cast<uint4 *>(&xs_s[0][tk][u * kQChunk + 16 * part]);
-                uint4 *dl = reinterpret_cast<uint4 *>(&xs_s[1][tk][u * kQChunk + 16 * part]);
+                uint4 *dh = reinterpret_cast<uint4 *>(xs_at(0, tk, u * kQChunk + 16 * part));
+                uint4 *dl = reinterpret_cast<uint4 *>(xs_at(1, tk, u * kQChunk + 16 * part));
                 dh[0] = {hw[0], hw[1], hw[2], hw[3]};
                 dh[1] = {hw[4], hw[5], hw[6], hw[7]};
                 dl[0] = {lw[0], lw[1], lw[2], lw[3]};
@@ -516,11 +522,15 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
     // decoded once for the TT token tiles.
     auto compute = [&](const QC &r, const QC &r2, int cs, float live) {
         constexpr int S = QC::kSteps;
+        // steps per pass: the products of at most 16 (step, tile) pairs in registers
+        constexpr int P = S * TT > 16 ? 16 / TT : S;
         const qf4v zero = {0.f, 0.f, 0.f, 0.f};
         qf4v dv[TT][S], dv2[TT][S];
         float sv[S], mv[S], sv2[S], mv2[S];
 #pragma unroll
-        for (int j = 0; j < S; j++) {
+        for (int j0 = 0; j0 < S; j0 += P) {
+#pragma unroll
+        for (int j = j0; j < j0 + P; j++) {
             mv[j] = 0.f, sv2[j] = 0.f, mv2[j] = 0.f;
             const int kx = cs * kQChunk + kSub * j;
             if constexpr (kSub == 32) {
@@ -529,8 +539,8 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
                 if (kPair) b2 = as_bf8(r2.step(j, sv2[j], mv2[j]));
 #pragma unroll
                 for (int t = 0; t < TT; t++) {
-                    const bf8v ah = as_bf8(*reinterpret_cast<const uint4 *>(&xs_s[0][16 * t + li][kx + 8 * lg]));
-                    const bf8v al = as_bf8(*reinterpret_cast<const uint4 *>(&xs_s[1][16 * t + li][kx + 8 * lg]));
+                    const bf8v ah = as_bf8(*reinterpret_cast<const uint4 *>(xs_at(0, 16 * t + li, kx + 8 * lg)));
+                    const bf8v al = as_bf8(*reinterpret_cast<const uint4 *>(xs_at(1, 16 * t + li, kx + 8 * lg)));
                     dv[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, zero, 0, 0, 0);
                     dv[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, dv[t][j], 0, 0, 0);
                     dv2[t][j] = zero;
@@ -545,8 +555,8 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
                 if (kPair) b2 = as_s4(r2.step(j, sv2[j]));
 #pragma unroll
                 for (int t = 0; t < TT; t++) {
-                    const s4v ah = as_s4(*reinterpret_cast<const uint2 *>(&xs_s[0][16 * t + li][kx + 4 * lg]));
-                    const s4v al = as_s4(*reinterpret_cast<const uint2 *>(&xs_s[1][16 * t + li][kx + 4 * lg]));
+                    const s4v ah = as_s4(*reinterpret_cast<const uint2 *>(xs_at(0, 16 * t + li, kx + 4 * lg)));
+                    const s4v al = as_s4(*reinterpret_cast<const uint2 *>(xs_at(1, 16 * t + li, kx + 4 * lg)));
                     dv[t][j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, b, zero, 0, 0, 0);
                     dv[t][j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, b, dv[t][j], 0, 0, 0);
                     dv2[t][j] = zero;
@@ -558,7 +568,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
             }
         }
 #pragma unroll
-        for (int j = 0; j < S; j++) {
+        for (int j = j0; j < j0 + P; j++) {
             const float s = sv[j] * live, s2 = sv2[j] * live;
             const float c = fmaf(QC::kOff, sv[j], mv[j]) * live, c2 = fmaf(QC::kOff, sv2[j], mv2[j]) * live;
 #pragma unroll
@@ -581,6 +591,7 @@ __global__ void __launch_bounds__(256) qgemm_kernel(QGemmParams p) {
                     }
                 }
             }
+        }
         }
     };
 
