@@ -92,7 +92,7 @@ def gemm_probe(args) -> None:
     """The program of the matrix-core counter runs: only the M >= 8 passes, few launches each.
     verify  Qwen3-8B-shaped Q8_0: an 8-token prompt (one batched pass of 7 rows), then --iters verify passes
             of the pending token and 8 seeded drafts (M = 9) at the same position;
-    prompt  Llama-3.1-8B-shaped Q4_K_M: one 129-token prompt (two batched passes of 64 rows);
+    prompt  Llama-3.1-8B-shaped Q4_K_M: one 257-token prompt (one batched pass of 256 rows);
     moe     4 layers of the MoE FFN stack (hidden 2048, 256 IQ4_XS experts of FFN 512, top-8, Q3_K
             shared expert): one 512-row prefill (grouped expert GEMMs)."""
     import numpy as np
@@ -113,11 +113,11 @@ def gemm_probe(args) -> None:
             print(f"verify {i} at position {p0}: {n} emitted", flush=True)
         s.close()
     elif args.what == "prompt":
-        spec = synth.llama8b_spec(context=256)
+        spec = synth.llama8b_spec(context=320)
         img = synth.build(spec, seed=args.seed)
-        s = hip.Session(ctx, img, context=256)
-        _, st = s.generate(synth.prompt_tokens(args.seed, 129, spec.vocab), 0)
-        print(f"prompt of 129 tokens: {st.prompt_ns / 1e6:.2f} ms", flush=True)
+        s = hip.Session(ctx, img, context=320)
+        _, st = s.generate(synth.prompt_tokens(args.seed, 257, spec.vocab), 0)
+        print(f"prompt of 257 tokens: {st.prompt_ns / 1e6:.2f} ms", flush=True)
         s.close()
     else:
         spec = synth.moe_config5_spec(4)
