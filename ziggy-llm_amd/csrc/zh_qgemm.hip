@@ -349,12 +349,12 @@ __device__ __forceinline__ uint32_t ordered_bits_q(float v) {
 // XP: the input comes split (XPlanes) and a workgroup takes two token tiles
 // (32 tokens): every decoded code serves both tiles' products.
 template <int F, int OUT, bool GROUPED, int R, bool XP>
-__global__ void __launch_bounds__(256, XP || (GROUPED && OUT != OUT_SWIGLU) ? 2 : 1) qgemm_kernel(QGemmParams p) {
+__global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(QGemmParams p) {
     constexpr bool kPair = OUT == OUT_SWIGLU;
     constexpr int TT = XP ? 2 : 1;  // token tiles of 16 per workgroup
-    // LDS for two workgroups per CU (the two-tile and the grouped kernels;
-    // three for the grouped single products, whose registers allow it)
-    constexpr int OCC = GROUPED && !kPair ? 3 : XP || GROUPED ? 2 : 1;
+    // LDS for two workgroups per CU (three for the grouped single products,
+    // whose registers allow it; one for the dense SWIGLU pair)
+    constexpr int OCC = GROUPED && !kPair ? 3 : XP || GROUPED || !kPair ? 2 : 1;
     using QC = QChunk<F>;
     using G = QGeom<F, kPair, TT, OCC>;
     constexpr int kSub = QC::kSub, kCB = QC::kCB, kShm = QC::kShm;
@@ -787,8 +787,8 @@ template <int F, bool G, int R, bool XP> static QGemmKernel pick_q(int out) {
             return out == OUT_STORE ? qgemm_kernel<F, OUT_STORE, G, R, XP>
                    : out == OUT_ADD ? qgemm_kernel<F, OUT_ADD, G, R, XP>
                                     : nullptr;
-    } else if constexpr (G && R != 2) {
-        return nullptr;  // grouped: ring depth 2 (their stages may hold two chunks)
+    } else if constexpr (R != 2) {
+        return nullptr;  // ring depth 2: stages may hold two chunks
     } else {
         switch (out) {
         case OUT_STORE: return qgemm_kernel<F, OUT_STORE, G, R, XP>;
@@ -810,7 +810,9 @@ template <int F, bool G, int R, bool XP> static QGemmKernel pick_q(int out) {
 // flight), for reduction ranges of two chunks, for two token tiles (the
 // products' registers) and for the grouped kernels (stages of two chunks)
 template <bool G, bool XP> static QGemmKernel pick_qf(int fmt, int out, int K) {
-    const bool r2 = K / kQChunk <= 2 || out == OUT_SWIGLU || XP || G;
+    const bool r2 = true;  // every kernel at depth 2 (two workgroups per CU leave stages of two chunks)
+    (void)K;
+    (void)out;
     switch (fmt) {
     case Q4_K: return r2 ? pick_q<Q4_K, G, 2, XP>(out) : pick_q<Q4_K, G, 4, XP>(out);
     case Q6_K: return r2 ? pick_q<Q6_K, G, 2, XP>(out) : pick_q<Q6_K, G, 4, XP>(out);
@@ -903,7 +905,7 @@ hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float 
     const int target = qgemm_target_wgs();
     const int stage = use_xp                ? stage_chunks_of<false, 2, 2>(fmt)
                       : out == OUT_SWIGLU ? stage_chunks_of<true>(fmt)
-                                          : stage_chunks_of<false>(fmt);
+                                          : stage_chunks_of<false, 1, 2>(fmt);
     // Reduction split ks (a power of two; results added atomically, plain
     // stores and adds only) and workgroups per split pg, each taking every
     // pg-th row group.  Several groups per workgroup need a one-stage range:
