@@ -335,6 +335,7 @@ template <int F, bool kPair, int TT = 1, int OCC = 1> struct QGeom {
     static constexpr int kStage = OCC > 1 && lds_bytes(2048) <= kPart   ? 2048
                                   : OCC > 1 && lds_bytes(1024) <= kPart ? 1024
                                   : OCC > 1 && lds_bytes(512) <= kPart  ? 512
+                                  : OCC > 1 && lds_bytes(256) <= kPart  ? 256
                                   : lds_bytes(2048) <= kAll             ? 2048
                                   : lds_bytes(1024) <= kAll             ? 1024
                                                                         : 512;
@@ -361,7 +362,8 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
     constexpr int kMats = G::kMats, kWin = G::kWin, kRowW = G::kRowW, kPieces = G::kPieces, kP = G::kP;
     constexpr bool kXsum = G::kXsum;
     constexpr int kStage = G::kStage, kStageChunks = G::kStageChunks;
-    static_assert(kStageChunks % R == 0 && R % 2 == 0, "stages hold whole rings of an even depth");
+    static_assert((kStageChunks % R == 0 || (kStageChunks == 1 && R == 2)) && R % 2 == 0,
+                  "stages hold whole rings of an even depth, or one chunk at depth 2");
 
     touch_params(p);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
@@ -763,15 +765,43 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
         stage_store(nst);
         __syncthreads();
         fetch(0, 0, fa);
-        run_stage(0, nst);
+        if constexpr (kStageChunks == 1) {
+            fetch(1, 1, fb);  // chunk 0 only; the pairs below start at chunk 1
+            compute(fa[0], fa[kMats - 1], 0, 1.f);
+        } else {
+            run_stage(0, nst);
+        }
     }
-    for (int s0 = kStageChunks; s0 < nspan; s0 += kStageChunks) {
-        const int nst = min(kStageChunks, nspan - s0);
-        __syncthreads();  // every wavefront is done with the previous stage
-        stage_load(kbeg + s0 * kQChunk, nst);
-        stage_store(nst);
-        __syncthreads();
-        run_stage(s0, nst);
+    if constexpr (kStageChunks == 1) {
+        // One-chunk stages (depth 2): chunks in pairs, so that the field set
+        // and the ring slot of a chunk are its parity at compile time.
+        for (int s0 = 1; s0 < nspan; s0 += 2) {
+            __syncthreads();  // every wavefront is done with the previous stage
+            stage_load(kbeg + s0 * kQChunk, 1);
+            stage_store(1);
+            __syncthreads();
+            fetch(0, s0 + 1, fa);
+            compute(fb[0], fb[kMats - 1], 0, 1.f);
+            // chunk s0 + 1 (past the range: a dead step, so the pairs stay whole)
+            const bool more = s0 + 1 < nspan;
+            __syncthreads();
+            if (more) {
+                stage_load(kbeg + (s0 + 1) * kQChunk, 1);
+                stage_store(1);
+            }
+            __syncthreads();
+            fetch(1, s0 + 2, fb);
+            compute(fa[0], fa[kMats - 1], 0, more ? 1.f : 0.f);
+        }
+    } else {
+        for (int s0 = kStageChunks; s0 < nspan; s0 += kStageChunks) {
+            const int nst = min(kStageChunks, nspan - s0);
+            __syncthreads();  // every wavefront is done with the previous stage
+            stage_load(kbeg + s0 * kQChunk, nst);
+            stage_store(nst);
+            __syncthreads();
+            run_stage(s0, nst);
+        }
     }
     epilogue(blockIdx.x);
 }
