@@ -36,6 +36,10 @@ MODELS = {
                               default_type=Q8_0, attn_v_type=Q8_0, output_type=Q8_0, embd_type=Q8_0, context=512,
                               rope_theta=1000000.0),
     "llama-hd96-g4": dict(arch="llama", hidden=768, ffn=1024, n_head=8, n_kv=2, head_dim=96, context=512),
+    # Q8_0 with odd chunk counts (768 and 1280 values): the two-tile product's one-chunk stages end on a
+    # chunk whose pair partner is past the range
+    "llama-q8-odd-chunks": dict(arch="llama", hidden=768, ffn=1280, n_head=6, n_kv=2, head_dim=128,
+                                default_type=Q8_0, attn_v_type=Q8_0, output_type=Q8_0, embd_type=Q8_0, context=512),
 }
 
 
