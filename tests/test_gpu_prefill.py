@@ -44,7 +44,9 @@ MODELS = {
 
 
 @pytest.mark.parametrize("name", list(MODELS))
-@pytest.mark.parametrize("plen", [2, 65, 300])
+# 18: one pass of 17 rows (the two-token-tile products with a second tile of one row); 65 and 300: full
+# and partial tiles over one or two passes
+@pytest.mark.parametrize("plen", [2, 18, 65, 300])
 def test_batched_prefill_matches_the_token_by_token_prompt(hip_ctx, name, plen):
     say(f"prefill {name} prompt {plen}")
     spec = synth.small_spec(**MODELS[name])
