@@ -662,9 +662,10 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     const int n_total = pos + 1 - p.window_start;
     const int units = (n_total + TP - 1) / TP;
     // tiles per split; a single query takes at least kMinTiles per split
-    // (fewer partials to merge: 12.8 -> 12.4 us at 4k positions, the same
-    // grid at 16k, where every split holds more)
-    constexpr int kMinTiles = MQ ? 1 : 6;
+    // (fewer partials to merge: 6 tiles took 12.8 -> 12.5 us at 4k positions,
+    // 8 tiles 12.3 us, 10 tiles 14.6 us, the same grid at 16k, where every
+    // split holds more)
+    constexpr int kMinTiles = MQ ? 1 : 8;
     const int per = max((units + p.max_splits - 1) / p.max_splits, kMinTiles);
     const int nsplit = (units + per - 1) / per;
     if (split >= nsplit) return;
