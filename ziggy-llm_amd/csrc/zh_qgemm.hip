@@ -13,8 +13,10 @@
 // enters as bf16 hi + lo, x = hi + lo to 2^-17 relative).  So a weight is
 // never rounded, only the activations are, at 2^-17 -- well inside the
 // 1e-4 relative-L2 bar.  Q4_K codes enter as 128 + c, built from their bits
-// without a conversion; the products' excess, 128 times the sub-block's
-// activation sum, goes with the minimum term.
+// without a conversion; each product starts from -128 times the sub-block's
+// activation sum, which cancels that excess inside the product, and the
+// minimum terms of a chunk's eight sub-blocks are two f32 matrix products
+// (min / 128 against the same staged sums).
 //
 // Product layout (v_mfma_f32_16x16x32_bf16 / 16x16x16_bf16, wave64):
 // A = activations (row i = token), B = codes (column j = weight row),
@@ -195,6 +197,16 @@ template <> struct QChunk<Q4_K> {
         const uint2 w = q[j >> 1];
         const int sh = (j & 1) ? 4 : 0;
         return codes_m8((w.x >> sh) & 0x0F0F0F0Fu, (w.y >> sh) & 0x0F0F0F0Fu);
+    }
+    // min_j / kOff of sub-blocks j = lg and j = 4 + lg (a runtime lane
+    // group; the same minimums as step's), the minimum term's coefficients
+    // against the staged sums -kOff X
+    __device__ __forceinline__ void min_coef(int lg, float &c0, float &c1) const {
+        const int o = 8 * lg;
+        const uint32_t bz = (hd.z >> o) & 0xFFu, bw = (hd.w >> o) & 0xFFu;
+        const float dm = h2f(hd.x >> 16);
+        c0 = dm * (float)(bz & 63) * (1.f / kOff);
+        c1 = dm * (float)((bw >> 4) | ((bz >> 6) << 4)) * (1.f / kOff);
     }
 };
 
@@ -421,7 +433,7 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
     constexpr int kXRow = kStage + 8;
     __shared__ __align__(16) unsigned short xs_raw[(2 * NT - 1) * kXRow + kStage];
     auto xs_at = [&](int piece, int tok, int k) -> unsigned short * { return &xs_raw[(piece * NT + tok) * kXRow + k]; };
-    __shared__ __align__(16) float xsum_s[kXsum ? kStage / kSub : 1][kXsum ? NT : 1];  // [sub-block][token]
+    __shared__ __align__(16) float xsum_s[kXsum ? kStage / kSub : 1][kXsum ? NT : 1];  // [sub-block][token]: -kOff X
     __shared__ __align__(16) uint32_t code_s[4][kMats][16 * kRowW];        // [wavefront][matrix][row image]
     const int tt = tid >> 4, part = tid & 15;
     static_assert(!XP || !kXsum || kSub == 32, "split inputs carry 32-value sums");
@@ -510,8 +522,8 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
                 dh[1] = {hw[4], hw[5], hw[6], hw[7]};
                 dl[0] = {lw[0], lw[1], lw[2], lw[3]};
                 dl[1] = {lw[4], lw[5], lw[6], lw[7]};
-                if (kXsum && kSub == 32 && !(part & 1)) xsum_s[u * 8 + (part >> 1)][tk] = sum;
-                if (kXsum && kSub == 16) xsum_s[u * 16 + part][tk] = sum;
+                if (kXsum && kSub == 32 && !(part & 1)) xsum_s[u * 8 + (part >> 1)][tk] = -QC::kOff * sum;
+                if (kXsum && kSub == 16) xsum_s[u * 16 + part][tk] = -QC::kOff * sum;
             }
     };
 
@@ -543,11 +555,17 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
                 for (int t = 0; t < TT; t++) {
                     const bf8v ah = as_bf8(*reinterpret_cast<const uint4 *>(xs_at(0, 16 * t + li, kx + 8 * lg)));
                     const bf8v al = as_bf8(*reinterpret_cast<const uint4 *>(xs_at(1, 16 * t + li, kx + 8 * lg)));
-                    dv[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, zero, 0, 0, 0);
+                    // kOff codes: the products start from -kOff X (the staged
+                    // sums of tokens 4 lg .. 4 lg + 3), so the code offset
+                    // cancels inside the product: D, not D + kOff X
+                    qf4v c0 = zero;
+                    if constexpr (kXsum)
+                        c0 = *reinterpret_cast<const qf4v *>(&xsum_s[cs * (kQChunk / kSub) + j][16 * t + 4 * lg]);
+                    dv[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, c0, 0, 0, 0);
                     dv[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, dv[t][j], 0, 0, 0);
                     dv2[t][j] = zero;
                     if (kPair) {
-                        dv2[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b2, zero, 0, 0, 0);
+                        dv2[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b2, c0, 0, 0, 0);
                         dv2[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b2, dv2[t][j], 0, 0, 0);
                     }
                 }
@@ -572,28 +590,36 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
 #pragma unroll
         for (int j = j0; j < j0 + P; j++) {
             const float s = sv[j] * live, s2 = sv2[j] * live;
-            const float c = fmaf(QC::kOff, sv[j], mv[j]) * live, c2 = fmaf(QC::kOff, sv2[j], mv2[j]) * live;
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    acc[t][q] = fmaf(s, dv[t][j][q], acc[t][q]);
+                    if (kPair) acc2[t][q] = fmaf(s2, dv2[t][j][q], acc2[t][q]);
+                }
+        }
+        }
+        if constexpr (kXsum) {
+            // s D - min X, X the sub-block's activation sum: the minimum
+            // terms of the chunk's 8 sub-blocks as two f32 products (no
+            // FMAs per result and step), A = -kOff X[token][sub-block
+            // 4 h + lg], B = min / kOff of row li (v_mfma_f32_16x16x4_f32,
+            // D[token][row]: the layout of acc)
+            static_assert(kSub == 32, "eight sub-blocks per chunk");
+            float c0, c1, e0 = 0.f, e1 = 0.f;
+            r.min_coef(lg, c0, c1);
+            c0 *= live, c1 *= live;
+            if (kPair) r2.min_coef(lg, e0, e1), e0 *= live, e1 *= live;
 #pragma unroll
             for (int t = 0; t < TT; t++) {
-                if (kXsum) {
-                    // s (D + kOff X) - (kOff s + min) X, X the sub-block's activation sum
-                    const float4 xsm =
-                        *reinterpret_cast<const float4 *>(&xsum_s[cs * (kQChunk / kSub) + j][16 * t + 4 * lg]);
-                    const float xm[4] = {xsm.x, xsm.y, xsm.z, xsm.w};
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        acc[t][q] = fmaf(s, dv[t][j][q], fmaf(-c, xm[q], acc[t][q]));
-                        if (kPair) acc2[t][q] = fmaf(s2, dv2[t][j][q], fmaf(-c2, xm[q], acc2[t][q]));
-                    }
-                } else {
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        acc[t][q] = fmaf(s, dv[t][j][q], acc[t][q]);
-                        if (kPair) acc2[t][q] = fmaf(s2, dv2[t][j][q], acc2[t][q]);
-                    }
+                const float x0 = xsum_s[cs * 8 + lg][16 * t + li], x1 = xsum_s[cs * 8 + 4 + lg][16 * t + li];
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x0, c0, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x1, c1, acc[t], 0, 0, 0);
+                if (kPair) {
+                    acc2[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x0, e0, acc2[t], 0, 0, 0);
+                    acc2[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x1, e1, acc2[t], 0, 0, 0);
                 }
             }
-        }
         }
     };
 
