@@ -783,6 +783,19 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
     }
     // Several stages (one group per workgroup): the first stage as above,
     // later stages wait for the ring's loads ahead of their activations.
+    // kPre: the next stage's inputs are loaded into registers while this
+    // stage computes, where the registers allow it without spills (the
+    // one-tile single products but Q3_K's, the split-input Q4_K / IQ4_XS
+    // ones and the grouped IQ4_XS pair); the last stage re-loads itself, so
+    // the loads stay unconditional.
+    constexpr bool kPre = kStageChunks > 1 && (XP ? (F == Q4_K || F == IQ4_XS)
+                                               : GROUPED ? (kPair && F == IQ4_XS)
+                                                         : (!kPair && F != Q3_K));
+    const int last_s0 = (nspan - 1) / kStageChunks * kStageChunks;
+    auto prefetch = [&](int s0) {
+        const int sn = min(s0, last_s0);
+        stage_load(kbeg + sn * kQChunk, min(kStageChunks, nspan - sn));
+    };
     {
         const int nst = kStageChunks;
         stage_load(kbeg, nst);
@@ -791,6 +804,7 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
         stage_store(nst);
         __syncthreads();
         fetch(0, 0, fa);
+        if constexpr (kPre) prefetch(kStageChunks);
         if constexpr (kStageChunks == 1) {
             fetch(1, 1, fb);  // chunk 0 only; the pairs below start at chunk 1
             compute(fa[0], fa[kMats - 1], 0, 1.f);
@@ -823,9 +837,10 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
         for (int s0 = kStageChunks; s0 < nspan; s0 += kStageChunks) {
             const int nst = min(kStageChunks, nspan - s0);
             __syncthreads();  // every wavefront is done with the previous stage
-            stage_load(kbeg + s0 * kQChunk, nst);
+            if constexpr (!kPre) stage_load(kbeg + s0 * kQChunk, nst);
             stage_store(nst);
             __syncthreads();
+            if constexpr (kPre) prefetch(s0 + kStageChunks);
             run_stage(s0, nst);
         }
     }
