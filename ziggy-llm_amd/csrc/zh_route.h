@@ -85,42 +85,35 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
     // route_ordered_bits), then, among the entries holding it, the lowest
     // index (ballots: entry l + 64 i, i first, then the lane).  The round's
     // value is the selected probability itself, so no lane read follows.
-    uint32_t ob[4];
-    bool live[4];  // in range and not yet taken
+    // Keys: live entries at least 1, entries out of range or taken 0, so a
+    // round is maxima and selects only (no flags, no branch per lane); a
+    // best key of 0 means no live entry is left (index -1, as before).
+    uint32_t key[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        ob[i] = route_ordered_bits(pr[i]);
-        live[i] = l + 64 * i < E;
-    }
+    for (int i = 0; i < 4; i++) key[i] = l + 64 * i < E ? max(route_ordered_bits(pr[i]), 1u) : 0u;
     // (loops over r run to the compile-time bound kRouteMaxK with a uniform
-    // r < k guard: sel and w stay in registers, indexed statically)
+    // r < k guard: sel and w stay in scalar registers, indexed statically)
     uint32_t sel[kRouteMaxK];
     float w[kRouteMaxK];
 #pragma unroll
+    for (int r = 0; r < kRouteMaxK; r++) sel[r] = 0u, w[r] = 0.f;
+#pragma unroll
     for (int r = 0; r < kRouteMaxK; r++) {
-        sel[r] = 0u;
-        w[r] = 0.f;
-        if (r >= k) continue;
-        uint32_t mine = 0u;
-        bool any = false;
+        if (r < k) {
+            const uint32_t best = (uint32_t)__builtin_amdgcn_readfirstlane(
+                (int)wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3]))));
+            const unsigned long long b0 = __ballot(key[0] == best), b1 = __ballot(key[1] == best),
+                                     b2 = __ballot(key[2] == best), b3 = __ballot(key[3] == best);
+            // the first set bit of the 256-entry mask b3:b2:b1:b0 (scalar
+            // minima, no branches: an empty mask gives 64 past its block)
+            int idx = min(min(__builtin_ctzg(b0, 256), 64 + __builtin_ctzg(b1, 192)),
+                          min(128 + __builtin_ctzg(b2, 128), 192 + __builtin_ctzg(b3, 64)));
+            if (best == 0u) idx = -1;
+            sel[r] = (uint32_t)idx;
+            w[r] = __uint_as_float((best & 0x80000000u) ? (best & 0x7FFFFFFFu) : ~best);
+            const bool mine = idx >= 0 && (idx & 63) == l;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            if (live[i] && (!any || ob[i] > mine)) mine = ob[i];
-            any = any || live[i];
-        }
-        const uint32_t best = wave_max_u32(mine);
-        int idx = -1;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const unsigned long long b = __ballot(live[i] && ob[i] == best);
-            if (idx < 0 && b) idx = 64 * i + __builtin_ctzll(b);
-        }
-        sel[r] = (uint32_t)idx;
-        w[r] = __uint_as_float((best & 0x80000000u) ? (best & 0x7FFFFFFFu) : ~best);
-        if ((idx & 63) == l) {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                if (i == (idx >> 6)) live[i] = false;
+            for (int i = 0; i < 4; i++) key[i] = (mine && (idx >> 6) == i) ? 0u : key[i];
         }
     }
     if (l == 0) {
