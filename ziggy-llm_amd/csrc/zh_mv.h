@@ -277,33 +277,41 @@ __device__ __forceinline__ void coop_finish(XDig &xs, const XRun &r, int nruns, 
 
 // The fused combine of the previous MoE layer (MvParams::pro_in, NORM): CPT
 // float4 chunks of the row per thread, every load (hidden, the k routed rows,
-// the shared row) in flight before any arithmetic, then combine_value's
-// operations in its order per element; the row goes to LDS (and from the
-// writer workgroup to pro_out).  Loads past the row re-read its last chunk.
-template <int CPT>
-__device__ __forceinline__ void combine_prologue(const MvParams &p, float *xc, bool writer) {
-    const int H = p.cols, k = (int)(p.pro_cfg & 0xF);
-    const bool shared = p.pro_cfg >> 4 & 1;
+// the shared row, the route's weights) in flight before any arithmetic
+// (combine_load), then combine_value's operations in its order per element
+// (combine_finish); the row goes to LDS (and from the writer workgroup to
+// pro_out).  Loads past the row re-read its last chunk.
+template <int CPT> struct CombineIn {
     float4 hv[CPT], tv[CPT][kRouteMaxK], sv[CPT];
+    float w[kRouteMaxK], g;
+};
+template <int CPT> __device__ __forceinline__ void combine_load(CombineIn<CPT> &ci, const MvParams &p) {
+    const int H = p.cols, k = (int)(p.pro_cfg & 0xF);
 #pragma unroll
     for (int c = 0; c < CPT; c++) {
         const int i4 = min((int)threadIdx.x + c * kThreads, H / 4 - 1);
-        hv[c] = *reinterpret_cast<const float4 *>(p.x + 4 * i4);
+        ci.hv[c] = *reinterpret_cast<const float4 *>(p.x + 4 * i4);
 #pragma unroll
         for (int s = 0; s < kRouteMaxK; s++)
-            tv[c][s] = *reinterpret_cast<const float4 *>(p.pro_in + (size_t)min(s, k - 1) * H + 4 * i4);
-        sv[c] = *reinterpret_cast<const float4 *>(p.pro_in + (size_t)k * H + 4 * i4);
+            ci.tv[c][s] = *reinterpret_cast<const float4 *>(p.pro_in + (size_t)min(s, k - 1) * H + 4 * i4);
+        ci.sv[c] = *reinterpret_cast<const float4 *>(p.pro_in + (size_t)k * H + 4 * i4);
     }
-    float w[kRouteMaxK];
 #pragma unroll
-    for (int s = 0; s < kRouteMaxK; s++) w[s] = __uint_as_float(p.expert[2 * min(s, k - 1) + 1]);
-    const float g = __uint_as_float(p.expert[2 * k]);
+    for (int s = 0; s < kRouteMaxK; s++) ci.w[s] = __uint_as_float(p.expert[2 * min(s, k - 1) + 1]);
+    ci.g = __uint_as_float(p.expert[2 * k]);
+}
+template <int CPT>
+__device__ __forceinline__ void combine_finish(const CombineIn<CPT> &ci, const MvParams &p, float *xc, bool writer) {
+    const int H = p.cols, k = (int)(p.pro_cfg & 0xF);
+    const bool shared = p.pro_cfg >> 4 & 1;
     float *out = static_cast<float *>(p.pro_out);
 #pragma unroll
     for (int c = 0; c < CPT; c++) {
         const int i4 = (int)threadIdx.x + c * kThreads;
         if (i4 >= H / 4) continue;
-        float hs[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w}, ss[4] = {sv[c].x, sv[c].y, sv[c].z, sv[c].w}, r[4];
+        const float hs[4] = {ci.hv[c].x, ci.hv[c].y, ci.hv[c].z, ci.hv[c].w};
+        const float ss[4] = {ci.sv[c].x, ci.sv[c].y, ci.sv[c].z, ci.sv[c].w};
+        float r[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             // combine_value (zh_route.h), operation for operation
@@ -311,16 +319,24 @@ __device__ __forceinline__ void combine_prologue(const MvParams &p, float *xc, b
 #pragma unroll
             for (int s = 0; s < kRouteMaxK; s++) {
                 if (s >= k) break;
-                const float d = e == 0 ? tv[c][s].x : e == 1 ? tv[c][s].y : e == 2 ? tv[c][s].z : tv[c][s].w;
-                o = w[s] == 1.0f ? o + d : fmaf(d, w[s], o);
+                const float4 &t = ci.tv[c][s];
+                const float d = e == 0 ? t.x : e == 1 ? t.y : e == 2 ? t.z : t.w;
+                o = ci.w[s] == 1.0f ? o + d : fmaf(d, ci.w[s], o);
             }
-            if (shared) o = g == 1.0f ? o + ss[e] : fmaf(ss[e], g, o);
+            if (shared) o = ci.g == 1.0f ? o + ss[e] : fmaf(ss[e], ci.g, o);
             r[e] = hs[e] + o;
         }
         const float4 v = make_float4(r[0], r[1], r[2], r[3]);
         *reinterpret_cast<float4 *>(xc + 4 * i4) = v;
         if (writer) *reinterpret_cast<float4 *>(out + 4 * i4) = v;
     }
+}
+// The whole combine before the product (rows of more than 2048 values).
+template <int CPT>
+__device__ __forceinline__ void combine_prologue(const MvParams &p, float *xc, bool writer) {
+    CombineIn<CPT> ci;
+    combine_load<CPT>(ci, p);
+    combine_finish<CPT>(ci, p, xc, writer);
 }
 
 template <int F, int IN, int OUT>
@@ -353,6 +369,17 @@ __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int 
     // depend on it, so HBM latency overlaps the staging and the norm.
     // The residual read of ADD / WADD rides in the same ring: a late load of
     // y[r] would make the in-order vmcnt wait cover the prefetched rows too.
+    // kComb (the router launch with the previous layer's combine fused, rows
+    // up to 2048 values): the combine's loads go first, then the ring, so the
+    // combine waits only for its own loads and the ring streams meanwhile.
+    constexpr bool kComb = IN == IN_NORM && OUT == OUT_STORE && F == F32;
+    const bool comb = kComb && p.pro_in && p.cols <= kCombineFastCols;
+    __shared__ __align__(16) float xcomb[kComb ? kCombineFastCols : 4];
+    CombineIn<kComb ? 2 : 1> ci;
+    if constexpr (kComb) {
+        if (comb) combine_load<2>(ci, p);
+        __builtin_amdgcn_sched_barrier(0);  // the combine's loads stay ahead of the ring's
+    }
     constexpr bool kReadY = OUT == OUT_ADD || OUT == OUT_WADD;
     Raw<F> ra[D], rb[D];
     float ry[D];
@@ -363,7 +390,17 @@ __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int 
         if (kReadY) ry[k] = sg.y[row_of(k)];
     }
     XOf_t<F> xs;
-    stage_x<F, IN>(xs, lane, active, p, sg.x ? sg.x : p.x, T, lds);
+    bool staged = false;
+    if constexpr (kComb) {
+        if (comb) {
+            // the row from LDS (LDS reads: their wait does not cover the ring)
+            combine_finish<2>(ci, p, xcomb, blockIdx.x == 0);
+            __syncthreads();
+            stage_x<F, IN>(xs, lane, active, p, xcomb, T, lds);
+            staged = true;
+        }
+    }
+    if (!staged) stage_x<F, IN>(xs, lane, active, p, sg.x ? sg.x : p.x, T, lds);
 
     float best_v = -INFINITY;
     int best_r = 0x7fffffff;
@@ -622,12 +659,12 @@ __global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
         }
     }
     if constexpr (IN == IN_NORM && OUT == OUT_STORE && F1 == F32 && F2 == F32) {
-        if (p.pro_in) {  // the previous MoE layer's combine, then the norm as usual
+        // the previous MoE layer's combine, then the norm as usual: rows up
+        // to kCombineFastCols inside the product (its loads ahead of the
+        // weights'), wider rows here
+        if (p.pro_in && p.cols > kCombineFastCols) {
             __shared__ __align__(16) float xc[kCombineMaxCols];
-            if (p.cols <= 2 * 4 * kThreads)
-                combine_prologue<2>(p, xc, wg == 0);
-            else
-                combine_prologue<kCombineMaxCols / (4 * kThreads)>(p, xc, wg == 0);
+            combine_prologue<kCombineMaxCols / (4 * kThreads)>(p, xc, wg == 0);
             __syncthreads();
             sg.x = xc;
         }

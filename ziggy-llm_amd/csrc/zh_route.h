@@ -169,6 +169,7 @@ __device__ __forceinline__ float combine_value(const float *hidden, const float 
     return hidden[r] + out;
 }
 
-constexpr int kCombineMaxCols = 4096;  // hidden size of the fused combine at most
+constexpr int kCombineMaxCols = 4096;   // hidden size of the fused combine at most
+constexpr int kCombineFastCols = 2048;  // rows combined inside the product (two float4 per thread)
 
 }  // namespace zh
