@@ -235,13 +235,14 @@ struct MvParams {
     float weight_scale;               // WADD: y += scale * dot (scale from entries if expert set)
     const int *gate_flag;             // optional device flag (argmax output only): kernel exits if *gate_flag == 0
     // Fused prologues of the MoE decode launches (pro_in null: none).
-    //   SWIGLU  the routing: each workgroup of a routed segment (and
-    //           workgroup 0) routes the token from the router logits pro_in
-    //           (route_wave, one wavefront) and offsets its segment by the id
-    //           it finds; workgroup 0 writes the route (uint32 entries) to
-    //           pro_out.  pro_cfg = E | k << 16 | gating << 20 |
-    //           weights_norm << 24 | shared_gate << 25, pro_scale = weights
-    //           scale; `expert` is unused.
+    //   SWIGLU  the routing: every wavefront of a routed segment's workgroups
+    //           finds its segment's expert from the router logits pro_in
+    //           (route_id: softmax, top-k up to the slot) and offsets the
+    //           segment by it; one more workgroup, route_wg (set by the
+    //           launcher, past the segments), writes the whole route
+    //           (uint32 entries, route_wave) to pro_out.  pro_cfg = E | k << 16 |
+    //           gating << 20 | weights_norm << 24 | shared_gate << 25,
+    //           pro_scale = weights scale; `expert` is unused.
     //   NORM    (f32 router) the previous layer's combine: the input is
     //           x + combine(pro_in rows, route at `expert`), computed per
     //           workgroup into LDS (cols <= kCombineMaxCols); workgroup 0
@@ -250,6 +251,7 @@ struct MvParams {
     void *pro_out;
     uint32_t pro_cfg;
     float pro_scale;
+    int route_wg;  // SWIGLU routing: the route writer workgroup (launch_matvec sets it)
 };
 
 // Values of a row one team covers (256 lanes of 64); longer rows of plain or

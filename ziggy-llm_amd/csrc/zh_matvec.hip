@@ -156,8 +156,10 @@ static hipError_t launch_matvec_team(const MvParams &p_in, int in, int out, hipS
         k = pick_mv_moe(f1, f2, in, out, p.cols);
     }
     if (!k) return hipErrorInvalidValue;
-    const int grid = total_wgs(p);
+    int grid = total_wgs(p);
     if (grid <= 0) return hipSuccess;
+    // the SWIGLU routing prologue: one more workgroup writes the route
+    p.route_wg = out == OUT_SWIGLU && p.pro_in ? grid++ : -1;
     hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), 0, s, p);
     return hipGetLastError();
 }

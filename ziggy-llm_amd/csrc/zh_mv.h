@@ -636,20 +636,23 @@ __global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
     // loads, not one dependent round trip per use
     MvSeg sg = p.seg[si];
     if constexpr (OUT == OUT_SWIGLU) {
-        if (p.pro_in && (sg.expert_slot >= 0 || wg == 0)) {  // uniform over the workgroup
-            __shared__ uint32_t route_s[2 * kRouteMaxK + 2];
-            if (threadIdx.x < 64) {
-                const uint32_t c = p.pro_cfg;
-                uint32_t *out = static_cast<uint32_t *>(p.pro_out);
-                route_wave(p.pro_in, (int)(c & 0xFFFF), (int)(c >> 16 & 0xF), (int)(c >> 20 & 0xF),
-                           (int)(c >> 24 & 1), p.pro_scale, (int)(c >> 25 & 1), [&](int i, uint32_t v) {
-                               route_s[i] = v;
-                               if (wg == 0) out[i] = v;
-                           });
+        if (p.pro_in) {  // uniform over the workgroup
+            const uint32_t c = p.pro_cfg;
+            const int E = (int)(c & 0xFFFF), gating = (int)(c >> 20 & 0xF);
+            if (wg == p.route_wg) {
+                // the route writer (a workgroup of its own, no rows): the
+                // whole route, weights and shared gate included, to pro_out
+                if (threadIdx.x < 64) {
+                    uint32_t *out = static_cast<uint32_t *>(p.pro_out);
+                    route_wave(p.pro_in, E, (int)(c >> 16 & 0xF), gating, (int)(c >> 24 & 1), p.pro_scale,
+                               (int)(c >> 25 & 1), [&](int i, uint32_t v) { out[i] = v; });
+                }
+                return;
             }
-            __syncthreads();
             if (sg.expert_slot >= 0) {
-                const uint32_t e = (uint32_t)__builtin_amdgcn_readfirstlane((int)route_s[2 * sg.expert_slot]);
+                // every wavefront finds this segment's expert itself: the
+                // softmax and the top-k up to its slot (no barrier, no weights)
+                const uint32_t e = route_id(p.pro_in, E, gating, sg.expert_slot);
                 if (e >= (uint32_t)p.expert_limit) return;  // uniform over the segment: no rows are read
                 const uint64_t off = (uint64_t)e * (uint64_t)p.rows_per_expert * sg.stride;
                 sg.w += off;

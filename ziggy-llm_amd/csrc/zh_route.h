@@ -58,15 +58,12 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return max(a, b);
 }
 
-template <class Put>
-__device__ __forceinline__ void route_wave(const float *__restrict__ logits, int E, int k, int gating,
-                                           int weights_norm, float weights_scale, int has_shared_gate, Put put) {
+// The softmax (gating 1, 2) of the E router logits, four entries per lane
+// (entry l + 64 i in pr[i]; -INFINITY past E).
+__device__ __forceinline__ void route_probs(const float *__restrict__ logits, int E, int gating, float (&pr)[4]) {
     const int l = threadIdx.x & 63;
-    float pr[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) pr[i] = l + 64 * i < E ? logits[l + 64 * i] : -INFINITY;
-    // the shared expert's gate logit, loaded with the others (not after the top-k)
-    const float gate_logit = has_shared_gate ? logits[E] : 0.f;
     if (gating == 1 || gating == 2) {
         // softmaxInPlace (model/loader.zig:4160-4170): max, exp(v - max), / sum
         float m = fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3]));
@@ -81,6 +78,13 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
 #pragma unroll
         for (int i = 0; i < 4; i++) pr[i] = l + 64 * i < E ? pr[i] / s : -INFINITY;
     }
+}
+
+// The first k selections (k <= kRouteMaxK) of the top-k over pr: ids in
+// sel[r] and probabilities in w[r] (uniform over the wavefront).
+__device__ __forceinline__ void route_topk(const float (&pr)[4], int E, int k, uint32_t (&sel)[kRouteMaxK],
+                                           float (&w)[kRouteMaxK]) {
+    const int l = threadIdx.x & 63;
     // k rounds: the largest value not yet taken (in the total order of
     // route_ordered_bits), then, among the entries holding it, the lowest
     // index (ballots: entry l + 64 i, i first, then the lane).  The round's
@@ -93,8 +97,6 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
     for (int i = 0; i < 4; i++) key[i] = l + 64 * i < E ? max(route_ordered_bits(pr[i]), 1u) : 0u;
     // (loops over r run to the compile-time bound kRouteMaxK with a uniform
     // r < k guard: sel and w stay in scalar registers, indexed statically)
-    uint32_t sel[kRouteMaxK];
-    float w[kRouteMaxK];
 #pragma unroll
     for (int r = 0; r < kRouteMaxK; r++) sel[r] = 0u, w[r] = 0.f;
 #pragma unroll
@@ -116,6 +118,34 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ logits, int
             for (int i = 0; i < 4; i++) key[i] = (mine && (idx >> 6) == i) ? 0u : key[i];
         }
     }
+}
+
+// Expert id of selection `slot` (< kRouteMaxK): the softmax and the first
+// slot + 1 rounds of the top-k, no weights (every wavefront of a workgroup
+// can run it for itself).
+__device__ __forceinline__ uint32_t route_id(const float *__restrict__ logits, int E, int gating, int slot) {
+    float pr[4];
+    route_probs(logits, E, gating, pr);
+    uint32_t sel[kRouteMaxK];
+    float w[kRouteMaxK];
+    route_topk(pr, E, slot + 1, sel, w);
+    uint32_t e = 0u;
+#pragma unroll
+    for (int r = 0; r < kRouteMaxK; r++) e = r == slot ? sel[r] : e;
+    return e;
+}
+
+template <class Put>
+__device__ __forceinline__ void route_wave(const float *__restrict__ logits, int E, int k, int gating,
+                                           int weights_norm, float weights_scale, int has_shared_gate, Put put) {
+    const int l = threadIdx.x & 63;
+    float pr[4];
+    route_probs(logits, E, gating, pr);
+    // the shared expert's gate logit, loaded with the others (not after the top-k)
+    const float gate_logit = has_shared_gate ? logits[E] : 0.f;
+    uint32_t sel[kRouteMaxK];
+    float w[kRouteMaxK];
+    route_topk(pr, E, k, sel, w);
     if (l == 0) {
         if (weights_norm) {
             float sum = 0.f;
