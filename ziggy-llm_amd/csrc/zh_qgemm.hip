@@ -148,7 +148,7 @@ static_assert(bf16_of_int(1) == 0x3F80u && bf16_of_int(113) == 0x42E2u && bf16_o
 // mod 16): load(r, sh, lg) reads the words lane group lg needs from the row
 // image r.  Steps: kSteps sub-blocks of kSub values; step(j) gives the lane's
 // codes for values kSub/4 * lg .. of sub-block j and the sub-block's scale
-// (and min).
+// (Q4_K's minimums: min_coef).
 
 // bytes o .. o + 3 of a staged row image (o even)
 template <int SHM> __device__ __forceinline__ uint32_t rw4(const uint32_t *r, int o) {
@@ -182,18 +182,11 @@ template <> struct QChunk<Q4_K> {
         const uint32_t w = k < 4 ? hd.y : k < 8 ? hd.z : hd.w;
         return (w >> (8 * (k & 3))) & 0xFFu;
     }
-    // getScaleMinK4 (model/loader.zig:3814-3825)
-    __device__ __forceinline__ uint4 step(int j, float &s, float &mn) const {
-        uint32_t sc, m;
-        if (j < 4) {
-            sc = sbyte(j) & 63;
-            m = sbyte(j + 4) & 63;
-        } else {
-            sc = (sbyte(j + 4) & 0x0F) | ((sbyte(j - 4) >> 6) << 4);
-            m = (sbyte(j + 4) >> 4) | ((sbyte(j) >> 6) << 4);
-        }
+    // getScaleMinK4 (model/loader.zig:3814-3825): the scale here, the
+    // minimum in min_coef
+    __device__ __forceinline__ uint4 step(int j, float &s) const {
+        const uint32_t sc = j < 4 ? sbyte(j) & 63 : (sbyte(j + 4) & 0x0F) | ((sbyte(j - 4) >> 6) << 4);
         s = h2f(hd.x) * (float)sc;
-        mn = h2f(hd.x >> 16) * (float)m;
         const uint2 w = q[j >> 1];
         const int sh = (j & 1) ? 4 : 0;
         return codes_m8((w.x >> sh) & 0x0F0F0F0Fu, (w.y >> sh) & 0x0F0F0F0Fu);
@@ -222,9 +215,8 @@ template <> struct QChunk<Q8_0> {
             d[b] = rw2(r, sh + 34 * b);
         }
     }
-    __device__ __forceinline__ uint4 step(int j, float &s, float &mn) const {
+    __device__ __forceinline__ uint4 step(int j, float &s) const {
         s = h2f(d[j]);
-        mn = 0.f;
         return codes_s8(q[j].x, q[j].y);
     }
 };
@@ -245,11 +237,10 @@ template <> struct QChunk<IQ4_XS> {
         hi = lg >> 1;
     }
     // dequantizeRowIQ4XS (model/quant_extra.zig:191-246): dl = d * (ls - 32)
-    __device__ __forceinline__ uint4 step(int j, float &s, float &mn) const {
+    __device__ __forceinline__ uint4 step(int j, float &s) const {
         const uint32_t low = (hd.y >> (8 * (j >> 1) + 4 * (j & 1))) & 0x0F;
         const uint32_t high = (hd.x >> (16 + 2 * j)) & 3;
         s = h2f(hd.x) * (float)((int)(low | (high << 4)) - 32);
-        mn = 0.f;
         const int sh = hi ? 4 : 0;
         const uint2 a = iq4_bf16_lookup4((q[j].x >> sh) & 0x0F0F0F0Fu), b = iq4_bf16_lookup4((q[j].y >> sh) & 0x0F0F0F0Fu);
         return {a.x, a.y, b.x, b.y};
@@ -540,17 +531,17 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
         constexpr int P = S * TT > 16 ? 16 / TT : S;
         const qf4v zero = {0.f, 0.f, 0.f, 0.f};
         qf4v dv[TT][S], dv2[TT][S];
-        float sv[S], mv[S], sv2[S], mv2[S];
+        float sv[S], sv2[S];
 #pragma unroll
         for (int j0 = 0; j0 < S; j0 += P) {
 #pragma unroll
         for (int j = j0; j < j0 + P; j++) {
-            mv[j] = 0.f, sv2[j] = 0.f, mv2[j] = 0.f;
+            sv2[j] = 0.f;
             const int kx = cs * kQChunk + kSub * j;
             if constexpr (kSub == 32) {
-                const bf8v b = as_bf8(r.step(j, sv[j], mv[j]));
+                const bf8v b = as_bf8(r.step(j, sv[j]));
                 bf8v b2 = b;
-                if (kPair) b2 = as_bf8(r2.step(j, sv2[j], mv2[j]));
+                if (kPair) b2 = as_bf8(r2.step(j, sv2[j]));
 #pragma unroll
                 for (int t = 0; t < TT; t++) {
                     const bf8v ah = as_bf8(*reinterpret_cast<const uint4 *>(xs_at(0, 16 * t + li, kx + 8 * lg)));
