@@ -779,6 +779,8 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
     // one-tile single products but Q3_K's, the split-input Q4_K / IQ4_XS
     // ones and the grouped IQ4_XS pair); the last stage re-loads itself, so
     // the loads stay unconditional.
+    // kPre1: the same for the one-chunk stages of the split-input Q8_0 kernel
+    constexpr bool kPre1 = XP && kStageChunks == 1 && F == Q8_0;
     constexpr bool kPre = kStageChunks > 1 && (XP ? (F == Q4_K || F == IQ4_XS)
                                                : GROUPED ? (kPair && F == IQ4_XS)
                                                          : (!kPair && F != Q3_K));
@@ -795,7 +797,7 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
         stage_store(nst);
         __syncthreads();
         fetch(0, 0, fa);
-        if constexpr (kPre) prefetch(kStageChunks);
+        if constexpr (kPre || kPre1) prefetch(kStageChunks);
         if constexpr (kStageChunks == 1) {
             fetch(1, 1, fb);  // chunk 0 only; the pairs below start at chunk 1
             compute(fa[0], fa[kMats - 1], 0, 1.f);
@@ -808,19 +810,23 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
         // and the ring slot of a chunk are its parity at compile time.
         for (int s0 = 1; s0 < nspan; s0 += 2) {
             __syncthreads();  // every wavefront is done with the previous stage
-            stage_load(kbeg + s0 * kQChunk, 1);
+            if constexpr (!kPre1) stage_load(kbeg + s0 * kQChunk, 1);
             stage_store(1);
             __syncthreads();
+            if constexpr (kPre1) prefetch(s0 + 1);
             fetch(0, s0 + 1, fa);
             compute(fb[0], fb[kMats - 1], 0, 1.f);
             // chunk s0 + 1 (past the range: a dead step, so the pairs stay whole)
             const bool more = s0 + 1 < nspan;
             __syncthreads();
-            if (more) {
+            if constexpr (kPre1) {
+                stage_store(more ? 1 : 0);  // (the loads land either way)
+            } else if (more) {
                 stage_load(kbeg + (s0 + 1) * kQChunk, 1);
                 stage_store(1);
             }
             __syncthreads();
+            if constexpr (kPre1) prefetch(s0 + 2);
             fetch(1, s0 + 2, fb);
             compute(fa[0], fa[kMats - 1], 0, more ? 1.f : 0.f);
         }
