@@ -376,14 +376,20 @@ hipError_t launch_moe_group(const uint32_t *route, int route_stride, int M, int 
 // token): out[m] = (scale_m * x[m]) * w; one workgroup per token.  V: rows of
 // up to 8192 values (multiples of 4, 16-byte aligned) held in registers, every
 // load in flight at once.  The workgroups also clear up to three float ranges
-// (outputs that products then accumulate onto).
+// (outputs that products then accumulate onto).  SPLIT (V rows of up to
+// 4096 values, a multiple of 32): the normed row also goes out as the GEMM's
+// pieces (XPlanes), through LDS, one 16-value run per thread as
+// split_rows_kernel splits it: the same values, pieces and sums.
 struct NormClear {
     float *p[3];
     size_t n[3];
 };
-template <bool V>
+constexpr int kNormSplitMax = 4096;
+template <bool V, bool SPLIT = false>
 __global__ void __launch_bounds__(256) rms_norm_rows_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                            float *__restrict__ out, int n, float eps, NormClear cl) {
+                                                            float *__restrict__ out, int n, float eps, NormClear cl,
+                                                            XPlanes xp = XPlanes{}) {
+    static_assert(!SPLIT || V, "the split takes the register rows");
     const int tid = threadIdx.x;
     const float *xr = x + (size_t)blockIdx.x * n;
     float *orow = out + (size_t)blockIdx.x * n;
@@ -411,11 +417,37 @@ __global__ void __launch_bounds__(256) rms_norm_rows_kernel(const float *__restr
     const float scale = 1.0f / sqrtf(tot / (float)n + eps);
     if (V) {
         float4 *o4 = reinterpret_cast<float4 *>(orow);
+        __shared__ __align__(16) float rowv[SPLIT ? kNormSplitMax : 4];
 #pragma unroll
         for (int j = 0; j < 8; j++)
-            if (tid + 256 * j < n4)
-                o4[tid + 256 * j] = {(scale * v[j].x) * wv[j].x, (scale * v[j].y) * wv[j].y,
-                                     (scale * v[j].z) * wv[j].z, (scale * v[j].w) * wv[j].w};
+            if (tid + 256 * j < n4) {
+                const float4 o = {(scale * v[j].x) * wv[j].x, (scale * v[j].y) * wv[j].y, (scale * v[j].z) * wv[j].z,
+                                  (scale * v[j].w) * wv[j].w};
+                o4[tid + 256 * j] = o;
+                if (SPLIT) *reinterpret_cast<float4 *>(&rowv[4 * (tid + 256 * j)]) = o;
+            }
+        if constexpr (SPLIT) {
+            __syncthreads();
+            const int runs = n >> 4, r = min(tid, runs - 1);
+            float rv[16];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float4 q = *reinterpret_cast<const float4 *>(&rowv[16 * r + 4 * c]);
+                rv[4 * c] = q.x, rv[4 * c + 1] = q.y, rv[4 * c + 2] = q.z, rv[4 * c + 3] = q.w;
+            }
+            uint32_t hw[8], lw[8];
+            float sum = split_run16(rv, hw, lw);
+            sum += __shfl_xor(sum, 1, 64);  // the other run of the 32-value sum
+            if (tid < runs) {
+                uint4 *dh = reinterpret_cast<uint4 *>(xp.hi + (size_t)blockIdx.x * xp.ld + 16 * r);
+                uint4 *dl = reinterpret_cast<uint4 *>(xp.lo + (size_t)blockIdx.x * xp.ld + 16 * r);
+                dh[0] = {hw[0], hw[1], hw[2], hw[3]};
+                dh[1] = {hw[4], hw[5], hw[6], hw[7]};
+                dl[0] = {lw[0], lw[1], lw[2], lw[3]};
+                dl[1] = {lw[4], lw[5], lw[6], lw[7]};
+                if (!(r & 1)) xp.sum[(size_t)blockIdx.x * (xp.ld / 32) + (r >> 1)] = sum;
+            }
+        }
     } else {
         for (int i = tid; i < n; i += 256) orow[i] = (scale * xr[i]) * w[i];
     }
@@ -425,10 +457,21 @@ __global__ void __launch_bounds__(256) rms_norm_rows_kernel(const float *__restr
 }
 
 hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps, hipStream_t s,
-                                float *clear0, size_t n0, float *clear1, size_t n1, float *clear2, size_t n2) {
+                                float *clear0, size_t n0, float *clear1, size_t n1, float *clear2, size_t n2,
+                                const XPlanes *xp) {
     if (rows < 1 || n < 1 || (n0 && !clear0) || (n1 && !clear1) || (n2 && !clear2)) return hipErrorInvalidValue;
     const NormClear cl{{clear0, clear1, clear2}, {n0, n1, n2}};
     const bool v = n % 4 == 0 && n <= 8 * 256 * 4 && ((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) % 16 == 0;
+    if (xp) {
+        // the split in the norm's launch where it fits, else a split launch after it
+        if (v && n % 32 == 0 && n <= kNormSplitMax && xp->hi && xp->lo && xp->sum && xp->ld % 32 == 0 && xp->ld >= n) {
+            hipLaunchKernelGGL((rms_norm_rows_kernel<true, true>), dim3(rows), dim3(256), 0, s, x, w, out, n, eps, cl,
+                               *xp);
+            return hipGetLastError();
+        }
+        hipError_t e = launch_rms_norm_rows(x, w, out, rows, n, eps, s, clear0, n0, clear1, n1, clear2, n2);
+        return e != hipSuccess ? e : launch_split_rows(out, n, rows, n, *xp, s);
+    }
     if (v)
         hipLaunchKernelGGL(rms_norm_rows_kernel<true>, dim3(rows), dim3(256), 0, s, x, w, out, n, eps, cl);
     else

@@ -321,9 +321,11 @@ hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t st
 hipError_t launch_gemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
                              const int *N, uint64_t stride, const float *x, int ldx, int M, int K, int out,
                              hipStream_t s, int max_split = 16, const XPlanes *xp = nullptr);
+// xp (optional): the normed rows also split into xp (as launch_split_rows),
+// in the same launch where the row fits.
 hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps, hipStream_t s,
                                 float *clear0 = nullptr, size_t n0 = 0, float *clear1 = nullptr, size_t n1 = 0,
-                                float *clear2 = nullptr, size_t n2 = 0);
+                                float *clear2 = nullptr, size_t n2 = 0, const XPlanes *xp = nullptr);
 // Grouped by expert (MoE prefill): token tiles from launch_moe_group; W of expert e
 // starts expert_stride bytes after W of expert e - 1; x row = id / x_div, y row = id.
 hipError_t launch_gemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, uint64_t expert_stride,

@@ -208,7 +208,12 @@ hipError_t enqueue_prefill_layer(ZiggyHipMoeStack *s, int l, int M, hipStream_t 
     const int H = (int)d.hidden, E = (int)d.expert_count, K = (int)d.expert_used_count, FF = (int)d.expert_ff_length,
               SF = (int)d.shared_ff_length;
     uint32_t *route = s->p_route + (size_t)l * s->pre_max * s->route_stride;
-    hipError_t e = launch_rms_norm_rows(s->p_hidden, (const float *)L.norm.p, s->p_normed, M, H, d.rms_norm_eps, st);
+    // the shared expert on split inputs (more than one token tile): the norm
+    // also splits its rows; gate and up as two stores in one launch, then
+    // SiLU * up split for down
+    const bool sh_split = s->shared && M > 16 && H % 32 == 0 && SF % 32 == 0 && s->p_xp.hi;
+    hipError_t e = launch_rms_norm_rows(s->p_hidden, (const float *)L.norm.p, s->p_normed, M, H, d.rms_norm_eps, st,
+                                        nullptr, 0, nullptr, 0, nullptr, 0, sh_split ? &s->p_xp : nullptr);
     // the shared gate row, stored right after the router's rows, is row E of one launch
     const bool gate_row_next = s->shared_gate && L.gate_inp_sh.p == L.router.p + (uint64_t)E * L.router.stride &&
                                L.gate_inp_sh.stride == L.router.stride;
@@ -228,11 +233,7 @@ hipError_t enqueue_prefill_layer(ZiggyHipMoeStack *s, int l, int M, hipStream_t 
         e = launch_gemm_grouped(L.gate.type, L.gate.p, L.up.p, L.gate.stride, (uint64_t)FF * L.gate.stride,
                                 s->p_normed, H, K, s->p_act, FF, FF, H, OUT_SWIGLU, s->p_tiles, s->p_list,
                                 s->p_ntiles, max_tiles, st);
-    // the shared expert on split inputs (more than one token tile): gate and up
-    // as two stores in one launch, then SiLU * up split for down
-    const bool sh_split = s->shared && M > 16 && H % 32 == 0 && SF % 32 == 0 && s->p_xp.hi;
     if (e == hipSuccess && sh_split) {
-        e = launch_split_rows(s->p_normed, H, M, H, s->p_xp, st);
         const uint8_t *ws[2] = {L.gate_sh.p, L.up_sh.p};
         float *ys[2] = {s->p_act_sh, s->p_up_sh};
         const int lds[2] = {SF, SF}, Ns[2] = {SF, SF};

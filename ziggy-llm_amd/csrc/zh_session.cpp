@@ -970,8 +970,8 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
         const LayerW &L = s->layers[l];
         // the norm clears the q/k/v rows, which the products then accumulate onto
         e = launch_rms_norm_rows(s->b_hidden, (const float *)L.attn_norm.p, s->b_normed, M, H, eps, st, s->b_q,
-                                 (size_t)M * Q, s->b_k, (size_t)M * KV, s->b_v, (size_t)M * KV);
-        if (split_in && e == hipSuccess) e = launch_split_rows(s->b_normed, H, M, H, s->xp, st);
+                                 (size_t)M * Q, s->b_k, (size_t)M * KV, s->b_v, (size_t)M * KV,
+                                 split_in ? &s->xp : nullptr);
         multi3(L.q, s->b_q, Q, L.k, s->b_k, KV, &L.v, s->b_v, KV, split_in ? &s->xp : nullptr);
         const size_t layer_base = kv_layer_base(s, l);
         if (s->b_counters && e == hipSuccess) {
@@ -1060,8 +1060,8 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
             // may split its reduction), then SiLU(gate) * up
             if (e == hipSuccess)
                 e = launch_rms_norm_rows(s->b_hidden, (const float *)L.ffn_norm.p, s->b_normed, M, H, eps, st,
-                                         s->b_act, (size_t)M * F, s->b_up, (size_t)M * F);
-            if (split_in && e == hipSuccess) e = launch_split_rows(s->b_normed, H, M, H, s->xp, st);
+                                         s->b_act, (size_t)M * F, s->b_up, (size_t)M * F, nullptr, 0,
+                                         split_in ? &s->xp : nullptr);
             multi3(L.gate, s->b_act, F, L.up, s->b_up, F, nullptr, nullptr, 0, split_in ? &s->xp : nullptr);
             down_split = split_down;
             if (e == hipSuccess)
