@@ -35,7 +35,9 @@ template <int F> __device__ void embed_row(const uint8_t *__restrict__ row, int 
     }
 }
 
-__global__ void step_begin_kernel(StepState *st, const uint32_t *prompt, uint32_t *history, const uint8_t *embd,
+// One workgroup of 1024 threads: the embedding row's loads (up to 8192
+// values) all in flight in one round after the token is known.
+__global__ void __launch_bounds__(1024) step_begin_kernel(StepState *st, const uint32_t *prompt, uint32_t *history, const uint8_t *embd,
                                   uint64_t embd_stride, int embd_rows, int embd_type, int cols, float *hidden) {
     __shared__ uint32_t tok;
     if (threadIdx.x == 0) {
@@ -114,7 +116,7 @@ hipError_t launch_embed_rows(const uint32_t *tokens, int count, const uint8_t *e
 hipError_t launch_step_begin(StepState *st, const uint32_t *prompt, uint32_t *history, const uint8_t *embd,
                              uint64_t embd_stride, int embd_rows, int embd_type, int cols, float *hidden,
                              hipStream_t s) {
-    hipLaunchKernelGGL(step_begin_kernel, dim3(1), dim3(256), 0, s, st, prompt, history, embd, embd_stride,
+    hipLaunchKernelGGL(step_begin_kernel, dim3(1), dim3(1024), 0, s, st, prompt, history, embd, embd_stride,
                        embd_rows, embd_type, cols, hidden);
     return hipGetLastError();
 }
