@@ -929,7 +929,8 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
                                      s->b_hidden, st);
     // Prompt chunks are deterministic: no reduction split onto the residual,
     // at most two onto cleared rows (0 + a + b is the same sum in either
-    // order); their token tiles fill the chip.  Verify passes (one token
+    // order), none for gate/up, which store their rows; their token tiles
+    // fill the chip.  Verify passes (one token
     // tile) keep the split for speed; their sums vary in the last bits.
     const bool det = !output;
     const int split_add = det ? 1 : 16, split_clear = det ? 2 : 16;
@@ -946,9 +947,10 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
     const bool split_in = det && M > 16 && H % 32 == 0, split_o = det && M > 16 && Q % 32 == 0,
                split_down = F % 32 == 0;
     // products of the normed rows that accumulate (OUT_ADD) onto cleared
-    // outputs: one launch for the matrices that share a format and row size
+    // outputs, or store them (no reduction split): one launch for the
+    // matrices that share a format and row size
     auto multi3 = [&](const DT &a, float *ya, int lda, const DT &b, float *yb, int ldb, const DT *c, float *yc,
-                      int ldc, const XPlanes *xp) {
+                      int ldc, const XPlanes *xp, bool store = false) {
         if (e != hipSuccess) return;
         const DT *d[3] = {&a, &b, c};
         float *ys[3] = {ya, yb, yc};
@@ -962,7 +964,7 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
             int Ns[3];
             for (int k = i; k < j; k++) ws[k - i] = d[k]->p, Ns[k - i] = (int)d[k]->rows;
             e = launch_gemm_multi(d[i]->type, j - i, ws, ys + i, lds + i, Ns, d[i]->stride, s->b_normed, H, M,
-                                  (int)d[i]->cols, OUT_ADD, st, split_clear, xp);  // onto rows the norm cleared
+                                  (int)d[i]->cols, store ? OUT_STORE : OUT_ADD, st, store ? 1 : split_clear, xp);
             i = j;
         }
     };
@@ -1056,13 +1058,14 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
                 e = launch_rms_norm_rows(s->b_hidden, (const float *)L.ffn_norm.p, s->b_normed, M, H, eps, st);
             gemm(L.gate, &L.up, s->b_normed, H, s->b_act, F, OUT_SWIGLU);
         } else {
-            // gate and up accumulate onto rows the norm clears (each product
-            // may split its reduction), then SiLU(gate) * up
+            // gate and up (prompt chunks: stores; verify passes: onto rows
+            // the norm clears, each product may split its reduction), then
+            // SiLU(gate) * up
             if (e == hipSuccess)
                 e = launch_rms_norm_rows(s->b_hidden, (const float *)L.ffn_norm.p, s->b_normed, M, H, eps, st,
-                                         s->b_act, (size_t)M * F, s->b_up, (size_t)M * F, nullptr, 0,
-                                         split_in ? &s->xp : nullptr);
-            multi3(L.gate, s->b_act, F, L.up, s->b_up, F, nullptr, nullptr, 0, split_in ? &s->xp : nullptr);
+                                         det ? nullptr : s->b_act, det ? 0 : (size_t)M * F, det ? nullptr : s->b_up,
+                                         det ? 0 : (size_t)M * F, nullptr, 0, split_in ? &s->xp : nullptr);
+            multi3(L.gate, s->b_act, F, L.up, s->b_up, F, nullptr, nullptr, 0, split_in ? &s->xp : nullptr, det);
             down_split = split_down;
             if (e == hipSuccess)
                 e = down_split ? launch_silu_mul_split(s->b_act, s->b_up, M, F, s->xp, st)
