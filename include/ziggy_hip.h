@@ -242,8 +242,11 @@ int ziggy_hip_store_kv_half(ZiggyHipContext *ctx, const ZiggyHipBuffer *src, Zig
 /* GQA decode attention over the binary16 cache; split-K flash decoding whose
  * last split to finish merges the others (replaces
  * ziggy_metal_attention_fused_f32, bridge.h:459-477).  q is the roped query;
- * the cache already holds the current position.  head_dim 64, 96, 128 or
- * 256; softcap must be 0 (softcapping belongs to Gemma, outside this path). */
+ * the cache already holds the current position.  Positions
+ * [window_start, position] are attended (any window_start <= position: the
+ * reference's sliding-window layers pass position + 1 - sliding_window,
+ * model/loader.zig:1440-1444).  head_dim 64, 96, 128 or 256; softcap must be
+ * 0 (softcapping belongs to Gemma, outside this path). */
 int ziggy_hip_attention_fused_f32(ZiggyHipContext *ctx, const ZiggyHipBuffer *q, const ZiggyHipBuffer *k_cache,
                                   const ZiggyHipBuffer *v_cache, ZiggyHipBuffer *output, uint32_t head_count,
                                   uint32_t head_count_kv, uint32_t head_dim, uint32_t kv_dim,

@@ -70,6 +70,9 @@ enum {
 
 /* ---- format primitives (model/loader.zig, model/quant_extra.zig) ---- */
 float zo_f16_to_f32(uint16_t h);
+/* f32 -> binary16 -> f32 as the f16 KV cache stores it (Metal store_kv_half,
+ * runtime/metal/matvec.metal:246-255): round to nearest even. */
+float zo_round_f16(float f);
 /* Bytes per row for a tensor type (model/loader.zig:3325-3389, correct rows only). */
 int zo_row_bytes(int type, size_t row_len, size_t *out_bytes);
 /* getScaleMinK4 (model/loader.zig:3814-3825): out[0]=scale, out[1]=min. */

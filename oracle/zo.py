@@ -51,6 +51,7 @@ def lib() -> ctypes.CDLL:
                                   ctypes.c_uint64, ctypes.c_float)
         sigs = {
             "zo_f16_to_f32": ([ctypes.c_uint16], f),
+            "zo_round_f16": ([f], f),
             "zo_row_bytes": ([i, sz, ctypes.POINTER(sz)], i),
             "zo_scale_min_k4": ([i, vp, vp], None),
             "zo_dequantize_row": ([i, vp, sz, vp], i),
@@ -101,6 +102,13 @@ def _ptr(a: np.ndarray) -> int:
 def _check(st: int, what: str) -> None:
     if st:
         raise RuntimeError(f"oracle {what} failed with status {st}")
+
+
+def round_f16(values) -> np.ndarray:
+    """zo_round_f16 over an array: f32 -> binary16 -> f32 as the f16 KV cache stores it."""
+    v = np.ascontiguousarray(values, np.float32).ravel()
+    f = lib().zo_round_f16
+    return np.array([f(float(x)) for x in v], np.float32)
 
 
 def row_bytes(ttype: int, cols: int) -> int:
@@ -156,14 +164,14 @@ def rope(v, head_count, head_dim, rope_dim, position, base, style):
     return v
 
 
-def attention(q, k_cache, v_cache, head_count, head_count_kv, head_dim, position):
+def attention(q, k_cache, v_cache, head_count, head_count_kv, head_dim, position, window_start=0):
     q = np.ascontiguousarray(q, np.float32)
     kc = np.ascontiguousarray(k_cache, np.float32)
     vc = np.ascontiguousarray(v_cache, np.float32)
     out = np.empty(head_count * head_dim, np.float32)
     scores = np.empty(position + 1, np.float32)
     lib().zo_attention(_ptr(out), _ptr(q), _ptr(kc), _ptr(vc), head_count, head_count_kv, head_dim,
-                       head_count_kv * head_dim, position, 0, _ptr(scores))
+                       head_count_kv * head_dim, position, window_start, _ptr(scores))
     return out
 
 

@@ -502,8 +502,11 @@ int zo_session_set_position(zo_session *s, uint32_t pos) {
     return ZO_OK;
 }
 
-/* f32 -> binary16 (round to nearest even) -> f32, for the f16 KV cache mode. */
-static float round_f16(float f) {
+/* f32 -> binary16 (round to nearest even) -> f32, for the f16 KV cache mode:
+ * Metal's store_kv_half writes half(src[i]) (runtime/metal/matvec.metal:246-255),
+ * a round-to-nearest-even conversion with gradual underflow and overflow to
+ * infinity from 65520 on. */
+float zo_round_f16(float f) {
     uint32_t x;
     memcpy(&x, &f, 4);
     uint32_t sign = x & 0x80000000u, ax = x & 0x7fffffffu;
@@ -616,8 +619,8 @@ static int run_token_core(zo_session *s, uint32_t token) {
         /* storeKv (:1390-1395) */
         size_t base = (size_t)l * s->ctx * kvs + (size_t)s->position * kvs;
         for (size_t i = 0; i < kvs; i++) {
-            s->kc[base + i] = s->kv_f16 ? round_f16(s->k[i]) : s->k[i];
-            s->vc[base + i] = s->kv_f16 ? round_f16(s->v[i]) : s->v[i];
+            s->kc[base + i] = s->kv_f16 ? zo_round_f16(s->k[i]) : s->k[i];
+            s->vc[base + i] = s->kv_f16 ? zo_round_f16(s->v[i]) : s->v[i];
         }
         size_t lb = (size_t)l * s->ctx * kvs;
         zo_attention(s->attn_out, s->q, s->kc + lb, s->vc + lb, hc, hkv, hd, kvs, s->position, 0, s->scores);

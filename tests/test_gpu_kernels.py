@@ -194,6 +194,27 @@ def test_attention_parity(hip_ctx, heads, kv_heads, hd, pos):
     assert rel_l2(out.read(), want) < REL_L2
 
 
+# Sliding windows: the reference passes window_start = position + 1 - sliding_window
+# (model/loader.zig:1440-1444), any value up to the position; tiles of the
+# matrix-core kernel start on a 32-position boundary at or below it and mask
+# the positions before it.
+@pytest.mark.parametrize("heads,kv_heads,hd", [(32, 8, 128), (32, 4, 64), (3, 1, 96), (1, 1, 256)])
+@pytest.mark.parametrize("pos,window", [(300, 37), (300, 100), (4095, 4000), (1000, 1000), (64, 63), (4095, 31)])
+def test_attention_window_parity(hip_ctx, heads, kv_heads, hd, pos, window):
+    say(f"attention {heads}/{kv_heads}x{hd} pos {pos} window {window}")
+    rng = np.random.default_rng(pos * 5 + window)
+    kv_dim = kv_heads * hd
+    ctx_len = pos + 1
+    q = rng.standard_normal(heads * hd).astype(np.float32)
+    k = rng.standard_normal(ctx_len * kv_dim).astype(np.float16)
+    v = rng.standard_normal(ctx_len * kv_dim).astype(np.float16)
+    want = zo.attention(q, k.astype(np.float32), v.astype(np.float32), heads, kv_heads, hd, pos, window)
+    out = hip_ctx.empty(heads * hd * 4)
+    hip_ctx.attention(hip_ctx.buffer(q), hip_ctx.buffer(k), hip_ctx.buffer(v), out, heads, kv_heads, hd, kv_dim,
+                      ctx_len, pos, window_start=window)
+    assert rel_l2(out.read(), want) < REL_L2
+
+
 def test_attention_reference_case_head_dim_96(hip_ctx):
     # runtime/metal_backend_test.zig:691-766: 3 query heads on 1 kv head of 96, 5 positions, query at 4, scale
     # 0.125; the reference's expected values come from f32 caches, its kernel reads binary16 ones (tolerance

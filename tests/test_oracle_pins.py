@@ -408,3 +408,23 @@ def test_rms_norm_per_head_closed_form():
     xd = x.reshape(heads, hd).astype(np.float64)
     want = xd / np.sqrt((xd ** 2).mean(axis=1, keepdims=True) + 1e-6) * w
     assert np.max(np.abs(got.reshape(heads, hd) - want)) < 1e-5
+
+
+def test_attention_window_is_the_truncated_cache():
+    # computeAttention attends to [window_start, position] (model/loader.zig:1397-1438): with a window
+    # it equals the attention over the cache rows from window_start on, at position - window_start
+    rng = np.random.default_rng(3)
+    heads, kvh, hd, pos = 8, 2, 64, 90
+    kv_dim = kvh * hd
+    q = rng.standard_normal(heads * hd).astype(np.float32)
+    k = rng.standard_normal((pos + 1) * kv_dim).astype(np.float32)
+    v = rng.standard_normal((pos + 1) * kv_dim).astype(np.float32)
+    for w in (0, 1, 37, 64, 90):
+        got = zo.attention(q, k, v, heads, kvh, hd, pos, w)
+        want = zo.attention(q, k[w * kv_dim:], v[w * kv_dim:], heads, kvh, hd, pos - w)
+        assert np.array_equal(got, want), w
+    # a one-position window is that position's value row, per kv head
+    got = zo.attention(q, k, v, heads, kvh, hd, pos, pos).reshape(heads, hd)
+    vr = v[pos * kv_dim:(pos + 1) * kv_dim].reshape(kvh, hd)
+    for h in range(heads):
+        assert np.allclose(got[h], vr[h // (heads // kvh)], rtol=0, atol=1e-6)

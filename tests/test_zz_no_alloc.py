@@ -27,7 +27,7 @@ def rel_l2(a, b):
     return float(np.linalg.norm(np.asarray(a, np.float64) - b) / max(np.linalg.norm(b), 1e-30))
 
 
-def run_both(ctx, heads, kvh, hd, pos, seed):
+def run_both(ctx, heads, kvh, hd, pos, seed, window=0):
     rng = np.random.default_rng(seed)
     kv_dim = kvh * hd
     ctx_len = pos + 1
@@ -37,9 +37,9 @@ def run_both(ctx, heads, kvh, hd, pos, seed):
     bq, bk, bv = ctx.buffer(q), ctx.buffer(k), ctx.buffer(v)
     out_ctx = ctx.empty(heads * hd * 4)
     out_na = ctx.empty(heads * hd * 4)
-    ctx.attention(bq, bk, bv, out_ctx, heads, kvh, hd, kv_dim, ctx_len, pos)
-    ctx.attention_noalloc(bq, bk, bv, out_na, heads, kvh, hd, kv_dim, ctx_len, pos)
-    want = zo.attention(q, k.astype(np.float32), v.astype(np.float32), heads, kvh, hd, pos)
+    ctx.attention(bq, bk, bv, out_ctx, heads, kvh, hd, kv_dim, ctx_len, pos, window_start=window)
+    ctx.attention_noalloc(bq, bk, bv, out_na, heads, kvh, hd, kv_dim, ctx_len, pos, window_start=window)
+    want = zo.attention(q, k.astype(np.float32), v.astype(np.float32), heads, kvh, hd, pos, window)
     return out_ctx.read(), out_na.read(), want
 
 
@@ -50,6 +50,16 @@ def test_noalloc_attention_matches_context_entry(hip_ctx):
         say(f"noalloc attention {heads}/{kvh}x{hd} pos {pos}")
         got_ctx, got_na, want = run_both(hip_ctx, heads, kvh, hd, pos, seed)
         assert np.array_equal(got_na, got_ctx), (heads, kvh, hd, pos)
+        assert rel_l2(got_na, want) < 1e-4
+
+
+def test_noalloc_attention_sliding_window(hip_ctx):
+    # window starts that are not a multiple of the 32-position tile (sliding-window layers,
+    # model/loader.zig:1440-1444), the larger call first
+    for heads, kvh, hd, pos, window, seed in [(32, 8, 128, 4095, 100, 3), (8, 2, 64, 300, 37, 4)]:
+        say(f"noalloc attention {heads}/{kvh}x{hd} pos {pos} window {window}")
+        got_ctx, got_na, want = run_both(hip_ctx, heads, kvh, hd, pos, seed, window)
+        assert np.array_equal(got_na, got_ctx), (heads, kvh, hd, pos, window)
         assert rel_l2(got_na, want) < 1e-4
 
 

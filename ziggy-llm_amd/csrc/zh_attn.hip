@@ -659,7 +659,10 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     int pos_col[NT];                         // causal end of column li of tile nt
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) pos_col[nt] = MQ ? pos0 + qbase + ((li >> 1) + 8 * nt) / Gq : pos;
-    const int n_total = pos + 1 - p.window_start;
+    // tiles start on a multiple of 32 positions at or below window_start, so
+    // a tile never crosses a page; positions below the window are masked
+    const int wb = p.window_start & ~(TP - 1);
+    const int n_total = pos + 1 - wb;
     const int units = (n_total + TP - 1) / TP;
     // tiles per split; a single query takes at least kMinTiles per split
     // (fewer partials to merge: 6 tiles took 12.8 -> 12.5 us at 4k positions,
@@ -691,12 +694,12 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     // reads below, are uniform, so the reads are scalar loads whose waits do
     // not cover the vector loads in flight
     const int wv = __builtin_amdgcn_readfirstlane(wave);
-    auto p0_of = [&](int t) { return p.window_start + (u_begin + wv + 4 * t) * TP; };
+    auto p0_of = [&](int t) { return wb + (u_begin + wv + 4 * t) * TP; };
     // where tile t's loads go: past the wavefront's own tiles (the first two
     // are loaded whatever its count, the ring refills in pairs) they re-read
     // the split's last tile, which the workgroup reads anyway, rather than
     // the next split's rows (5.6 MB more HBM reads per launch at 4k)
-    auto lp0_of = [&](int t) { return p.window_start + (u_begin + min(wv + 4 * t, nu - 1)) * TP; };
+    auto lp0_of = [&](int t) { return wb + (u_begin + min(wv + 4 * t, nu - 1)) * TP; };
     // a tile's 32 positions lie in one page (tiles start at multiples of 32 and
     // pages hold 64 or more): one table read per tile, rows of the page after
     // it.  A tile past pos (its rows all clamp to pos) reads pos's entry, so
@@ -875,7 +878,8 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
                         // rows 4 lg + r of the tile; the two pieces of a head sit in lanes 2g, 2g + 1
                         float v = acc[r];
                         v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
-                        const bool valid = have && col_ok[nt] && b + 16 * rt + 4 * lg + r <= pos_col[nt];
+                        const int pr = b + 16 * rt + 4 * lg + r;
+                        const bool valid = have && col_ok[nt] && pr <= pos_col[nt] && pr >= p.window_start;
                         sc[nt][tt][rt][r] = valid ? v : -INFINITY;
                     }
                 }
@@ -1160,8 +1164,9 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
     if (p.head_count_kv <= 0 || p.head_count % p.head_count_kv || p.head_count / p.head_count_kv > kMaxGroup ||
         p.max_splits < 1 || !p.counters || !norms_fit(p))
         return hipErrorInvalidValue;
-    // pages of kKvPageShift (two 32-position tiles), the window on a page boundary
-    if (!p.page_table || p.page_shift != kKvPageShift || (p.window_start & ((1 << kKvPageShift) - 1)))
+    // pages of kKvPageShift (two 32-position tiles); any window start
+    if (!p.page_table || p.page_shift != kKvPageShift || p.window_start < 0 ||
+        (!p.position_dev && p.window_start > p.position))
         return hipErrorInvalidValue;
     const int G = p.head_count / p.head_count_kv;
     if (p.n_query > 1) {

@@ -116,7 +116,7 @@ int attention_call_params(const ZiggyHipBuffer *q, const ZiggyHipBuffer *kc, con
                           float softcap, AttnParams *p, char *err, size_t err_len) {
     if (heads == 0 || heads_kv == 0 || heads % heads_kv || heads / heads_kv > 8 ||
         (hd != 64 && hd != 96 && hd != 128 && hd != 256) || kv_dim != heads_kv * hd || pos >= ctx_len || window_start > pos ||
-        (uint64_t)ctx_len > ((uint64_t)kIdentityPages << kKvPageShift) || (window_start & ((1u << kKvPageShift) - 1))) {
+        (uint64_t)ctx_len > ((uint64_t)kIdentityPages << kKvPageShift)) {
         set_err(err, err_len, "unsupported attention shape");
         return ZIGGY_HIP_INVALID_ARGUMENT;
     }
