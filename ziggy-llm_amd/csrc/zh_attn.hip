@@ -287,6 +287,110 @@ __device__ __forceinline__ void split_merge(const AttnParams &p, int kvh, int G,
     if (tid == 0) __hip_atomic_store(&p.counters[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---- polled merge (AttnParams::poll_merge) ----
+
+// Refills this workgroup's partials slot of the other set with kPollEmpty
+// (VS heads of HD values and their (m, l) pairs), for the next launch.
+template <int HD, int VS>
+__device__ __forceinline__ void poll_reset_slot(const AttnParams &p, int kvh, int split) {
+    const size_t e = ((size_t)kvh * p.max_splits + split) * VS;
+    uint4 *o = reinterpret_cast<uint4 *>(p.reset_o + e * HD);
+    const uint4 empty = make_uint4(kPollEmpty, kPollEmpty, kPollEmpty, kPollEmpty);
+    for (int i = threadIdx.x; i < VS * HD / 4; i += 256) o[i] = empty;
+    if (threadIdx.x < VS) reinterpret_cast<uint2 *>(p.reset_ml)[e + threadIdx.x] = make_uint2(kPollEmpty, kPollEmpty);
+}
+
+__device__ __forceinline__ bool poll_empty(unsigned long long v) {
+    return (uint32_t)v == kPollEmpty || (uint32_t)(v >> 32) == kPollEmpty;
+}
+
+// Bound of a polled wait: about a quarter of a second, far past any real wait
+// (microseconds); on expiry the flag is set and the workgroup goes on.
+constexpr long kPollSpin = 1L << 18;
+
+// Split `split` of nsplit merges pairs [split * per, (split + 1) * per) of the
+// head's G * HD / 2 output pairs, per = ceil(pairs / nsplit): eight pairs at a
+// time, 32 lanes each holding splits lane, lane + 32 (at most 64 splits).
+// Each lane polls its splits' partial pair and (m, l) until neither is
+// kPollEmpty (device-scope loads: the partials come from other CUs), then
+// the half-wavefront folds them: M = max m_s, w_s = 2^(m_s - M), out =
+// (sum w_s o_s) / (sum w_s l_s).  The fold's order is fixed by the lanes, so
+// the result does not depend on which split stored first.
+template <int HD, int VS>
+__device__ __forceinline__ void polled_merge(const AttnParams &p, int kvh, int split, int G, int nsplit, float *out) {
+    const int tid = threadIdx.x, lane = tid & 31, row = tid >> 5;
+    const int npairs = G * HD / 2;
+    const int per = (npairs + nsplit - 1) / nsplit;
+    const int first = split * per, last = min(first + per, npairs);
+    const unsigned long long *po = reinterpret_cast<const unsigned long long *>(p.part_o) +
+                                   (size_t)kvh * p.max_splits * VS * (HD / 2);
+    const unsigned long long *ml = reinterpret_cast<const unsigned long long *>(p.part_ml) +
+                                   (size_t)kvh * p.max_splits * VS;
+    constexpr int kC = 2;  // splits per lane
+    for (int i0 = first; i0 < last; i0 += 8) {
+        const int it = min(i0 + row, last - 1);
+        const int g = it / (HD / 2), d2 = it % (HD / 2);
+        unsigned long long ov[kC], mv[kC];
+        bool need[kC];
+#pragma unroll
+        for (int c = 0; c < kC; c++) {
+            need[c] = lane + 32 * c < nsplit;
+            ov[c] = mv[c] = 0ull;
+        }
+        long spin = 0;
+        for (;;) {
+#pragma unroll
+            for (int c = 0; c < kC; c++) {
+                const int sp = min(lane + 32 * c, nsplit - 1);
+                if (need[c]) {
+                    ov[c] = __hip_atomic_load(po + ((size_t)sp * VS + g) * (HD / 2) + d2, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+                    mv[c] = __hip_atomic_load(ml + (size_t)sp * VS + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            bool waiting = false;
+#pragma unroll
+            for (int c = 0; c < kC; c++) {
+                need[c] = need[c] && (poll_empty(ov[c]) || poll_empty(mv[c]));
+                waiting = waiting || need[c];
+            }
+            if (!__any(waiting)) break;
+            if (++spin > kPollSpin) {
+                if (lane == 0) __hip_atomic_store(p.poll_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        float m[kC], mx = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < kC; c++) {
+            m[c] = lane + 32 * c < nsplit ? __uint_as_float((uint32_t)mv[c]) : -INFINITY;
+            mx = fmaxf(mx, m[c]);
+        }
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        float O0 = 0.f, O1 = 0.f, L = 0.f;
+#pragma unroll
+        for (int c = 0; c < kC; c++) {
+            const float w = m[c] == -INFINITY ? 0.f : exp2f(m[c] - mx);
+            O0 = fmaf(__uint_as_float((uint32_t)ov[c]), w, O0);
+            O1 = fmaf(__uint_as_float((uint32_t)(ov[c] >> 32)), w, O1);
+            L = fmaf(__uint_as_float((uint32_t)(mv[c] >> 32)), w, L);
+        }
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) {
+            O0 += __shfl_xor(O0, o, 64);
+            O1 += __shfl_xor(O1, o, 64);
+            L += __shfl_xor(L, o, 64);
+        }
+        if (lane == 0 && i0 + row < last) {
+            float *dst = out + (size_t)g * HD + 2 * d2;
+            dst[0] = O0 / L;
+            dst[1] = O1 / L;
+        }
+    }
+}
+
 // Workgroup (split, kv head) attends over a contiguous range of positions,
 // in passes of PPP positions: lane (position pw, dims block sub) of wavefront
 // w takes position pw + PPW w of each pass and dims 16 sub .. 16 sub + 15
@@ -668,9 +772,11 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     // (fewer partials to merge: 6 tiles took 12.8 -> 12.5 us at 4k positions,
     // 8 tiles 12.3 us, 10 tiles 14.6 us, the same grid at 16k, where every
     // split holds more)
-    constexpr int kMinTiles = MQ ? 1 : 8;
-    const int per = max((units + p.max_splits - 1) / p.max_splits, kMinTiles);
+    const int min_tiles = MQ ? 1 : p.min_tiles > 0 ? p.min_tiles : 8;
+    const int per = max((units + p.max_splits - 1) / p.max_splits, min_tiles);
     const int nsplit = (units + per - 1) / per;
+    const bool polled = !MQ && p.poll_merge;
+    if (polled) poll_reset_slot<HD, VG>(p, kvh, split);
     if (split >= nsplit) return;
     const int u_begin = split * per, nu = min(per, units - u_begin);
     const int ntw = nu > wave ? (nu - wave + 3) / 4 : 0;  // this wavefront's tiles
@@ -1042,6 +1148,10 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
         __hip_atomic_store(reinterpret_cast<unsigned long long *>(p.part_ml) + e, v, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (polled) {
+        polled_merge<HD, VG>(p, kvh, split, G, nsplit, p.out + (size_t)kvh * G * HD);
+        return;
+    }
     // MQ: up to 16 virtual heads, 16 splits per round of the merge
     split_merge<HD, (GG && !MQ) ? GG : VG, decltype(out_of), VG, 256 / VG>(p, slot, G, nsplit, &last_s, out_of);
 }
@@ -1070,6 +1180,20 @@ static bool attention_valu() {
         return e && strcmp(e, "valu") == 0;
     }();
     return v;
+}
+
+bool attention_poll_supported(int head_dim, int max_splits) {
+    if (getenv("ZIGGY_HIP_ATTN_POLL") && getenv("ZIGGY_HIP_ATTN_POLL")[0] == '0') return false;
+    return (head_dim == 64 || head_dim == 96 || head_dim == 128) && !attention_valu() && max_splits <= 64;
+}
+
+int attention_poll_min_tiles() {
+    static const int t = [] {
+        const char *e = getenv("ZIGGY_HIP_ATTN_MIN_TILES");
+        const int v = e ? atoi(e) : 8;
+        return v > 0 ? v : 8;
+    }();
+    return t;
 }
 
 int attention_splits(int kv_heads, int max_positions) {

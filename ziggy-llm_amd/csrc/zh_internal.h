@@ -388,8 +388,25 @@ struct AttnParams {
     // several queries (plain mode, matrix-core kernel): queries at positions
     // position .. position + n_query - 1, rows q_stride / out_stride floats apart
     int n_query, q_stride, out_stride;
+    // Polled merge (single query, matrix-core kernel; no counters): every word
+    // of part_o / part_ml starts as kPollEmpty, the splits store their partials
+    // with device-scope stores, and each split merges its own slice of the
+    // head's outputs as soon as every split's partials of that slice are there.
+    // The launch refills the other set (reset_o / reset_ml, laid out as
+    // part_o / part_ml) with kPollEmpty for the next launch; `poll_err` is set
+    // when a wait runs out of its bound (a split never came), and the output
+    // is then not valid.
+    float *reset_o, *reset_ml;
+    int *poll_err;
+    int poll_merge;
+    int min_tiles;  // 32-position tiles per split at least (0: the default)
 };
+constexpr uint32_t kPollEmpty = 0xFFFFFFFFu;  // a NaN pattern no arithmetic here produces
 hipError_t launch_attention(const AttnParams &p, hipStream_t s);
+// The polled merge covers the single-query matrix-core kernel with at most 64 splits.
+bool attention_poll_supported(int head_dim, int max_splits);
+// Minimum tiles per split of a polled launch (ZIGGY_HIP_ATTN_MIN_TILES, a tuning knob; default 8).
+int attention_poll_min_tiles();
 constexpr int kKvPageShift = 6;  // a session's KV page: 64 positions (two 32-position attention tiles)
 constexpr int kIdentityPages = 65536;  // a context's identity table: contiguous caches of up to 4M positions
 hipError_t launch_iota_u32(uint32_t *p, int n, hipStream_t s);

@@ -52,6 +52,15 @@ struct ZiggyHipSession {
     float *logits = nullptr, *part_o = nullptr, *part_ml = nullptr;
     float *rope_denom = nullptr;  // [rope_dim / 2] RoPE denominators from the host's powf
     unsigned *counters = nullptr;  // attention arrival counters (zero between launches)
+    // polled attention merge: two partials sets (part_o/part_ml and part_o2/part_ml2, each all
+    // kPollEmpty until used); a launch uses the set the previous one did not and refills that
+    // one.  attn_set: the set of the last launch enqueued; graph_set0 / graph_set1: the sets of
+    // the step graph's first and last attention launch.
+    bool attn_poll = false;
+    float *part_o2 = nullptr, *part_ml2 = nullptr;
+    int *poll_err = nullptr;
+    int attn_set = 1, graph_set0 = 0, graph_set1 = 1;
+    size_t attn_scratch = 0;
     // binary16 K/V, paged: per layer kv_pages pages of 64 positions ([page][row in page][kv_dim]);
     // page_table[logical page] = the page's index in every layer's pool
     __half *kc = nullptr, *vc = nullptr;
@@ -171,6 +180,17 @@ hipError_t enqueue_kernel(ZiggyHipSession *s, int id, int l, const int *pos_dev,
         a.rope_dim = (int)md.rope_dim;
         a.rope_style = (int)md.rope_style;
         a.ctx = (int)md.context_length;
+        if (s->attn_poll) {
+            const int set = s->attn_set ^ 1;
+            a.part_o = set ? s->part_o2 : s->part_o;
+            a.part_ml = set ? s->part_ml2 : s->part_ml;
+            a.reset_o = set ? s->part_o : s->part_o2;
+            a.reset_ml = set ? s->part_ml : s->part_ml2;
+            a.poll_merge = 1;
+            a.poll_err = s->poll_err;
+            a.min_tiles = attention_poll_min_tiles();
+            s->attn_set = set;
+        }
         return launch_attention(a, st);
     }
     case ZIGGY_HIP_KERNEL_O_PROJ: {
@@ -278,7 +298,25 @@ hipError_t enqueue_step(ZiggyHipSession *s, hipStream_t st) {
 // a profiler that cannot intercept graph launches) the same kernels enqueued
 // directly; both read token and position from the device step state.
 hipError_t launch_step(ZiggyHipSession *s, hipStream_t st) {
-    return s->graph ? hipGraphLaunch(s->graph, st) : enqueue_step(s, st);
+    if (!s->graph) return enqueue_step(s, st);
+    if (s->attn_poll && s->attn_set == s->graph_set0) {
+        // the graph's first attention launch takes the set the last launch used: refill it
+        hipError_t e = launch_fill_u64(reinterpret_cast<unsigned long long *>(s->graph_set0 ? s->part_o2 : s->part_o),
+                                       ~0ull, (int)(s->attn_scratch / 2), st);
+        if (e != hipSuccess) return e;
+    }
+    s->attn_set = s->graph_set1;
+    return hipGraphLaunch(s->graph, st);
+}
+
+// The polled attention's error flag: set when one of its waits ran out (the
+// step's outputs are then not valid); read after the stream is synchronized.
+int poll_check(ZiggyHipSession *s, char *err, size_t err_len) {
+    if (!s->attn_poll) return ZIGGY_HIP_OK;
+    int flag = 0;
+    ZH_TRY(hipMemcpy(&flag, s->poll_err, 4, hipMemcpyDeviceToHost), "poll flag");
+    if (flag) return fail(err, err_len, ZIGGY_HIP_EXECUTION_FAILED, "an attention split never arrived (polled merge)");
+    return ZIGGY_HIP_OK;
 }
 
 bool graphs_enabled() {
@@ -291,8 +329,14 @@ int build_graph(ZiggyHipSession *s, char *err, size_t err_len) {
     hipStream_t st = s->ctx->stream;
     hipGraph_t g = nullptr;
     ZH_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "graph capture begin");
+    // capture runs nothing: the partials sets the graph bakes in are recorded and the
+    // host's record of the last set used is put back
+    const int set_before = s->attn_set;
     hipError_t e = enqueue_step(s, st);
     hipError_t e2 = hipStreamEndCapture(st, &g);
+    s->graph_set0 = set_before ^ 1;
+    s->graph_set1 = s->attn_set;
+    s->attn_set = set_before;
     if (e != hipSuccess) {
         if (g) hipGraphDestroy(g);
         return hip_fail(e, "graph capture", err, err_len);
@@ -431,6 +475,23 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
         s->allocs.push_back(*r.p);
     }
     s->part_ml = s->part_o + (size_t)md.head_count * s->max_splits * 8 * md.head_dim;
+    s->attn_scratch = attn_scratch;
+    s->attn_poll = attention_poll_supported((int)md.head_dim, s->max_splits);
+    if (s->attn_poll) {
+        // the second partials set and the flag; both sets start all kPollEmpty
+        e = hipMalloc((void **)&s->part_o2, attn_scratch * 4);
+        if (e == hipSuccess) s->allocs.push_back(s->part_o2);
+        if (e == hipSuccess) e = hipMalloc((void **)&s->poll_err, 4);
+        if (e == hipSuccess) s->allocs.push_back(s->poll_err);
+        if (e == hipSuccess) e = hipMemsetAsync(s->poll_err, 0, 4, ctx->stream);
+        if (e == hipSuccess) e = hipMemsetAsync(s->part_o, 0xFF, attn_scratch * 4, ctx->stream);
+        if (e == hipSuccess) e = hipMemsetAsync(s->part_o2, 0xFF, attn_scratch * 4, ctx->stream);
+        if (e != hipSuccess) {
+            free_session(s);
+            return hip_fail(e, "attention partials allocation", err, err_len);
+        }
+        s->part_ml2 = s->part_o2 + (s->part_ml - s->part_o);
+    }
     // pages in order until the caller sets a block table
     s->pages.resize(s->kv_pages);
     for (uint32_t i = 0; i < s->kv_pages; i++) s->pages[i] = i;
@@ -665,6 +726,7 @@ static int host_step(ZiggyHipSession *s, uint32_t token, bool output, uint32_t *
     ZH_TRY(launch_step(s, st), "step graph");
     if (output) ZH_TRY(hipMemcpyAsync(h, s->st, sizeof(StepState), hipMemcpyDeviceToHost, st), "step readback");
     ZH_TRY(hipStreamSynchronize(st), "step");
+    if (int pe = poll_check(s, err, err_len)) return pe;
     s->fed.resize(s->position);
     s->fed.push_back(token);
     s->position++;
@@ -833,6 +895,7 @@ int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint3
     if (steps) ZH_TRY(hipMemcpy(out_tokens, s->history, (size_t)steps * 4, hipMemcpyDeviceToHost), "history");
     ZH_TRY(hipMemcpy(h, s->st, sizeof(StepState), hipMemcpyDeviceToHost), "state readback");
     if (h->error) return fail(err, err_len, ZIGGY_HIP_EXECUTION_FAILED, "a generated token was out of range");
+    if (int pe = poll_check(s, err, err_len)) return pe;
     // rows of the prompt, then of each generated token but the last (still pending)
     s->fed.resize(s->position);
     s->fed.insert(s->fed.end(), prompt, prompt + prompt_len);
@@ -1016,6 +1079,8 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
             a.max_splits = s->max_splits;
             if (e == hipSuccess) e = launch_attention(a, st);
         }
+        // token by token where the multi-query kernel does not serve the shape (head_dim 256, the
+        // vector kernel): never with the polled merge, which needs the matrix-core kernel too
         for (int m = 0; m < M && e == hipSuccess && !s->b_counters; m++) {
             AttnParams a{};
             a.q = s->b_q + (size_t)m * Q;
