@@ -58,10 +58,20 @@ __device__ __forceinline__ size_t kv_row(const AttnParams &p, int t) {
 
 // This thread's RoPE denominator base^(2t / n_rot) (t = threadIdx.x < n_rot / 2): the host's table when
 // given, read early so that its wait does not cover the K/V loads issued after it.
-__device__ __forceinline__ float rope_den(int n_rot, float base, const float *denom) {
+// Split in two so a kernel can issue the table read early and use it late:
+// rope_den_load reads the table entry unconditionally (a valid dummy
+// address without the table), rope_den_finish picks the value.
+__device__ __forceinline__ float rope_den_load(int n_rot, const float *denom, const float *dummy) {
+    const int half = n_rot / 2 > 0 ? n_rot / 2 : 1;
+    return (denom ? denom : dummy)[min((int)threadIdx.x, half - 1)];
+}
+__device__ __forceinline__ float rope_den_finish(float d, int n_rot, float base, const float *denom) {
     const int t = threadIdx.x;
     if (t >= n_rot / 2) return 1.f;
-    return denom ? denom[t] : powf(base, (float)(2 * t) / (float)n_rot);
+    return denom ? d : powf(base, (float)(2 * t) / (float)n_rot);
+}
+__device__ __forceinline__ float rope_den(int n_rot, float base, const float *denom, const float *dummy) {
+    return rope_den_finish(rope_den_load(n_rot, denom, dummy), n_rot, base, denom);
 }
 __device__ __forceinline__ void rope_table(int n_rot, float den, int pos, float *cs, float *sn) {
     const int t = threadIdx.x;
@@ -488,7 +498,7 @@ __global__ void __launch_bounds__(256) attn_kernel(AttnParams p) {
 
     if (fused) {
         const int n_rot = p.rope_dim < HD ? p.rope_dim : HD;
-        rope_table(n_rot, rope_den(n_rot, p.rope_base, p.rope_denom), pos, cs_s, sn_s);
+        rope_table(n_rot, rope_den(n_rot, p.rope_base, p.rope_denom, p.q), pos, cs_s, sn_s);
         norm_rope<HD, QV>(qv, nq, p.q_norm, p.eps, n_rot, p.rope_style, cs_s, sn_s, &q_s[0][0], red16);
         if (own_pos) {
             norm_rope<HD, 1>(kx, HD, p.k_norm, p.eps, n_rot, p.rope_style, cs_s, sn_s, kn_s, red16);
@@ -758,7 +768,50 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     const int qpw = MQ ? VG / Gq : 1, qbase = MQ ? blockIdx.z * qpw : 0;
     const int nqw = MQ ? min(qpw, p.n_query - qbase) : 1;
     const int slot = MQ ? kvh + p.head_count_kv * blockIdx.z : kvh;  // partials / arrival counter
-    const int pos0 = p.position_dev ? *p.position_dev : p.position;
+    const int G = MQ ? nqw * Gq : Gq;                                  // (virtual) heads of the workgroup
+    const bool fused = !MQ && p.k_new != nullptr;
+    const size_t kv_off = (size_t)kvh * HD;
+    constexpr int QV = VG * HD / 256;
+    const int nq = G * HD;
+    const int n_rot_f = p.rope_dim < HD ? p.rope_dim : HD;
+
+    // The prologue's loads first, none depending on the position, all
+    // unconditional (clamped indices, a valid dummy address for an absent
+    // bias or norm), and none used before the K loads are issued: a load
+    // under a branch, or one whose value is used at once, makes the compiler
+    // wait for it there, and each such wait is a memory round trip before
+    // the K stream starts.
+    float qv[QV], qb[QV], kx[1] = {0.f}, kb = 0.f, vx = 0.f, vb = 0.f, qnw[QV], knw[1];
+    const float rden_raw = rope_den_load(n_rot_f, p.rope_denom, p.q);
+    {
+        const float *qn = p.q_norm ? p.q_norm : p.q, *kn = p.k_norm ? p.k_norm : p.q;
+#pragma unroll
+        for (int i = 0; i < QV; i++) qnw[i] = qn[(tid + 256 * i) % HD];
+        knw[0] = kn[tid % HD];
+        const float *qbp = fused && p.q_bias ? p.q_bias : p.q;
+#pragma unroll
+        for (int i = 0; i < QV; i++) {
+            const int idx = min(tid + 256 * i, nq - 1);
+            if (MQ) {
+                const int gv = idx / HD, j = gv / Gq;
+                qv[i] = p.q[(size_t)(qbase + j) * p.q_stride + (size_t)(kvh * Gq + gv - j * Gq) * HD + idx % HD];
+            } else {
+                qv[i] = p.q[(size_t)kvh * nq + idx];
+                qb[i] = qbp[(size_t)kvh * nq + idx];
+            }
+        }
+        // plain mode reads q in place of the absent k / v and ignores it
+        const float *knp = fused ? p.k_new : p.q, *vnp = fused ? p.v_new : p.q;
+        const float *kbp = fused && p.k_bias ? p.k_bias : p.q, *vbp = fused && p.v_bias ? p.v_bias : p.q;
+        kx[0] = knp[kv_off + tid % HD];
+        vx = vnp[kv_off + tid % HD];
+        kb = kbp[kv_off + tid % HD];
+        vb = vbp[kv_off + tid % HD];
+    }
+    // the position through the scalar cache (a scalar load: its wait does not
+    // cover the vector loads above)
+    typedef const __attribute__((address_space(4))) int *const_i32_ptr;
+    const int pos0 = p.position_dev ? *(const_i32_ptr)p.position_dev : p.position;
     const int pos = pos0 + qbase + nqw - 1;  // the last query's position
     int pos_col[NT];                         // causal end of column li of tile nt
 #pragma unroll
@@ -776,13 +829,18 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     const int per = max((units + p.max_splits - 1) / p.max_splits, min_tiles);
     const int nsplit = (units + per - 1) / per;
     const bool polled = !MQ && p.poll_merge;
-    if (polled) poll_reset_slot<HD, VG>(p, kvh, split);
-    if (split >= nsplit) return;
+    // the other set's slot of this workgroup, refilled for the next launch
+    // (at the end: stores ahead of the K loads would delay them)
+    auto refill_other = [&]() {
+        if (polled) poll_reset_slot<HD, VG>(p, kvh, split);
+    };
+    if (split >= nsplit) {
+        refill_other();
+        return;
+    }
     const int u_begin = split * per, nu = min(per, units - u_begin);
     const int ntw = nu > wave ? (nu - wave + 3) / 4 : 0;  // this wavefront's tiles
-    const int G = MQ ? nqw * Gq : Gq;                         // (virtual) heads of the workgroup
     const bool two = NT > 1 && G > kMaxGroup;                 // the second query tile is in use
-    const bool fused = !MQ && p.k_new != nullptr;
     const bool own_pos = fused && u_begin + nu == units;  // this split holds the current position
 
     __shared__ float q_s[VG][HD];
@@ -814,47 +872,8 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
         const int bb = min(b, pos);
         return (long long)kv_row(p, bb) - bb;
     };
-    // the first two tiles' pages, read before the q loads are issued: their
-    // scalar loads overlap that issue, and the K loads wait only for them
+    // the first two tiles' pages (scalar loads), then the K loads
     const long long tb_first[2] = {tile_row(lp0_of(0)), tile_row(lp0_of(1))};
-    const size_t kv_off = (size_t)kvh * HD;
-    constexpr int QV = VG * HD / 256;
-    const int nq = G * HD;
-    float qv[QV], kx[1] = {0.f}, vx = 0.f, qnw[QV], knw[1];
-    const int n_rot_f = p.rope_dim < HD ? p.rope_dim : HD;
-    const float rden = fused ? rope_den(n_rot_f, p.rope_base, p.rope_denom) : 1.f;
-    {
-        // norm weights too (dummy reads of q when absent): see the K/V loads
-        const float *qn = p.q_norm ? p.q_norm : p.q, *kn = p.k_norm ? p.k_norm : p.q;
-#pragma unroll
-        for (int i = 0; i < QV; i++) qnw[i] = qn[(tid + 256 * i) % HD];
-        knw[0] = kn[tid % HD];
-    }
-#pragma unroll
-    for (int i = 0; i < QV; i++) {
-        const int idx = tid + 256 * i;
-        qv[i] = 0.f;
-        if (idx < nq) {
-            if (MQ) {
-                const int gv = idx / HD, j = gv / Gq;
-                qv[i] = p.q[(size_t)(qbase + j) * p.q_stride + (size_t)(kvh * Gq + gv - j * Gq) * HD + idx % HD];
-            } else {
-                qv[i] = p.q[(size_t)kvh * nq + idx];
-                if (fused && p.q_bias) qv[i] += p.q_bias[(size_t)kvh * nq + idx];
-            }
-        }
-    }
-    {
-        // unconditional for the same reason as the K/V loads below (plain
-        // mode reads q in place of the absent k / v and ignores it)
-        const float *kn = fused ? p.k_new : p.q, *vn = fused ? p.v_new : p.q;
-        kx[0] = kn[kv_off + tid % HD];
-        vx = vn[kv_off + tid % HD];
-        if (own_pos && tid < HD) {
-            if (p.k_bias) kx[0] += p.k_bias[kv_off + tid];
-            if (p.v_bias) vx += p.v_bias[kv_off + tid];
-        }
-    }
     __builtin_amdgcn_sched_barrier(0);
 
     // tile t: positions p0(t) .. p0(t) + 31; K fragments [row tile][k-step]
@@ -889,6 +908,20 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     uint4 vr[2][8];
     load_k(0, kr[0]);
     load_k(1, kr[1]);
+    const float rden = fused ? rope_den_finish(rden_raw, n_rot_f, p.rope_base, p.rope_denom) : 1.f;
+    // the projection biases (the bias reads above are dummies when absent)
+    if (fused) {
+#pragma unroll
+        for (int i = 0; i < QV; i++)
+            if (p.q_bias && tid + 256 * i < nq) qv[i] += qb[i];
+        if (own_pos && tid < HD) {
+            if (p.k_bias) kx[0] += kb;
+            if (p.v_bias) vx += vb;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < QV; i++)
+        if (tid + 256 * i >= nq) qv[i] = 0.f;
 
     if (fused) {
         const int n_rot = n_rot_f;
@@ -1140,7 +1173,10 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
                                __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    if (nsplit == 1) return;
+    if (nsplit == 1) {
+        refill_other();
+        return;
+    }
     if (tid < G) {
         const size_t e = ((size_t)slot * p.max_splits + split) * VG + tid;
         const unsigned long long v = (unsigned long long)__float_as_uint(fm_s[tid]) |
@@ -1150,6 +1186,7 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     }
     if (polled) {
         polled_merge<HD, VG>(p, kvh, split, G, nsplit, p.out + (size_t)kvh * G * HD);
+        refill_other();
         return;
     }
     // MQ: up to 16 virtual heads, 16 splits per round of the merge
@@ -1239,7 +1276,7 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(AttnParams p, float *q_o
         if (p.v_bias) vx += p.v_bias[(size_t)kvh * HD + tid];
     }
     const int n_rot = p.rope_dim < HD ? p.rope_dim : HD;
-    rope_table(n_rot, rope_den(n_rot, p.rope_base, p.rope_denom), pos, cs_s, sn_s);
+    rope_table(n_rot, rope_den(n_rot, p.rope_base, p.rope_denom, p.q), pos, cs_s, sn_s);
     norm_rope<HD, QV>(qv, nq, p.q_norm, p.eps, n_rot, p.rope_style, cs_s, sn_s, q_s, red16);
     norm_rope<HD, 1>(kx, HD, p.k_norm, p.eps, n_rot, p.rope_style, cs_s, sn_s, kn_s, red16);
     float *qo = q_out + (size_t)m * p.q_stride + (size_t)kvh * nq;

@@ -453,7 +453,9 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
     s->kv_pages = (md.context_length + (1u << kKvPageShift) - 1) >> kKvPageShift;
     const size_t cache_elems = (size_t)md.block_count * ((size_t)s->kv_pages << kKvPageShift) * KV;
     const size_t logits_len = md.vocab_size > F ? md.vocab_size : F;
-    const size_t attn_scratch = attention_scratch_floats((int)md.head_count, (int)md.head_dim, s->max_splits);
+    // the attention partials (an even count: the polled sets are refilled as u64 words)
+    const size_t attn_scratch =
+        (attention_scratch_floats((int)md.head_count, (int)md.head_dim, s->max_splits) + 1) & ~(size_t)1;
     struct {
         void **p;
         size_t bytes;
