@@ -1,10 +1,10 @@
 """Batched prompt prefill on the matrix cores against the oracle's token-by-token prompt.
 
 The reference feeds a prompt one token at a time (runPrompt, model/loader.zig:1016-1036); the session
-runs every prompt token but the last in batched passes of up to 64 tokens (exact-code GEMMs, multi-query
+runs every prompt token but the last in batched passes of up to 256 tokens (exact-code GEMMs, multi-query
 causal attention over the rows the pass itself stores), then the last one through the decode step.  The
 logits after the prompt must be within 1e-4 relative L2 of the oracle's, and the next 64 greedy tokens
-equal its stream.  Prompts of 300 tokens take five passes, the last one ragged; the models cover query
+equal its stream.  Prompts of 300 tokens take two passes, the last one ragged; the models cover query
 heads per kv head 1, 2 and 8, head sizes 64 and 128, per-head QK norm and Q4_K_M / Q8_0 weights.
 """
 import sys

@@ -72,6 +72,7 @@ struct ZiggyHipSession {
     uint32_t *prompt = nullptr, *history = nullptr;
     uint32_t prompt_cap = 0, history_cap = 0;
     hipGraphExec_t graph = nullptr;
+    const uint32_t *graph_prompt = nullptr, *graph_history = nullptr;  // the buffers the graph's step_begin reads
     // batched verify (allocated on first use): [kVerifyMax] rows each
     float *b_hidden = nullptr, *b_normed = nullptr, *b_q = nullptr, *b_k = nullptr, *b_v = nullptr;
     float *b_attn = nullptr, *b_act = nullptr, *b_up = nullptr, *b_logits = nullptr;
@@ -345,6 +346,8 @@ int build_graph(ZiggyHipSession *s, char *err, size_t err_len) {
     e = hipGraphInstantiate(&s->graph, g, nullptr, nullptr, 0);
     hipGraphDestroy(g);
     if (e != hipSuccess) return hip_fail(e, "graph instantiate", err, err_len);
+    s->graph_prompt = s->prompt;
+    s->graph_history = s->history;
     return ZIGGY_HIP_OK;
 }
 
@@ -854,13 +857,15 @@ int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint3
         s->allocs.push_back(s->history);
         s->history_cap = cap;
     }
-    // step_begin reads the prompt/history pointers baked into the graph: rebuild it if they moved
-    if (s->graph) {
+    // step_begin reads the prompt/history pointers baked into the graph: rebuild it only if they moved
+    if (s->graph && (s->graph_prompt != s->prompt || s->graph_history != s->history)) {
         hipGraphExecDestroy(s->graph);
         s->graph = nullptr;
     }
-    int bst = build_graph(s, err, err_len);
-    if (bst) return bst;
+    if (!s->graph && graphs_enabled()) {
+        int bst = build_graph(s, err, err_len);
+        if (bst) return bst;
+    }
     ZH_TRY(hipMemcpyAsync(s->prompt, prompt, (size_t)prompt_len * 4, hipMemcpyHostToDevice, st), "prompt upload");
     // every prompt row but the last in batched passes of up to prefill_chunk()
     // tokens (GEMMs on the matrix cores, multi-query causal attention), the
@@ -1010,7 +1015,7 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
     // tiles per workgroup, and no workgroup splits the rows again.  (A verify
     // pass, one token tile, lets the products split their own.)
     const bool split_in = det && M > 16 && H % 32 == 0, split_o = det && M > 16 && Q % 32 == 0,
-               split_down = F % 32 == 0;
+               split_down = det && M > 16 && F % 32 == 0;
     // products of the normed rows that accumulate (OUT_ADD) onto cleared
     // outputs, or store them (no reduction split): one launch for the
     // matrices that share a format and row size

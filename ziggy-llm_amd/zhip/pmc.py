@@ -296,7 +296,9 @@ CLOCK_GHZ = 2.4  # peak engine clock
 
 
 def _dispatch_rows(dirname: str) -> dict[str, dict]:
-    """{dispatch id: {"name", "counters": {name: value}, "ns"}} from a --pmc run (with --kernel-trace)."""
+    """{dispatch id: {"name", "counters": {name: value}, "ns"}} from a --pmc run.  Counters are collected
+    in runs of their own, never with --kernel-trace: that combination once ended a profiled process with
+    a SIGSEGV in a profiler thread (no GPU fault)."""
     files = glob.glob(os.path.join(dirname, "**", "*counter_collection.csv"), recursive=True)
     if not files:
         raise SystemExit(f"no counter_collection.csv under {dirname}")
@@ -309,11 +311,6 @@ def _dispatch_rows(dirname: str) -> dict[str, dict]:
             c[k] = max(c.get(k, v), v) if k.startswith("GRBM_") or k == "MfmaUtil" else c.get(k, 0.0) + v
             if r.get("Start_Timestamp") and r.get("End_Timestamp"):
                 d["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
-    for f in glob.glob(os.path.join(dirname, "**", "*kernel_trace.csv"), recursive=True):
-        for r in csv.DictReader(open(f)):
-            d = out.get(r["Dispatch_Id"])
-            if d is not None:
-                d["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
     return out
 
 
@@ -321,9 +318,9 @@ def mfma(args) -> None:
     """Matrix-core use per kernel shape from one --pmc run of SQ_INSTS_VALU_MFMA_MOPS_F16,
     SQ_INSTS_VALU_MFMA_MOPS_BF16, SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE and MfmaUtil.  One MOPS unit is
     512 flops; MfmaUtil = MFMA-busy cycles summed over the SIMDs / (GPU-active cycles x 1024 SIMDs).  The
-    launch time is the GPU-active cycles at the 2.4 GHz peak engine clock (counter collection serialises
-    launches), or the traced duration when the run also had --kernel-trace.  Dispatches of one kernel
-    with the same flops are one shape."""
+    launch time is the counter row's own duration when it has one, else the GPU-active cycles at the
+    2.4 GHz peak engine clock (counter collection serialises launches).  Dispatches of one kernel with
+    the same flops are one shape."""
     rows = _dispatch_rows(args.pmc_dir)
     groups: dict[tuple[str, int], list[dict]] = {}
     for d in rows.values():
