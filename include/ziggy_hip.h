@@ -336,6 +336,33 @@ typedef struct {
     uint64_t prompt_ns;        /* host clock around the prompt (batched passes and its last step) */
 } ZiggyHipGenerateStats;
 
+/* ---- measurement probes (no counterpart in the reference: they time the
+ * hardware under the decode step's launch structure; python -m zhip.microbench
+ * --chain / --sync) ---- */
+typedef struct {
+    uint64_t bytes;         /* bytes streamed (each entry rounded down to 16 bytes per workgroup) */
+    uint32_t kernels;       /* entries of the plan */
+    uint32_t workgroups;    /* grid of every launch: the CU count */
+    double one_kernel_ms;   /* all the bytes as one streaming kernel */
+    double chain_ms;        /* one streaming kernel per entry, captured in a HIP graph */
+    double empty_chain_ms;  /* as many empty kernels in a graph */
+} ZiggyHipChainProbe;
+/* Streams a byte plan (bytes[i]: what launch i of a decode step reads) three
+ * ways; best of `reps` runs after one warm-up. */
+int ziggy_hip_probe_chain(ZiggyHipContext *ctx, const uint64_t *bytes, uint32_t count, uint32_t reps,
+                          ZiggyHipChainProbe *out, char *error_message, size_t error_message_len);
+typedef struct {
+    uint32_t workgroups;        /* the barriers' grid: the CU count */
+    int32_t timed_out;          /* a wait ran out of its bound: the figures are not valid */
+    double handoff_relaxed_us;  /* one-way hand-off between two CUs, relaxed device-scope store / load */
+    double handoff_acqrel_us;   /* the same with release store / acquire load */
+    double barrier_flags_us;    /* barrier of the grid: arrival words polled by one wavefront */
+    double barrier_counter_us;  /* barrier of the grid: one arrival counter */
+} ZiggyHipSyncProbe;
+/* Latencies of in-launch dependencies between workgroups, averaged over `rounds`. */
+int ziggy_hip_probe_sync(ZiggyHipContext *ctx, uint32_t rounds, ZiggyHipSyncProbe *out, char *error_message,
+                         size_t error_message_len);
+
 /* Kernels of one decode step, for ziggy_hip_session_time_kernel. */
 enum {
     ZIGGY_HIP_KERNEL_QKV = 0,      /* fused RMSNorm + q/k/v projections */

@@ -319,16 +319,17 @@ __device__ __forceinline__ bool poll_empty(unsigned long long v) {
 constexpr long kPollSpin = 1L << 18;
 
 // Split `split` of nsplit merges pairs [split * per, (split + 1) * per) of the
-// head's G * HD / 2 output pairs, per = ceil(pairs / nsplit): eight pairs at a
-// time, 32 lanes each holding splits lane, lane + 32 (at most 64 splits).
+// head's G * HD / 2 output pairs, per = ceil(pairs / nsplit).  SL lanes serve
+// one pair (SL = the power of two at or above nsplit, at least 4 and at most
+// 32; a lane holds splits lane, lane + SL, ... up to 64), so 256 / SL pairs go
+// at once and one round of polls covers the slice whenever per <= 256 / SL.
 // Each lane polls its splits' partial pair and (m, l) until neither is
-// kPollEmpty (device-scope loads: the partials come from other CUs), then
-// the half-wavefront folds them: M = max m_s, w_s = 2^(m_s - M), out =
-// (sum w_s o_s) / (sum w_s l_s).  The fold's order is fixed by the lanes, so
-// the result does not depend on which split stored first.
+// kPollEmpty (device-scope loads: the partials come from other CUs), then the
+// SL lanes fold them: M = max m_s, w_s = 2^(m_s - M), out = (sum w_s o_s) /
+// (sum w_s l_s).  The fold's order is fixed by the lanes, so the result does
+// not depend on which split stored first.
 template <int HD, int VS>
 __device__ __forceinline__ void polled_merge(const AttnParams &p, int kvh, int split, int G, int nsplit, float *out) {
-    const int tid = threadIdx.x, lane = tid & 31, row = tid >> 5;
     const int npairs = G * HD / 2;
     const int per = (npairs + nsplit - 1) / nsplit;
     const int first = split * per, last = min(first + per, npairs);
@@ -336,22 +337,24 @@ __device__ __forceinline__ void polled_merge(const AttnParams &p, int kvh, int s
                                    (size_t)kvh * p.max_splits * VS * (HD / 2);
     const unsigned long long *ml = reinterpret_cast<const unsigned long long *>(p.part_ml) +
                                    (size_t)kvh * p.max_splits * VS;
-    constexpr int kC = 2;  // splits per lane
-    for (int i0 = first; i0 < last; i0 += 8) {
+    const int SL = nsplit <= 4 ? 4 : nsplit <= 8 ? 8 : nsplit <= 16 ? 16 : 32;
+    const int tid = threadIdx.x, lane = tid & (SL - 1), row = tid / SL, rows = 256 / SL;
+    constexpr int kC = 2;  // splits per lane (SL = 32: 64 splits)
+    for (int i0 = first; i0 < last; i0 += rows) {
         const int it = min(i0 + row, last - 1);
         const int g = it / (HD / 2), d2 = it % (HD / 2);
         unsigned long long ov[kC], mv[kC];
         bool need[kC];
 #pragma unroll
         for (int c = 0; c < kC; c++) {
-            need[c] = lane + 32 * c < nsplit;
+            need[c] = lane + SL * c < nsplit;
             ov[c] = mv[c] = 0ull;
         }
         long spin = 0;
         for (;;) {
 #pragma unroll
             for (int c = 0; c < kC; c++) {
-                const int sp = min(lane + 32 * c, nsplit - 1);
+                const int sp = min(lane + SL * c, nsplit - 1);
                 if (need[c]) {
                     ov[c] = __hip_atomic_load(po + ((size_t)sp * VS + g) * (HD / 2) + d2, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
@@ -366,7 +369,7 @@ __device__ __forceinline__ void polled_merge(const AttnParams &p, int kvh, int s
             }
             if (!__any(waiting)) break;
             if (++spin > kPollSpin) {
-                if (lane == 0) __hip_atomic_store(p.poll_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((tid & 63) == 0) __hip_atomic_store(p.poll_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
@@ -374,11 +377,10 @@ __device__ __forceinline__ void polled_merge(const AttnParams &p, int kvh, int s
         float m[kC], mx = -INFINITY;
 #pragma unroll
         for (int c = 0; c < kC; c++) {
-            m[c] = lane + 32 * c < nsplit ? __uint_as_float((uint32_t)mv[c]) : -INFINITY;
+            m[c] = lane + SL * c < nsplit ? __uint_as_float((uint32_t)mv[c]) : -INFINITY;
             mx = fmaxf(mx, m[c]);
         }
-#pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        for (int o = SL / 2; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
         float O0 = 0.f, O1 = 0.f, L = 0.f;
 #pragma unroll
         for (int c = 0; c < kC; c++) {
@@ -387,8 +389,7 @@ __device__ __forceinline__ void polled_merge(const AttnParams &p, int kvh, int s
             O1 = fmaf(__uint_as_float((uint32_t)(ov[c] >> 32)), w, O1);
             L = fmaf(__uint_as_float((uint32_t)(mv[c] >> 32)), w, L);
         }
-#pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) {
+        for (int o = SL / 2; o >= 1; o >>= 1) {
             O0 += __shfl_xor(O0, o, 64);
             O1 += __shfl_xor(O1, o, 64);
             L += __shfl_xor(L, o, 64);
@@ -1227,8 +1228,8 @@ bool attention_poll_supported(int head_dim, int max_splits) {
 int attention_poll_min_tiles() {
     static const int t = [] {
         const char *e = getenv("ZIGGY_HIP_ATTN_MIN_TILES");
-        const int v = e ? atoi(e) : 8;
-        return v > 0 ? v : 8;
+        const int v = e ? atoi(e) : 4;
+        return v > 0 ? v : 4;
     }();
     return t;
 }

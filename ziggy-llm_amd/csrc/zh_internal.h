@@ -405,7 +405,7 @@ constexpr uint32_t kPollEmpty = 0xFFFFFFFFu;  // a NaN pattern no arithmetic her
 hipError_t launch_attention(const AttnParams &p, hipStream_t s);
 // The polled merge covers the single-query matrix-core kernel with at most 64 splits.
 bool attention_poll_supported(int head_dim, int max_splits);
-// Minimum tiles per split of a polled launch (ZIGGY_HIP_ATTN_MIN_TILES, a tuning knob; default 8).
+// Minimum tiles per split of a polled launch (ZIGGY_HIP_ATTN_MIN_TILES, a tuning knob; default 4).
 int attention_poll_min_tiles();
 constexpr int kKvPageShift = 6;  // a session's KV page: 64 positions (two 32-position attention tiles)
 constexpr int kIdentityPages = 65536;  // a context's identity table: contiguous caches of up to 4M positions

@@ -58,6 +58,17 @@ class ModelDesc(ctypes.Structure):
                                                                ("rope_freq_base", ctypes.c_float)]
 
 
+class ChainProbe(ctypes.Structure):
+    _fields_ = [("bytes", ctypes.c_uint64), ("kernels", ctypes.c_uint32), ("workgroups", ctypes.c_uint32),
+                ("one_kernel_ms", ctypes.c_double), ("chain_ms", ctypes.c_double), ("empty_chain_ms", ctypes.c_double)]
+
+
+class SyncProbe(ctypes.Structure):
+    _fields_ = [("workgroups", ctypes.c_uint32), ("timed_out", ctypes.c_int32),
+                ("handoff_relaxed_us", ctypes.c_double), ("handoff_acqrel_us", ctypes.c_double),
+                ("barrier_flags_us", ctypes.c_double), ("barrier_counter_us", ctypes.c_double)]
+
+
 class GenerateStats(ctypes.Structure):
     _fields_ = [("steps", ctypes.c_uint64), ("gpu_elapsed_ns", ctypes.c_uint64), ("wall_ns", ctypes.c_uint64),
                 ("next_token", ctypes.c_uint32), ("reserved", ctypes.c_uint32), ("prompt_ns", ctypes.c_uint64)]
@@ -122,6 +133,8 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_run_matvec_argmax": [vp, u32, vp, vp, vp, u32, u32] + E,
         "ziggy_hip_dequantize_rows": [vp, u32, vp, sz, vp, u32, u32] + E,
         "ziggy_hip_time_matvec": [vp, u32, vp, u32, sz, vp, vp, u32, u32, u32, ctypes.POINTER(ctypes.c_uint64)] + E,
+        "ziggy_hip_probe_chain": [vp, vp, u32, u32, ctypes.POINTER(ChainProbe)] + E,
+        "ziggy_hip_probe_sync": [vp, u32, ctypes.POINTER(SyncProbe)] + E,
         "ziggy_hip_indexed_matvec": [vp, u32, vp, vp, vp, u32, u32, vp, u32, u32, i] + E,
         "ziggy_hip_run_gemm": [vp, u32, vp, vp, vp, u32, u32, u32, i] + E,
         "ziggy_hip_dual_indexed_matvec": [vp, u32, vp, vp, vp, vp, vp, u32, u32, vp, u32, u32] + E,
@@ -269,6 +282,20 @@ class Context:
         _call("ziggy_hip_time_matvec", self.h, ttype, mats.h, copies, copy_stride, x.h, y.h, rows, cols, iterations,
               ctypes.byref(ns))
         return ns.value
+
+    def probe_chain(self, plan, reps: int = 5) -> ChainProbe:
+        """The byte plan (bytes per launch) as one kernel, as a graph of one kernel per entry, and as a
+        graph of as many empty kernels (ziggy_hip_probe_chain)."""
+        b = np.ascontiguousarray(plan, np.uint64)
+        out = ChainProbe()
+        _call("ziggy_hip_probe_chain", self.h, b.ctypes.data, b.size, reps, ctypes.byref(out))
+        return out
+
+    def probe_sync(self, rounds: int = 2000) -> SyncProbe:
+        """In-launch hand-off and grid-barrier latencies (ziggy_hip_probe_sync)."""
+        out = SyncProbe()
+        _call("ziggy_hip_probe_sync", self.h, rounds, ctypes.byref(out))
+        return out
 
     def copy(self, src: Buffer, src_off: int, dst: Buffer, dst_off: int, nbytes: int):
         _call("ziggy_hip_copy_buffer_region", self.h, src.h, src_off, dst.h, dst_off, nbytes)

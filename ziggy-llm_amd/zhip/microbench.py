@@ -12,6 +12,13 @@ GB/s counts the weight bytes plus x and y (rows*cols*bytes_per_weight +
 Usage: python -m zhip.microbench [--iters N] [--formats q4_k,q6_k,q8_0]
                                  [--shapes 4096x4096,14336x4096] [--out FILE.md]
 Prints one JSON object per case; --out also writes them as a markdown table.
+
+Two probes of the launch structure (no quantized work; they time the hardware):
+  --chain [--position P]  the Llama-3.1-8B-shaped decode step's byte plan (each launch's weight or K/V
+                          bytes at position P, in launch order) as one streaming kernel, as a HIP graph
+                          of one streaming kernel per launch, and as a graph of as many empty kernels;
+  --sync                  one-way hand-off latency between two CUs and the latency of a barrier of a
+                          CU-sized grid, inside one launch.
 """
 from __future__ import annotations
 
@@ -53,14 +60,100 @@ def run(ctx: hip.Context, ttype: int, rows: int, cols: int, iters: int, min_byte
             "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def step_plan(spec, position: int) -> list:
+    """Bytes each launch of one decode step streams, in launch order: the step-begin kernel (one
+    embedding row), per layer q/k/v, attention (K/V rows 0..position), o_proj, gate/up and down, then the
+    output head (the session's step graph, zh_session.cpp enqueue_step)."""
+    t = {x.name: x for x in spec.tensors()}
+    kv = spec.n_kv * spec.head_dim * 2 * 2 * (position + 1)
+    plan = [row_bytes(t["token_embd.weight"].ttype, spec.hidden)]
+    for i in range(spec.n_layers):
+        b = lambda n: t[f"blk.{i}.{n}.weight"].nbytes  # noqa: E731
+        plan += [b("attn_q") + b("attn_k") + b("attn_v"), kv, b("attn_output"), b("ffn_gate") + b("ffn_up"),
+                 b("ffn_down")]
+    plan.append(t["output.weight"].nbytes)
+    return plan
+
+
+def chain(args) -> dict:
+    spec = synth.llama8b_spec(context=args.position + 16)
+    plan = step_plan(spec, args.position)
+    ctx = hip.Context(0)
+    r = ctx.probe_chain(plan, reps=args.reps)
+    ctx.close()
+    gbs = lambda ms: r.bytes / (ms * 1e-3) / 1e9  # noqa: E731
+    out = {"probe": "chain", "model": spec.name, "position": args.position, "kernels": r.kernels,
+           "workgroups": r.workgroups, "bytes": r.bytes,
+           "one_kernel_ms": round(r.one_kernel_ms, 4), "one_kernel_gbs": round(gbs(r.one_kernel_ms), 1),
+           "chain_ms": round(r.chain_ms, 4), "chain_gbs": round(gbs(r.chain_ms), 1),
+           "empty_chain_ms": round(r.empty_chain_ms, 4),
+           "empty_us_per_kernel": round(1e3 * r.empty_chain_ms / r.kernels, 3)}
+    print(json.dumps(out), flush=True)
+    if args.out:
+        lines = ["# Launch-structure probe: the decode step's byte plan, one MI355X", "",
+                 "Command (from ziggy-llm_amd/):", "",
+                 f"    python3 -m zhip.microbench --chain --position {args.position} --reps {args.reps} --out <file>",
+                 "",
+                 f"Plan: the {spec.name} step at position {args.position}: {r.kernels} launches (step begin, per "
+                 "layer q/k/v, attention K/V, o_proj, gate/up, down, then the output head), each streaming its "
+                 "bytes in equal shares over a grid of one workgroup per CU. Best of "
+                 f"{args.reps} runs after a warm-up, HIP events around each.", "",
+                 "| form | ms | GB/s | % of 8 TB/s |", "|---|---|---|---|",
+                 f"| one streaming kernel over all {r.bytes} bytes | {out['one_kernel_ms']} | "
+                 f"{out['one_kernel_gbs']} | {100 * out['one_kernel_gbs'] / HBM_PEAK_GBS:.1f} |",
+                 f"| {r.kernels} streaming kernels in a graph | {out['chain_ms']} | {out['chain_gbs']} | "
+                 f"{100 * out['chain_gbs'] / HBM_PEAK_GBS:.1f} |",
+                 f"| {r.kernels} empty kernels in a graph | {out['empty_chain_ms']} | - | - |", "",
+                 f"Empty kernels: {out['empty_us_per_kernel']} us per launch."]
+        with open(args.out, "w") as fh:
+            fh.write("\n".join(lines) + "\n")
+    return out
+
+
+def sync(args) -> dict:
+    ctx = hip.Context(0)
+    r = ctx.probe_sync(args.rounds)
+    ctx.close()
+    out = {"probe": "sync", "workgroups": r.workgroups, "timed_out": bool(r.timed_out), "rounds": args.rounds,
+           "handoff_relaxed_us": round(r.handoff_relaxed_us, 3), "handoff_acqrel_us": round(r.handoff_acqrel_us, 3),
+           "barrier_flags_us": round(r.barrier_flags_us, 3), "barrier_counter_us": round(r.barrier_counter_us, 3)}
+    print(json.dumps(out), flush=True)
+    if r.timed_out:
+        raise SystemExit("a probe wait ran out of its bound: the figures are not valid")
+    if args.out:
+        lines = ["# In-launch dependency latencies, one MI355X", "", "Command (from ziggy-llm_amd/):", "",
+                 f"    python3 -m zhip.microbench --sync --rounds {args.rounds} --out <file>", "",
+                 f"Averages over {args.rounds} rounds, timed on the device (s_memrealtime, 100 MHz).", "",
+                 "| dependency | us |", "|---|---|",
+                 f"| one-way hand-off between two CUs, relaxed device-scope store and load | {out['handoff_relaxed_us']} |",
+                 f"| the same, release store and acquire load | {out['handoff_acqrel_us']} |",
+                 f"| barrier of {r.workgroups} workgroups: arrival words polled by one wavefront | "
+                 f"{out['barrier_flags_us']} |",
+                 f"| barrier of {r.workgroups} workgroups: one arrival counter | {out['barrier_counter_us']} |"]
+        with open(args.out, "w") as fh:
+            fh.write("\n".join(lines) + "\n")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
+    ap.add_argument("--chain", action="store_true", help="the decode step's launch-structure probe")
+    ap.add_argument("--sync", action="store_true", help="in-launch dependency latencies")
+    ap.add_argument("--position", type=int, default=4096)
+    ap.add_argument("--reps", type=int, default=5)
+    ap.add_argument("--rounds", type=int, default=2000)
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--formats", default="q4_k,q6_k,q8_0")
     ap.add_argument("--shapes", default=",".join(f"{r}x{c}" for r, c in SHAPES),
                     help="comma-separated ROWSxCOLS list")
     ap.add_argument("--out", help="also write the results as a markdown table")
     args = ap.parse_args()
+    if args.chain or args.sync:
+        if args.chain:
+            chain(args)
+        if args.sync:
+            sync(args)
+        return
     shapes = [tuple(int(v) for v in s.split("x")) for s in args.shapes.split(",")]
     ctx = hip.Context(0)
     results = []
