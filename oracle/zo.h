@@ -27,7 +27,9 @@
  *     tolerance only.
  * Everything else is pinned by the reference's known-answer tests, its
  * fixture blocks and golden text, closed forms and brute-force layouts
- * (tests/test_oracle_pins.py, tests/test_golden.py).  The MoE composition
+ * (tests/test_oracle_pins.py, tests/test_golden.py); zo_round_f16 (the
+ * binary16 K/V store) against numpy's IEEE conversion at every exponent,
+ * tie, subnormal and overflow boundary (tests/test_round_f16_pin.py).  The MoE composition
  * (zo_moe_ffn: router, gating, top-k, normalisation, scale, expert row
  * offsets, SwiGLU, slot-order combine, sigmoid-gated shared expert) is pinned
  * against an independent float64 composition over the dequantized weights,
