@@ -340,7 +340,7 @@ typedef struct {
  * hardware under the decode step's launch structure; python -m zhip.microbench
  * --chain / --sync) ---- */
 typedef struct {
-    uint64_t bytes;         /* bytes streamed (each entry rounded down to 16 bytes per workgroup) */
+    uint64_t bytes;         /* bytes streamed (each entry rounded down to whole 16-byte words) */
     uint32_t kernels;       /* entries of the plan */
     uint32_t workgroups;    /* grid of every launch: the CU count */
     double one_kernel_ms;   /* all the bytes as one streaming kernel */

@@ -26,19 +26,52 @@ namespace {
 
 constexpr long kProbeSpin = 1L << 20;
 
-// Streams n16 16-byte words of buf, an equal share per workgroup, with 16-byte
-// loads, 4 in flight per thread (then the share's tail); one value per
-// workgroup keeps the loads live.
+// Streams n16 16-byte words of buf (128-byte aligned) with 16-byte loads, 8
+// to 16 in flight per thread.  The shares are whole
+// 128-byte lines, as equal as the line count allows (the last workgroup also
+// takes the words past the last whole line), so every wavefront's 1 KiB load
+// covers whole lines, as the decode kernels' row-aligned streams do.  One
+// value per workgroup keeps the loads live.
 __global__ void __launch_bounds__(256) probe_stream(const uint4 *buf, uint64_t n16, float *sink) {
-    const uint64_t per = n16 / gridDim.x;
-    const uint4 *p = buf + (uint64_t)blockIdx.x * per;
+    const uint64_t lines = n16 >> 3, q = lines / gridDim.x, r = lines % gridDim.x, b = blockIdx.x;
+    uint64_t per = 8 * (q + (b < r ? 1 : 0));
+    if (b == gridDim.x - 1) per += n16 & 7;
+    const uint4 *p = buf + 8 * (b * q + (b < r ? b : r));
+    if (per == 0) return;
+    // every component feeds the value (a load whose other words go unused is
+    // narrowed by the compiler to the words used).  Two register sets of
+    // eight loads alternate: one set is issued before the other is consumed,
+    // and neither is copied (a copy of a register still being loaded waits
+    // for the load).  Loads are clamped to the share's last word: those past
+    // the end re-read a line already fetched.
+    const uint64_t last = per - 1;
     uint32_t acc = 0;
+    uint4 va[8], vb[8];
+    auto issue = [&](uint4 (&v)[8], uint64_t i) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = p[min(i + 256 * k, last)];
+    };
+    auto consume = [&](uint4 (&v)[8], uint64_t i) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            // opaque here, so the fold stays after the other set's issue
+            asm volatile("" : "+v"(v[k].x), "+v"(v[k].y), "+v"(v[k].z), "+v"(v[k].w));
+            const uint32_t f = v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+            acc ^= i + 256 * k < per ? f : 0u;
+        }
+    };
     uint64_t i = threadIdx.x;
-    for (; i + 768 < per; i += 1024) {
-        const uint4 a = p[i], b = p[i + 256], c = p[i + 512], d = p[i + 768];
-        acc ^= a.x ^ b.y ^ c.z ^ d.w;
+    issue(va, i);
+    for (; i < per; i += 16 * 256) {
+        issue(vb, i + 8 * 256);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(va, i);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(va, i + 16 * 256);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(vb, i + 8 * 256);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    for (; i < per; i += 256) acc ^= p[i].x;
     if (acc == 0x12345678u) sink[blockIdx.x] = (float)acc;
 }
 
@@ -134,15 +167,17 @@ int ziggy_hip_probe_chain(ZiggyHipContext *ctx, const uint64_t *bytes, uint32_t 
     }
     hipSetDevice(ctx->device);
     const int G = cu_count(ctx->device);
-    const uint64_t share = 16ull * G;  // every launch streams whole 16-byte words per workgroup
+    // every entry streams its bytes in whole 16-byte words, from a 256-byte
+    // aligned offset of one buffer
     std::vector<uint64_t> off(n), len(n);
-    uint64_t total = 0;
+    uint64_t total = 0, streamed = 0;
     for (uint32_t i = 0; i < n; i++) {
-        len[i] = bytes[i] / share * share;
+        len[i] = bytes[i] & ~15ull;
         off[i] = total;
-        total += len[i];
+        total += (len[i] + 255) & ~255ull;
+        streamed += len[i];
     }
-    if (!total) {
+    if (!streamed) {
         set_err(err, err_len, "probe_chain: the plan streams nothing");
         return ZIGGY_HIP_INVALID_ARGUMENT;
     }
@@ -179,7 +214,7 @@ int ziggy_hip_probe_chain(ZiggyHipContext *ctx, const uint64_t *bytes, uint32_t 
             e = hipEventRecord(e0, st);
             if (e == hipSuccess) {
                 if (k == 0) {
-                    hipLaunchKernelGGL(probe_stream, dim3(G), dim3(256), 0, st, (const uint4 *)buf, total / 16, sink);
+                    hipLaunchKernelGGL(probe_stream, dim3(G), dim3(256), 0, st, (const uint4 *)buf, streamed / 16, sink);
                     e = hipGetLastError();
                 } else {
                     e = hipGraphLaunch(k == 1 ? x1 : x2, st);
@@ -202,7 +237,7 @@ int ziggy_hip_probe_chain(ZiggyHipContext *ctx, const uint64_t *bytes, uint32_t 
     if (buf) hipFree(buf);
     if (sink) hipFree(sink);
     if (e != hipSuccess) return hip_fail(e, "probe_chain", err, err_len);
-    out->bytes = total;
+    out->bytes = streamed;
     out->kernels = n;
     out->workgroups = (uint32_t)G;
     out->one_kernel_ms = best[0];

@@ -96,7 +96,7 @@ def chain(args) -> dict:
                  "",
                  f"Plan: the {spec.name} step at position {args.position}: {r.kernels} launches (step begin, per "
                  "layer q/k/v, attention K/V, o_proj, gate/up, down, then the output head), each streaming its "
-                 "bytes in equal shares over a grid of one workgroup per CU. Best of "
+                 "bytes in shares of whole 128-byte lines over a grid of one workgroup per CU. Best of "
                  f"{args.reps} runs after a warm-up, HIP events around each.", "",
                  "| form | ms | GB/s | % of 8 TB/s |", "|---|---|---|---|",
                  f"| one streaming kernel over all {r.bytes} bytes | {out['one_kernel_ms']} | "
