@@ -49,12 +49,12 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def context_length(model, prompt, warmup, steps):
+def context_length(model, prompt, warmup, steps, profile_steps=0):
     """KV rows the run needs.  The GPU decode uses prompt + warmup rows, then 1 + steps more (the pending
-    token and the timed steps); time_kernel needs one free row after that; the CPU baseline fills its cache
-    to pos0 = prompt + warmup + 1 and then decodes up to CPU_MAX_STEPS steps; config 4's verify adds three
-    passes of 9 rows (drafts decoded, the position rewound, then verified)."""
-    rows = prompt + warmup + 1 + max(steps + 1, CPU_MAX_STEPS)
+    token and the timed steps), then the profiled steps; time_kernel needs one free row after that; the CPU
+    baseline fills its cache to pos0 = prompt + warmup + 1 and then decodes up to CPU_MAX_STEPS steps;
+    config 4's verify adds three passes of 9 rows (drafts decoded, the position rewound, then verified)."""
+    rows = prompt + warmup + 1 + max(steps + 1 + profile_steps, CPU_MAX_STEPS)
     if model == "qwen3":
         rows += 3 * 9
     return rows + 8
@@ -78,6 +78,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=64)
+    ap.add_argument("--profile-steps", type=int, default=0,
+                    help="after the timed decode, this many more steps with every launch timed by HIP events "
+                         "under the reference's profile categories (its --metal-profile report)")
+    ap.add_argument("--profile-out", default=None, help="file for the profile summary (default: stderr)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -92,7 +96,7 @@ def main():
     if args.model == "moe":
         return bench_moe(args)
 
-    ctx_len = context_length(args.model, args.prompt, args.warmup, args.steps)
+    ctx_len = context_length(args.model, args.prompt, args.warmup, args.steps, args.profile_steps)
     spec = {"llama8b": synth.llama8b_spec, "tinyllama": synth.tinyllama_spec,
             "qwen3": synth.qwen3_8b_spec}[args.model](context=ctx_len)
     t0 = time.time()
@@ -137,6 +141,27 @@ def main():
     hbm_frac = bytes_per_token * tok_s / (HBM_PEAK_GBS * 1e9)
     log(f"decode: {tok_s:.1f} tok/s ({ms_per_step:.3f} ms/step, gpu events {st.gpu_elapsed_ns / 1e6 / args.steps:.3f}"
         f" ms/step), {bytes_per_token / 1e9:.3f} GB/token -> {100 * hbm_frac:.1f}% of HBM peak")
+    next_tok = int(st.next_token)
+
+    profile = None
+    if args.profile_steps > 0:
+        # the reference's decode profile (runtime/metal_profile.zig; printed as "metal_profile:" by
+        # runtime/mod.zig:177-178): direct launches, so these steps are slower than the timed ones
+        ptoks, recs = sess.profile_decode(next_tok, args.profile_steps)
+        next_tok = int(ptoks[-1])
+        text = hip.render_profile(recs)
+        kv = hip.parse_profile(text)
+        if args.profile_out:
+            with open(args.profile_out, "w") as f:
+                f.write(text)
+        else:
+            print("metal_profile:\n" + text, file=sys.stderr, end="", flush=True)
+        profile = {"steps": args.profile_steps, "decode_ns": int(kv["profiled_decode_ns"]),
+                   "commit_wait_gpu_ns": int(kv["profile.commit_wait.gpu_ns"]),
+                   "share_pct": {c: float(kv[f"profile.{c}.share_pct"]) for c in hip.PROFILE_CATEGORIES},
+                   "top_bottlenecks": [kv[f"profile.top_bottleneck_{i}"] for i in (1, 2, 3)],
+                   "out": args.profile_out}
+        log(f"profile: {args.profile_steps} steps, top {profile['top_bottlenecks']}")
 
     verify = None
     if args.model == "qwen3":
@@ -147,7 +172,7 @@ def main():
         # prediction may differ from the decoded draft only where the decode step's top-2 logits are
         # within a near-tie margin; any other difference fails the bench.
         times, mismatches, accepted = [], 0, []
-        cur = int(st.next_token)
+        cur = next_tok
         for _ in range(3):
             p0 = sess.position
             drafts, margins, t = [], [], cur
@@ -255,6 +280,7 @@ def main():
         "verify": verify,
         "prefill": prefill,
         "cold": cold,
+        "profile": profile,
         "tokens_head": [int(t) for t in toks[:8]],
     }
     print(json.dumps(line), flush=True)

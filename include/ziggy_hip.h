@@ -538,6 +538,58 @@ int ziggy_hip_session_time_kernel(ZiggyHipSession *session, uint32_t kernel, uin
                                   uint64_t *avg_ns, uint64_t *bytes_per_launch, char *error_message,
                                   size_t error_message_len);
 
+/* ---- decode profiler (runtime/metal_profile.zig) ----
+ * Record kinds: the reference's Category values (metal_profile.zig:3-27), in
+ * its order, then the profiler calls that are not categories. */
+enum {
+    ZIGGY_HIP_PROFILE_PROJECTIONS = 0,
+    ZIGGY_HIP_PROFILE_ATTENTION = 1,
+    ZIGGY_HIP_PROFILE_KV_WRITES = 2,
+    ZIGGY_HIP_PROFILE_NORMALIZATION = 3,
+    ZIGGY_HIP_PROFILE_ELEMENTWISE_OPS = 4,
+    ZIGGY_HIP_PROFILE_OUTPUT_REDUCE = 5,
+    ZIGGY_HIP_PROFILE_COMMIT_WAIT = 6,
+    ZIGGY_HIP_PROFILE_HOST_READBACK = 7,
+    ZIGGY_HIP_PROFILE_CPU_SAMPLING = 8,
+    ZIGGY_HIP_PROFILE_COMMIT_WAIT_GPU = 16, /* recordCommitWaitGpu (:193-197) */
+    ZIGGY_HIP_PROFILE_MOON_QUANT = 17,      /* recordMoonQuantProjection (:171-191); this backend emits none */
+    ZIGGY_HIP_PROFILE_TOKEN_BEGIN = 32,     /* beginDecodeToken (:120-126) */
+    ZIGGY_HIP_PROFILE_TOKEN_END = 33,       /* endDecodeToken (:128-137) */
+};
+typedef struct {
+    uint32_t kind;        /* ZIGGY_HIP_PROFILE_* */
+    uint32_t has_shape;   /* 1: recordWithShape (:146-169), 0: record (:139-144) */
+    uint64_t ns;
+    uint64_t rows, cols, depth, extra; /* ShapeDesc (:35-41) */
+    uint32_t tensor_type, reserved;
+} ZiggyHipProfileRecord; /* 56 bytes */
+/* Folds a record stream as the reference's Profiler does and writes its
+ * renderSummary text (metal_profile.zig:201-316): the same keys in the same
+ * order.  out_length receives the text's length; the call fails with
+ * ZIGGY_HIP_INVALID_ARGUMENT when capacity is below out_length + 1 (the text
+ * is then not written) or a record kind is unknown.  Host code only. */
+int ziggy_hip_profile_render(const ZiggyHipProfileRecord *records, size_t count, char *out, size_t capacity,
+                             size_t *out_length);
+/* `steps` greedy decode steps from `token` (Session.stepGreedy, as
+ * generateLoaded drives them with the profiler on: model/loader.zig:2137-2159)
+ * with every kernel launched directly and a HIP event after each, on the
+ * session stream.  Per token it emits TOKEN_BEGIN, one record per launch with
+ * the launch's device time (hipEventElapsedTime of the events around it) under
+ * the category of the reference's op (the step begin's embedding gather:
+ * elementwise_ops; q/k/v, o, gate/up and down: projections, each with its
+ * RMSNorm / SwiGLU fused; attention, with the q/k norms, RoPE and the K/V
+ * store fused: attention, shaped as session.zig:445-450; the output head
+ * fused with argmax: output_reduce, shaped as session.zig:633-645), then
+ * COMMIT_WAIT (host time blocked in the stream synchronization),
+ * COMMIT_WAIT_GPU (device time from the first event to the last),
+ * HOST_READBACK (the token's device-to-host copy) and TOKEN_END.  out_tokens
+ * receives the `steps` greedy tokens; the position advances by `steps`.
+ * *out_count receives the records written, or, when `capacity` is too small
+ * (the call then fails before any work), the count needed. */
+int ziggy_hip_session_profile_decode(ZiggyHipSession *session, uint32_t token, uint32_t steps, uint32_t *out_tokens,
+                                     ZiggyHipProfileRecord *records, size_t capacity, size_t *out_count,
+                                     char *error_message, size_t error_message_len);
+
 /* ---- MoE FFN layer stack (batch-1 decode) ----
  * The MoE FFN block of a layer, hidden += computeMoeFfn(rmsNorm(hidden,
  * ffn_norm)) (model/loader.zig:1262-1285, 1718-1749), as the Metal session

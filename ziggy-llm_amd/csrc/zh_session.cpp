@@ -1228,4 +1228,143 @@ int ziggy_hip_session_time_kernel(ZiggyHipSession *s, uint32_t kernel, uint32_t 
     return ZIGGY_HIP_OK;
 }
 
+int ziggy_hip_session_profile_decode(ZiggyHipSession *s, uint32_t token, uint32_t steps, uint32_t *out_tokens,
+                                     ZiggyHipProfileRecord *records, size_t capacity, size_t *out_count, char *err,
+                                     size_t err_len) {
+    if (!s || !steps || !out_tokens || !out_count)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "invalid profile_decode arguments");
+    const ZiggyHipModelDesc &md = s->md;
+    const int L = (int)md.block_count;
+    const size_t per_step = 5 * (size_t)L + 7;  // markers, step begin, 5 per layer, output, wait, gpu, readback
+    *out_count = per_step * steps;
+    if (!records || capacity < per_step * steps)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "profile record buffer too small");
+    if ((uint64_t)s->position + steps > md.context_length)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "context overflow");
+    if (token >= s->embd.rows) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "token id out of range");
+    *out_count = 0;
+    hipStream_t st = s->ctx->stream;
+    const int nev = 5 * L + 3;  // before the step, after the step begin, after each launch
+    std::vector<hipEvent_t> ev(nev, nullptr);
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < nev && e == hipSuccess; i++) e = hipEventCreate(&ev[i]);
+    auto release = [&] {
+        for (hipEvent_t x : ev)
+            if (x) hipEventDestroy(x);
+    };
+    if (e != hipSuccess) {
+        release();
+        return hip_fail(e, "profile events", err, err_len);
+    }
+    const int H = (int)md.embedding_length;
+    // the op of each launch, under the reference's category and shape
+    struct Op {
+        uint32_t kind;
+        uint64_t rows, cols, depth, extra;
+        uint32_t type;
+    };
+    const Op argmax_shape{ZIGGY_HIP_PROFILE_OUTPUT_REDUCE, 1, 1, md.vocab_size, 0, (uint32_t)s->out.type};
+    size_t n = 0;
+    auto put = [&](uint32_t kind, uint64_t ns, const Op *shape) {
+        ZiggyHipProfileRecord &r = records[n++];
+        r = ZiggyHipProfileRecord{};
+        r.kind = kind;
+        r.ns = ns;
+        if (shape) {
+            r.has_shape = 1;
+            r.rows = shape->rows, r.cols = shape->cols, r.depth = shape->depth, r.extra = shape->extra;
+            r.tensor_type = shape->type;
+        }
+    };
+    static const int kLayerKernels[5] = {ZIGGY_HIP_KERNEL_QKV, ZIGGY_HIP_KERNEL_ATTENTION, ZIGGY_HIP_KERNEL_O_PROJ,
+                                         ZIGGY_HIP_KERNEL_GATE_UP, ZIGGY_HIP_KERNEL_DOWN};
+    std::vector<Op> ops(nev - 1);
+    for (uint32_t t = 0; t < steps && e == hipSuccess; t++) {
+        const int pos = (int)s->position;
+        StepState *h = s->st_host;
+        memset(h, 0, sizeof(*h));
+        h->pos = pos;
+        h->out_flag = 1;
+        h->token = token;
+        e = hipMemcpyAsync(s->st, h, sizeof(StepState), hipMemcpyHostToDevice, st);
+        // the step's launches (enqueue_step's order), an event after each
+        int k = 0;
+        if (e == hipSuccess) e = hipEventRecord(ev[k], st);
+        if (e == hipSuccess)
+            e = launch_step_begin(s->st, s->prompt, s->history, s->embd.p, s->embd.stride, (int)s->embd.rows,
+                                  s->embd.type, H, s->hidden, st);
+        ops[k] = Op{ZIGGY_HIP_PROFILE_ELEMENTWISE_OPS, 1, (uint64_t)H, 0, 0, 0};
+        if (e == hipSuccess) e = hipEventRecord(ev[++k], st);
+        for (int l = 0; l < L && e == hipSuccess; l++) {
+            const LayerW &W = s->layers[l];
+            for (int id : kLayerKernels) {
+                if (e == hipSuccess) e = enqueue_kernel(s, id, l, &s->st->pos, 0, st);
+                switch (id) {
+                case ZIGGY_HIP_KERNEL_QKV:
+                    ops[k] = Op{ZIGGY_HIP_PROFILE_PROJECTIONS, W.q.rows + W.k.rows + W.v.rows, W.q.cols, 0, 3,
+                                (uint32_t)W.q.type};
+                    break;
+                case ZIGGY_HIP_KERNEL_ATTENTION:  // session.zig:445-450
+                    ops[k] = Op{ZIGGY_HIP_PROFILE_ATTENTION, md.head_count, md.rope_dim, (uint64_t)pos + 1,
+                                md.head_count_kv, 0};
+                    break;
+                case ZIGGY_HIP_KERNEL_O_PROJ:
+                    ops[k] = Op{ZIGGY_HIP_PROFILE_PROJECTIONS, W.o.rows, W.o.cols, 0, 0, (uint32_t)W.o.type};
+                    break;
+                case ZIGGY_HIP_KERNEL_GATE_UP:  // the pair and its SwiGLU
+                    ops[k] = Op{ZIGGY_HIP_PROFILE_PROJECTIONS, W.gate.rows, W.gate.cols, 0, 2, (uint32_t)W.gate.type};
+                    break;
+                default:
+                    ops[k] = Op{ZIGGY_HIP_PROFILE_PROJECTIONS, W.down.rows, W.down.cols, 0, 0, (uint32_t)W.down.type};
+                    break;
+                }
+                if (e == hipSuccess) e = hipEventRecord(ev[++k], st);
+            }
+        }
+        if (e == hipSuccess) e = enqueue_kernel(s, ZIGGY_HIP_KERNEL_OUTPUT, 0, &s->st->pos, 0, st);
+        ops[k] = argmax_shape;
+        if (e == hipSuccess) e = hipEventRecord(ev[++k], st);
+        // commit and wait (commitOutputSequence), then read the token back
+        const auto w0 = std::chrono::steady_clock::now();
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        const auto w1 = std::chrono::steady_clock::now();
+        if (e == hipSuccess) e = hipMemcpy(h, s->st, sizeof(StepState), hipMemcpyDeviceToHost);
+        const auto w2 = std::chrono::steady_clock::now();
+        if (e != hipSuccess) break;
+        if (int pe = poll_check(s, err, err_len)) {
+            release();
+            return pe;
+        }
+        put(ZIGGY_HIP_PROFILE_TOKEN_BEGIN, 0, nullptr);
+        for (int i = 0; i < k && e == hipSuccess; i++) {
+            float ms = 0.f;
+            e = hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+            put(ops[i].kind, (uint64_t)((double)ms * 1e6), &ops[i]);
+        }
+        float total_ms = 0.f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&total_ms, ev[0], ev[k]);
+        if (e != hipSuccess) break;
+        Op wait_shape = argmax_shape;
+        wait_shape.kind = ZIGGY_HIP_PROFILE_COMMIT_WAIT;
+        put(ZIGGY_HIP_PROFILE_COMMIT_WAIT,
+            (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(w1 - w0).count(), &wait_shape);
+        put(ZIGGY_HIP_PROFILE_COMMIT_WAIT_GPU, (uint64_t)((double)total_ms * 1e6), nullptr);
+        Op rb_shape = argmax_shape;
+        rb_shape.kind = ZIGGY_HIP_PROFILE_HOST_READBACK;
+        put(ZIGGY_HIP_PROFILE_HOST_READBACK,
+            (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(w2 - w1).count(), &rb_shape);
+        put(ZIGGY_HIP_PROFILE_TOKEN_END, 0, nullptr);
+        *out_count = n;
+        s->fed.resize(s->position);
+        s->fed.push_back(token);
+        s->position++;
+        s->logits_valid = true;
+        token = 0xFFFFFFFFu - (uint32_t)(h->argmax & 0xFFFFFFFFull);
+        out_tokens[t] = token;
+    }
+    release();
+    if (e != hipSuccess) return hip_fail(e, "profile_decode", err, err_len);
+    return ZIGGY_HIP_OK;
+}
+
 }  // extern "C"

@@ -103,6 +103,16 @@ class MoeDesc(ctypes.Structure):
 
 KERNELS = {"qkv": 0, "rope_kv": 1, "attention": 2, "o_proj": 3, "gate_up": 4, "down": 5, "output": 6}
 
+# the decode profiler's record kinds (ZIGGY_HIP_PROFILE_*): the reference's
+# Category values (runtime/metal_profile.zig:3-27), then the calls that are not
+PROFILE_CATEGORIES = ["projections", "attention", "kv_writes", "normalization", "elementwise_ops", "output_reduce",
+                      "commit_wait", "host_readback", "cpu_sampling"]
+PROFILE_KINDS = {**{n: k for k, n in enumerate(PROFILE_CATEGORIES)}, "commit_wait_gpu": 16, "moon_quant": 17,
+                 "token_begin": 32, "token_end": 33}
+PROFILE_RECORD = np.dtype([("kind", "<u4"), ("has_shape", "<u4"), ("ns", "<u8"), ("rows", "<u8"), ("cols", "<u8"),
+                           ("depth", "<u8"), ("extra", "<u8"), ("tensor_type", "<u4"), ("reserved", "<u4")])
+assert PROFILE_RECORD.itemsize == 56
+
 
 _typed = False
 
@@ -185,6 +195,8 @@ def lib() -> ctypes.CDLL:
                                     ctypes.POINTER(u32)],
         "ziggy_hip_session_time_kernel": [vp, u32, u32, ctypes.POINTER(ctypes.c_uint64),
                                           ctypes.POINTER(ctypes.c_uint64)] + E,
+        "ziggy_hip_profile_render": [vp, sz, vp, sz, ctypes.POINTER(sz)],
+        "ziggy_hip_session_profile_decode": [vp, u32, u32, vp, vp, sz, ctypes.POINTER(sz)] + E,
         "ziggy_hip_moe_stack_create": [vp, ctypes.POINTER(MoeDesc), ctypes.POINTER(MoeLayerDesc), u32,
                                        ctypes.POINTER(vp)] + E,
         "ziggy_hip_moe_stack_destroy": [vp],
@@ -504,6 +516,19 @@ class Session:
         _call("ziggy_hip_session_time_kernel", self.h, KERNELS[name], iterations, ctypes.byref(ns), ctypes.byref(nb))
         return ns.value, nb.value
 
+    def profile_decode(self, token: int, steps: int):
+        """`steps` greedy decode steps from `token`, each launch timed by HIP
+        events (ziggy_hip_session_profile_decode): the greedy tokens and the
+        record stream (PROFILE_RECORD), which render_profile turns into the
+        reference's profile summary."""
+        toks = np.zeros(steps, np.uint32)
+        cap = (5 * self.md.block_count + 7) * steps
+        recs = np.zeros(cap, PROFILE_RECORD)
+        n = ctypes.c_size_t()
+        _call("ziggy_hip_session_profile_decode", self.h, token, steps, toks.ctypes.data, recs.ctypes.data, cap,
+              ctypes.byref(n))
+        return toks, recs[:n.value]
+
     def logits(self) -> np.ndarray:
         out = np.empty(self.md.vocab_size, np.float32)
         _call("ziggy_hip_session_read_logits", self.h, out.ctypes.data)
@@ -638,6 +663,27 @@ class MoeStack:
         if getattr(self, "h", None):
             lib().ziggy_hip_moe_stack_destroy(self.h)
             self.h = None
+
+
+def render_profile(records) -> str:
+    """The reference's profile summary (Profiler.renderSummary,
+    runtime/metal_profile.zig:201-316) of a record stream; host code only."""
+    recs = np.ascontiguousarray(records, PROFILE_RECORD)
+    need = ctypes.c_size_t()
+    ptr = recs.ctypes.data if recs.size else None
+    st = lib().ziggy_hip_profile_render(ptr, recs.size, None, 0, ctypes.byref(need))
+    if need.value == 0 and st:
+        raise HipError(st, "render_profile: unknown record kind")
+    buf = ctypes.create_string_buffer(need.value + 1)
+    st = lib().ziggy_hip_profile_render(ptr, recs.size, buf, need.value + 1, ctypes.byref(need))
+    if st:
+        raise HipError(st, "render_profile: unknown record kind")
+    return buf.value.decode()
+
+
+def parse_profile(text: str) -> dict:
+    """key=value lines of a profile summary as a dict (values as text)."""
+    return dict(line.split("=", 1) for line in text.splitlines() if "=" in line)
 
 
 def _sample_status(st: int, name: str):
