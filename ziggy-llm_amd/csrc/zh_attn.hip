@@ -1250,10 +1250,12 @@ int attention_splits(int kv_heads, int max_positions) {
 // position + m -- the arithmetic of the fused single-query kernel, in the
 // same order and thread layout.
 template <int HD>
-__global__ void __launch_bounds__(256) attn_prep_kernel(AttnParams p, float *q_out) {
+__global__ void __launch_bounds__(256) attn_prep_kernel(AttnParams p, float *q_out, RowScale rs, ZeroSpans z) {
     constexpr int QV = kMaxGroup * HD / 256;
     const int m = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int G = p.head_count / p.head_count_kv, nq = G * HD, pos = p.position + m;
+    // the deferred RMSNorm of the q/k/v products' input row
+    const float r = rs.ss ? 1.0f / sqrtf(rs.ss[m] / (float)rs.n + rs.eps) : 1.0f;
     __shared__ float q_s[kMaxGroup * HD];
     __shared__ float kn_s[HD];
     __shared__ float red16[4 * QV_MAX];
@@ -1266,12 +1268,12 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(AttnParams p, float *q_o
         const int idx = tid + 256 * i;
         qv[i] = 0.f;
         if (idx < nq) {
-            qv[i] = qrow[idx];
+            qv[i] = r * qrow[idx];
             if (p.q_bias) qv[i] += p.q_bias[(size_t)kvh * nq + idx];
         }
     }
-    kx[0] = p.k_new[kv_off + tid % HD];
-    float vx = p.v_new[kv_off + tid % HD];
+    kx[0] = r * p.k_new[kv_off + tid % HD];
+    float vx = r * p.v_new[kv_off + tid % HD];
     if (tid < HD) {
         if (p.k_bias) kx[0] += p.k_bias[(size_t)kvh * HD + tid];
         if (p.v_bias) vx += p.v_bias[(size_t)kvh * HD + tid];
@@ -1287,13 +1289,22 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(AttnParams p, float *q_o
         p.k_cache[idx] = __float2half_rn(kn_s[tid]);
         p.v_cache[idx] = __float2half_rn(vx);
     }
+    // the spans the pass clears here (inputs of later accumulating products)
+    const size_t nthr = (size_t)gridDim.x * gridDim.y * 256,
+                 gt = ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 256 + tid;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        for (size_t i = gt; i < z.n[j]; i += nthr) z.p[j][i] = 0.f;
 }
 
 // The per-head norm reduces over whole wavefronts: heads of 64, 128 or 256
 // values (no QK-norm for head_dim 96)
 static bool norms_fit(const AttnParams &p) { return !(p.q_norm || p.k_norm) || p.head_dim % 64 == 0; }
 
-hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t s) {
+hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t s, RowScale rs, const ZeroSpans &z) {
+    for (int j = 0; j < 4; j++)
+        if (z.n[j] && !z.p[j]) return hipErrorInvalidValue;
+    if (rs.ss && rs.n < 1) return hipErrorInvalidValue;
     if (!p.page_table || p.page_shift != kKvPageShift) return hipErrorInvalidValue;
     if (p.head_count_kv <= 0 || p.head_count % p.head_count_kv || p.head_count / p.head_count_kv > kMaxGroup ||
         p.n_query < 1 || !p.q || !p.k_new || !p.v_new || !q_out || p.q_stride < p.head_count * p.head_dim)
@@ -1301,10 +1312,10 @@ hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t 
     if (!norms_fit(p)) return hipErrorInvalidValue;
     const dim3 grid(p.n_query, p.head_count_kv);
     switch (p.head_dim) {
-    case 64: hipLaunchKernelGGL(attn_prep_kernel<64>, grid, dim3(256), 0, s, p, q_out); break;
-    case 96: hipLaunchKernelGGL(attn_prep_kernel<96>, grid, dim3(256), 0, s, p, q_out); break;
-    case 128: hipLaunchKernelGGL(attn_prep_kernel<128>, grid, dim3(256), 0, s, p, q_out); break;
-    case 256: hipLaunchKernelGGL(attn_prep_kernel<256>, grid, dim3(256), 0, s, p, q_out); break;
+    case 64: hipLaunchKernelGGL(attn_prep_kernel<64>, grid, dim3(256), 0, s, p, q_out, rs, z); break;
+    case 96: hipLaunchKernelGGL(attn_prep_kernel<96>, grid, dim3(256), 0, s, p, q_out, rs, z); break;
+    case 128: hipLaunchKernelGGL(attn_prep_kernel<128>, grid, dim3(256), 0, s, p, q_out, rs, z); break;
+    case 256: hipLaunchKernelGGL(attn_prep_kernel<256>, grid, dim3(256), 0, s, p, q_out, rs, z); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

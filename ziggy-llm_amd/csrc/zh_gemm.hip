@@ -265,15 +265,20 @@ hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t st
     return hipGetLastError();
 }
 
+bool gemm_rownorm_supported(int fmt, int K, const void *w, uint64_t stride) {
+    return qgemm_enabled() && qgemm_supported(fmt, K, w, nullptr, stride, 0);
+}
+
 hipError_t launch_gemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
                              const int *N, uint64_t stride, const float *x, int ldx, int M, int K, int out,
-                             hipStream_t s, int max_split, const XPlanes *xp) {
+                             hipStream_t s, int max_split, const XPlanes *xp, const RowNorm *rn) {
     if (nseg < 1 || nseg > 3 || (out != OUT_STORE && out != OUT_ADD)) return hipErrorInvalidValue;
     bool one = qgemm_enabled();
     for (int i = 0; i < nseg && one; i++) one = qgemm_supported(fmt, K, w[i], nullptr, stride, 0);
     if (one)
         return launch_qgemm_multi(fmt, nseg, w, y, ldy, N, nullptr, stride, x, ldx, M, K, out, nullptr, s, max_split,
-                                  xp);
+                                  xp, rn);
+    if (rn) return hipErrorInvalidValue;  // the other kernels take normed rows
     for (int i = 0; i < nseg; i++) {
         const hipError_t e = launch_gemm(fmt, w[i], nullptr, stride, x, ldx, y[i], ldy[i], M, N[i], K, out, nullptr, s);
         if (e != hipSuccess) return e;

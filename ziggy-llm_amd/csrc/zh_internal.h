@@ -273,6 +273,24 @@ hipError_t launch_rope(const float *src, float *dst, int heads, int hd, int rope
                        int style, hipStream_t s);
 hipError_t launch_store_kv_half(const float *src, __half *dst, int count, hipStream_t s);
 hipError_t launch_silu_mul(float *gate, const float *up, int n, hipStream_t s);
+// Spans of floats a pass kernel clears on the way, for the accumulating
+// products after it (up to four; n 0: none).
+struct ZeroSpans {
+    float *p[4];
+    size_t n[4];
+};
+// The deferred RMSNorm's scale of row m (RowNorm): 1 / sqrt(ss[m] / n + eps);
+// ss null: 1.
+struct RowScale {
+    const float *ss;
+    int n;
+    float eps;
+};
+// rows x n: gate = silu(r gate) * (r up), r the row's scale (silu_mul with
+// the deferred norm of the gate/up products), clearing z on the way
+hipError_t launch_silu_mul_rows(float *gate, const float *up, int rows, int n, RowScale rs, const ZeroSpans &z,
+                                hipStream_t s);
+hipError_t launch_zero_spans(const ZeroSpans &z, hipStream_t s);
 hipError_t launch_add(float *dst, const float *src, int n, hipStream_t s);
 hipError_t launch_argmax(const float *x, int n, uint32_t *out_token, unsigned long long *tmp, hipStream_t s);
 hipError_t launch_topk(const float *x, int n, int k, void *entries, hipStream_t s);
@@ -315,12 +333,24 @@ hipError_t launch_silu_mul_split(float *gate, const float *up, int rows, int n, 
 hipError_t launch_gemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride, const float *x, int ldx,
                        float *y, int ldy, int M, int N, int K, int out, unsigned long long *argmax, hipStream_t s,
                        bool precise = false, int max_split = 16, const XPlanes *xp = nullptr);
+// The deferred RMSNorm of a product's input rows (rmsNorm, model/loader.zig:
+// 3404-3426, with its scale moved past the product): the product takes
+// x * w, and each row's sum of squares of x is added to ss[row] (when ss is
+// set), so that its reader scales the result by 1 / sqrt(ss / K + eps).
+struct RowNorm {
+    const float *w;
+    float *ss;
+};
 // Up to three matrices of one format, row stride and reduction length against
 // one input (stores or adds): one launch on the exact-code kernel, else one
-// product each.
+// product each.  rn (the exact-code kernel only; see gemm_rownorm_supported):
+// the deferred norm of the input.
 hipError_t launch_gemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
                              const int *N, uint64_t stride, const float *x, int ldx, int M, int K, int out,
-                             hipStream_t s, int max_split = 16, const XPlanes *xp = nullptr);
+                             hipStream_t s, int max_split = 16, const XPlanes *xp = nullptr,
+                             const RowNorm *rn = nullptr);
+// whether launch_gemm_multi takes a RowNorm for these matrices
+bool gemm_rownorm_supported(int fmt, int K, const void *w, uint64_t stride);
 // xp (optional): the normed rows also split into xp (as launch_split_rows),
 // in the same launch where the row fits.
 hipError_t launch_rms_norm_rows(const float *x, const float *w, float *out, int rows, int n, float eps, hipStream_t s,
@@ -341,7 +371,7 @@ hipError_t launch_qgemm(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t s
 hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
                               const int *N, const uint8_t *w2, uint64_t stride, const float *x, int ldx, int M, int K,
                               int out, unsigned long long *argmax, hipStream_t s, int max_split = 16,
-                              const XPlanes *xp = nullptr);
+                              const XPlanes *xp = nullptr, const RowNorm *rn = nullptr);
 hipError_t launch_qgemm_grouped(int fmt, const uint8_t *w, const uint8_t *w2, uint64_t stride,
                                 uint64_t expert_stride, const float *x, int ldx, int x_div, float *y, int ldy, int N,
                                 int K, int out, const int *tiles, const int *list, const int *ntiles, int max_tiles,
@@ -412,7 +442,10 @@ constexpr int kIdentityPages = 65536;  // a context's identity table: contiguous
 hipError_t launch_iota_u32(uint32_t *p, int n, hipStream_t s);
 // q/k/v epilogue of n_query tokens (rows q_stride / kv_dim apart): roped q to
 // q_out (may be q), k and v stored to the cache at position + m.
-hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t s);
+// rs: the q/k/v rows come from products with a deferred norm (RowNorm): each
+// token's row is scaled first.  z: spans cleared on the way.
+hipError_t launch_attention_prep(const AttnParams &p, float *q_out, hipStream_t s, RowScale rs = RowScale{},
+                                 const ZeroSpans &z = ZeroSpans{});
 bool attention_multi_supported(int head_dim);
 // workgroups along the query axis of a multi-query launch (its partials and
 // arrival counters: head_count_kv * groups slots of kMultiHeads heads each)

@@ -84,6 +84,30 @@ __global__ void silu_mul_kernel(float *__restrict__ g, const float *__restrict__
     }
 }
 
+// silu_mul over rows x n with the deferred norm of the gate/up products:
+// g = silu(r g) * (r u), r the row's scale; then the spans z cleared.
+__global__ void silu_mul_rows_kernel(float *__restrict__ g, const float *__restrict__ u, int rows, int n,
+                                     RowScale rs, ZeroSpans z) {
+    const size_t total = (size_t)rows * n, nthr = (size_t)gridDim.x * blockDim.x;
+    const size_t gi = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (size_t i = gi; i < total; i += nthr) {
+        const int row = (int)(i / n);
+        const float r = rs.ss ? 1.0f / sqrtf(rs.ss[row] / (float)rs.n + rs.eps) : 1.0f;
+        const float v = r * g[i];
+        g[i] = (v / (1.0f + expf(-v))) * (r * u[i]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        for (size_t i = gi; i < z.n[j]; i += nthr) z.p[j][i] = 0.f;
+}
+
+__global__ void zero_spans_kernel(ZeroSpans z) {
+    const size_t nthr = (size_t)gridDim.x * blockDim.x, gi = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        for (size_t i = gi; i < z.n[j]; i += nthr) z.p[j][i] = 0.f;
+}
+
 // Rows of x into the exact-code GEMM's pieces (split_run16): thread t takes
 // run t of the row-major runs (16 values; n a multiple of 32, so the two runs
 // of a 32-value sum sit in neighbouring lanes).  SILU: the values are
@@ -322,6 +346,32 @@ hipError_t launch_store_kv_half(const float *src, __half *dst, int count, hipStr
     hipLaunchKernelGGL(store_kv_half_kernel, dim3(cdiv(count, 256)), dim3(256), 0, s, src, dst, count);
     return hipGetLastError();
 }
+static bool spans_ok(const ZeroSpans &z) {
+    for (int j = 0; j < 4; j++)
+        if (z.n[j] && !z.p[j]) return false;
+    return true;
+}
+
+hipError_t launch_silu_mul_rows(float *gate, const float *up, int rows, int n, RowScale rs, const ZeroSpans &z,
+                                hipStream_t s) {
+    if (!gate || !up || rows < 1 || n < 1 || !spans_ok(z) || (rs.ss && rs.n < 1)) return hipErrorInvalidValue;
+    const size_t total = (size_t)rows * n, want = (total + 255) / 256;
+    const int blocks = (int)(want < 2048 ? want : 2048);
+    hipLaunchKernelGGL(silu_mul_rows_kernel, dim3(blocks), dim3(256), 0, s, gate, up, rows, n, rs, z);
+    return hipGetLastError();
+}
+
+hipError_t launch_zero_spans(const ZeroSpans &z, hipStream_t s) {
+    if (!spans_ok(z)) return hipErrorInvalidValue;
+    size_t most = 0;
+    for (int j = 0; j < 4; j++) most = z.n[j] > most ? z.n[j] : most;
+    if (!most) return hipSuccess;
+    const size_t want = (most + 255) / 256;
+    const int blocks = (int)(want < 1024 ? want : 1024);
+    hipLaunchKernelGGL(zero_spans_kernel, dim3(blocks), dim3(256), 0, s, z);
+    return hipGetLastError();
+}
+
 hipError_t launch_silu_mul(float *gate, const float *up, int n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(silu_mul_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, gate, up, n);

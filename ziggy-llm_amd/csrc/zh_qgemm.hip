@@ -49,6 +49,7 @@ typedef uint32_t qu4v __attribute__((ext_vector_type(4)));
 
 constexpr int kQRows = 64;    // weight rows per workgroup (16 per wavefront)
 constexpr int kQChunk = 256;  // reduction values per staged chunk
+constexpr int kNrmStage = 512;  // the longest stage of the deferred-norm (NRM) kernels
 
 struct QGemmParams {
     const uint8_t *w, *w2;  // W row 0 (w2: the up matrix of SWIGLU)
@@ -74,6 +75,11 @@ struct QGemmParams {
     const uint16_t *xh, *xl;
     const float *xsum;
     int ldxs;
+    // NRM kernels: the deferred RMSNorm of the input rows -- the products take
+    // x * norm_w (per reduction index), and the row's sum of squares of x
+    // over this reduction range adds to row_ss[row] (one workgroup per range)
+    const float *norm_w;
+    float *row_ss;
 };
 
 // bf16 bits of two small integers held as f32 (exact: the high halves)
@@ -352,8 +358,9 @@ __device__ __forceinline__ uint32_t ordered_bits_q(float v) {
 
 // XP: the input comes split (XPlanes) and a workgroup takes two token tiles
 // (32 tokens): every decoded code serves both tiles' products.
-template <int F, int OUT, bool GROUPED, int R, bool XP>
+template <int F, int OUT, bool GROUPED, int R, bool XP, bool NRM = false>
 __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(QGemmParams p) {
+    static_assert(!NRM || (!XP && !GROUPED), "the deferred norm stages plain rows");
     constexpr bool kPair = OUT == OUT_SWIGLU;
     constexpr int TT = XP ? 2 : 1;  // token tiles of 16 per workgroup
     // LDS for two workgroups per CU (three for the grouped single products,
@@ -364,7 +371,9 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
     constexpr int kSub = QC::kSub, kCB = QC::kCB, kShm = QC::kShm;
     constexpr int kMats = G::kMats, kWin = G::kWin, kRowW = G::kRowW, kPieces = G::kPieces, kP = G::kP;
     constexpr bool kXsum = G::kXsum;
-    constexpr int kStage = G::kStage, kStageChunks = G::kStageChunks;
+    // NRM: stages of at most two chunks (the norm weights are staged beside
+    // the activations; a longer stage's registers spill)
+    constexpr int kStage = NRM && G::kStage > kNrmStage ? kNrmStage : G::kStage, kStageChunks = kStage / kQChunk;
     static_assert((kStageChunks % R == 0 || (kStageChunks == 1 && R == 2)) && R % 2 == 0,
                   "stages hold whole rings of an even depth, or one chunk at depth 2");
 
@@ -430,6 +439,8 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
     static_assert(!XP || !kXsum || kSub == 32, "split inputs carry 32-value sums");
     bool tok_ok[TT];
     const float *xrow[TT];
+    const float *nwrow = NRM ? p.norm_w + 16 * part : nullptr;
+    float ssq = 0.f;  // NRM: this thread's sum of squares of its token's staged values
     const uint16_t *xhrow[TT], *xlrow[TT];
     const float *xsrow[TT];
 #pragma unroll
@@ -450,6 +461,7 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
     // XP: the pieces and sums as split by the producer (tokens past M repeat
     // the last row; their results are never stored).
     float4 ld[TT][kStageChunks][4];
+    float4 ldw[NRM ? kStageChunks : 1][4];
     float lsum[TT][XP ? kStageChunks : 1];
     auto stage_load = [&](int kb, int nc) {
 #pragma unroll
@@ -469,6 +481,11 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
                     const float4 *src = reinterpret_cast<const float4 *>(xrow[t] + ko);
 #pragma unroll
                     for (int i = 0; i < 4; i++) ld[t][u][i] = src[i];
+                    if (NRM && t == 0) {
+                        const float4 *nw = reinterpret_cast<const float4 *>(nwrow + ko);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) ldw[u][i] = nw[i];
+                    }
                 }
             }
     };
@@ -485,6 +502,11 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
                         __asm__ volatile("" ::"v"(ld[t][u][i].x), "v"(ld[t][u][i].y), "v"(ld[t][u][i].z),
                                          "v"(ld[t][u][i].w));
                     if (XP && kXsum) __asm__ volatile("" ::"v"(lsum[t][XP ? u : 0]));
+                    if (NRM && t == 0)
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            __asm__ volatile("" ::"v"(ldw[u][i].x), "v"(ldw[u][i].y), "v"(ldw[u][i].z),
+                                             "v"(ldw[u][i].w));
                     continue;
                 }
                 uint32_t hw[8], lw[8];
@@ -502,6 +524,17 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
                         v[4 * i + 1] = tok_ok[t] ? ld[t][u][i].y : 0.f;
                         v[4 * i + 2] = tok_ok[t] ? ld[t][u][i].z : 0.f;
                         v[4 * i + 3] = tok_ok[t] ? ld[t][u][i].w : 0.f;
+                    }
+                    if constexpr (NRM) {
+                        // rmsNorm's (scale x) w with the scale deferred to the
+                        // product's reader: the sum of squares of x, then x w
+#pragma unroll
+                        for (int i = 0; i < 16; i++) ssq = fmaf(v[i], v[i], ssq);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            v[4 * i] *= ldw[u][i].x, v[4 * i + 1] *= ldw[u][i].y;
+                            v[4 * i + 2] *= ldw[u][i].z, v[4 * i + 3] *= ldw[u][i].w;
+                        }
                     }
                     sum = split_run16(v, hw, lw);
                     if (kXsum && kSub == 32) sum += __shfl_xor(sum, 1, 64);  // the other half of the 32-value sub-block
@@ -697,6 +730,15 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
             }
         }
     };
+    // NRM: the token's sum of squares over this reduction range (the 16
+    // threads of a token are 16 neighbouring lanes), added once per range
+    auto flush_ss = [&] {
+        if constexpr (NRM) {
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) ssq += __shfl_xor(ssq, o, 64);
+            if (p.row_ss && blockIdx.x == 0 && part == 0 && tok_ok[0]) atomicAdd(p.row_ss + (m0 + tt), ssq);
+        }
+    };
     // The results of group g: D[token 16 t + 4 lg + r][row li]; acc cleared after.
     auto epilogue = [&](int g) {
         const Seg sg = seg_of(g);
@@ -753,6 +795,7 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
 #pragma unroll
         for (int q = 0; q < R; q++) ring_load(q, q);
         stage_store(nspan);
+        flush_ss();
         __syncthreads();
         fetch(0, 0, fa);
         for (int t0 = 0; t0 < nitems; t0 += R) {
@@ -841,12 +884,20 @@ __global__ void __launch_bounds__(256, OUT != OUT_SWIGLU ? 2 : 1) qgemm_kernel(Q
             run_stage(s0, nst);
         }
     }
+    flush_ss();
     epilogue(blockIdx.x);
 }
 
 typedef void (*QGemmKernel)(QGemmParams);
 
-template <int F, bool G, int R, bool XP> static QGemmKernel pick_q(int out) {
+template <int F, bool G, int R, bool XP> static QGemmKernel pick_q(int out, bool nrm = false) {
+    if constexpr (!XP && !G && R == 2) {
+        if (nrm) return out == OUT_ADD ? qgemm_kernel<F, OUT_ADD, false, 2, false, true>
+                        : out == OUT_STORE ? qgemm_kernel<F, OUT_STORE, false, 2, false, true>
+                                           : nullptr;
+    } else {
+        if (nrm) return nullptr;
+    }
     if constexpr (XP) {
         // split inputs, two token tiles: the dense stores and adds of the batched passes
         if constexpr (G || R != 2)
@@ -877,16 +928,14 @@ template <int F, bool G, int R, bool XP> static QGemmKernel pick_q(int out) {
 // ring depth: 4 chunks, or 2 for the two matrices of SWIGLU (the same bytes in
 // flight), for reduction ranges of two chunks, for two token tiles (the
 // products' registers) and for the grouped kernels (stages of two chunks)
-template <bool G, bool XP> static QGemmKernel pick_qf(int fmt, int out, int K) {
-    const bool r2 = true;  // every kernel at depth 2 (two workgroups per CU leave stages of two chunks)
+template <bool G, bool XP> static QGemmKernel pick_qf(int fmt, int out, int K, bool nrm = false) {
     (void)K;
-    (void)out;
-    switch (fmt) {
-    case Q4_K: return r2 ? pick_q<Q4_K, G, 2, XP>(out) : pick_q<Q4_K, G, 4, XP>(out);
-    case Q6_K: return r2 ? pick_q<Q6_K, G, 2, XP>(out) : pick_q<Q6_K, G, 4, XP>(out);
-    case Q8_0: return r2 ? pick_q<Q8_0, G, 2, XP>(out) : pick_q<Q8_0, G, 4, XP>(out);
-    case IQ4_XS: return r2 ? pick_q<IQ4_XS, G, 2, XP>(out) : pick_q<IQ4_XS, G, 4, XP>(out);
-    case Q3_K: return r2 ? pick_q<Q3_K, G, 2, XP>(out) : pick_q<Q3_K, G, 4, XP>(out);
+    switch (fmt) {  // every kernel at depth 2 (two workgroups per CU leave stages of two chunks)
+    case Q4_K: return pick_q<Q4_K, G, 2, XP>(out, nrm);
+    case Q6_K: return pick_q<Q6_K, G, 2, XP>(out, nrm);
+    case Q8_0: return pick_q<Q8_0, G, 2, XP>(out, nrm);
+    case IQ4_XS: return pick_q<IQ4_XS, G, 2, XP>(out, nrm);
+    case Q3_K: return pick_q<Q3_K, G, 2, XP>(out, nrm);
     default: return nullptr;
     }
 }
@@ -923,14 +972,17 @@ __global__ void zero_rows_kernel(float *y, int ldy, int M, int N) {
     if (i < M * N) y[(size_t)(i / N) * ldy + i % N] = 0.f;
 }
 
-// Workgroups wanted for one product: every CU streams weights.
+// Workgroups wanted for one product: every CU streams weights
+// (ZIGGY_HIP_QGEMM_WPC: workgroups per CU, a tuning knob).
 static int qgemm_target_wgs() {
     static int t = [] {
         int dev = 0, n = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
             n = 256;
-        return n;
+        const char *e = getenv("ZIGGY_HIP_QGEMM_WPC");
+        const int w = e ? atoi(e) : 1;
+        return n * (w >= 1 && w <= 8 ? w : 1);
     }();
     return t;
 }
@@ -947,9 +999,11 @@ static double qgemm_stage_weight() {
 
 hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float *const *y, const int *ldy,
                               const int *N, const uint8_t *w2, uint64_t stride, const float *x, int ldx, int M, int K,
-                              int out, unsigned long long *argmax, hipStream_t s, int max_split, const XPlanes *xp) {
+                              int out, unsigned long long *argmax, hipStream_t s, int max_split, const XPlanes *xp,
+                              const RowNorm *rn) {
     if (nseg < 1 || nseg > 3 || M < 1 || ldx % 4 || (nseg > 1 && (out == OUT_SWIGLU || out == OUT_ARGMAX)))
         return hipErrorInvalidValue;
+    if (rn && (!rn->w || (out != OUT_STORE && out != OUT_ADD) || (uintptr_t)rn->w % 16)) return hipErrorInvalidValue;
     QGemmParams p{w[0], w2, stride, x, y[0], M, N[0], K, ldx, ldy[0], argmax, nullptr, nullptr, nullptr, 1, 0, 1};
     int groups = 0;
     for (int i = 0; i < nseg; i++) {
@@ -966,14 +1020,15 @@ hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float 
     p.groups = groups;
     p.nseg = nseg;
     // split inputs (more than one token tile): the XP kernels, two token tiles per workgroup
-    const bool use_xp = xp && xp->hi && xp->lo && xp->sum && xp->ld % 32 == 0 && K <= xp->ld && M > 16 &&
+    const bool use_xp = !rn && xp && xp->hi && xp->lo && xp->sum && xp->ld % 32 == 0 && K <= xp->ld && M > 16 &&
                         (out == OUT_STORE || out == OUT_ADD);
     const int TT = use_xp ? 2 : 1;
     const int tiles = (M + 16 * TT - 1) / (16 * TT), chunks = K / kQChunk;
     const int target = qgemm_target_wgs();
-    const int stage = use_xp                ? stage_chunks_of<false, 2, 2>(fmt)
-                      : out == OUT_SWIGLU ? stage_chunks_of<true>(fmt)
-                                          : stage_chunks_of<false, 1, 2>(fmt);
+    int stage = use_xp                ? stage_chunks_of<false, 2, 2>(fmt)
+                : out == OUT_SWIGLU ? stage_chunks_of<true>(fmt)
+                                    : stage_chunks_of<false, 1, 2>(fmt);
+    if (rn && stage > kNrmStage / kQChunk) stage = kNrmStage / kQChunk;  // the NRM kernels' stages
     // Reduction split ks (a power of two; results added atomically, plain
     // stores and adds only) and workgroups per split pg, each taking every
     // pg-th row group.  Several groups per workgroup need a one-stage range:
@@ -998,8 +1053,12 @@ hipError_t launch_qgemm_multi(int fmt, int nseg, const uint8_t *const *w, float 
             while (groups * tiles * ks * 2 <= target && chunks % (ks * 2) == 0 && ks * 2 <= max_split) ks *= 2;
     }
     p.ksplit = ks;
-    QGemmKernel k = use_xp ? pick_qf<false, true>(fmt, out, K / ks) : pick_qf<false, false>(fmt, out, K / ks);
+    QGemmKernel k = use_xp ? pick_qf<false, true>(fmt, out, K / ks) : pick_qf<false, false>(fmt, out, K / ks, rn);
     if (!k) return hipErrorInvalidValue;
+    if (rn) {
+        p.norm_w = rn->w;
+        p.row_ss = rn->ss;  // none: another launch over the same rows adds the sums
+    }
     if (use_xp) p.xh = xp->hi, p.xl = xp->lo, p.xsum = xp->sum, p.ldxs = xp->ld;
     if (ks > 1 && out == OUT_STORE) {
         for (int i = 0; i < nseg; i++) {

@@ -76,6 +76,7 @@ struct ZiggyHipSession {
     // batched verify (allocated on first use): [kVerifyMax] rows each
     float *b_hidden = nullptr, *b_normed = nullptr, *b_q = nullptr, *b_k = nullptr, *b_v = nullptr;
     float *b_attn = nullptr, *b_act = nullptr, *b_up = nullptr, *b_logits = nullptr;
+    float *b_ss = nullptr;  // verify: the deferred norms' row sums of squares, [2][kPassMax]
     // output shortlist (allocated on first use): packed keys, entries
     unsigned long long *sl_keys = nullptr;
     uint32_t *sl_entries = nullptr;
@@ -938,7 +939,8 @@ static hipError_t pass_alloc(ZiggyHipSession *s) {
     } reqs[] = {{(void **)&s->b_hidden, M * H * 4}, {(void **)&s->b_normed, M * H * 4}, {(void **)&s->b_q, M * Q * 4},
                 {(void **)&s->b_k, M * KV * 4},      {(void **)&s->b_v, M * KV * 4},      {(void **)&s->b_attn, M * Q * 4},
                 {(void **)&s->b_act, M * F * 4},     {(void **)&s->b_up, M * F * 4},      {(void **)&s->b_tokens, M * 4},
-                {(void **)&s->b_argmax, M * 8},     {(void **)&s->b_logits, kVerifyMax * s->md.vocab_size * 4}};
+                {(void **)&s->b_argmax, M * 8},     {(void **)&s->b_logits, kVerifyMax * s->md.vocab_size * 4},
+                {(void **)&s->b_ss, 2 * M * 4}};
     for (auto &r : reqs) {
         hipError_t e = hipMalloc(r.p, r.bytes);
         if (e != hipSuccess) return e;
@@ -1020,8 +1022,10 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
     // outputs, or store them (no reduction split): one launch for the
     // matrices that share a format and row size
     auto multi3 = [&](const DT &a, float *ya, int lda, const DT &b, float *yb, int ldb, const DT *c, float *yc,
-                      int ldc, const XPlanes *xp, bool store = false) {
+                      int ldc, const XPlanes *xp, bool store = false, const float *xin = nullptr,
+                      const RowNorm *rn = nullptr) {
         if (e != hipSuccess) return;
+        if (!xin) xin = s->b_normed;
         const DT *d[3] = {&a, &b, c};
         float *ys[3] = {ya, yb, yc};
         const int lds[3] = {lda, ldb, ldc};
@@ -1033,18 +1037,43 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
             const uint8_t *ws[3];
             int Ns[3];
             for (int k = i; k < j; k++) ws[k - i] = d[k]->p, Ns[k - i] = (int)d[k]->rows;
-            e = launch_gemm_multi(d[i]->type, j - i, ws, ys + i, lds + i, Ns, d[i]->stride, s->b_normed, H, M,
-                                  (int)d[i]->cols, store ? OUT_STORE : OUT_ADD, st, store ? 1 : split_clear, xp);
+            // the deferred norm's row sums once: with the first run of matrices
+            const RowNorm rn_i = rn ? RowNorm{rn->w, i == 0 ? rn->ss : nullptr} : RowNorm{};
+            e = launch_gemm_multi(d[i]->type, j - i, ws, ys + i, lds + i, Ns, d[i]->stride, xin, H, M,
+                                  (int)d[i]->cols, store ? OUT_STORE : OUT_ADD, st, store ? 1 : split_clear, xp,
+                                  rn ? &rn_i : nullptr);
             i = j;
         }
     };
+    // Verify passes defer the RMSNorms (RowNorm): the q/k/v and gate/up
+    // products take hidden * norm weights and add each row's sum of squares
+    // to ss_attn / ss_ffn; attention prep and SiLU * up scale their rows by
+    // 1 / sqrt(ss / H + eps).  No norm launches: the rows the accumulating
+    // products add onto are cleared by the launch before them (the q/k/v rows
+    // and ss_attn by SiLU * up of the layer before, or here for layer 0; the
+    // gate/up rows and ss_ffn by attention prep).
+    bool dn = !det && s->b_counters && s->b_ss && !fused_swiglu;
+    for (int l = 0; l < (int)md.block_count && dn; l++) {
+        const LayerW &L = s->layers[l];
+        for (const DT *d : {&L.q, &L.k, &L.v, &L.gate, &L.up})
+            dn = dn && gemm_rownorm_supported(d->type, (int)d->cols, d->p, d->stride);
+    }
+    float *ss_attn = s->b_ss, *ss_ffn = s->b_ss ? s->b_ss + kPassMax : nullptr;
+    const ZeroSpans clear_qkv{{s->b_q, s->b_k, s->b_v, ss_attn}, {(size_t)M * Q, (size_t)M * KV, (size_t)M * KV, (size_t)M}};
+    const ZeroSpans clear_ffn{{s->b_act, s->b_up, ss_ffn, nullptr}, {(size_t)M * F, (size_t)M * F, (size_t)M, 0}};
+    if (dn && e == hipSuccess) e = launch_zero_spans(clear_qkv, st);
     for (int l = 0; l < (int)md.block_count && e == hipSuccess; l++) {
         const LayerW &L = s->layers[l];
-        // the norm clears the q/k/v rows, which the products then accumulate onto
-        e = launch_rms_norm_rows(s->b_hidden, (const float *)L.attn_norm.p, s->b_normed, M, H, eps, st, s->b_q,
-                                 (size_t)M * Q, s->b_k, (size_t)M * KV, s->b_v, (size_t)M * KV,
-                                 split_in ? &s->xp : nullptr);
-        multi3(L.q, s->b_q, Q, L.k, s->b_k, KV, &L.v, s->b_v, KV, split_in ? &s->xp : nullptr);
+        if (dn) {
+            const RowNorm rn{(const float *)L.attn_norm.p, ss_attn};
+            multi3(L.q, s->b_q, Q, L.k, s->b_k, KV, &L.v, s->b_v, KV, nullptr, false, s->b_hidden, &rn);
+        } else {
+            // the norm clears the q/k/v rows, which the products then accumulate onto
+            e = launch_rms_norm_rows(s->b_hidden, (const float *)L.attn_norm.p, s->b_normed, M, H, eps, st, s->b_q,
+                                     (size_t)M * Q, s->b_k, (size_t)M * KV, s->b_v, (size_t)M * KV,
+                                     split_in ? &s->xp : nullptr);
+            multi3(L.q, s->b_q, Q, L.k, s->b_k, KV, &L.v, s->b_v, KV, split_in ? &s->xp : nullptr);
+        }
         const size_t layer_base = kv_layer_base(s, l);
         if (s->b_counters && e == hipSuccess) {
             AttnParams a{};
@@ -1074,7 +1103,8 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
             a.n_query = M;
             a.q_stride = Q;
             a.out_stride = Q;
-            e = launch_attention_prep(a, s->b_q, st);
+            e = dn ? launch_attention_prep(a, s->b_q, st, RowScale{ss_attn, H, eps}, clear_ffn)
+                   : launch_attention_prep(a, s->b_q, st);
             // plain mode over the stored rows
             a.k_new = a.v_new = nullptr;
             a.out = s->b_attn;
@@ -1125,7 +1155,11 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
         if (split_o && e == hipSuccess) e = launch_split_rows(s->b_attn, Q, M, Q, s->xp, st);
         gemm(L.o, nullptr, s->b_attn, Q, s->b_hidden, H, OUT_ADD, split_o ? &s->xp : nullptr);
         bool down_split = false;
-        if (fused_swiglu && L.gate.type == L.up.type) {
+        if (dn) {
+            const RowNorm rn{(const float *)L.ffn_norm.p, ss_ffn};
+            multi3(L.gate, s->b_act, F, L.up, s->b_up, F, nullptr, nullptr, 0, nullptr, false, s->b_hidden, &rn);
+            if (e == hipSuccess) e = launch_silu_mul_rows(s->b_act, s->b_up, M, F, RowScale{ss_ffn, H, eps}, clear_qkv, st);
+        } else if (fused_swiglu && L.gate.type == L.up.type) {
             if (e == hipSuccess)
                 e = launch_rms_norm_rows(s->b_hidden, (const float *)L.ffn_norm.p, s->b_normed, M, H, eps, st);
             gemm(L.gate, &L.up, s->b_normed, H, s->b_act, F, OUT_SWIGLU);
