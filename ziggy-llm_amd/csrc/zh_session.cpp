@@ -1005,7 +1005,13 @@ static hipError_t pass_enqueue(ZiggyHipSession *s, const uint32_t *tokens, int M
     // fill the chip.  Verify passes (one token
     // tile) keep the split for speed; their sums vary in the last bits.
     const bool det = !output;
-    const int split_add = det ? 1 : 16, split_clear = det ? 2 : 16;
+    // ZIGGY_HIP_VERIFY_SPLIT: the verify pass's largest reduction split (a tuning knob)
+    static const int vsplit = [] {
+        const char *v = getenv("ZIGGY_HIP_VERIFY_SPLIT");
+        const int n = v ? atoi(v) : 16;
+        return n == 1 || n == 2 || n == 4 || n == 8 || n == 16 ? n : 16;
+    }();
+    const int split_add = det ? 1 : vsplit, split_clear = det ? 2 : vsplit;
     auto gemm = [&](const DT &w, const DT *w2, const float *x, int ldx, float *y, int ldy, int out,
                     const XPlanes *xp = nullptr) {
         if (e != hipSuccess) return;
