@@ -369,6 +369,72 @@ def mfma(args) -> None:
     print(text)
 
 
+def sq(args) -> None:
+    """Instruction mix and stall shares per kernel shape from several --pmc runs of one program (each
+    run its own counters; a run's dispatch ids follow the program's launch order, so the runs merge by
+    dispatch id).  Dispatches of one kernel and grid with the same matrix-core instruction count are one
+    shape.  Per wavefront: instructions by type (SQ_INSTS_*); shares of the wavefront's lifetime
+    (SQ_WAVE_CYCLES, in quad cycles like the SQ_ACTIVE_INST_* and SQ_WAIT_* counters): issuing VALU / LDS /
+    any instruction, waiting; matrix-core busy cycles per SIMD over the lifetime; LDS bank-conflict cycles
+    over LDS-active cycles."""
+    runs = [_dispatch_rows(d) for d in args.pmc_dirs]
+    grids = {}
+    for d in args.pmc_dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                grids[r["Dispatch_Id"]] = int(r.get("Grid_Size") or 0)
+    merged: dict[str, dict] = {}
+    for run in runs:
+        for did, d in run.items():
+            m = merged.setdefault(did, {"name": d["name"], "counters": {}})
+            if m["name"] != d["name"]:
+                raise SystemExit(f"dispatch {did} is {m['name']} in one run and {d['name']} in another")
+            m["counters"].update(d["counters"])
+    groups: dict[tuple, list[dict]] = {}
+    for did, d in merged.items():
+        c = d["counters"]
+        if not c.get("SQ_WAVES"):
+            continue
+        key = (d["name"], grids.get(did, 0), int(c.get("SQ_INSTS_MFMA", 0)))
+        groups.setdefault(key, []).append(c)
+    wanted = [n for n in args.kernels.split(",") if n]
+    lines = [f"# {args.title}", "", "Command:", "", f"    {args.command}", "",
+             "One row per kernel shape (kernel, grid in threads, matrix-core instructions). Per wavefront:",
+             "instructions by type; % of the wavefront's lifetime issuing VALU, LDS or any instruction, and",
+             "waiting (SQ_ACTIVE_INST_* and SQ_WAIT_ANY over SQ_WAVE_CYCLES); MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES",
+             "per wavefront over its lifetime in cycles; LDS conflict = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE.",
+             "Medians over the shape's dispatches.", "",
+             "| kernel | grid | launches | VALU | SALU | LDS | MFMA | VMEM rd | % VALU | % LDS | % any | % wait | "
+             "% MFMA busy | % LDS conflict |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    med = statistics.median
+    rows = sorted(groups.items(), key=lambda kv: -sum(c.get("SQ_WAVE_CYCLES", 0.0) for c in kv[1]))
+    for (name, grid, _), cs in rows[: args.top]:
+        if wanted and not any(w in name for w in wanted):
+            continue
+
+        def pw(k):
+            return med([c.get(k, 0.0) / c["SQ_WAVES"] for c in cs])
+
+        def share(k, scale=1.0):
+            v = [scale * c.get(k, 0.0) / c["SQ_WAVE_CYCLES"] for c in cs if c.get("SQ_WAVE_CYCLES")]
+            return 100.0 * med(v) if v else float("nan")
+        conf = [c["SQ_LDS_BANK_CONFLICT"] / c["SQ_LDS_IDX_ACTIVE"] for c in cs if c.get("SQ_LDS_IDX_ACTIVE")]
+        nm = name.split("(")[0].replace("void ", "").replace("|", "/")
+        lines.append(f"| `{nm}` | {grid} | {len(cs)} | {pw('SQ_INSTS_VALU'):.0f} | {pw('SQ_INSTS_SALU'):.0f} | "
+                     f"{pw('SQ_INSTS_LDS'):.0f} | {pw('SQ_INSTS_MFMA'):.0f} | {pw('SQ_INSTS_VMEM_RD'):.0f} | "
+                     f"{share('SQ_ACTIVE_INST_VALU'):.1f} | {share('SQ_ACTIVE_INST_LDS'):.1f} | "
+                     f"{share('SQ_ACTIVE_INST_ANY'):.1f} | {share('SQ_WAIT_ANY'):.1f} | "
+                     f"{share('SQ_VALU_MFMA_BUSY_CYCLES', 0.25):.1f} | "
+                     f"{100 * med(conf) if conf else float('nan'):.1f} |")
+    lines.append("")
+    text = "\n".join(lines)
+    if args.out:
+        with open(args.out, "w") as fh:
+            fh.write(text)
+    print(text)
+
+
 def read_traffic(path: str) -> int | None:
     """traffic_bytes_per_launch from a summary written by `summarize`, or None."""
     try:
@@ -414,8 +480,16 @@ def main(argv=None) -> None:
     t.add_argument("--command", required=True)
     t.add_argument("--top", type=int, default=14)
     t.add_argument("--out")
+    q = sub.add_parser("sq")
+    q.add_argument("pmc_dirs", nargs="+")
+    q.add_argument("--title", required=True)
+    q.add_argument("--command", required=True)
+    q.add_argument("--kernels", default="", help="comma-separated name fragments to keep (default: all)")
+    q.add_argument("--top", type=int, default=16)
+    q.add_argument("--out")
     args = ap.parse_args(argv)
-    {"probe": probe, "gemm-probe": gemm_probe, "summarize": summarize, "reqsize": reqsize, "mfma": mfma, "stats": stats}[args.cmd](args)
+    {"probe": probe, "gemm-probe": gemm_probe, "summarize": summarize, "reqsize": reqsize, "mfma": mfma, "stats": stats,
+     "sq": sq}[args.cmd](args)
 
 
 if __name__ == "__main__":
