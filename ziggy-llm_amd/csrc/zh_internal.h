@@ -261,6 +261,17 @@ constexpr int kMaxMatvecRowLen = 4 * kMaxMatvecCols;  // plain / SiLU rows the w
 // Builds the launch plan (team size, rows per team, workgroup ranges) and launches.
 hipError_t launch_matvec(const MvParams &p, int in_mode, int out_mode, hipStream_t s);
 void plan_matvec(MvParams &p, int target_wgs);
+// An MoE layer's gate/up (NORM, SWIGLU with the routing prologue) and down
+// (PLAIN, STORE) products in one launch (moe_ffn_kernel): gate/up publishes
+// its act rows, the down workgroups find their experts from gu.pro_in's
+// logits and read their act rows as they are published.  Every act word
+// must hold kPollEmpty before the launch; the route writer refills `refill`
+// (refill_n words: the next layer's act rows) for the next launch.
+// poll_err is set when a wait ran out.
+hipError_t launch_moe_ffn(const MvParams &gu, const MvParams &down, int *poll_err, float *refill, int refill_n,
+                          hipStream_t s);
+// whether launch_moe_ffn serves these formats and row lengths
+bool moe_ffn_supported(int f1, int f2, int gate_cols, int down_cols);
 
 hipError_t launch_dequant(int fmt, const uint8_t *w, uint64_t stride, float *out, int rows, int cols,
                           hipStream_t s);

@@ -1,6 +1,8 @@
 // zh_matvec.hip -- host-side planning and dispatch of the batch-1
 // dequant-matvec kernels (templates in zh_mv.h, instantiated by the
 // zh_mv_*.hip files), and the bit-exact dequant kernels.
+#include <utility>
+
 #include "zh_mv.h"
 
 namespace zh {
@@ -161,6 +163,46 @@ static hipError_t launch_matvec_team(const MvParams &p_in, int in, int out, hipS
     // the SWIGLU routing prologue: one more workgroup writes the route
     p.route_wg = out == OUT_SWIGLU && p.pro_in ? grid++ : -1;
     hipLaunchKernelGGL(k, dim3(grid), dim3(kThreads), 0, s, p);
+    return hipGetLastError();
+}
+
+static bool seg_formats(const MvParams &p, int &f1, int &f2) {
+    f1 = p.seg[0].fmt, f2 = f1;
+    for (int i = 1; i < p.nseg; i++)
+        if (p.seg[i].fmt != f1) f2 = p.seg[i].fmt;
+    for (int i = 0; i < p.nseg; i++)
+        if (p.seg[i].fmt != f1 && p.seg[i].fmt != f2) return false;
+    return true;
+}
+
+bool moe_ffn_supported(int f1, int f2, int gate_cols, int down_cols) {
+    return gate_cols <= kMaxMatvecCols && down_cols <= kPollRowMax && pick_moe_ffn(f1, f2, gate_cols, down_cols);
+}
+
+hipError_t launch_moe_ffn(const MvParams &gu, const MvParams &down, int *poll_err, float *refill, int refill_n,
+                          hipStream_t s) {
+    MvParams pg = gu, pd = down;
+    int f1, f2, d1, d2;
+    if (!seg_formats(pg, f1, f2) || !seg_formats(pd, d1, d2) || !poll_err || !pg.pro_in || !pd.pro_in ||
+        pg.expert || pd.expert || (refill_n && !refill))
+        return hipErrorInvalidValue;
+    // the down segments take the gate/up launch's two formats
+    if ((d1 != f1 && d1 != f2) || (d2 != f1 && d2 != f2)) return hipErrorInvalidValue;
+    if (f1 != IQ4_XS) std::swap(f1, f2);
+    const MoeFfnKernel k = pg.cols <= kMaxMatvecCols && pd.cols <= kPollRowMax ? pick_moe_ffn(f1, f2, pg.cols, pd.cols)
+                                                                               : nullptr;
+    if (!k) return hipErrorInvalidValue;
+    // each part planned for the whole chip: the down workgroups wait while
+    // gate/up streams, then stream their own rows
+    const int target = (int)(device_cus() * workgroups_per_cu() + 0.5f);
+    plan_matvec(pg, target);
+    plan_matvec(pd, target);
+    int ng = total_wgs(pg);
+    pg.route_wg = ng++;  // the route writer: the last gate/up workgroup
+    pd.route_wg = -1;
+    const int nd = total_wgs(pd);
+    if (ng <= 0 || nd <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k, dim3(ng + nd), dim3(kThreads), 0, s, pg, pd, ng, MvFuse{poll_err, refill, refill_n});
     return hipGetLastError();
 }
 

@@ -2,6 +2,7 @@
 // weight residency, buffers, and the per-layer launch sequence of zh_moe.hip
 // captured into one HIP graph.
 #include <algorithm>
+#include <cstdlib>
 #include <new>
 #include <vector>
 
@@ -33,6 +34,14 @@ struct ZiggyHipMoeStack {
     bool fuse_combine = false;
     uint32_t *route = nullptr;  // [layers][2k + 2]
     int act_stride = 0, route_stride = 0;
+    // fuse_ffn: each layer's gate/up and down run as one launch
+    // (launch_moe_ffn).  The act rows then come in act_sets sets, layer l
+    // using set l % act_sets, every word kPollEmpty until published; layer l's
+    // launch refills the set of layer l + 1 (cyclically), which differs from
+    // its own: act_sets is the smallest n >= 2 with (layers - 1) % n != 0.
+    bool fuse_ffn = false;
+    int act_sets = 1;
+    int *poll_err = nullptr;
     bool shared = false, shared_gate = false;
     hipGraphExec_t graph = nullptr;
     std::vector<void *> allocs;
@@ -50,6 +59,18 @@ namespace {
 int fail(char *err, size_t err_len, int code, const char *msg) {
     set_err(err, err_len, "%s", msg);
     return code;
+}
+
+// The fused launches' error flag: set when a wait for an act row ran out
+// (the outputs are then not valid); read and cleared after the stream is
+// synchronized.
+int poll_check_moe(ZiggyHipMoeStack *s, char *err, size_t err_len) {
+    if (!s->fuse_ffn) return ZIGGY_HIP_OK;
+    int flag = 0;
+    ZH_TRY(hipMemcpy(&flag, s->poll_err, 4, hipMemcpyDeviceToHost), "MoE poll flag");
+    if (!flag) return ZIGGY_HIP_OK;
+    ZH_TRY(hipMemset(s->poll_err, 0, 4), "MoE poll flag");
+    return fail(err, err_len, ZIGGY_HIP_EXECUTION_FAILED, "an MoE act row never arrived (fused expert launch)");
 }
 
 void free_stack(ZiggyHipMoeStack *s) {
@@ -74,6 +95,11 @@ MvSeg seg_of(const DT &t, float *y) {
     return g;
 }
 
+float *act_of(const ZiggyHipMoeStack *s, int l) {
+    const size_t set = (size_t)((l % (int)s->layers.size()) % s->act_sets);
+    return s->act + set * (s->d.expert_used_count + 1) * (size_t)s->act_stride;
+}
+
 // The hidden state layer l reads (and its gate/up normalises).
 float *hidden_of(const ZiggyHipMoeStack *s, int l) {
     if (!s->fuse_combine) return s->hidden;
@@ -87,6 +113,7 @@ hipError_t enqueue_layer(ZiggyHipMoeStack *s, int l, hipStream_t st) {
     const int H = (int)d.hidden, E = (int)d.expert_count, K = (int)d.expert_used_count, FF = (int)d.expert_ff_length;
     uint32_t *route = s->route + (size_t)l * s->route_stride;
     float *hidden = hidden_of(s, l);
+    float *act = act_of(s, l);
     // router (+ the shared expert's gate row) on the normed hidden state;
     // with fuse_combine, layer l - 1's combine first (its result to `hidden`)
     {
@@ -116,6 +143,50 @@ hipError_t enqueue_layer(ZiggyHipMoeStack *s, int l, hipStream_t st) {
     // after it; more experts take the routing kernel
     const bool route_in_gate_up = E <= kRouteWaveExperts && K <= kRouteMaxK && d.gating_func <= 15;
     hipError_t e = hipSuccess;
+    const uint32_t route_cfg = (uint32_t)E | (uint32_t)K << 16 | d.gating_func << 20 | (d.weights_norm ? 1u : 0u) << 24 |
+                               (s->shared_gate ? 1u : 0u) << 25;
+    if (s->fuse_ffn) {
+        // gate/up and down in one launch: the down workgroups route
+        // themselves and read the act rows as gate/up publishes them
+        MvParams pg{}, pd{};
+        for (int k = 0; k < K; k++) {
+            pg.seg[k] = seg_of(L.gate, act + (size_t)k * s->act_stride);
+            pg.seg[k].rows = FF;
+            pg.seg[k].w2 = L.up.p;
+            pg.seg[k].expert_slot = k;
+            pd.seg[k] = seg_of(L.down, s->tmp + (size_t)k * H);
+            pd.seg[k].rows = H;
+            pd.seg[k].x = act + (size_t)k * s->act_stride;
+            pd.seg[k].expert_slot = k;
+        }
+        pg.nseg = pd.nseg = K;
+        if (s->shared) {
+            pg.seg[K] = seg_of(L.gate_sh, act + (size_t)K * s->act_stride);
+            pg.seg[K].w2 = L.up_sh.p;
+            pd.seg[K] = seg_of(L.down_sh, s->tmp + (size_t)K * H);
+            pd.seg[K].x = act + (size_t)K * s->act_stride;
+            pg.nseg = pd.nseg = K + 1;
+        }
+        pg.cols = H;
+        pg.x = hidden;
+        pg.norm_w = (const float *)L.norm.p;
+        pg.eps = d.rms_norm_eps;
+        pg.rows_per_expert = FF;
+        pg.expert_limit = E;
+        pg.pro_in = s->logits;
+        pg.pro_out = route;
+        pg.pro_cfg = route_cfg;
+        pg.pro_scale = d.weights_scale;
+        pd.cols = FF;
+        pd.rows_per_expert = H;
+        pd.expert_limit = E;
+        pd.pro_in = s->logits;
+        pd.pro_cfg = route_cfg;
+        e = launch_moe_ffn(pg, pd, s->poll_err, act_of(s, l + 1), (K + 1) * s->act_stride, st);
+        if (e != hipSuccess) return e;
+        if (s->fuse_combine && l + 1 < (int)s->layers.size()) return hipSuccess;
+        return launch_moe_combine(hidden, s->tmp, route, H, K, s->shared ? 1 : 0, st);
+    }
     if (!route_in_gate_up) {
         e = launch_moe_route(s->logits, E, K, (int)d.gating_func, (int)d.weights_norm, d.weights_scale,
                              s->shared_gate ? 1 : 0, route, st);
@@ -145,8 +216,7 @@ hipError_t enqueue_layer(ZiggyHipMoeStack *s, int l, hipStream_t st) {
         if (route_in_gate_up) {
             p.pro_in = s->logits;
             p.pro_out = route;
-            p.pro_cfg = (uint32_t)E | (uint32_t)K << 16 | d.gating_func << 20 | (d.weights_norm ? 1u : 0u) << 24 |
-                        (s->shared_gate ? 1u : 0u) << 25;
+            p.pro_cfg = route_cfg;
             p.pro_scale = d.weights_scale;
         } else {
             p.expert = route;
@@ -393,6 +463,20 @@ int ziggy_hip_moe_stack_create(ZiggyHipContext *ctx, const ZiggyHipMoeDesc *desc
     }
     s->act_stride = (int)(FF > SF ? FF : SF);
     s->route_stride = (int)(2 * K + 2);
+    // gate/up and down fused: routing in the gate/up launch, the shared
+    // expert's down rows as long as the routed ones, a served kernel, and
+    // more than one layer (ZIGGY_HIP_MOE_FUSE=0 keeps separate launches)
+    {
+        const char *env = getenv("ZIGGY_HIP_MOE_FUSE");
+        const MoeLayerW &L0 = s->layers[0];
+        s->fuse_ffn = !(env && env[0] == '0') && layer_count >= 2 && E <= (uint64_t)kRouteWaveExperts &&
+                      K <= (uint64_t)kRouteMaxK && (!s->shared || SF == FF) &&
+                      moe_ffn_supported(L0.gate.type, s->shared ? L0.gate_sh.type : L0.gate.type, (int)H, (int)FF);
+        if (s->fuse_ffn) {
+            s->act_sets = 2;
+            while ((layer_count - 1) % s->act_sets == 0) s->act_sets++;
+        }
+    }
     struct {
         void **p;
         size_t bytes;
@@ -400,13 +484,16 @@ int ziggy_hip_moe_stack_create(ZiggyHipContext *ctx, const ZiggyHipMoeDesc *desc
         {(void **)&s->hidden, H * 4},
         {(void **)&s->hidden2, H * 4},
         {(void **)&s->logits, (E + 1) * 4},
-        {(void **)&s->act, (K + 1) * (size_t)s->act_stride * 4},
+        {(void **)&s->act, (size_t)s->act_sets * (K + 1) * (size_t)s->act_stride * 4},
+        {(void **)&s->poll_err, 4},
         {(void **)&s->tmp, (K + 1) * H * 4},
         {(void **)&s->route, (size_t)layer_count * s->route_stride * 4},
     };
     for (auto &r : reqs) {
         e = hipMalloc(r.p, r.bytes);
-        if (e == hipSuccess) e = hipMemsetAsync(*r.p, 0, r.bytes, ctx->stream);
+        // the fused launches' act words start as kPollEmpty (outside any graph)
+        const int fill = r.p == (void **)&s->act && s->fuse_ffn ? 0xFF : 0;
+        if (e == hipSuccess) e = hipMemsetAsync(*r.p, fill, r.bytes, ctx->stream);
         if (e != hipSuccess) {
             free_stack(s);
             return hip_fail(e, "MoE buffer allocation", err, err_len);
@@ -459,6 +546,7 @@ int ziggy_hip_moe_stack_forward(ZiggyHipMoeStack *s, const float *hidden_in, flo
         ZH_TRY(hipMemcpyAsync(r.data(), s->route, r.size() * 4, hipMemcpyDeviceToHost, st), "MoE routing");
     }
     ZH_TRY(hipStreamSynchronize(st), "MoE stack");
+    if (int pe = poll_check_moe(s, err, err_len)) return pe;
     for (size_t l = 0; l < r.size() / s->route_stride; l++)
         for (size_t k = 0; k < K; k++) {
             const uint32_t *e = &r[l * s->route_stride + 2 * k];
@@ -544,6 +632,7 @@ int ziggy_hip_moe_stack_time(ZiggyHipMoeStack *s, uint32_t iterations, uint64_t 
     hipEventDestroy(e0);
     if (e1) hipEventDestroy(e1);
     if (e != hipSuccess) return hip_fail(e, "MoE time", err, err_len);
+    if (int pe = poll_check_moe(s, err, err_len)) return pe;
     *avg_ns = (uint64_t)((double)ms * 1e6 / iterations);
     return ZIGGY_HIP_OK;
 }

@@ -171,6 +171,65 @@ __device__ __forceinline__ void stage_x(XOf_t<F> &xs, int s, bool active, const 
     stage_finish<F, IN>(xs, r, p, T, lds, active);
 }
 
+// Matvec bodies inside one fused launch (moe_ffn_kernel): MV_PUBLISH stores
+// its outputs with device-scope stores, for workgroups of the same launch;
+// MV_POLL finds a routed segment's expert from the router logits itself and
+// reads its input as another workgroup of the launch publishes it, over
+// words that hold kPollEmpty until then.
+enum MvMode : int { MV_PLAIN = 0, MV_PUBLISH = 1, MV_POLL = 2 };
+struct MvFuse {
+    int *poll_err;   // MV_POLL: set when a wait ran out (the launch's outputs are then not valid)
+    float *refill;   // MV_PUBLISH: the route writer refills these words with kPollEmpty
+    int refill_n;
+};
+constexpr long kMvPollSpin = 1L << 18;
+
+__device__ __forceinline__ void store_published(float *y, float v) {
+    __hip_atomic_store(reinterpret_cast<uint32_t *>(y), __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// MV_POLL staging of a plain input row (every team of the workgroup reads
+// the same row): thread 0 watches the row's last word while the other
+// wavefronts wait at the barrier; then the workgroup reads the row once with
+// device-scope loads into LDS, again while any word still holds kPollEmpty
+// (bounded: on expiry the error flag is set and the values are taken as they
+// are), and every lane stages its slot from LDS.  The loads wait for the
+// weight ring issued before them (vmcnt completes in order); the input is
+// not there sooner anyway.
+constexpr int kPollRowMax = 1024;  // values of a polled row (the generic body's rows)
+template <int F>
+__device__ __forceinline__ void stage_x_polled(XOf_t<F> &xs, int s, bool active, const MvParams &p,
+                                               const float *x, int T, float *lds, const MvFuse &fx) {
+    __shared__ __align__(16) float xrow[kPollRowMax];
+    const int n = p.cols;  // a multiple of 64, at most kPollRowMax (checked by the launcher)
+    if (threadIdx.x == 0) {
+        const uint32_t *last = reinterpret_cast<const uint32_t *>(x) + (n - 1);
+        long spin = 0;
+        while (__hip_atomic_load(last, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kPollEmpty && ++spin <= kMvPollSpin)
+            __builtin_amdgcn_s_sleep(2);
+    }
+    __syncthreads();
+    const unsigned long long *x8 = reinterpret_cast<const unsigned long long *>(x);
+    for (long spin = 0;; spin++) {
+        int empty = 0;
+        for (int i = threadIdx.x; i < n / 2; i += kThreads) {
+            const unsigned long long v = __hip_atomic_load(x8 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+            empty |= lo == kPollEmpty || hi == kPollEmpty;
+            xrow[2 * i] = __uint_as_float(lo);
+            xrow[2 * i + 1] = __uint_as_float(hi);
+        }
+        if (!__syncthreads_or(empty)) break;
+        if (spin > kMvPollSpin) {
+            if (threadIdx.x == 0) __hip_atomic_store(fx.poll_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    stage_x<F, IN_PLAIN>(xs, s, active, p, xrow, T, lds);
+}
+
 // Workgroup-cooperative staging for teams of 64 lanes (up to 64 slots; four
 // teams per workgroup share one input vector).  Thread t loads run t of x
 // (x[16t .. 16t + 15], with the norm weights or the up half of the fused
@@ -339,8 +398,10 @@ __device__ __forceinline__ void combine_prologue(const MvParams &p, float *xc, b
     combine_finish<CPT>(ci, p, xc, writer);
 }
 
-template <int F, int IN, int OUT>
-__device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int wg_in_seg, float *lds) {
+template <int F, int IN, int OUT, int MODE = MV_PLAIN>
+__device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int wg_in_seg, float *lds,
+                                        const MvFuse &fx = MvFuse{}) {
+    static_assert(MODE != MV_POLL || IN == IN_PLAIN, "polled inputs are plain rows");
     constexpr int D = ring_depth<F, OUT>();
     const int tid = threadIdx.x, T = p.team, teams = kThreads / T;
     const int team = tid / T, lane = tid % T;
@@ -400,7 +461,11 @@ __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int 
             staged = true;
         }
     }
-    if (!staged) stage_x<F, IN>(xs, lane, active, p, sg.x ? sg.x : p.x, T, lds);
+    if constexpr (MODE == MV_POLL) {
+        stage_x_polled<F>(xs, lane, active, p, sg.x ? sg.x : p.x, T, lds, fx);
+    } else {
+        if (!staged) stage_x<F, IN>(xs, lane, active, p, sg.x ? sg.x : p.x, T, lds);
+    }
 
     float best_v = -INFINITY;
     int best_r = 0x7fffffff;
@@ -426,7 +491,9 @@ __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int 
                     } else if (OUT == OUT_WADD) {
                         sg.y[r] = fmaf(v, wscale, ry[k]);
                     } else if (OUT == OUT_SWIGLU) {
-                        sg.y[r] = (v / (1.0f + expf(-v))) * v2;  // siluInPlace then gate * up
+                        const float a = (v / (1.0f + expf(-v))) * v2;  // siluInPlace then gate * up
+                        if constexpr (MODE == MV_PUBLISH) store_published(&sg.y[r], a);
+                        else sg.y[r] = a;
                     } else if (OUT == OUT_ARGMAX) {
                         if (sg.y) sg.y[r] = v;
                         if (v > best_v || (v == best_v && r < best_r)) {
@@ -465,8 +532,9 @@ __device__ __forceinline__ void mv_body(const MvParams &p, const MvSeg &sg, int 
 // kMaxYB batches per team) are all loaded before the ring, so waiting for
 // them never waits for weight loads (vmcnt completes in order).
 constexpr int kMaxYB = 8;
-template <int F, int IN, int OUT, int TT, int NB>
+template <int F, int IN, int OUT, int TT, int NB, int MODE = MV_PLAIN>
 __device__ __forceinline__ void mv_body_fast(const MvParams &p, const MvSeg &sg, int wg_in_seg, float *lds) {
+    static_assert(MODE != MV_POLL, "polled inputs take the generic body");
     constexpr bool kPair = OUT == OUT_SWIGLU;
     constexpr int B = kPair ? 2 : 4;  // ring slots per batch: rows (or gate/up row pairs)
     constexpr int D = NB * B;         // ring slots
@@ -570,7 +638,11 @@ __device__ __forceinline__ void mv_body_fast(const MvParams &p, const MvSeg &sg,
                 const float up = dpp_mov<0xF5>(c);  // quad_perm [1,1,3,3]: the up half next to its gate
                 const int k = l4 >> 1;
                 const int r = r0 + (ib + k) * teams;
-                if (lane < 4 && !(l4 & 1) && ib + k < n && r < r_end) sg.y[r] = (c / (1.0f + expf(-c))) * up;
+                if (lane < 4 && !(l4 & 1) && ib + k < n && r < r_end) {
+                    const float a = (c / (1.0f + expf(-c))) * up;
+                    if constexpr (MODE == MV_PUBLISH) store_published(&sg.y[r], a);
+                    else sg.y[r] = a;
+                }
             } else {
                 const int r = r0 + (ib + l4) * teams;
                 if (lane < 4 && ib + l4 < n && r < r_end) {
@@ -610,24 +682,24 @@ __device__ __forceinline__ void mv_body_fast(const MvParams &p, const MvSeg &sg,
     }
 }
 
-template <int F, int IN, int OUT, int TT, int NB>
-__device__ __forceinline__ void mv_dispatch(const MvParams &p, const MvSeg &sg, int wg_in_seg, float *lds) {
+template <int F, int IN, int OUT, int TT, int NB, int MODE = MV_PLAIN>
+__device__ __forceinline__ void mv_dispatch(const MvParams &p, const MvSeg &sg, int wg_in_seg, float *lds,
+                                            const MvFuse &fx) {
     if constexpr (TT != 0)
-        mv_body_fast<F, IN, OUT, TT, NB>(p, sg, wg_in_seg, lds);
+        mv_body_fast<F, IN, OUT, TT, NB, MODE>(p, sg, wg_in_seg, lds);
     else
-        mv_body<F, IN, OUT>(p, sg, wg_in_seg, lds);
+        mv_body<F, IN, OUT, MODE>(p, sg, wg_in_seg, lds, fx);
 }
 
 // TT: compile-time team width (64 or 256) of the fast path, 0 for any width;
-// NB: batches of four values in the fast path's load ring.
-template <int F1, int F2, int IN, int OUT, int TT, int NB>
-__global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
-    __shared__ float lds[36];
+// NB: batches of four values in the fast path's load ring.  wg: the
+// workgroup's index in this matvec's grid.
+template <int F1, int F2, int IN, int OUT, int TT, int NB, int MODE = MV_PLAIN>
+__device__ __forceinline__ void mv_run(const MvParams &p, int wg, float *lds, const MvFuse &fx) {
     touch_params(p);  // the segment search, the segment's fields, the inputs' addresses
     // only the output head is gated (prompt steps skip it): the other
     // kernels do not wait for the flag's loads before issuing their own
     if (OUT == OUT_ARGMAX && p.gate_flag && *p.gate_flag == 0) return;
-    const int wg = blockIdx.x;
     int si = 0;
 #pragma unroll
     for (int i = 1; i < kMaxSeg; i++)
@@ -635,17 +707,22 @@ __global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
     // a copy: every field of the segment is read in one batch of scalar
     // loads, not one dependent round trip per use
     MvSeg sg = p.seg[si];
-    if constexpr (OUT == OUT_SWIGLU) {
+    if constexpr (OUT == OUT_SWIGLU || MODE == MV_POLL) {
         if (p.pro_in) {  // uniform over the workgroup
             const uint32_t c = p.pro_cfg;
             const int E = (int)(c & 0xFFFF), gating = (int)(c >> 20 & 0xF);
-            if (wg == p.route_wg) {
+            if (OUT == OUT_SWIGLU && wg == p.route_wg) {
                 // the route writer (a workgroup of its own, no rows): the
                 // whole route, weights and shared gate included, to pro_out
                 if (threadIdx.x < 64) {
                     uint32_t *out = static_cast<uint32_t *>(p.pro_out);
                     route_wave(p.pro_in, E, (int)(c >> 16 & 0xF), gating, (int)(c >> 24 & 1), p.pro_scale,
                                (int)(c >> 25 & 1), [&](int i, uint32_t v) { out[i] = v; });
+                }
+                if constexpr (MODE == MV_PUBLISH) {
+                    // the other set of published words, for the next launch (its
+                    // start orders these stores before its loads)
+                    for (int i = threadIdx.x; i < fx.refill_n; i += kThreads) fx.refill[i] = __uint_as_float(kPollEmpty);
                 }
                 return;
             }
@@ -673,9 +750,31 @@ __global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
         }
     }
     if (F1 == F2 || sg.fmt == F1)
-        mv_dispatch<F1, IN, OUT, TT, NB>(p, sg, wg - sg.wg_begin, lds);
+        mv_dispatch<F1, IN, OUT, TT, NB, MODE>(p, sg, wg - sg.wg_begin, lds, fx);
     else
-        mv_dispatch<F2, IN, OUT, TT, NB>(p, sg, wg - sg.wg_begin, lds);
+        mv_dispatch<F2, IN, OUT, TT, NB, MODE>(p, sg, wg - sg.wg_begin, lds, fx);
+}
+
+template <int F1, int F2, int IN, int OUT, int TT, int NB>
+__global__ void __launch_bounds__(kThreads) mv_kernel(MvParams p) {
+    __shared__ float lds[36];
+    mv_run<F1, F2, IN, OUT, TT, NB>(p, blockIdx.x, lds, MvFuse{});
+}
+
+// An MoE layer's routed and shared expert FFNs in one launch: workgroups
+// [0, n_gu) run the gate/up product (fused RMSNorm, routing, SwiGLU;
+// MV_PUBLISH: its act rows with device-scope stores), the rest the down
+// products (MV_POLL: each routed wavefront finds its expert, issues its
+// weight loads, then reads its act row as the gate/up workgroups publish
+// it).  The gate/up workgroups come first in dispatch order, so no
+// workgroup waits for one that is not yet resident.
+template <int F1, int F2, int TTG>
+__global__ void __launch_bounds__(kThreads) moe_ffn_kernel(MvParams pg, MvParams pd, int n_gu, MvFuse fx) {
+    __shared__ float lds[36];
+    if ((int)blockIdx.x < n_gu)
+        mv_run<F1, F2, IN_NORM, OUT_SWIGLU, TTG, 1, MV_PUBLISH>(pg, blockIdx.x, lds, fx);
+    else
+        mv_run<F1, F2, IN_PLAIN, OUT_STORE, 0, 1, MV_POLL>(pd, (int)blockIdx.x - n_gu, lds, fx);
 }
 
 // Team width of a row of `cols` values: next power of two of the slot count,
@@ -762,5 +861,7 @@ MvKernel pick_mv_q8_0(int in, int out, int cols, int rows_per_team);
 MvKernel pick_mv_other(int fmt, int in, int out, int cols, int rows_per_team);
 MvKernel pick_mv_mixed(int f1, int f2, int cols, int rows_per_team);
 MvKernel pick_mv_moe(int f1, int f2, int in, int out, int cols);
+typedef void (*MoeFfnKernel)(MvParams, MvParams, int, MvFuse);
+MoeFfnKernel pick_moe_ffn(int f1, int f2, int gate_cols, int down_cols);
 
 }  // namespace zh

@@ -14,6 +14,19 @@ MvKernel pick_mv_other(int fmt, int in, int out, int cols, int n) {
     }
 }
 
+// the fused gate/up + down launch: routed IQ4_XS experts (with a Q3_K or
+// IQ4_XS shared expert); the polled down body is the generic one (rows of
+// fewer than 1024 values), gate/up the fast path of one wavefront per row or
+// the generic one
+MoeFfnKernel pick_moe_ffn(int f1, int f2, int gate_cols, int down_cols) {
+    if (f1 != IQ4_XS || team_width(down_cols) >= 64) return nullptr;
+    const int tg = team_width(gate_cols);
+    if (tg > 64) return nullptr;
+    if (f2 == Q3_K) return tg == 64 ? moe_ffn_kernel<IQ4_XS, Q3_K, 64> : moe_ffn_kernel<IQ4_XS, Q3_K, 0>;
+    if (f2 == IQ4_XS) return tg == 64 ? moe_ffn_kernel<IQ4_XS, IQ4_XS, 64> : moe_ffn_kernel<IQ4_XS, IQ4_XS, 0>;
+    return nullptr;
+}
+
 MvKernel pick_mv_moe(int f1, int f2, int in, int out, int cols) {
     if (f1 == IQ4_XS && f2 == Q3_K) {
         if (in == IN_NORM && out == OUT_SWIGLU) return pick_two<IQ4_XS, Q3_K, IN_NORM, OUT_SWIGLU>(cols);
