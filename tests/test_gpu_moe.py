@@ -117,6 +117,34 @@ def test_moe_stack_router_ties(hip_ctx, name):
     check_prefill(spec, layers, xs, pgot, psel, pw)
 
 
+@pytest.mark.parametrize("n_layers", [2, 5, 7])
+def test_moe_fused_ffn_matches_separate_launches(hip_ctx, monkeypatch, n_layers):
+    # The fused gate/up + down launch (down workgroups read each act row as gate/up publishes it)
+    # against ZIGGY_HIP_MOE_FUSE=0's separate launches: the same arithmetic on the same rows, so the
+    # same bits.  2, 5 and 7 layers take 2, 3 and 4 act-row sets; timed replays in between leave
+    # the sets re-armed for the next forward.
+    spec = synth.MoeSpec("small-moe-fuse", n_layers, 256, 16, 4, 256, 256)
+    say(f"moe fused vs separate: {n_layers} layers")
+    layers = synth.build_moe_stack(spec, seed=23)
+    x = synth.normal_row(6, 0, spec.hidden, 0.0, 1.0)
+    monkeypatch.setenv("ZIGGY_HIP_MOE_FUSE", "0")
+    sep = hip.MoeStack(hip_ctx, synth.moe_desc(spec), layers)
+    want, want_sel, want_w = sep.forward(x)
+    sep.close()
+    monkeypatch.delenv("ZIGGY_HIP_MOE_FUSE")
+    st = hip.MoeStack(hip_ctx, synth.moe_desc(spec), layers)
+    got, sel, w = st.forward(x)
+    assert st.time(3) > 0
+    got2, sel2, w2 = st.forward(x)
+    st.close()
+    for g, s, ww in ((got, sel, w), (got2, sel2, w2)):
+        assert np.array_equal(s, want_sel)
+        assert np.array_equal(ww, want_w)
+        assert np.array_equal(g, want)
+    ref, ref_sel, _ = oracle_stack(spec, layers, x)
+    assert np.array_equal(sel, ref_sel) and rel_l2(got, ref) < 1e-4
+
+
 def test_moe_stack_rejects_bad_shapes(hip_ctx):
     spec = synth.small_moe_spec(1)
     layers = synth.build_moe_stack(spec, seed=1)
