@@ -23,7 +23,13 @@ Also reported, on the same JSON line:
                    (profiles/decode_kernels_llama8b_4k_hbm_traffic.md), else null;
   cpu_baseline  -- the CPU oracle (a C restatement of the reference's CPU
                    decode path, same threads policy: 1 + min(11, ncpu - 1))
-                   decoding the same model at the same context on host cores.
+                   decoding the same model at the same context on host cores;
+  other_configs -- the other BASELINE configs in the same run (skip with
+                   --no-other-configs): TinyLlama decode of 128 tokens after a
+                   32-token prompt; the matvec microbench (Q4_K, Q6_K, Q8_0 at
+                   its four shapes); Qwen3-8B Q8_0 decode of 128 tokens at 16k
+                   context and its verify step (1 + 8 drafts); the 40-layer MoE
+                   stack's decode and 512-row prefill.
 """
 import argparse
 import json
@@ -65,6 +71,108 @@ def cpu_step_budget(ctx_len, pos0):
     return max(0, min(CPU_MAX_STEPS, ctx_len - pos0))
 
 
+def verify_passes(sess, cur, ms_per_step, spec, passes=3):
+    """Config 4's speculative-verify step: the pending token and 8 drafts in one batched pass on the
+    matrix cores, against the 9 decode steps it replaces.  The drafts are the stream's own next tokens
+    (decoded one step at a time with their top-2 logits, then the position rewound), so all are
+    accepted.  The pass adds its products in another order than the decode step, so a prediction may
+    differ from the decoded draft only where the decode step's top-2 logits are within a near-tie
+    margin; any other difference fails the bench.  The median of `passes` passes is reported."""
+    times, mismatches, accepted = [], 0, []
+    for _ in range(passes):
+        p0 = sess.position
+        drafts, margins, t = [], [], cur
+        for _ in range(8):
+            ids, lg = sess.step_shortlist(t, 2)
+            drafts.append(int(ids[0]))
+            margins.append((float(lg[0]) - float(lg[1]), float(abs(lg[0]))))
+            t = int(ids[0])
+        sess.rewind(p0)
+        t1 = time.perf_counter()
+        pred, n = sess.verify(cur, drafts)
+        times.append(time.perf_counter() - t1)
+        for j, (a, b) in enumerate(zip(pred[:8], drafts)):
+            if int(a) != int(b):
+                mismatches += 1
+                gap, mag = margins[j]
+                if gap > VERIFY_TIE_ABS + VERIFY_TIE_REL * mag:
+                    raise SystemExit(f"verify pass: prediction {j} is {int(a)}, the decode step's is {b} "
+                                     f"with a top-2 margin of {gap:.3g} (not a near-tie)")
+        accepted.append(int(n))
+        cur = int(pred[n - 1])
+    tv = sorted(times)[len(times) // 2]
+    # the pass reads every weight once (the output head included) for its 9 rows
+    wbytes = spec.weight_bytes_per_token()
+    log(f"verify (1 + 8 drafts, MFMA GEMMs): {1e3 * tv:.3f} ms vs {9 * ms_per_step:.3f} ms for 9 decode steps")
+    return {"tokens": 9, "drafts": 8, "ms": round(1e3 * tv, 3), "accepted": accepted,
+            "prediction_mismatches": mismatches, "tok_s_equiv": round(9 / tv, 1),
+            "decode_ms_for_9": round(9 * ms_per_step, 3),
+            "weight_bytes": wbytes, "weights_hbm_fraction": round(wbytes / tv / (HBM_PEAK_GBS * 1e9), 4)}
+
+
+def decode_measure(model, prompt_len, steps, seed, warmup=4, verify=False):
+    """A decode run of config 1 (tinyllama) or 4 (qwen3) for the headline line's other_configs: the
+    prompt in batched passes, `warmup` untimed steps, `steps` timed greedy steps (one graph replay
+    each), and for config 4 the speculative-verify passes (verify_passes)."""
+    import numpy as np
+
+    from zhip import hip, synth
+
+    ctx_len = prompt_len + warmup + 1 + steps + 1 + (3 * 9 + 8 if verify else 0) + 8
+    spec = {"tinyllama": synth.tinyllama_spec, "qwen3": synth.qwen3_8b_spec}[model](context=ctx_len)
+    t0 = time.time()
+    img = synth.build(spec, seed=seed)
+    ctx = hip.Context(0)
+    sess = hip.Session(ctx, img, context=ctx_len)
+    prompt = synth.prompt_tokens(seed, prompt_len, spec.vocab)
+    _, wst = sess.generate(prompt, warmup)
+    _, st = sess.generate(np.array([wst.next_token], np.uint32), steps)
+    wall_s = st.wall_ns / 1e9
+    tok_s, ms = steps / wall_s, 1e3 * wall_s / steps
+    pos0 = prompt_len + warmup + 1
+    bpt = spec.weight_bytes_per_token() + spec.kv_bytes_per_token(int(round(pos0 + (steps - 1) / 2.0)))
+    frac = bpt * tok_s / (HBM_PEAK_GBS * 1e9)
+    out = {"workload": f"{spec.name} greedy decode, batch 1, positions {pos0}-{pos0 + steps - 1} after a "
+                       f"{prompt_len}-token prompt",
+           "tok_s": round(tok_s, 3), "ms_per_step": round(ms, 4), "hbm_fraction": round(frac, 4),
+           "bytes_per_token": bpt, "prompt_ms": round(wst.prompt_ns / 1e6, 3)}
+    log(f"{spec.name}: {tok_s:.1f} tok/s ({ms:.3f} ms/step) at positions {pos0}-{pos0 + steps - 1}, "
+        f"{100 * frac:.1f}% of HBM peak ({time.time() - t0:.1f}s with the build)")
+    if verify:
+        out["verify"] = verify_passes(sess, int(st.next_token), ms, spec)
+    sess.close()
+    ctx.close()
+    return out
+
+
+def matvec_measure(iters):
+    """Config 2: the dequant-matvec microbench (zhip.microbench) over its formats and shapes."""
+    from zhip import hip, microbench
+
+    ctx = hip.Context(0)
+    res = []
+    for name, fmt in microbench.FORMATS.items():
+        for rows, cols in microbench.SHAPES:
+            r = microbench.run(ctx, fmt, rows, cols, iters)
+            res.append({k: r[k] for k in ("format", "rows", "cols", "avg_us", "gbs", "frac_of_peak")})
+    ctx.close()
+    log("matvec microbench: " + ", ".join(f"{r['format']} {r['rows']}x{r['cols']} {r['gbs']:.0f} GB/s" for r in res))
+    return res
+
+
+def other_configs(args):
+    """The other BASELINE configs, measured in the same run at their own workloads (shorter samples
+    than their own --model lines): 1 TinyLlama decode, 2 the matvec microbench, 4 Qwen3-8B decode at
+    16k plus the verify step, 5 the MoE stack's decode and 512-row prefill."""
+    out = {"config1_tinyllama": decode_measure("tinyllama", 32, 128, args.seed),
+           "config2_matvec": matvec_measure(64),
+           "config4_qwen3_16k": decode_measure("qwen3", 16384, 128, args.seed, verify=True)}
+    _, _, dec, prefill = moe_measure(args.seed, 64, 4)
+    out["config5_moe"] = {"workload": "qwen3.5-moe-ffn-stack, 40 layers, batch-1 decode and a 512-row prefill",
+                          "decode": dec, "prefill": prefill}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -82,6 +190,8 @@ def main():
                     help="after the timed decode, this many more steps with every launch timed by HIP events "
                          "under the reference's profile categories (its --metal-profile report)")
     ap.add_argument("--profile-out", default=None, help="file for the profile summary (default: stderr)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the other BASELINE configs the headline run also measures (other_configs)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -165,43 +275,7 @@ def main():
 
     verify = None
     if args.model == "qwen3":
-        # config 4's speculative-verify step: the pending token and 8 drafts in one batched pass on the
-        # matrix cores, against the 9 decode steps it replaces.  The drafts are the stream's own next
-        # tokens (decoded one step at a time with their top-2 logits, then the position rewound), so all
-        # are accepted.  The pass adds its products in another order than the decode step, so a
-        # prediction may differ from the decoded draft only where the decode step's top-2 logits are
-        # within a near-tie margin; any other difference fails the bench.
-        times, mismatches, accepted = [], 0, []
-        cur = next_tok
-        for _ in range(3):
-            p0 = sess.position
-            drafts, margins, t = [], [], cur
-            for _ in range(8):
-                ids, lg = sess.step_shortlist(t, 2)
-                drafts.append(int(ids[0]))
-                margins.append((float(lg[0]) - float(lg[1]), float(abs(lg[0]))))
-                t = int(ids[0])
-            sess.rewind(p0)
-            t1 = time.perf_counter()
-            pred, n = sess.verify(cur, drafts)
-            times.append(time.perf_counter() - t1)
-            for j, (a, b) in enumerate(zip(pred[:8], drafts)):
-                if int(a) != int(b):
-                    mismatches += 1
-                    gap, mag = margins[j]
-                    if gap > VERIFY_TIE_ABS + VERIFY_TIE_REL * mag:
-                        raise SystemExit(f"verify pass: prediction {j} is {int(a)}, the decode step's is {b} "
-                                         f"with a top-2 margin of {gap:.3g} (not a near-tie)")
-            accepted.append(int(n))
-            cur = int(pred[n - 1])
-        tv = sorted(times)[1]
-        # the pass reads every weight once (the output head included) for its 9 rows
-        wbytes = spec.weight_bytes_per_token()
-        verify = {"tokens": 9, "drafts": 8, "ms": round(1e3 * tv, 3), "accepted": accepted,
-                  "prediction_mismatches": mismatches, "tok_s_equiv": round(9 / tv, 1),
-                  "decode_ms_for_9": round(9 * ms_per_step, 3),
-                  "weight_bytes": wbytes, "weights_hbm_fraction": round(wbytes / tv / (HBM_PEAK_GBS * 1e9), 4)}
-        log(f"verify (1 + 8 drafts, MFMA GEMMs): {1e3 * tv:.3f} ms vs {9 * ms_per_step:.3f} ms for 9 decode steps")
+        verify = verify_passes(sess, next_tok, ms_per_step, spec)
 
     kernels = {}
     for name in ("qkv", "attention", "o_proj", "gate_up", "down", "output"):
@@ -221,6 +295,10 @@ def main():
                 "bytes_per_launch": dom["bytes"], "avg_launch_us": dom["avg_us"]}
     sess.close()
     ctx.close()
+
+    others = None
+    if args.model == "llama8b" and not args.no_other_configs:
+        others = other_configs(args)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -282,28 +360,30 @@ def main():
         "cold": cold,
         "profile": profile,
         "tokens_head": [int(t) for t in toks[:8]],
+        "other_configs": others,
     }
     print(json.dumps(line), flush=True)
 
 
-def bench_moe(args):
+def moe_measure(seed, steps, warmup):
     """Config 5: 40 Qwen3.5-MoE-style sparse FFN layers (hidden 2048, 256 IQ4_XS experts of FFN 512, top-8
     softmax routing, a Q3_K shared expert with a sigmoid gate) at batch-1 decode.  A step is one token's
-    hidden state through the whole stack (one graph replay); weights resident in HBM."""
+    hidden state through the whole stack (one graph replay); weights resident in HBM.  Also the
+    512-row prefill.  Returns the spec, the layers (host copies) and the decode and prefill figures."""
     import numpy as np
 
     from zhip import hip, synth
 
     spec = synth.moe_config5_spec(40)
     t0 = time.time()
-    layers = synth.build_moe_stack(spec, seed=args.seed)
+    layers = synth.build_moe_stack(spec, seed=seed)
     log(f"built {spec.name}: {spec.n_layers} layers in {time.time() - t0:.1f}s")
     ctx = hip.Context(0)
     st = hip.MoeStack(ctx, synth.moe_desc(spec), layers)
-    x = synth.normal_row(args.seed, 0, spec.hidden, 0.0, 1.0)
-    for _ in range(max(1, args.warmup)):
+    x = synth.normal_row(seed, 0, spec.hidden, 0.0, 1.0)
+    for _ in range(max(1, warmup)):
         x, _, _ = st.forward(x)
-    ns = st.time(args.steps)
+    ns = st.time(steps)
     tok_s = 1e9 / ns
     bpt = spec.weight_bytes_per_token()
     frac = bpt * tok_s / (HBM_PEAK_GBS * 1e9)
@@ -311,9 +391,9 @@ def bench_moe(args):
         f"{100 * frac:.1f}% of HBM peak")
     # the 512-token prefill: rows grouped by routed expert per layer, expert GEMMs on the matrix cores
     ptok = 512
-    xs = np.stack([synth.normal_row(args.seed + 1, t, spec.hidden, 0.0, 1.0) for t in range(ptok)])
+    xs = np.stack([synth.normal_row(seed + 1, t, spec.hidden, 0.0, 1.0) for t in range(ptok)])
     _, psel, _ = st.prefill(xs)
-    pns = st.time_prefill(ptok, max(1, min(args.steps, 8)))
+    pns = st.time_prefill(ptok, max(1, min(steps, 8)))
     touched = float(np.mean([len(np.unique(psel[:, l, :])) for l in range(spec.n_layers)]))
     pbytes = spec.weight_bytes_all()
     pflops = spec.flops_per_token() * ptok
@@ -327,6 +407,19 @@ def bench_moe(args):
         f"{prefill['tflops']} TFLOP/s")
     st.close()
     ctx.close()
+    decode = {"tok_s": round(tok_s, 3), "ms_per_step": round(ns / 1e6, 4), "hbm_fraction": round(frac, 4),
+              "bytes_per_token": bpt}
+    return spec, layers, decode, prefill
+
+
+def bench_moe(args):
+    """Config 5 as the bench's own line (--model moe), with its CPU baseline."""
+    import numpy as np
+
+    from zhip import synth
+
+    spec, layers, dec, prefill = moe_measure(args.seed, args.steps, args.warmup)
+    tok_s, ns, bpt, frac = dec["tok_s"], dec["ms_per_step"] * 1e6, dec["bytes_per_token"], dec["hbm_fraction"]
     cpu = None
     if not args.no_cpu_baseline:
         # the oracle's MoE path (computeMoeFfn restated, zo_moe_ffn), layer by layer, with the
@@ -359,11 +452,11 @@ def bench_moe(args):
         log(f"cpu baseline: {cpu['value']} tok/s over {n} tokens ({t_cpu:.1f}s)")
     line = {
         "metric": "MoE FFN stack decode tok/s + % of HBM roofline, 40 x (256 IQ4_XS experts top-8 + Q3_K shared)",
-        "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "value": tok_s, "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ns / 1e6, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"{spec.name}, {spec.n_layers} layers, batch 1", "batch": 1, "parallelism": "none"},
-        "hbm_fraction": round(frac, 4), "bytes_per_token": bpt, "cpu_baseline": cpu, "prefill": prefill,
+        "hbm_fraction": frac, "bytes_per_token": bpt, "cpu_baseline": cpu, "prefill": prefill,
     }
     print(json.dumps(line), flush=True)
 
