@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "zh_internal.h"
+#include "zh_mv.h"
 #include "zh_quant.h"
 
 namespace zh {
@@ -308,6 +309,22 @@ __device__ __forceinline__ void poll_reset_slot(const AttnParams &p, int kvh, in
     const uint4 empty = make_uint4(kPollEmpty, kPollEmpty, kPollEmpty, kPollEmpty);
     for (int i = threadIdx.x; i < VS * HD / 4; i += 256) o[i] = empty;
     if (threadIdx.x < VS) reinterpret_cast<uint2 *>(p.reset_ml)[e + threadIdx.x] = make_uint2(kPollEmpty, kPollEmpty);
+}
+
+// PQ: this workgroup's slice (split of max_splits) of kv head kvh's words of
+// the next launch's q, k and v ([q: head_count HD][k: kv_dim][v: kv_dim]
+// from qkv_refill) back to kPollEmpty.
+template <int HD>
+__device__ __forceinline__ void qkv_reset_slice(const AttnParams &p, int kvh, int split, int nq) {
+    const int per_head = nq + 2 * HD, per = (per_head + p.max_splits - 1) / p.max_splits;
+    const int lo = split * per, hi = min(lo + per, per_head);
+    const size_t Q = (size_t)p.head_count * HD, KV = (size_t)p.head_count_kv * HD;
+    for (int i = lo + (int)threadIdx.x; i < hi; i += 256) {
+        const size_t o = i < nq        ? (size_t)kvh * nq + i
+                         : i < nq + HD ? Q + (size_t)kvh * HD + (i - nq)
+                                       : Q + KV + (size_t)kvh * HD + (i - nq - HD);
+        p.qkv_refill[o] = __uint_as_float(kPollEmpty);
+    }
 }
 
 __device__ __forceinline__ bool poll_empty(unsigned long long v) {
@@ -753,8 +770,16 @@ __device__ __forceinline__ h8v as_h8(uint4 v) {
 // its own position; splits cover the range of the last query.  A wavefront
 // holds two 16-column query tiles (virtual heads 0-7 and 8-15) against the
 // same K/V registers, so the K/V range is read once per 16 virtual heads.
-template <int HD, int GG, bool MQ>
-__global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
+// PQ (single query, fused mode): the projection's q, k and v come from
+// workgroups of the same launch (qkv_attn_kernel) with device-scope stores
+// over words that hold kPollEmpty until then.  They are read after the K and
+// V tile loads are issued, again while any word of the head's still holds
+// kPollEmpty (bounded: on expiry the error flag is set and the values are
+// taken as they are); each workgroup then refills its slice of the next
+// launch's q/k/v words (qkv_refill) with kPollEmpty.
+template <int HD, int GG, bool MQ, bool PQ = false>
+__device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int split, const int kvh, const int qz) {
+    static_assert(!PQ || !MQ, "polled q/k/v: single query");
     constexpr int KS = HD / 32;  // 32-dim steps of the scores, 32-dim chunks of the values
     constexpr int TP = 32;       // positions per wavefront tile
     constexpr int QS = HD + 8;   // padded row of the query pieces (binary16)
@@ -763,12 +788,12 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     constexpr int VG = kMaxGroup * NT;  // (virtual) heads per workgroup at most
     static_assert(!MQ || VG == kMultiHeads, "multi-query partials are sized by kMultiHeads");
     touch_params(p);
-    const int split = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, li = lane & 15, lg = lane >> 4;
     const int Gq = GG ? GG : p.head_count / p.head_count_kv;  // query heads per kv head
-    const int qpw = MQ ? VG / Gq : 1, qbase = MQ ? blockIdx.z * qpw : 0;
+    const int qpw = MQ ? VG / Gq : 1, qbase = MQ ? qz * qpw : 0;
     const int nqw = MQ ? min(qpw, p.n_query - qbase) : 1;
-    const int slot = MQ ? kvh + p.head_count_kv * blockIdx.z : kvh;  // partials / arrival counter
+    const int slot = MQ ? kvh + p.head_count_kv * qz : kvh;  // partials / arrival counter
     const int G = MQ ? nqw * Gq : Gq;                                  // (virtual) heads of the workgroup
     const bool fused = !MQ && p.k_new != nullptr;
     const size_t kv_off = (size_t)kvh * HD;
@@ -797,15 +822,17 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
                 const int gv = idx / HD, j = gv / Gq;
                 qv[i] = p.q[(size_t)(qbase + j) * p.q_stride + (size_t)(kvh * Gq + gv - j * Gq) * HD + idx % HD];
             } else {
-                qv[i] = p.q[(size_t)kvh * nq + idx];
+                if constexpr (!PQ) qv[i] = p.q[(size_t)kvh * nq + idx];  // PQ: polled below
                 qb[i] = qbp[(size_t)kvh * nq + idx];
             }
         }
         // plain mode reads q in place of the absent k / v and ignores it
         const float *knp = fused ? p.k_new : p.q, *vnp = fused ? p.v_new : p.q;
         const float *kbp = fused && p.k_bias ? p.k_bias : p.q, *vbp = fused && p.v_bias ? p.v_bias : p.q;
-        kx[0] = knp[kv_off + tid % HD];
-        vx = vnp[kv_off + tid % HD];
+        if constexpr (!PQ) {
+            kx[0] = knp[kv_off + tid % HD];
+            vx = vnp[kv_off + tid % HD];
+        }
         kb = kbp[kv_off + tid % HD];
         vb = vbp[kv_off + tid % HD];
     }
@@ -834,6 +861,7 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     // (at the end: stores ahead of the K loads would delay them)
     auto refill_other = [&]() {
         if (polled) poll_reset_slot<HD, VG>(p, kvh, split);
+        if constexpr (PQ) qkv_reset_slice<HD>(p, kvh, split, nq);
     };
     if (split >= nsplit) {
         refill_other();
@@ -909,6 +937,33 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     uint4 vr[2][8];
     load_k(0, kr[0]);
     load_k(1, kr[1]);
+    if constexpr (PQ) {
+        // this head's q, k and v as the projection workgroups store them
+        const uint32_t *qw = reinterpret_cast<const uint32_t *>(p.q) + (size_t)kvh * nq;
+        const uint32_t *kw = reinterpret_cast<const uint32_t *>(p.k_new) + kv_off + tid % HD;
+        const uint32_t *vw = reinterpret_cast<const uint32_t *>(p.v_new) + kv_off + tid % HD;
+        for (long spin = 0;; spin++) {
+            bool empty = false;
+#pragma unroll
+            for (int i = 0; i < QV; i++) {
+                const uint32_t u = __hip_atomic_load(qw + min(tid + 256 * i, nq - 1), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                qv[i] = __uint_as_float(u);
+                empty = empty || u == kPollEmpty;
+            }
+            const uint32_t uk = __hip_atomic_load(kw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t uv = __hip_atomic_load(vw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            kx[0] = __uint_as_float(uk);
+            vx = __uint_as_float(uv);
+            empty = empty || uk == kPollEmpty || uv == kPollEmpty;
+            if (!__syncthreads_or(empty)) break;
+            if (spin > kPollSpin) {
+                if (tid == 0) __hip_atomic_store(p.poll_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
     const float rden = fused ? rope_den_finish(rden_raw, n_rot_f, p.rope_base, p.rope_denom) : 1.f;
     // the projection biases (the bias reads above are dummies when absent)
     if (fused) {
@@ -1194,6 +1249,11 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
     split_merge<HD, (GG && !MQ) ? GG : VG, decltype(out_of), VG, 256 / VG>(p, slot, G, nsplit, &last_s, out_of);
 }
 
+template <int HD, int GG, bool MQ>
+__global__ void __launch_bounds__(256) attn_mfma_kernel(AttnParams p) {
+    attn_mfma_body<HD, GG, MQ>(p, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
 size_t attention_scratch_floats(int head_count, int head_dim, int max_splits) {
     // part_o + part_ml for up to `head_count` kv heads
     return (size_t)head_count * max_splits * kMaxGroup * (head_dim + 2);
@@ -1401,6 +1461,73 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
     case 256: go(std::integral_constant<int, 256>{}); break;
     default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+
+// ---- the q/k/v projection and the attention in one launch ----
+// Workgroups [0, n_qkv) run the fused RMSNorm + q/k/v matvec (teams of 64,
+// device-scope stores), the rest the single-query attention (PQ: K loads
+// first, then the head's q/k/v as they land).  Launch bounds of two
+// workgroups per CU, so a projection and an attention workgroup share a CU;
+// the projection workgroups come first in dispatch order, so no workgroup
+// waits for one that is not yet resident.
+template <int F1, int F2, int HD, int GG>
+__global__ void __launch_bounds__(256, 2) qkv_attn_kernel(MvParams pq, AttnParams pa, int n_qkv) {
+    if ((int)blockIdx.x < n_qkv) {
+        __shared__ float lds[36];
+        mv_run<F1, F2, IN_NORM, OUT_STORE, 64, 1, MV_PUBLISH>(pq, blockIdx.x, lds, MvFuse{});
+    } else {
+        const int a = (int)blockIdx.x - n_qkv;
+        attn_mfma_body<HD, GG, false, true>(pa, a % pa.max_splits, a / pa.max_splits, 0);
+    }
+}
+
+typedef void (*QkvAttnKernel)(MvParams, AttnParams, int);
+
+// Q4_K q/k with a Q6_K v (a Q4_K_M layer) or Q8_0 throughout; head_dim 128
+// with four query heads per kv head, or 64 with eight
+static QkvAttnKernel pick_qkv_attn(int f1, int f2, int hd, int g) {
+    if (hd == 128 && g == 4) {
+        if (f1 == Q4_K && f2 == Q6_K) return qkv_attn_kernel<Q4_K, Q6_K, 128, 4>;
+        if (f1 == Q8_0 && f2 == Q8_0) return qkv_attn_kernel<Q8_0, Q8_0, 128, 4>;
+    }
+    if (hd == 64 && g == 8 && f1 == Q4_K && f2 == Q6_K) return qkv_attn_kernel<Q4_K, Q6_K, 64, 8>;
+    return nullptr;
+}
+
+bool qkv_attention_supported(int f1, int f2, int hidden, int head_dim, int group) {
+    return hidden > 0 && hidden % 64 == 0 && hidden <= kMaxMatvecCols && team_width(hidden) == 64 &&
+           pick_qkv_attn(f1, f2, head_dim, group) != nullptr;
+}
+
+hipError_t launch_qkv_attention(const MvParams &qkv, const AttnParams &a, hipStream_t s) {
+    MvParams pq = qkv;
+    if (pq.nseg < 1 || pq.nseg > 3 || !pq.norm_w || pq.expert || pq.pro_in || pq.x2) return hipErrorInvalidValue;
+    int f1 = pq.seg[0].fmt, f2 = f1;
+    for (int i = 1; i < pq.nseg; i++)
+        if (pq.seg[i].fmt != f1) f2 = pq.seg[i].fmt;
+    for (int i = 0; i < pq.nseg; i++)
+        if (pq.seg[i].fmt != f1 && pq.seg[i].fmt != f2) return hipErrorInvalidValue;
+    // the attention side: the single-query fused mode with the polled merge
+    if (a.head_count_kv <= 0 || a.head_count % a.head_count_kv || a.head_count / a.head_count_kv > kMaxGroup ||
+        a.max_splits < 1 || !a.counters || !norms_fit(a) || !a.page_table || a.page_shift != kKvPageShift ||
+        a.window_start != 0 || a.n_query > 1 || !a.q || !a.k_new || !a.v_new || !a.out || !a.poll_merge ||
+        !a.poll_err || !a.qkv_refill || !a.reset_o || !a.reset_ml ||
+        !attention_poll_supported(a.head_dim, a.max_splits))
+        return hipErrorInvalidValue;
+    const int G = a.head_count / a.head_count_kv;
+    const QkvAttnKernel k = qkv_attention_supported(f1, f2, pq.cols, a.head_dim, G)
+                                ? pick_qkv_attn(f1, f2, a.head_dim, G)
+                                : nullptr;
+    if (!k) return hipErrorInvalidValue;
+    plan_matvec(pq, matvec_target_wgs());
+    if (pq.team != 64) return hipErrorInvalidValue;
+    int n_qkv = 0;
+    for (int i = 0; i < pq.nseg; i++) n_qkv += (pq.seg[i].rows + pq.seg[i].rows_per_wg - 1) / pq.seg[i].rows_per_wg;
+    pq.route_wg = -1;
+    if (n_qkv <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k, dim3(n_qkv + a.max_splits * a.head_count_kv), dim3(256), 0, s, pq, a, n_qkv);
     return hipGetLastError();
 }
 

@@ -261,6 +261,8 @@ constexpr int kMaxMatvecRowLen = 4 * kMaxMatvecCols;  // plain / SiLU rows the w
 // Builds the launch plan (team size, rows per team, workgroup ranges) and launches.
 hipError_t launch_matvec(const MvParams &p, int in_mode, int out_mode, hipStream_t s);
 void plan_matvec(MvParams &p, int target_wgs);
+// the workgroups a matvec grid is planned for (a whole multiple of the CU count)
+int matvec_target_wgs();
 // An MoE layer's gate/up (NORM, SWIGLU with the routing prologue) and down
 // (PLAIN, STORE) products in one launch (moe_ffn_kernel): gate/up publishes
 // its act rows, the down workgroups find their experts from gu.pro_in's
@@ -441,9 +443,24 @@ struct AttnParams {
     int *poll_err;
     int poll_merge;
     int min_tiles;  // 32-position tiles per split at least (0: the default)
+    // launch_qkv_attention: the next launch's q / k / v words ([q][k][v], laid
+    // out as q, k_new and v_new), refilled with kPollEmpty by this one
+    float *qkv_refill;
 };
 constexpr uint32_t kPollEmpty = 0xFFFFFFFFu;  // a NaN pattern no arithmetic here produces
 hipError_t launch_attention(const AttnParams &p, hipStream_t s);
+// A decode step's q/k/v projection (qkv: fused RMSNorm, up to three segments
+// in at most two formats, plain stores) and its single-query attention
+// (fused mode with the polled merge) in one launch (qkv_attn_kernel): the
+// projection workgroups store q, k and v with device-scope stores, the
+// attention workgroups issue their K loads first and read their head's q, k
+// and v as they land.  Every q/k/v word (a.q, a.k_new, a.v_new: the
+// segments' outputs) must hold kPollEmpty before the launch; the launch
+// refills a.qkv_refill (the same layout) for the next one.
+hipError_t launch_qkv_attention(const MvParams &qkv, const AttnParams &a, hipStream_t s);
+// whether launch_qkv_attention serves these formats (q's, and the other
+// segments' if different) and shapes
+bool qkv_attention_supported(int f1, int f2, int hidden, int head_dim, int group);
 // The polled merge covers the single-query matrix-core kernel with at most 64 splits.
 bool attention_poll_supported(int head_dim, int max_splits);
 // Minimum tiles per split of a polled launch (ZIGGY_HIP_ATTN_MIN_TILES, a tuning knob; default 4).

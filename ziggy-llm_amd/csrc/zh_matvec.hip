@@ -108,6 +108,8 @@ static uint64_t column_bytes(int fmt, int c) {
 
 static hipError_t launch_matvec_team(const MvParams &p_in, int in, int out, hipStream_t s);
 
+int matvec_target_wgs() { return (int)(device_cus() * workgroups_per_cu() + 0.5f); }
+
 // A row longer than one team covers (kMaxMatvecCols values: 256 lanes of 64)
 // runs as column windows of that length, the first with the call's output
 // mode and the rest adding onto it.  Plain and SiLU inputs only (a norm needs

@@ -647,7 +647,8 @@ __device__ __forceinline__ void mv_body_fast(const MvParams &p, const MvSeg &sg,
                 const int r = r0 + (ib + l4) * teams;
                 if (lane < 4 && ib + l4 < n && r < r_end) {
                     if (OUT == OUT_STORE) {
-                        sg.y[r] = c;
+                        if constexpr (MODE == MV_PUBLISH) store_published(&sg.y[r], c);
+                        else sg.y[r] = c;
                     } else if (OUT == OUT_ADD) {
                         sg.y[r] = ry[0] + c;
                     } else if (OUT == OUT_WADD) {

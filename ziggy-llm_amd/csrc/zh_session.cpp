@@ -61,6 +61,15 @@ struct ZiggyHipSession {
     int *poll_err = nullptr;
     int attn_set = 1, graph_set0 = 0, graph_set1 = 1;
     size_t attn_scratch = 0;
+    // qkv_fuse: each decode step's q/k/v projection and attention run as one
+    // launch (launch_qkv_attention).  Their q/k/v words come in qkv_sets sets
+    // of [q][k][v], layer l using set l % qkv_sets, every word kPollEmpty
+    // until used; layer l's launch refills the set of layer l + 1 (of layer 0
+    // after the last), which is never its own: qkv_sets is the smallest n >= 2
+    // with (layers - 1) % n != 0.  Only whole steps (layers in order) use them.
+    bool qkv_fuse = false;
+    int qkv_sets = 1;
+    float *qkv_buf = nullptr;
     // binary16 K/V, paged: per layer kv_pages pages of 64 positions ([page][row in page][kv_dim]);
     // page_table[logical page] = the page's index in every layer's pool
     __half *kc = nullptr, *vc = nullptr;
@@ -131,6 +140,60 @@ MvParams mv_params(const ZiggyHipSession *s, const DT *const *mats, float *const
     return p;
 }
 
+// The decode step's single-query attention parameters for layer l (fused
+// mode: the projection's q, k, v epilogue and the K/V store), with the polled
+// merge's partials sets taken in turn.
+AttnParams step_attention_params(ZiggyHipSession *s, int l, const int *pos_dev, int pos, const float *q,
+                             const float *k, const float *v) {
+    const ZiggyHipModelDesc &md = s->md;
+    const LayerW &L = s->layers[l < 0 ? 0 : l];
+    const size_t layer_base = kv_layer_base(s, l < 0 ? 0 : l);
+    AttnParams a{};
+    a.q = q;
+    a.k_new = k;
+    a.v_new = v;
+    a.q_bias = L.q_bias.present ? (const float *)L.q_bias.p : nullptr;
+    a.k_bias = L.k_bias.present ? (const float *)L.k_bias.p : nullptr;
+    a.v_bias = L.v_bias.present ? (const float *)L.v_bias.p : nullptr;
+    a.q_norm = L.q_norm.present ? (const float *)L.q_norm.p : nullptr;
+    a.k_norm = L.k_norm.present ? (const float *)L.k_norm.p : nullptr;
+    a.k_cache = s->kc + layer_base;
+    a.v_cache = s->vc + layer_base;
+    a.page_table = s->page_table;
+    a.page_shift = kKvPageShift;
+    a.out = s->attn;
+    a.part_o = s->part_o;
+    a.part_ml = s->part_ml;
+    a.counters = s->counters;
+    a.head_count = (int)md.head_count;
+    a.head_count_kv = (int)md.head_count_kv;
+    a.head_dim = (int)md.head_dim;
+    a.kv_dim = s->kv_size;
+    a.position = pos;
+    a.position_dev = pos_dev;
+    a.window_start = 0;
+    a.scale = 1.0f / sqrtf((float)md.head_dim);
+    a.max_splits = s->max_splits;
+    a.eps = md.rms_norm_eps;
+    a.rope_base = md.rope_freq_base;
+    a.rope_denom = s->rope_denom;
+    a.rope_dim = (int)md.rope_dim;
+    a.rope_style = (int)md.rope_style;
+    a.ctx = (int)md.context_length;
+    if (s->attn_poll) {
+        const int set = s->attn_set ^ 1;
+        a.part_o = set ? s->part_o2 : s->part_o;
+        a.part_ml = set ? s->part_ml2 : s->part_ml;
+        a.reset_o = set ? s->part_o : s->part_o2;
+        a.reset_ml = set ? s->part_ml : s->part_ml2;
+        a.poll_merge = 1;
+        a.poll_err = s->poll_err;
+        a.min_tiles = attention_poll_min_tiles();
+        s->attn_set = set;
+    }
+    return a;
+}
+
 // Enqueues one kernel of the step (ZIGGY_HIP_KERNEL_*) for layer l.  With
 // pos_dev set the position comes from device memory (graph replay).
 hipError_t enqueue_kernel(ZiggyHipSession *s, int id, int l, const int *pos_dev, int pos, hipStream_t st) {
@@ -150,49 +213,7 @@ hipError_t enqueue_kernel(ZiggyHipSession *s, int id, int l, const int *pos_dev,
         // the q/k/v epilogue and the K/V store run inside the attention kernel
         return hipSuccess;
     case ZIGGY_HIP_KERNEL_ATTENTION: {
-        AttnParams a{};
-        a.q = s->q;
-        a.k_new = s->k;
-        a.v_new = s->v;
-        a.q_bias = L.q_bias.present ? (const float *)L.q_bias.p : nullptr;
-        a.k_bias = L.k_bias.present ? (const float *)L.k_bias.p : nullptr;
-        a.v_bias = L.v_bias.present ? (const float *)L.v_bias.p : nullptr;
-        a.q_norm = L.q_norm.present ? (const float *)L.q_norm.p : nullptr;
-        a.k_norm = L.k_norm.present ? (const float *)L.k_norm.p : nullptr;
-        a.k_cache = s->kc + layer_base;
-        a.v_cache = s->vc + layer_base;
-        a.page_table = s->page_table;
-        a.page_shift = kKvPageShift;
-        a.out = s->attn;
-        a.part_o = s->part_o;
-        a.part_ml = s->part_ml;
-        a.counters = s->counters;
-        a.head_count = (int)md.head_count;
-        a.head_count_kv = (int)md.head_count_kv;
-        a.head_dim = (int)md.head_dim;
-        a.kv_dim = s->kv_size;
-        a.position = pos;
-        a.position_dev = pos_dev;
-        a.window_start = 0;
-        a.scale = 1.0f / sqrtf((float)md.head_dim);
-        a.max_splits = s->max_splits;
-        a.eps = md.rms_norm_eps;
-        a.rope_base = md.rope_freq_base;
-        a.rope_denom = s->rope_denom;
-        a.rope_dim = (int)md.rope_dim;
-        a.rope_style = (int)md.rope_style;
-        a.ctx = (int)md.context_length;
-        if (s->attn_poll) {
-            const int set = s->attn_set ^ 1;
-            a.part_o = set ? s->part_o2 : s->part_o;
-            a.part_ml = set ? s->part_ml2 : s->part_ml;
-            a.reset_o = set ? s->part_o : s->part_o2;
-            a.reset_ml = set ? s->part_ml : s->part_ml2;
-            a.poll_merge = 1;
-            a.poll_err = s->poll_err;
-            a.min_tiles = attention_poll_min_tiles();
-            s->attn_set = set;
-        }
+        AttnParams a = step_attention_params(s, l, pos_dev, pos, s->q, s->k, s->v);
         return launch_attention(a, st);
     }
     case ZIGGY_HIP_KERNEL_O_PROJ: {
@@ -251,6 +272,29 @@ hipError_t enqueue_attention_block(ZiggyHipSession *s, int l, const int *pos_dev
     return hipSuccess;
 }
 
+// The attention block of layer l inside a whole decode step: with qkv_fuse
+// the q/k/v projection and the attention in one launch (q/k/v in layer l's
+// set, the next layer's set refilled), then o_proj; otherwise the launches
+// of enqueue_attention_block.
+hipError_t enqueue_attention_step(ZiggyHipSession *s, int l, const int *pos_dev, hipStream_t st) {
+    if (!s->qkv_fuse) return enqueue_attention_block(s, l, pos_dev, 0, st);
+    const int L = (int)s->layers.size();
+    const LayerW &W = s->layers[l];
+    const size_t per = (size_t)s->q_size + 2 * (size_t)s->kv_size;
+    float *set = s->qkv_buf + (size_t)(l % s->qkv_sets) * per;
+    float *next = s->qkv_buf + (size_t)(((l + 1) % L) % s->qkv_sets) * per;
+    float *q = set, *k = set + s->q_size, *v = k + s->kv_size;
+    const DT *m[3] = {&W.q, &W.k, &W.v};
+    float *ys[3] = {q, k, v};
+    MvParams p = mv_params(s, m, ys, 3, (int)s->md.embedding_length, s->hidden);
+    p.norm_w = (const float *)W.attn_norm.p;
+    AttnParams a = step_attention_params(s, l, pos_dev, 0, q, k, v);
+    a.qkv_refill = next;
+    const hipError_t e = launch_qkv_attention(p, a, st);
+    if (e != hipSuccess) return e;
+    return enqueue_kernel(s, ZIGGY_HIP_KERNEL_O_PROJ, l, pos_dev, 0, st);
+}
+
 // The FFN block of one layer (session.zig:468-513).
 hipError_t enqueue_ffn_block(ZiggyHipSession *s, int l, hipStream_t st) {
     hipError_t e = enqueue_kernel(s, ZIGGY_HIP_KERNEL_GATE_UP, l, nullptr, 0, st);
@@ -288,7 +332,7 @@ hipError_t enqueue_step(ZiggyHipSession *s, hipStream_t st) {
                                      s->embd.type, (int)s->md.embedding_length, s->hidden, st);
     if (e != hipSuccess) return e;
     for (int l = 0; l < (int)s->md.block_count; l++) {
-        e = enqueue_attention_block(s, l, &s->st->pos, 0, st);
+        e = enqueue_attention_step(s, l, &s->st->pos, st);
         if (e != hipSuccess) return e;
         e = enqueue_ffn_block(s, l, st);
         if (e != hipSuccess) return e;
@@ -497,6 +541,37 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
             return hip_fail(e, "attention partials allocation", err, err_len);
         }
         s->part_ml2 = s->part_o2 + (s->part_ml - s->part_o);
+    }
+    {
+        // the q/k/v projection and the attention in one launch: every layer with a served
+        // format pair and shape, the polled merge, more than one layer (ZIGGY_HIP_QKV_FUSE=0
+        // keeps two launches)
+        const char *env = getenv("ZIGGY_HIP_QKV_FUSE");
+        bool fuse = !(env && env[0] == '0') && md.block_count >= 2 && s->attn_poll;
+        for (uint32_t l = 0; l < md.block_count && fuse; l++) {
+            const LayerW &W = s->layers[l];
+            const int f1 = W.q.type;
+            int f2 = f1;
+            for (const DT *d : {&W.k, &W.v})
+                if (d->type != f1) f2 = d->type;
+            fuse = (W.k.type == f1 || W.k.type == f2) && (W.v.type == f1 || W.v.type == f2) &&
+                   qkv_attention_supported(f1, f2, (int)H, (int)md.head_dim,
+                                           (int)(md.head_count / md.head_count_kv));
+        }
+        if (fuse) {
+            int n = 2;
+            while ((md.block_count - 1) % n == 0) n++;
+            const size_t bytes = (size_t)n * (Q + 2 * KV) * 4;
+            e = hipMalloc((void **)&s->qkv_buf, bytes);
+            if (e == hipSuccess) s->allocs.push_back(s->qkv_buf);
+            if (e == hipSuccess) e = hipMemsetAsync(s->qkv_buf, 0xFF, bytes, ctx->stream);
+            if (e != hipSuccess) {
+                free_session(s);
+                return hip_fail(e, "q/k/v sets allocation", err, err_len);
+            }
+            s->qkv_fuse = true;
+            s->qkv_sets = n;
+        }
     }
     // pages in order until the caller sets a block table
     s->pages.resize(s->kv_pages);
@@ -1275,7 +1350,9 @@ int ziggy_hip_session_profile_decode(ZiggyHipSession *s, uint32_t token, uint32_
         return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "invalid profile_decode arguments");
     const ZiggyHipModelDesc &md = s->md;
     const int L = (int)md.block_count;
-    const size_t per_step = 5 * (size_t)L + 7;  // markers, step begin, 5 per layer, output, wait, gpu, readback
+    // the step's launches per layer: q/k/v, attention, o, gate/up, down (q/k/v with the attention when fused)
+    const int per_layer = s->qkv_fuse ? 4 : 5;
+    const size_t per_step = (size_t)per_layer * L + 7;  // markers, step begin, the layers', output, wait, gpu, readback
     *out_count = per_step * steps;
     if (!records || capacity < per_step * steps)
         return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "profile record buffer too small");
@@ -1284,7 +1361,7 @@ int ziggy_hip_session_profile_decode(ZiggyHipSession *s, uint32_t token, uint32_
     if (token >= s->embd.rows) return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "token id out of range");
     *out_count = 0;
     hipStream_t st = s->ctx->stream;
-    const int nev = 5 * L + 3;  // before the step, after the step begin, after each launch
+    const int nev = per_layer * L + 3;  // before the step, after the step begin, after each launch
     std::vector<hipEvent_t> ev(nev, nullptr);
     hipError_t e = hipSuccess;
     for (int i = 0; i < nev && e == hipSuccess; i++) e = hipEventCreate(&ev[i]);
@@ -1316,8 +1393,11 @@ int ziggy_hip_session_profile_decode(ZiggyHipSession *s, uint32_t token, uint32_
             r.tensor_type = shape->type;
         }
     };
-    static const int kLayerKernels[5] = {ZIGGY_HIP_KERNEL_QKV, ZIGGY_HIP_KERNEL_ATTENTION, ZIGGY_HIP_KERNEL_O_PROJ,
-                                         ZIGGY_HIP_KERNEL_GATE_UP, ZIGGY_HIP_KERNEL_DOWN};
+    constexpr int kQkvAttn = -1;  // the q/k/v projection and the attention in one launch
+    const int kSeparate[5] = {ZIGGY_HIP_KERNEL_QKV, ZIGGY_HIP_KERNEL_ATTENTION, ZIGGY_HIP_KERNEL_O_PROJ,
+                              ZIGGY_HIP_KERNEL_GATE_UP, ZIGGY_HIP_KERNEL_DOWN};
+    const int kFused[4] = {kQkvAttn, ZIGGY_HIP_KERNEL_O_PROJ, ZIGGY_HIP_KERNEL_GATE_UP, ZIGGY_HIP_KERNEL_DOWN};
+    const int *kLayerKernels = s->qkv_fuse ? kFused : kSeparate;
     std::vector<Op> ops(nev - 1);
     for (uint32_t t = 0; t < steps && e == hipSuccess; t++) {
         const int pos = (int)s->position;
@@ -1337,14 +1417,33 @@ int ziggy_hip_session_profile_decode(ZiggyHipSession *s, uint32_t token, uint32_
         if (e == hipSuccess) e = hipEventRecord(ev[++k], st);
         for (int l = 0; l < L && e == hipSuccess; l++) {
             const LayerW &W = s->layers[l];
-            for (int id : kLayerKernels) {
-                if (e == hipSuccess) e = enqueue_kernel(s, id, l, &s->st->pos, 0, st);
+            for (int j = 0; j < per_layer; j++) {
+                const int id = kLayerKernels[j];
+                if (e == hipSuccess) {
+                    if (id == kQkvAttn) {
+                        // the fused launch alone (enqueue_attention_step without its o_proj)
+                        const size_t per = (size_t)s->q_size + 2 * (size_t)s->kv_size;
+                        float *set = s->qkv_buf + (size_t)(l % s->qkv_sets) * per;
+                        float *next = s->qkv_buf + (size_t)(((l + 1) % L) % s->qkv_sets) * per;
+                        float *q = set, *k = set + s->q_size, *v = k + s->kv_size;
+                        const DT *m[3] = {&W.q, &W.k, &W.v};
+                        float *ys[3] = {q, k, v};
+                        MvParams p = mv_params(s, m, ys, 3, H, s->hidden);
+                        p.norm_w = (const float *)W.attn_norm.p;
+                        AttnParams a = step_attention_params(s, l, &s->st->pos, 0, q, k, v);
+                        a.qkv_refill = next;
+                        e = launch_qkv_attention(p, a, st);
+                    } else {
+                        e = enqueue_kernel(s, id, l, &s->st->pos, 0, st);
+                    }
+                }
                 switch (id) {
                 case ZIGGY_HIP_KERNEL_QKV:
                     ops[k] = Op{ZIGGY_HIP_PROFILE_PROJECTIONS, W.q.rows + W.k.rows + W.v.rows, W.q.cols, 0, 3,
                                 (uint32_t)W.q.type};
                     break;
                 case ZIGGY_HIP_KERNEL_ATTENTION:  // session.zig:445-450
+                case kQkvAttn:                    // (with the q/k/v projection inside)
                     ops[k] = Op{ZIGGY_HIP_PROFILE_ATTENTION, md.head_count, md.rope_dim, (uint64_t)pos + 1,
                                 md.head_count_kv, 0};
                     break;
