@@ -161,6 +161,26 @@ __device__ __forceinline__ float rows_sum16(float v, int n) {
     return v;
 }
 
+// Max / sum over aligned groups of n lanes (n = 4, 8, 16 or 32), valid in
+// every lane of the group: DPP within 16-lane rows, a lane swap across rows.
+// Each step pairs a lane with one holding the other half of its group's
+// partial (the mirrors reach the other quad / half row, whose lanes all hold
+// the same value by then), so the bits equal an xor butterfly's of ascending
+// distance.
+__device__ __forceinline__ float lanes_max(float v, int n) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    if (n >= 8) v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+    if (n >= 16) v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+    if (n >= 32) v = xmax<16>(v);
+    return v;
+}
+__device__ __forceinline__ float lanes_sum(float v, int n) {
+    v = group_sum16(v, min(n, 16));
+    if (n >= 32) v = xsum<16>(v);
+    return v;
+}
+
 // Max / sum over aligned groups of 32 lanes (half wavefronts); the total is
 // valid in every lane of the group.
 __device__ __forceinline__ float half_max32(float v) {
@@ -339,12 +359,15 @@ constexpr long kPollSpin = 1L << 18;
 // head's G * HD / 2 output pairs, per = ceil(pairs / nsplit).  SL lanes serve
 // one pair (SL = the power of two at or above nsplit, at least 4 and at most
 // 32; a lane holds splits lane, lane + SL, ... up to 64), so 256 / SL pairs go
-// at once and one round of polls covers the slice whenever per <= 256 / SL.
-// Each lane polls its splits' partial pair and (m, l) until neither is
-// kPollEmpty (device-scope loads: the partials come from other CUs), then the
-// SL lanes fold them: M = max m_s, w_s = 2^(m_s - M), out = (sum w_s o_s) /
-// (sum w_s l_s).  The fold's order is fixed by the lanes, so the result does
-// not depend on which split stored first.
+// at once, and kR such rounds are polled and folded together (at 4k
+// positions: 17 splits of 16 pairs, 8 pairs a round).  Each lane polls its
+// splits' partial pair and (m, l) until neither is kPollEmpty (device-scope
+// loads: the partials come from other CUs), then the SL lanes fold them:
+// M = max m_s, w_s = 2^(m_s - M), out = (sum w_s o_s) / (sum w_s l_s), with
+// register-to-register lane exchanges (lanes_max / lanes_sum: an LDS-path
+// shuffle took about 0.1 us a step here, and a round has ten steps).  The
+// fold's order is fixed by the lanes, so the result does not depend on which
+// split stored first.
 template <int HD, int VS>
 __device__ __forceinline__ void polled_merge(const AttnParams &p, int kvh, int split, int G, int nsplit, float *out) {
     const int npairs = G * HD / 2;
@@ -357,33 +380,44 @@ __device__ __forceinline__ void polled_merge(const AttnParams &p, int kvh, int s
     const int SL = nsplit <= 4 ? 4 : nsplit <= 8 ? 8 : nsplit <= 16 ? 16 : 32;
     const int tid = threadIdx.x, lane = tid & (SL - 1), row = tid / SL, rows = 256 / SL;
     constexpr int kC = 2;  // splits per lane (SL = 32: 64 splits)
-    for (int i0 = first; i0 < last; i0 += rows) {
-        const int it = min(i0 + row, last - 1);
-        const int g = it / (HD / 2), d2 = it % (HD / 2);
-        unsigned long long ov[kC], mv[kC];
-        bool need[kC];
+    constexpr int kR = 2;  // rounds of pairs polled together
+    for (int i0 = first; i0 < last; i0 += kR * rows) {
+        int g[kR], d2[kR];
+        unsigned long long ov[kR][kC], mv[kR][kC];
+        bool need[kR][kC];
 #pragma unroll
-        for (int c = 0; c < kC; c++) {
-            need[c] = lane + SL * c < nsplit;
-            ov[c] = mv[c] = 0ull;
+        for (int r = 0; r < kR; r++) {
+            const int it = min(i0 + r * rows + row, last - 1);
+            g[r] = it / (HD / 2);
+            d2[r] = it % (HD / 2);
+#pragma unroll
+            for (int c = 0; c < kC; c++) {
+                need[r][c] = lane + SL * c < nsplit && i0 + r * rows < last;
+                ov[r][c] = mv[r][c] = 0ull;
+            }
         }
         long spin = 0;
         for (;;) {
 #pragma unroll
-            for (int c = 0; c < kC; c++) {
-                const int sp = min(lane + SL * c, nsplit - 1);
-                if (need[c]) {
-                    ov[c] = __hip_atomic_load(po + ((size_t)sp * VS + g) * (HD / 2) + d2, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-                    mv[c] = __hip_atomic_load(ml + (size_t)sp * VS + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int r = 0; r < kR; r++)
+#pragma unroll
+                for (int c = 0; c < kC; c++) {
+                    const int sp = min(lane + SL * c, nsplit - 1);
+                    if (need[r][c]) {
+                        ov[r][c] = __hip_atomic_load(po + ((size_t)sp * VS + g[r]) * (HD / 2) + d2[r],
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        mv[r][c] = __hip_atomic_load(ml + (size_t)sp * VS + g[r], __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                    }
                 }
-            }
             bool waiting = false;
 #pragma unroll
-            for (int c = 0; c < kC; c++) {
-                need[c] = need[c] && (poll_empty(ov[c]) || poll_empty(mv[c]));
-                waiting = waiting || need[c];
-            }
+            for (int r = 0; r < kR; r++)
+#pragma unroll
+                for (int c = 0; c < kC; c++) {
+                    need[r][c] = need[r][c] && (poll_empty(ov[r][c]) || poll_empty(mv[r][c]));
+                    waiting = waiting || need[r][c];
+                }
             if (!__any(waiting)) break;
             if (++spin > kPollSpin) {
                 if ((tid & 63) == 0) __hip_atomic_store(p.poll_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -391,31 +425,39 @@ __device__ __forceinline__ void polled_merge(const AttnParams &p, int kvh, int s
             }
             __builtin_amdgcn_s_sleep(1);
         }
-        float m[kC], mx = -INFINITY;
+        // the kR folds side by side (independent chains; a round past the
+        // slice folds zeros and stores nothing)
+        float mx[kR], O0[kR], O1[kR], L[kR];
 #pragma unroll
-        for (int c = 0; c < kC; c++) {
-            m[c] = lane + SL * c < nsplit ? __uint_as_float((uint32_t)mv[c]) : -INFINITY;
-            mx = fmaxf(mx, m[c]);
-        }
-        for (int o = SL / 2; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        float O0 = 0.f, O1 = 0.f, L = 0.f;
+        for (int r = 0; r < kR; r++) {
+            mx[r] = -INFINITY;
 #pragma unroll
-        for (int c = 0; c < kC; c++) {
-            const float w = m[c] == -INFINITY ? 0.f : exp2f(m[c] - mx);
-            O0 = fmaf(__uint_as_float((uint32_t)ov[c]), w, O0);
-            O1 = fmaf(__uint_as_float((uint32_t)(ov[c] >> 32)), w, O1);
-            L = fmaf(__uint_as_float((uint32_t)(mv[c] >> 32)), w, L);
+            for (int c = 0; c < kC; c++)
+                if (lane + SL * c < nsplit) mx[r] = fmaxf(mx[r], __uint_as_float((uint32_t)mv[r][c]));
+            mx[r] = lanes_max(mx[r], SL);
         }
-        for (int o = SL / 2; o >= 1; o >>= 1) {
-            O0 += __shfl_xor(O0, o, 64);
-            O1 += __shfl_xor(O1, o, 64);
-            L += __shfl_xor(L, o, 64);
+#pragma unroll
+        for (int r = 0; r < kR; r++) {
+            O0[r] = O1[r] = L[r] = 0.f;
+#pragma unroll
+            for (int c = 0; c < kC; c++) {
+                const float m = lane + SL * c < nsplit ? __uint_as_float((uint32_t)mv[r][c]) : -INFINITY;
+                const float w = m == -INFINITY ? 0.f : exp2f(m - mx[r]);
+                O0[r] = fmaf(__uint_as_float((uint32_t)ov[r][c]), w, O0[r]);
+                O1[r] = fmaf(__uint_as_float((uint32_t)(ov[r][c] >> 32)), w, O1[r]);
+                L[r] = fmaf(__uint_as_float((uint32_t)(mv[r][c] >> 32)), w, L[r]);
+            }
+            O0[r] = lanes_sum(O0[r], SL);
+            O1[r] = lanes_sum(O1[r], SL);
+            L[r] = lanes_sum(L[r], SL);
         }
-        if (lane == 0 && i0 + row < last) {
-            float *dst = out + (size_t)g * HD + 2 * d2;
-            dst[0] = O0 / L;
-            dst[1] = O1 / L;
-        }
+#pragma unroll
+        for (int r = 0; r < kR; r++)
+            if (lane == 0 && i0 + r * rows + row < last) {
+                float *dst = out + (size_t)g[r] * HD + 2 * d2[r];
+                dst[0] = O0[r] / L[r];
+                dst[1] = O1[r] / L[r];
+            }
     }
 }
 
