@@ -578,7 +578,9 @@ int ziggy_hip_profile_render(const ZiggyHipProfileRecord *records, size_t count,
  * the category of the reference's op (the step begin's embedding gather:
  * elementwise_ops; q/k/v, o, gate/up and down: projections, each with its
  * RMSNorm / SwiGLU fused; attention, with the q/k norms, RoPE and the K/V
- * store fused: attention, shaped as session.zig:445-450; the output head
+ * store fused: attention, shaped as session.zig:445-450; where a layer's
+ * q/k/v projection and attention run as one launch, that launch is one
+ * attention record; the output head
  * fused with argmax: output_reduce, shaped as session.zig:633-645), then
  * COMMIT_WAIT (host time blocked in the stream synchronization),
  * COMMIT_WAIT_GPU (device time from the first event to the last),
