@@ -360,7 +360,7 @@ constexpr long kPollSpin = 1L << 18;
 // one pair (SL = the power of two at or above nsplit, at least 4 and at most
 // 32; a lane holds splits lane, lane + SL, ... up to 64), so 256 / SL pairs go
 // at once, and kR such rounds are polled and folded together (at 4k
-// positions: 17 splits of 16 pairs, 8 pairs a round).  Each lane polls its
+// positions: 23 splits of 12 pairs, 8 pairs a round).  Each lane polls its
 // splits' partial pair and (m, l) until neither is kPollEmpty (device-scope
 // loads: the partials come from other CUs), then the SL lanes fold them:
 // M = max m_s, w_s = 2^(m_s - M), out = (sum w_s o_s) / (sum w_s l_s), with
@@ -1330,8 +1330,8 @@ bool attention_poll_supported(int head_dim, int max_splits) {
 int attention_poll_min_tiles() {
     static const int t = [] {
         const char *e = getenv("ZIGGY_HIP_ATTN_MIN_TILES");
-        const int v = e ? atoi(e) : 4;
-        return v > 0 ? v : 4;
+        const int v = e ? atoi(e) : 6;
+        return v > 0 ? v : 6;
     }();
     return t;
 }

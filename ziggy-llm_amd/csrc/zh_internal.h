@@ -463,7 +463,7 @@ hipError_t launch_qkv_attention(const MvParams &qkv, const AttnParams &a, hipStr
 bool qkv_attention_supported(int f1, int f2, int hidden, int head_dim, int group);
 // The polled merge covers the single-query matrix-core kernel with at most 64 splits.
 bool attention_poll_supported(int head_dim, int max_splits);
-// Minimum tiles per split of a polled launch (ZIGGY_HIP_ATTN_MIN_TILES, a tuning knob; default 4).
+// Minimum tiles per split of a polled launch (ZIGGY_HIP_ATTN_MIN_TILES, a tuning knob; default 6).
 int attention_poll_min_tiles();
 constexpr int kKvPageShift = 6;  // a session's KV page: 64 positions (two 32-position attention tiles)
 constexpr int kIdentityPages = 65536;  // a context's identity table: contiguous caches of up to 4M positions
