@@ -7,7 +7,9 @@ launches of ZIGGY_HIP_QKV_FUSE=0, and against the CPU oracle.
 The two paths run the same arithmetic on the same values, so the greedy tokens
 and the logits must be the same bits.  The q/k/v words rotate through 2, 3 and
 4 sets (2, 3 and 7 layers); repeated generate calls replay the step graph,
-which must leave the sets re-armed.  The shapes are the smallest the fused
+which must leave the sets re-armed.  After a 6-token prompt each step's
+attention is one split per kv head; after a 300-token prompt it is two, merged
+by polling inside the fused launch.  The shapes are the smallest the fused
 launch serves: hidden 1024 (teams of 64 lanes), head_dim 128 with four query
 heads per kv head (Q4_K q/k with Q6_K v, or Q8_0 throughout).
 """
@@ -50,12 +52,14 @@ def run(hip_ctx, img, spec, prompt, steps):
     return toks, logits
 
 
-@pytest.mark.parametrize("name", list(CASES))
-def test_fused_qkv_attention_equals_two_launches_and_oracle(hip_ctx, monkeypatch, name):
-    spec = synth.small_spec(**CASES[name])
-    say(f"fused q/k/v + attention {name}: {spec.n_layers} layers, hidden {spec.hidden}")
+@pytest.mark.parametrize("name,prompt_len", [(n, 6) for n in CASES] + [("q4km-3-layers", 300), ("q8-7-layers", 300)])
+def test_fused_qkv_attention_equals_two_launches_and_oracle(hip_ctx, monkeypatch, name, prompt_len):
+    # a 6-token prompt keeps every step's attention in one split; after 300
+    # tokens each kv head has two splits and the launch merges them (polled)
+    spec = synth.small_spec(**dict(CASES[name], context=prompt_len + 40))
+    say(f"fused q/k/v + attention {name}: {spec.n_layers} layers, hidden {spec.hidden}, prompt {prompt_len}")
     img = synth.build(spec, seed=41)
-    prompt = synth.prompt_tokens(7, 6, spec.vocab)
+    prompt = synth.prompt_tokens(7, prompt_len, spec.vocab)
     steps = 24
     monkeypatch.setenv("ZIGGY_HIP_QKV_FUSE", "0")
     want, want_logits = run(hip_ctx, img, spec, prompt, steps)
