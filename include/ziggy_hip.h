@@ -373,6 +373,9 @@ enum {
     ZIGGY_HIP_KERNEL_GATE_UP = 4,  /* fused RMSNorm + gate/up + SiLU(gate) * up */
     ZIGGY_HIP_KERNEL_DOWN = 5,     /* down projection + residual */
     ZIGGY_HIP_KERNEL_OUTPUT = 6,   /* fused RMSNorm + output head + argmax */
+    ZIGGY_HIP_KERNEL_QKV_ATTENTION = 7, /* QKV and ATTENTION in one launch, as a whole step runs them
+                                           where the session serves it (no reference counterpart: its
+                                           step encodes them as separate dispatches) */
 };
 
 int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *model,
@@ -532,8 +535,11 @@ int ziggy_hip_sample_logits(const float *logits, uint32_t count, const uint32_t 
  * read distinct weights from HBM, between one pair of HIP events on the
  * session stream.  Reports the mean launch duration and the algorithmic bytes
  * one launch streams (weights + binary16 KV; activations excluded).  Leaves
- * the position as it was; overwrites the hidden state and (ATTENTION) the
- * cache row of the current position, which the next step writes anyway. */
+ * the position as it was; overwrites the hidden state and (ATTENTION,
+ * QKV_ATTENTION) the cache row of the current position, which the next step
+ * writes anyway.  QKV_ATTENTION fails with ZIGGY_HIP_INVALID_ARGUMENT where the
+ * session runs the two separately; its launches go through whole passes over
+ * the layers (`iterations` rounded up), as a step's do. */
 int ziggy_hip_session_time_kernel(ZiggyHipSession *session, uint32_t kernel, uint32_t iterations,
                                   uint64_t *avg_ns, uint64_t *bytes_per_launch, char *error_message,
                                   size_t error_message_len);

@@ -95,3 +95,35 @@ def test_fused_qkv_attention_profile_records(hip_ctx):
         assert (body == [K["attention"], K["projections"], K["projections"], K["projections"]]).all()
         att = per[t][2]
         assert att["rows"] == spec.n_head and att["extra"] == spec.n_kv
+
+
+def test_time_kernel_between_steps_keeps_the_stream(hip_ctx, monkeypatch):
+    # timing each launch of the step, the fused one included (whole passes
+    # over the layers), between greedy steps leaves the stream as it was
+    spec = synth.small_spec(**dict(CASES["q4km-3-layers"], context=80))
+    img = synth.build(spec, seed=47)
+    prompt = synth.prompt_tokens(11, 5, spec.vocab)
+    s = hip.Session(hip_ctx, img, context=spec.context)
+    want, _ = s.generate(prompt, 12)
+    s.reset()
+    for t in prompt[:-1]:
+        s.step_no_output(int(t))
+    got, tok = [], int(prompt[-1])
+    for i in range(12):
+        tok = s.step_greedy(tok)
+        got.append(tok)
+        if i == 5:
+            sizes = {}
+            for name in ("qkv", "attention", "qkv_attention", "o_proj", "gate_up", "down", "output"):
+                ns, nb = s.time_kernel(name, 5)
+                assert ns > 0 and nb > 0
+                sizes[name] = nb
+            assert sizes["qkv_attention"] == sizes["qkv"] + sizes["attention"]
+    assert got == [int(t) for t in want[:12]]
+    s.close()
+    # a session that keeps q/k/v and the attention apart has no fused launch to time
+    monkeypatch.setenv("ZIGGY_HIP_QKV_FUSE", "0")
+    s = hip.Session(hip_ctx, img, context=spec.context)
+    with pytest.raises(hip.HipError):
+        s.time_kernel("qkv_attention", 5)
+    s.close()

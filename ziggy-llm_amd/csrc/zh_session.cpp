@@ -272,12 +272,10 @@ hipError_t enqueue_attention_block(ZiggyHipSession *s, int l, const int *pos_dev
     return hipSuccess;
 }
 
-// The attention block of layer l inside a whole decode step: with qkv_fuse
-// the q/k/v projection and the attention in one launch (q/k/v in layer l's
-// set, the next layer's set refilled), then o_proj; otherwise the launches
-// of enqueue_attention_block.
-hipError_t enqueue_attention_step(ZiggyHipSession *s, int l, const int *pos_dev, hipStream_t st) {
-    if (!s->qkv_fuse) return enqueue_attention_block(s, l, pos_dev, 0, st);
+// Layer l's q/k/v projection and attention in one launch (qkv_fuse): q/k/v
+// in layer l's set, the next layer's set refilled.  The position comes from
+// pos_dev when set (graph replay), else pos.
+hipError_t launch_qkv_attention_layer(ZiggyHipSession *s, int l, const int *pos_dev, int pos, hipStream_t st) {
     const int L = (int)s->layers.size();
     const LayerW &W = s->layers[l];
     const size_t per = (size_t)s->q_size + 2 * (size_t)s->kv_size;
@@ -288,9 +286,17 @@ hipError_t enqueue_attention_step(ZiggyHipSession *s, int l, const int *pos_dev,
     float *ys[3] = {q, k, v};
     MvParams p = mv_params(s, m, ys, 3, (int)s->md.embedding_length, s->hidden);
     p.norm_w = (const float *)W.attn_norm.p;
-    AttnParams a = step_attention_params(s, l, pos_dev, 0, q, k, v);
+    AttnParams a = step_attention_params(s, l, pos_dev, pos, q, k, v);
     a.qkv_refill = next;
-    const hipError_t e = launch_qkv_attention(p, a, st);
+    return launch_qkv_attention(p, a, st);
+}
+
+// The attention block of layer l inside a whole decode step: with qkv_fuse
+// the q/k/v projection and the attention in one launch, then o_proj;
+// otherwise the launches of enqueue_attention_block.
+hipError_t enqueue_attention_step(ZiggyHipSession *s, int l, const int *pos_dev, hipStream_t st) {
+    if (!s->qkv_fuse) return enqueue_attention_block(s, l, pos_dev, 0, st);
+    const hipError_t e = launch_qkv_attention_layer(s, l, pos_dev, 0, st);
     if (e != hipSuccess) return e;
     return enqueue_kernel(s, ZIGGY_HIP_KERNEL_O_PROJ, l, pos_dev, 0, st);
 }
@@ -1309,8 +1315,11 @@ int ziggy_hip_session_verify(ZiggyHipSession *s, uint32_t current_token, const u
 
 int ziggy_hip_session_time_kernel(ZiggyHipSession *s, uint32_t kernel, uint32_t iterations, uint64_t *avg_ns,
                                   uint64_t *bytes_per_launch, char *err, size_t err_len) {
-    if (!s || kernel > ZIGGY_HIP_KERNEL_OUTPUT || iterations == 0 || !avg_ns || !bytes_per_launch)
+    if (!s || kernel > ZIGGY_HIP_KERNEL_QKV_ATTENTION || iterations == 0 || !avg_ns || !bytes_per_launch)
         return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "invalid time_kernel arguments");
+    const bool fused = kernel == ZIGGY_HIP_KERNEL_QKV_ATTENTION;
+    if (fused && !s->qkv_fuse)
+        return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "the session runs q/k/v and the attention separately");
     if (s->position >= s->md.context_length)
         return fail(err, err_len, ZIGGY_HIP_INVALID_ARGUMENT, "no free cache row to time at");
     const int pos = (int)s->position, L = (int)s->md.block_count;
@@ -1322,15 +1331,23 @@ int ziggy_hip_session_time_kernel(ZiggyHipSession *s, uint32_t kernel, uint32_t 
         return fail(err, err_len, ZIGGY_HIP_EXECUTION_FAILED, "event creation failed");
     }
     // one warm-up launch, then `iterations` back-to-back launches (rotating
-    // over the layers so weights stream from HBM) between one event pair
+    // over the layers so weights stream from HBM) between one event pair.
+    // The fused launch's q/k/v sets assume layers in order from layer 0: its
+    // launches end on the last layer, which re-arms layer 0's set.
+    if (fused) iterations = ((iterations + (uint32_t)L) / (uint32_t)L) * (uint32_t)L - 1;
+    auto launch = [&](int l) {
+        return fused ? launch_qkv_attention_layer(s, l, nullptr, pos, st)
+                     : enqueue_kernel(s, (int)kernel, l, nullptr, pos, st);
+    };
     uint64_t bytes = 0;
     float ms = 0.f;
-    hipError_t e = enqueue_kernel(s, (int)kernel, 0, nullptr, pos, st);
+    hipError_t e = launch(0);
     if (e == hipSuccess) e = hipEventRecord(e0, st);
     for (uint32_t i = 0; i < iterations && e == hipSuccess; i++) {
         const int l = (int)((i + 1) % (uint32_t)L);
-        e = enqueue_kernel(s, (int)kernel, l, nullptr, pos, st);
-        bytes += kernel_bytes(s, (int)kernel, l, pos);
+        e = launch(l);
+        bytes += fused ? kernel_bytes(s, ZIGGY_HIP_KERNEL_QKV, l, pos) + kernel_bytes(s, ZIGGY_HIP_KERNEL_ATTENTION, l, pos)
+                       : kernel_bytes(s, (int)kernel, l, pos);
     }
     if (e == hipSuccess) e = hipEventRecord(e1, st);
     if (e == hipSuccess) e = hipEventSynchronize(e1);
@@ -1420,22 +1437,9 @@ int ziggy_hip_session_profile_decode(ZiggyHipSession *s, uint32_t token, uint32_
             for (int j = 0; j < per_layer; j++) {
                 const int id = kLayerKernels[j];
                 if (e == hipSuccess) {
-                    if (id == kQkvAttn) {
-                        // the fused launch alone (enqueue_attention_step without its o_proj)
-                        const size_t per = (size_t)s->q_size + 2 * (size_t)s->kv_size;
-                        float *set = s->qkv_buf + (size_t)(l % s->qkv_sets) * per;
-                        float *next = s->qkv_buf + (size_t)(((l + 1) % L) % s->qkv_sets) * per;
-                        float *q = set, *k = set + s->q_size, *v = k + s->kv_size;
-                        const DT *m[3] = {&W.q, &W.k, &W.v};
-                        float *ys[3] = {q, k, v};
-                        MvParams p = mv_params(s, m, ys, 3, H, s->hidden);
-                        p.norm_w = (const float *)W.attn_norm.p;
-                        AttnParams a = step_attention_params(s, l, &s->st->pos, 0, q, k, v);
-                        a.qkv_refill = next;
-                        e = launch_qkv_attention(p, a, st);
-                    } else {
-                        e = enqueue_kernel(s, id, l, &s->st->pos, 0, st);
-                    }
+                    // the fused launch alone (enqueue_attention_step without its o_proj)
+                    if (id == kQkvAttn) e = launch_qkv_attention_layer(s, l, &s->st->pos, 0, st);
+                    else e = enqueue_kernel(s, id, l, &s->st->pos, 0, st);
                 }
                 switch (id) {
                 case ZIGGY_HIP_KERNEL_QKV:

@@ -101,7 +101,8 @@ class MoeDesc(ctypes.Structure):
         ("weights_scale", ctypes.c_float), ("rms_norm_eps", ctypes.c_float)]
 
 
-KERNELS = {"qkv": 0, "rope_kv": 1, "attention": 2, "o_proj": 3, "gate_up": 4, "down": 5, "output": 6}
+KERNELS = {"qkv": 0, "rope_kv": 1, "attention": 2, "o_proj": 3, "gate_up": 4, "down": 5, "output": 6,
+           "qkv_attention": 7}
 
 # the decode profiler's record kinds (ZIGGY_HIP_PROFILE_*): the reference's
 # Category values (runtime/metal_profile.zig:3-27), then the calls that are not
