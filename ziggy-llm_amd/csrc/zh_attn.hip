@@ -979,6 +979,11 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
     uint4 vr[2][8];
     load_k(0, kr[0]);
     load_k(1, kr[1]);
+    // the RoPE table depends only on the position: with q/k/v polled it is
+    // built while they are still on their way (the poll loop's barrier
+    // orders it before its readers)
+    const float rden = fused ? rope_den_finish(rden_raw, n_rot_f, p.rope_base, p.rope_denom) : 1.f;
+    if (PQ) rope_table(n_rot_f, rden, pos, cs_s, sn_s);
     if constexpr (PQ) {
         // this head's q, k and v as the projection workgroups store them
         const uint32_t *qw = reinterpret_cast<const uint32_t *>(p.q) + (size_t)kvh * nq;
@@ -1006,7 +1011,6 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
             __builtin_amdgcn_s_sleep(1);
         }
     }
-    const float rden = fused ? rope_den_finish(rden_raw, n_rot_f, p.rope_base, p.rope_denom) : 1.f;
     // the projection biases (the bias reads above are dummies when absent)
     if (fused) {
 #pragma unroll
@@ -1023,7 +1027,7 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
 
     if (fused) {
         const int n_rot = n_rot_f;
-        rope_table(n_rot, rden, pos, cs_s, sn_s);
+        if (!PQ) rope_table(n_rot, rden, pos, cs_s, sn_s);
         norm_rope_w<HD, QV>(qv, nq, p.q_norm != nullptr, qnw, p.eps, n_rot, p.rope_style, cs_s, sn_s, &q_s[0][0],
                             red16);
         if (own_pos) {
