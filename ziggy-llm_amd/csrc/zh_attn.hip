@@ -900,7 +900,8 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
     const int nsplit = (units + per - 1) / per;
     const bool polled = !MQ && p.poll_merge;
     // the other set's slot of this workgroup, refilled for the next launch
-    // (at the end: stores ahead of the K loads would delay them)
+    // (after the K loads: stores ahead of them would delay them; at the end,
+    // or with q/k/v polled while the workgroup waits for them)
     auto refill_other = [&]() {
         if (polled) poll_reset_slot<HD, VG>(p, kvh, split);
         if constexpr (PQ) qkv_reset_slice<HD>(p, kvh, split, nq);
@@ -979,6 +980,10 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
     uint4 vr[2][8];
     load_k(0, kr[0]);
     load_k(1, kr[1]);
+    // with q/k/v polled, the other sets' refill goes out while the workgroup
+    // waits (after the K loads, which it would otherwise delay; neither set
+    // is read by this launch), not at its end
+    if constexpr (PQ) refill_other();
     // the RoPE table depends only on the position: with q/k/v polled it is
     // built while they are still on their way (the poll loop's barrier
     // orders it before its readers)
@@ -1276,7 +1281,7 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
         }
     }
     if (nsplit == 1) {
-        refill_other();
+        if constexpr (!PQ) refill_other();
         return;
     }
     if (tid < G) {
@@ -1288,7 +1293,7 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
     }
     if (polled) {
         polled_merge<HD, VG>(p, kvh, split, G, nsplit, p.out + (size_t)kvh * G * HD);
-        refill_other();
+        if constexpr (!PQ) refill_other();
         return;
     }
     // MQ: up to 16 virtual heads, 16 splits per round of the merge
