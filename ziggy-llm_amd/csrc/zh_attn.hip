@@ -900,8 +900,7 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
     const int nsplit = (units + per - 1) / per;
     const bool polled = !MQ && p.poll_merge;
     // the other set's slot of this workgroup, refilled for the next launch
-    // (after the K loads: stores ahead of them would delay them; at the end,
-    // or with q/k/v polled while the workgroup waits for them)
+    // (after the K loads: stores ahead of them would delay them)
     auto refill_other = [&]() {
         if (polled) poll_reset_slot<HD, VG>(p, kvh, split);
         if constexpr (PQ) qkv_reset_slice<HD>(p, kvh, split, nq);
@@ -980,15 +979,15 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
     uint4 vr[2][8];
     load_k(0, kr[0]);
     load_k(1, kr[1]);
-    // with q/k/v polled, the other sets' refill goes out while the workgroup
-    // waits (after the K loads, which it would otherwise delay; neither set
+    // the other sets' refill goes out now, while the workgroup waits for q
+    // (after the K loads, which it would otherwise delay; no set it refills
     // is read by this launch), not at its end
-    if constexpr (PQ) refill_other();
-    // the RoPE table depends only on the position: with q/k/v polled it is
-    // built while they are still on their way (the poll loop's barrier
-    // orders it before its readers)
+    refill_other();
+    // the RoPE table depends only on the position: built while q is still
+    // on its way (a barrier orders it before its readers: the poll loop's,
+    // or norm_rope_w's own)
     const float rden = fused ? rope_den_finish(rden_raw, n_rot_f, p.rope_base, p.rope_denom) : 1.f;
-    if (PQ) rope_table(n_rot_f, rden, pos, cs_s, sn_s);
+    if (fused) rope_table(n_rot_f, rden, pos, cs_s, sn_s);
     if constexpr (PQ) {
         // this head's q, k and v as the projection workgroups store them
         const uint32_t *qw = reinterpret_cast<const uint32_t *>(p.q) + (size_t)kvh * nq;
@@ -1032,7 +1031,6 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
 
     if (fused) {
         const int n_rot = n_rot_f;
-        if (!PQ) rope_table(n_rot, rden, pos, cs_s, sn_s);
         norm_rope_w<HD, QV>(qv, nq, p.q_norm != nullptr, qnw, p.eps, n_rot, p.rope_style, cs_s, sn_s, &q_s[0][0],
                             red16);
         if (own_pos) {
@@ -1280,10 +1278,7 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
                                __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    if (nsplit == 1) {
-        if constexpr (!PQ) refill_other();
-        return;
-    }
+    if (nsplit == 1) return;
     if (tid < G) {
         const size_t e = ((size_t)slot * p.max_splits + split) * VG + tid;
         const unsigned long long v = (unsigned long long)__float_as_uint(fm_s[tid]) |
@@ -1293,7 +1288,6 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
     }
     if (polled) {
         polled_merge<HD, VG>(p, kvh, split, G, nsplit, p.out + (size_t)kvh * G * HD);
-        if constexpr (!PQ) refill_other();
         return;
     }
     // MQ: up to 16 virtual heads, 16 splits per round of the merge
