@@ -11,7 +11,8 @@ which must leave the sets re-armed.  After a 6-token prompt each step's
 attention is one split per kv head; after a 300-token prompt it is two, merged
 by polling inside the fused launch.  The shapes are the smallest the fused
 launch serves: hidden 1024 (teams of 64 lanes), head_dim 128 with four query
-heads per kv head (Q4_K q/k with Q6_K v, or Q8_0 throughout).
+heads per kv head (Q4_K q/k with Q6_K v, or Q8_0 throughout), and head_dim 64
+with eight (the TinyLlama shape's attention).
 """
 import sys
 
@@ -36,6 +37,8 @@ CASES = {
     "q4km-3-layers": dict(BASE, n_layers=3, down_q6k_layers=[0, 2]),
     "q8-7-layers": dict(BASE, arch="qwen3", n_layers=7, qk_norm=True, default_type=Q8_0, attn_v_type=Q8_0,
                         output_type=Q8_0, embd_type=Q8_0, rope_theta=1000000.0),
+    # head_dim 64 with eight query heads per kv head (the TinyLlama shape's attention)
+    "q4km-hd64-g8": dict(BASE, n_layers=3, n_head=16, n_kv=2, head_dim=64, down_q6k_layers=[1]),
 }
 
 
@@ -52,7 +55,8 @@ def run(hip_ctx, img, spec, prompt, steps):
     return toks, logits
 
 
-@pytest.mark.parametrize("name,prompt_len", [(n, 6) for n in CASES] + [("q4km-3-layers", 300), ("q8-7-layers", 300)])
+@pytest.mark.parametrize("name,prompt_len",
+                         [(n, 6) for n in CASES] + [("q4km-3-layers", 300), ("q8-7-layers", 300), ("q4km-hd64-g8", 300)])
 def test_fused_qkv_attention_equals_two_launches_and_oracle(hip_ctx, monkeypatch, name, prompt_len):
     # a 6-token prompt keeps every step's attention in one split; after 300
     # tokens each kv head has two splits and the launch merges them (polled)
