@@ -24,7 +24,7 @@ Also reported, on the same JSON line:
   cpu_baseline  -- the CPU oracle (a C restatement of the reference's CPU
                    decode path, same threads policy: 1 + min(11, ncpu - 1))
                    decoding the same model at the same context on host cores;
-  other_configs -- the other BASELINE configs in the same run (skip with
+  other_configs -- the other benchmark configurations in the same run (skip with
                    --no-other-configs): TinyLlama decode of 128 tokens after a
                    32-token prompt; the matvec microbench (Q4_K, Q6_K, Q8_0 at
                    its four shapes); Qwen3-8B Q8_0 decode of 128 tokens at 16k
@@ -161,7 +161,7 @@ def matvec_measure(iters):
 
 
 def other_configs(args):
-    """The other BASELINE configs, measured in the same run at their own workloads (shorter samples
+    """The other benchmark configurations, measured in the same run at their own workloads (shorter samples
     than their own --model lines): 1 TinyLlama decode, 2 the matvec microbench, 4 Qwen3-8B decode at
     16k plus the verify step, 5 the MoE stack's decode and 512-row prefill."""
     out = {"config1_tinyllama": decode_measure("tinyllama", 32, 128, args.seed),
@@ -191,12 +191,13 @@ def main():
                          "under the reference's profile categories (its --metal-profile report)")
     ap.add_argument("--profile-out", default=None, help="file for the profile summary (default: stderr)")
     ap.add_argument("--no-other-configs", action="store_true",
-                    help="skip the other BASELINE configs the headline run also measures (other_configs)")
+                    help="skip the other benchmark configurations the headline run also measures (other_configs)")
     args = ap.parse_args()
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (batch-1 decode of this "
-              f"model does not shard profitably; see DESIGN.md)", file=sys.stderr)
+              f"model does not shard profitably: each GPU would stream its share of every layer's weights in "
+              f"turn, with a collective per layer)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

@@ -1,7 +1,7 @@
 """Writes tests/golden/headline_streams.json (and headline_long_logits.npz): the CPU oracle's greedy
 streams on the headline shapes.
 
-The Llama-3.1-8B-shaped Q4_K_M model and the Qwen3-8B-shaped Q8_0 model (config 4),
+The Llama-3.1-8B-shaped Q4_K_M model (benchmark configuration 3) and the Qwen3-8B-shaped Q8_0 model (config 4),
 each built by zhip.synth from seed 1, get three oracle runs (oracle/, the C restatement of the reference's
 CPU decode path, fed token by token as runPrompt does, model/loader.zig:1016-1036):
   * `tokens`: an 8-token seeded prompt and 64 greedy tokens with the binary16 KV semantics of the

@@ -1,4 +1,4 @@
-"""GPU parity at the headline shapes: the Llama-3.1-8B-shaped Q4_K_M model and the
+"""GPU parity at the headline shapes: the Llama-3.1-8B-shaped Q4_K_M model (benchmark configuration 3) and the
 Qwen3-8B-shaped Q8_0 model (config 4), both from zhip.synth with seed 1.
 
 The reference pins its GPU path by equality with its CPU path (runtime/llama_runtime.zig:237-272); here

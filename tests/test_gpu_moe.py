@@ -73,7 +73,7 @@ def test_moe_stack_matches_oracle(hip_ctx, name):
 
 
 def test_moe_stack_config5_shape(hip_ctx):
-    # BASELINE config 5 layer shape (hidden 2048, 256 experts of FFN 512, top-8, shared expert),
+    # benchmark configuration 5 layer shape (hidden 2048, 256 experts of FFN 512, top-8, shared expert),
     # four layers of the forty
     spec = synth.moe_config5_spec(4)
     say(f"moe stack config-5 shape: {spec}")

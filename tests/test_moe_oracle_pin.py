@@ -117,7 +117,7 @@ def test_oracle_moe_ffn_matches_float64_composition(name):
 
 
 def test_config5_layer_shape():
-    """One layer of BASELINE config 5: hidden 2048, 256 IQ4_XS experts of FFN 512, top-8, Q3_K shared."""
+    """One layer of benchmark configuration 5: hidden 2048, 256 IQ4_XS experts of FFN 512, top-8, Q3_K shared."""
     spec = synth.moe_config5_spec(1)
     lay = synth.build_moe_stack(spec, seed=3)[0]
     x = zo.rms_norm(synth.normal_row(7, 0, spec.hidden, 0.0, 1.0), lay["ffn_norm"][0].view(np.float32), spec.eps)

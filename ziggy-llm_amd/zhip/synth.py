@@ -337,7 +337,7 @@ def toy_detokenize(ids) -> str:
 
 @dataclass
 class MoeSpec:
-    """A stack of Qwen3.5-MoE-style sparse FFN layers (BASELINE config 5 at full size)."""
+    """A stack of Qwen3.5-MoE-style sparse FFN layers (benchmark configuration 5 at full size)."""
     name: str
     n_layers: int
     hidden: int
