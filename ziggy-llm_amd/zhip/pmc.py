@@ -45,6 +45,8 @@ COPY_BYTES = 512 << 20
 KERNEL_NAMES = {
     "qkv": ["mv_kernel<12, 14, 1, 0, 64"],
     "attention": ["attn_mfma_kernel<128, 4, false>"],
+    # q/k/v and the attention in the one launch a decode step runs them in
+    "qkv_attention": ["qkv_attn_kernel<12, 14, 128, 4>"],
     "o_proj": ["mv_kernel<12, 12, 0, 1, 64"],
     "gate_up": ["mv_kernel<12, 12, 1, 2, 64"],
     "down": ["mv_kernel<12, 12, 0, 1, 256", "mv_kernel<14, 14, 0, 1, 256"],
@@ -453,7 +455,7 @@ def main(argv=None) -> None:
     p.add_argument("--iters", type=int, default=32)
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--position", type=int, default=4096)
-    p.add_argument("--kernels", default="qkv,attention,o_proj,gate_up,down")
+    p.add_argument("--kernels", default="qkv,attention,qkv_attention,o_proj,gate_up,down")
     p.add_argument("--meta")
     g = sub.add_parser("gemm-probe")
     g.add_argument("what", choices=["verify", "prompt", "moe"])
