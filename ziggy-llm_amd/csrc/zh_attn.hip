@@ -1359,34 +1359,55 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(AttnParams p, float *q_o
     constexpr int QV = kMaxGroup * HD / 256;
     const int m = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int G = p.head_count / p.head_count_kv, nq = G * HD, pos = p.position + m;
-    // the deferred RMSNorm of the q/k/v products' input row
-    const float r = rs.ss ? 1.0f / sqrtf(rs.ss[m] / (float)rs.n + rs.eps) : 1.0f;
     __shared__ float q_s[kMaxGroup * HD];
     __shared__ float kn_s[HD];
     __shared__ float red16[4 * QV_MAX];
     __shared__ float cs_s[HD / 2], sn_s[HD / 2];
     const float *qrow = p.q + (size_t)m * p.q_stride + (size_t)kvh * nq;
     const size_t kv_off = (size_t)m * p.kv_dim + (size_t)kvh * HD;
+    const int n_rot = p.rope_dim < HD ? p.rope_dim : HD;
+    // Every load first, none under a branch and none used before the last
+    // is issued (an absent tensor reads a valid dummy address, q's): one
+    // memory round trip where the row's sum of squares, then the biases one
+    // by one, then the norm weights inside the norm took one each.
+    const float ss = (rs.ss ? rs.ss : p.q)[rs.ss ? m : 0];
+    const float *qbp = p.q_bias ? p.q_bias : p.q, *kbp = p.k_bias ? p.k_bias : p.q, *vbp = p.v_bias ? p.v_bias : p.q;
+    const float *qn = p.q_norm ? p.q_norm : p.q, *kn = p.k_norm ? p.k_norm : p.q;
+    float qraw[QV], qb[QV], qnw[QV], knw[1];
+#pragma unroll
+    for (int i = 0; i < QV; i++) {
+        const int idx = min(tid + 256 * i, nq - 1);
+        qraw[i] = qrow[idx];
+        qb[i] = qbp[(size_t)kvh * nq + idx];
+        qnw[i] = qn[(tid + 256 * i) % HD];
+    }
+    const float kraw = p.k_new[kv_off + tid % HD], vraw = p.v_new[kv_off + tid % HD];
+    const float kbv = kbp[(size_t)kvh * HD + tid % HD], vbv = vbp[(size_t)kvh * HD + tid % HD];
+    knw[0] = kn[tid % HD];
+    const float rden_raw = rope_den_load(n_rot, p.rope_denom, p.q);
+    // then the arithmetic, in the stand-alone steps' order: the deferred
+    // RMSNorm of the q/k/v products' input row, the biases, the per-head
+    // norm and RoPE
+    const float r = rs.ss ? 1.0f / sqrtf(ss / (float)rs.n + rs.eps) : 1.0f;
     float qv[QV], kx[1];
 #pragma unroll
     for (int i = 0; i < QV; i++) {
         const int idx = tid + 256 * i;
         qv[i] = 0.f;
         if (idx < nq) {
-            qv[i] = r * qrow[idx];
-            if (p.q_bias) qv[i] += p.q_bias[(size_t)kvh * nq + idx];
+            qv[i] = r * qraw[i];
+            if (p.q_bias) qv[i] += qb[i];
         }
     }
-    kx[0] = r * p.k_new[kv_off + tid % HD];
-    float vx = r * p.v_new[kv_off + tid % HD];
+    kx[0] = r * kraw;
+    float vx = r * vraw;
     if (tid < HD) {
-        if (p.k_bias) kx[0] += p.k_bias[(size_t)kvh * HD + tid];
-        if (p.v_bias) vx += p.v_bias[(size_t)kvh * HD + tid];
+        if (p.k_bias) kx[0] += kbv;
+        if (p.v_bias) vx += vbv;
     }
-    const int n_rot = p.rope_dim < HD ? p.rope_dim : HD;
-    rope_table(n_rot, rope_den(n_rot, p.rope_base, p.rope_denom, p.q), pos, cs_s, sn_s);
-    norm_rope<HD, QV>(qv, nq, p.q_norm, p.eps, n_rot, p.rope_style, cs_s, sn_s, q_s, red16);
-    norm_rope<HD, 1>(kx, HD, p.k_norm, p.eps, n_rot, p.rope_style, cs_s, sn_s, kn_s, red16);
+    rope_table(n_rot, rope_den_finish(rden_raw, n_rot, p.rope_base, p.rope_denom), pos, cs_s, sn_s);
+    norm_rope_w<HD, QV>(qv, nq, p.q_norm != nullptr, qnw, p.eps, n_rot, p.rope_style, cs_s, sn_s, q_s, red16);
+    norm_rope_w<HD, 1>(kx, HD, p.k_norm != nullptr, knw, p.eps, n_rot, p.rope_style, cs_s, sn_s, kn_s, red16);
     float *qo = q_out + (size_t)m * p.q_stride + (size_t)kvh * nq;
     for (int idx = tid; idx < nq; idx += 256) qo[idx] = q_s[idx];
     if (tid < HD && pos < p.ctx) {
