@@ -9,7 +9,9 @@ and the logits must be the same bits.  The q/k/v words rotate through 2, 3 and
 4 sets (2, 3 and 7 layers); repeated generate calls replay the step graph,
 which must leave the sets re-armed.  After a 6-token prompt each step's
 attention is one split per kv head; after a 300-token prompt it is two, merged
-by polling inside the fused launch.  The shapes are the smallest the fused
+by polling inside the fused launch.  ZIGGY_HIP_ATTN_V_NOW=1 forces the
+variant long contexts use (the V tiles issued right after the q/k/v wait),
+which must give the same bits.  The shapes are the smallest the fused
 launch serves: hidden 1024 (teams of 64 lanes), head_dim 128 with four query
 heads per kv head (Q4_K q/k with Q6_K v, or Q8_0 throughout), and head_dim 64
 with eight (the TinyLlama shape's attention).
@@ -55,13 +57,18 @@ def run(hip_ctx, img, spec, prompt, steps):
     return toks, logits
 
 
-@pytest.mark.parametrize("name,prompt_len",
-                         [(n, 6) for n in CASES] + [("q4km-3-layers", 300), ("q8-7-layers", 300), ("q4km-hd64-g8", 300)])
-def test_fused_qkv_attention_equals_two_launches_and_oracle(hip_ctx, monkeypatch, name, prompt_len):
+@pytest.mark.parametrize("name,prompt_len,v_now",
+                         [(n, 6, "") for n in CASES] +
+                         [("q4km-3-layers", 300, ""), ("q8-7-layers", 300, ""), ("q4km-hd64-g8", 300, "")] +
+                         [("q8-7-layers", 6, "1"), ("q4km-3-layers", 300, "1"), ("q4km-hd64-g8", 300, "1")])
+def test_fused_qkv_attention_equals_two_launches_and_oracle(hip_ctx, monkeypatch, name, prompt_len, v_now):
     # a 6-token prompt keeps every step's attention in one split; after 300
     # tokens each kv head has two splits and the launch merges them (polled)
     spec = synth.small_spec(**dict(CASES[name], context=prompt_len + 40))
-    say(f"fused q/k/v + attention {name}: {spec.n_layers} layers, hidden {spec.hidden}, prompt {prompt_len}")
+    say(f"fused q/k/v + attention {name}: {spec.n_layers} layers, hidden {spec.hidden}, prompt {prompt_len}, "
+        f"v_now {v_now or 'auto'}")
+    if v_now:
+        monkeypatch.setenv("ZIGGY_HIP_ATTN_V_NOW", v_now)
     img = synth.build(spec, seed=41)
     prompt = synth.prompt_tokens(7, prompt_len, spec.vocab)
     steps = 24
@@ -74,6 +81,26 @@ def test_fused_qkv_attention_equals_two_launches_and_oracle(hip_ctx, monkeypatch
     o = zo.Session(zo.Model(img.buf), context=spec.context, kv_f16=True)
     ref, _ = o.generate(prompt, steps)
     assert list(got) == list(ref)
+
+
+def test_fused_variant_switch_rebuilds_the_step_graph(hip_ctx, monkeypatch):
+    # the session picks the fused launch's variant when generate builds the
+    # step graph; asking for the other one on the same session rebuilds it
+    spec = synth.small_spec(**dict(CASES["q4km-3-layers"], context=340))
+    img = synth.build(spec, seed=53)
+    prompt = synth.prompt_tokens(13, 300, spec.vocab)
+    steps = 16
+    monkeypatch.setenv("ZIGGY_HIP_ATTN_V_NOW", "0")
+    s = hip.Session(hip_ctx, img, context=spec.context)
+    want, _ = s.generate(prompt, steps)
+    want_logits = s.logits()
+    for flag in ("1", "0", "1"):
+        monkeypatch.setenv("ZIGGY_HIP_ATTN_V_NOW", flag)
+        s.reset()
+        got, _ = s.generate(prompt, steps)
+        assert list(got) == list(want), flag
+        assert np.array_equal(s.logits(), want_logits), flag
+    s.close()
 
 
 def test_fused_qkv_attention_profile_records(hip_ctx):

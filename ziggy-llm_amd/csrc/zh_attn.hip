@@ -819,7 +819,11 @@ __device__ __forceinline__ h8v as_h8(uint4 v) {
 // kPollEmpty (bounded: on expiry the error flag is set and the values are
 // taken as they are); each workgroup then refills its slice of the next
 // launch's q/k/v words (qkv_refill) with kPollEmpty.
-template <int HD, int GG, bool MQ, bool PQ = false>
+// VNOW (with PQ): the V tiles issued right after the q/k/v wait, under the q
+// prologue, instead of after it; the host picks it for long contexts (a
+// split's many tiles make the V stream the longer part there; with few, the
+// prologue is, and loads queued ahead of it delay it).
+template <int HD, int GG, bool MQ, bool PQ = false, bool VNOW = false>
 __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int split, const int kvh, const int qz) {
     static_assert(!PQ || !MQ, "polled q/k/v: single query");
     constexpr int KS = HD / 32;  // 32-dim steps of the scores, 32-dim chunks of the values
@@ -1014,6 +1018,10 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
             }
             __builtin_amdgcn_s_sleep(1);
         }
+        if constexpr (VNOW) {
+            load_v(0, vr[0]);
+            load_v(1, vr[1]);
+        }
     }
     // the projection biases (the bias reads above are dummies when absent)
     if (fused) {
@@ -1067,8 +1075,10 @@ __device__ __forceinline__ void attn_mfma_body(const AttnParams &p, const int sp
         qp_s[col][d] = h;
     }
     __syncthreads();
-    load_v(0, vr[0]);
-    load_v(1, vr[1]);
+    if constexpr (!(PQ && VNOW)) {
+        load_v(0, vr[0]);
+        load_v(1, vr[1]);
+    }
     h8v qf[NT][KS];
     bool col_ok[NT];
     float m[NT], lsum[NT];  // for column li of tile nt
@@ -1538,14 +1548,14 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t s) {
 // workgroups per CU, so a projection and an attention workgroup share a CU;
 // the projection workgroups come first in dispatch order, so no workgroup
 // waits for one that is not yet resident.
-template <int F1, int F2, int HD, int GG>
+template <int F1, int F2, int HD, int GG, bool VNOW>
 __global__ void __launch_bounds__(256, 2) qkv_attn_kernel(MvParams pq, AttnParams pa, int n_qkv) {
     if ((int)blockIdx.x < n_qkv) {
         __shared__ float lds[36];
         mv_run<F1, F2, IN_NORM, OUT_STORE, 64, 1, MV_PUBLISH>(pq, blockIdx.x, lds, MvFuse{});
     } else {
         const int a = (int)blockIdx.x - n_qkv;
-        attn_mfma_body<HD, GG, false, true>(pa, a % pa.max_splits, a / pa.max_splits, 0);
+        attn_mfma_body<HD, GG, false, true, VNOW>(pa, a % pa.max_splits, a / pa.max_splits, 0);
     }
 }
 
@@ -1553,13 +1563,27 @@ typedef void (*QkvAttnKernel)(MvParams, AttnParams, int);
 
 // Q4_K q/k with a Q6_K v (a Q4_K_M layer) or Q8_0 throughout; head_dim 128
 // with four query heads per kv head, or 64 with eight
-static QkvAttnKernel pick_qkv_attn(int f1, int f2, int hd, int g) {
+template <bool VNOW> static QkvAttnKernel pick_qkv_attn_v(int f1, int f2, int hd, int g) {
     if (hd == 128 && g == 4) {
-        if (f1 == Q4_K && f2 == Q6_K) return qkv_attn_kernel<Q4_K, Q6_K, 128, 4>;
-        if (f1 == Q8_0 && f2 == Q8_0) return qkv_attn_kernel<Q8_0, Q8_0, 128, 4>;
+        if (f1 == Q4_K && f2 == Q6_K) return qkv_attn_kernel<Q4_K, Q6_K, 128, 4, VNOW>;
+        if (f1 == Q8_0 && f2 == Q8_0) return qkv_attn_kernel<Q8_0, Q8_0, 128, 4, VNOW>;
     }
-    if (hd == 64 && g == 8 && f1 == Q4_K && f2 == Q6_K) return qkv_attn_kernel<Q4_K, Q6_K, 64, 8>;
+    if (hd == 64 && g == 8 && f1 == Q4_K && f2 == Q6_K) return qkv_attn_kernel<Q4_K, Q6_K, 64, 8, VNOW>;
     return nullptr;
+}
+static QkvAttnKernel pick_qkv_attn(int f1, int f2, int hd, int g, bool v_now = false) {
+    return v_now ? pick_qkv_attn_v<true>(f1, f2, hd, g) : pick_qkv_attn_v<false>(f1, f2, hd, g);
+}
+
+// Whether the fused launch issues its V tiles right after the q/k/v wait
+// (VNOW): from `position` on, each wavefront of a split holds three tiles or
+// more (measured: 371 against 367 tok/s at 16k; at 4k, 1-2 tiles, it lost
+// 0.8%).  ZIGGY_HIP_ATTN_V_NOW=1 / 0 forces it either way (tests).
+bool qkv_attention_v_now(int position, int max_splits) {
+    const char *e = getenv("ZIGGY_HIP_ATTN_V_NOW");
+    if (e && e[0]) return e[0] == '1';
+    // tiles per split at least 9 (every wavefront then holds three or more)
+    return (long)(position + 1) >= 9L * 32 * (max_splits > 0 ? max_splits : 1);
 }
 
 bool qkv_attention_supported(int f1, int f2, int hidden, int head_dim, int group) {
@@ -1567,7 +1591,7 @@ bool qkv_attention_supported(int f1, int f2, int hidden, int head_dim, int group
            pick_qkv_attn(f1, f2, head_dim, group) != nullptr;
 }
 
-hipError_t launch_qkv_attention(const MvParams &qkv, const AttnParams &a, hipStream_t s) {
+hipError_t launch_qkv_attention(const MvParams &qkv, const AttnParams &a, hipStream_t s, bool v_now) {
     MvParams pq = qkv;
     if (pq.nseg < 1 || pq.nseg > 3 || !pq.norm_w || pq.expert || pq.pro_in || pq.x2) return hipErrorInvalidValue;
     int f1 = pq.seg[0].fmt, f2 = f1;
@@ -1584,7 +1608,7 @@ hipError_t launch_qkv_attention(const MvParams &qkv, const AttnParams &a, hipStr
         return hipErrorInvalidValue;
     const int G = a.head_count / a.head_count_kv;
     const QkvAttnKernel k = qkv_attention_supported(f1, f2, pq.cols, a.head_dim, G)
-                                ? pick_qkv_attn(f1, f2, a.head_dim, G)
+                                ? pick_qkv_attn(f1, f2, a.head_dim, G, v_now)
                                 : nullptr;
     if (!k) return hipErrorInvalidValue;
     plan_matvec(pq, matvec_target_wgs());

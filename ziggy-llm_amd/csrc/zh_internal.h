@@ -457,7 +457,10 @@ hipError_t launch_attention(const AttnParams &p, hipStream_t s);
 // and v as they land.  Every q/k/v word (a.q, a.k_new, a.v_new: the
 // segments' outputs) must hold kPollEmpty before the launch; the launch
 // refills a.qkv_refill (the same layout) for the next one.
-hipError_t launch_qkv_attention(const MvParams &qkv, const AttnParams &a, hipStream_t s);
+hipError_t launch_qkv_attention(const MvParams &qkv, const AttnParams &a, hipStream_t s, bool v_now = false);
+// whether a decode from `position` wants launch_qkv_attention's v_now variant
+// (the V tiles issued right after the q/k/v wait, for long contexts)
+bool qkv_attention_v_now(int position, int max_splits);
 // whether launch_qkv_attention serves these formats (q's, and the other
 // segments' if different) and shapes
 bool qkv_attention_supported(int f1, int f2, int hidden, int head_dim, int group);

@@ -68,6 +68,9 @@ struct ZiggyHipSession {
     // after the last), which is never its own: qkv_sets is the smallest n >= 2
     // with (layers - 1) % n != 0.  Only whole steps (layers in order) use them.
     bool qkv_fuse = false;
+    // qkv_v_now: the fused launch's variant that issues its V tiles right
+    // after the q/k/v wait (long contexts); chosen when the step graph is built
+    bool qkv_v_now = false;
     int qkv_sets = 1;
     float *qkv_buf = nullptr;
     // binary16 K/V, paged: per layer kv_pages pages of 64 positions ([page][row in page][kv_dim]);
@@ -82,6 +85,7 @@ struct ZiggyHipSession {
     uint32_t prompt_cap = 0, history_cap = 0;
     hipGraphExec_t graph = nullptr;
     const uint32_t *graph_prompt = nullptr, *graph_history = nullptr;  // the buffers the graph's step_begin reads
+    bool graph_v_now = false;                                          // the graph's fused-launch variant
     // batched verify (allocated on first use): [kVerifyMax] rows each
     float *b_hidden = nullptr, *b_normed = nullptr, *b_q = nullptr, *b_k = nullptr, *b_v = nullptr;
     float *b_attn = nullptr, *b_act = nullptr, *b_up = nullptr, *b_logits = nullptr;
@@ -288,7 +292,7 @@ hipError_t launch_qkv_attention_layer(ZiggyHipSession *s, int l, const int *pos_
     p.norm_w = (const float *)W.attn_norm.p;
     AttnParams a = step_attention_params(s, l, pos_dev, pos, q, k, v);
     a.qkv_refill = next;
-    return launch_qkv_attention(p, a, st);
+    return launch_qkv_attention(p, a, st, s->qkv_v_now);
 }
 
 // The attention block of layer l inside a whole decode step: with qkv_fuse
@@ -399,6 +403,7 @@ int build_graph(ZiggyHipSession *s, char *err, size_t err_len) {
     if (e != hipSuccess) return hip_fail(e, "graph instantiate", err, err_len);
     s->graph_prompt = s->prompt;
     s->graph_history = s->history;
+    s->graph_v_now = s->qkv_v_now;
     return ZIGGY_HIP_OK;
 }
 
@@ -577,6 +582,7 @@ int ziggy_hip_session_create(ZiggyHipContext *ctx, const ZiggyHipModelDesc *mode
             }
             s->qkv_fuse = true;
             s->qkv_sets = n;
+            s->qkv_v_now = qkv_attention_v_now(0, s->max_splits);
         }
     }
     // pages in order until the caller sets a block table
@@ -939,8 +945,12 @@ int ziggy_hip_session_generate(ZiggyHipSession *s, const uint32_t *prompt, uint3
         s->allocs.push_back(s->history);
         s->history_cap = cap;
     }
-    // step_begin reads the prompt/history pointers baked into the graph: rebuild it only if they moved
-    if (s->graph && (s->graph_prompt != s->prompt || s->graph_history != s->history)) {
+    // step_begin reads the prompt/history pointers baked into the graph, and
+    // the fused launch's variant follows the position the decode starts at:
+    // rebuild it only if either changed
+    if (s->qkv_fuse) s->qkv_v_now = qkv_attention_v_now((int)(s->position + prompt_len - 1), s->max_splits);
+    if (s->graph && (s->graph_prompt != s->prompt || s->graph_history != s->history ||
+                     s->graph_v_now != s->qkv_v_now)) {
         hipGraphExecDestroy(s->graph);
         s->graph = nullptr;
     }
