@@ -338,7 +338,7 @@ typedef struct {
 
 /* ---- measurement probes (no counterpart in the reference: they time the
  * hardware under the decode step's launch structure; python -m zhip.microbench
- * --chain / --sync) ---- */
+ * --chain / --sync / --row-load) ---- */
 typedef struct {
     uint64_t bytes;         /* bytes streamed (each entry rounded down to whole 16-byte words) */
     uint32_t kernels;       /* entries of the plan */
@@ -362,6 +362,17 @@ typedef struct {
 /* Latencies of in-launch dependencies between workgroups, averaged over `rounds`. */
 int ziggy_hip_probe_sync(ZiggyHipContext *ctx, uint32_t rounds, ZiggyHipSyncProbe *out, char *error_message,
                          size_t error_message_len);
+typedef struct {
+    uint32_t workgroups;     /* two per CU, 256 lanes each */
+    uint32_t values;         /* floats per row (4096) */
+    double slot_us[2];       /* every lane loads its own 256-byte slot: [0] the row, [1] with a second row */
+    double coalesced_us[2];  /* coalesced 16-byte loads of the same bytes per wavefront */
+    double lds_us[2];        /* loaded once per workgroup into LDS, slots read there */
+} ZiggyHipRowLoadProbe;
+/* Median time per workgroup to bring a row written by the previous launch
+ * into every lane (python -m zhip.microbench --row-load), median of `reps`. */
+int ziggy_hip_probe_row_load(ZiggyHipContext *ctx, uint32_t reps, ZiggyHipRowLoadProbe *out, char *error_message,
+                             size_t error_message_len);
 
 /* Kernels of one decode step, for ziggy_hip_session_time_kernel. */
 enum {

@@ -13,9 +13,18 @@
 // CU-sized grid (per-workgroup arrival words polled by one wavefront; an
 // arrival counter).
 //
+// ziggy_hip_probe_row_load: what a matvec's input row costs to bring into
+// its lanes, per workgroup, right after the launch that wrote it: every lane
+// loading its own 256-byte slot (the 16-byte loads of a wavefront 256 bytes
+// apart), coalesced 16-byte loads of the same byte count, and the row loaded
+// once per workgroup, coalesced, through LDS, every lane then reading its
+// slot there; each for the row alone and with a second row of the same size
+// beside it (the RMSNorm weights).
+//
 // Every wait is bounded (a spin limit far above any real wait); on expiry the
 // result carries the flag and the timings are not valid.  The grids of the
 // waiting kernels are at most one workgroup per CU, so all are resident.
+#include <algorithm>
 #include <vector>
 
 #include "zh_internal.h"
@@ -153,6 +162,68 @@ int cu_count(int dev) {
     int cus = 0;
     hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     return cus > 0 ? cus : 1;
+}
+
+constexpr int kRowProbeValues = 4096;
+
+__global__ void __launch_bounds__(256) probe_row_write(float *row, float v) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < kRowProbeValues; i += gridDim.x * blockDim.x)
+        row[i] = v + (float)i;
+}
+
+// NIN rows (x, then w) of kRowProbeValues floats.  MODE 0: lane l loads
+// float4s 16l .. 16l + 15 of each row; 1: float4s 64j + l (coalesced, the
+// same bytes per wavefront); 2: the workgroup loads each row once,
+// coalesced, into LDS (one float4 of padding per 16) and lane l reads float4s
+// 16l .. 16l + 15 there.  t[2b], t[2b + 1]: workgroup b's clock before its
+// first load and after every lane holds its values.
+template <int NIN, int MODE>
+__global__ void __launch_bounds__(256, 2) probe_row_load(const float *x, const float *w, unsigned long long *t,
+                                                         float *sink) {
+    __shared__ float4 xs[MODE == 2 ? NIN * 1088 : 1];
+    const int lane = threadIdx.x & 63, tid = threadIdx.x;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x), *w4 = reinterpret_cast<const float4 *>(w);
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    float4 r[NIN][16];
+    if constexpr (MODE == 0 || MODE == 1) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int q = MODE == 0 ? lane * 16 + j : j * 64 + lane;
+            r[0][j] = x4[q];
+            if constexpr (NIN == 2) r[1][j] = w4[q];
+        }
+    } else {
+        float4 g[NIN][4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            g[0][j] = x4[j * 256 + tid];
+            if constexpr (NIN == 2) g[1][j] = w4[j * 256 + tid];
+        }
+#pragma unroll
+        for (int i = 0; i < NIN; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int q = j * 256 + tid;
+                xs[i * 1088 + q + (q >> 4)] = g[i][j];
+            }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NIN; i++)
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int q = lane * 16 + j;
+                r[i][j] = xs[i * 1088 + q + (q >> 4)];
+            }
+    }
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < NIN; i++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) a += (r[i][j].x + r[i][j].y) + (r[i][j].z + r[i][j].w);
+    __syncthreads();
+    const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
+    if (tid == 0) t[2 * blockIdx.x] = t0, t[2 * blockIdx.x + 1] = t1;
+    if (a == -1.f) sink[0] = a;  // keeps the loads live
 }
 
 }  // namespace
@@ -294,6 +365,63 @@ int ziggy_hip_probe_sync(ZiggyHipContext *ctx, uint32_t rounds, ZiggyHipSyncProb
     out->handoff_acqrel_us = res[1];
     out->barrier_flags_us = res[2];
     out->barrier_counter_us = res[3];
+    return ZIGGY_HIP_OK;
+}
+
+int ziggy_hip_probe_row_load(ZiggyHipContext *ctx, uint32_t reps, ZiggyHipRowLoadProbe *out, char *err,
+                             size_t err_len) {
+    if (!ctx || !out || reps == 0 || reps > 10000) {
+        set_err(err, err_len, "invalid probe_row_load arguments");
+        return ZIGGY_HIP_INVALID_ARGUMENT;
+    }
+    hipSetDevice(ctx->device);
+    const int G = 2 * cu_count(ctx->device);  // two workgroups per CU, as the decode matvecs
+    hipStream_t st = ctx->stream;
+    float *rows = nullptr, *sink = nullptr;
+    unsigned long long *t = nullptr;
+    hipError_t e = hipMalloc(&rows, 2 * kRowProbeValues * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&sink, 64);
+    if (e == hipSuccess) e = hipMalloc(&t, (size_t)G * 16);
+    if (e == hipSuccess) e = hipMemsetAsync(rows, 0, 2 * kRowProbeValues * sizeof(float), st);
+    std::vector<unsigned long long> h((size_t)G * 2);
+    double res[6] = {0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < 6 && e == hipSuccess; k++) {
+        std::vector<double> per_rep;
+        for (uint32_t r = 0; r <= reps && e == hipSuccess; r++) {  // rep 0 warms up
+            hipLaunchKernelGGL(probe_row_write, dim3(16), dim3(256), 0, st, rows, (float)r);
+            const float *x = rows, *w = rows + kRowProbeValues;
+            switch (k) {
+            case 0: hipLaunchKernelGGL((probe_row_load<1, 0>), dim3(G), dim3(256), 0, st, x, w, t, sink); break;
+            case 1: hipLaunchKernelGGL((probe_row_load<1, 1>), dim3(G), dim3(256), 0, st, x, w, t, sink); break;
+            case 2: hipLaunchKernelGGL((probe_row_load<1, 2>), dim3(G), dim3(256), 0, st, x, w, t, sink); break;
+            case 3: hipLaunchKernelGGL((probe_row_load<2, 0>), dim3(G), dim3(256), 0, st, x, w, t, sink); break;
+            case 4: hipLaunchKernelGGL((probe_row_load<2, 1>), dim3(G), dim3(256), 0, st, x, w, t, sink); break;
+            default: hipLaunchKernelGGL((probe_row_load<2, 2>), dim3(G), dim3(256), 0, st, x, w, t, sink); break;
+            }
+            e = hipGetLastError();
+            if (e == hipSuccess) e = hipMemcpyAsync(h.data(), t, (size_t)G * 16, hipMemcpyDeviceToHost, st);
+            if (e == hipSuccess) e = hipStreamSynchronize(st);
+            if (e != hipSuccess || r == 0) continue;
+            std::vector<double> d(G);
+            for (int b = 0; b < G; b++) d[b] = (double)(h[2 * b + 1] - h[2 * b]) * 0.01;  // 100 MHz clock
+            std::nth_element(d.begin(), d.begin() + G / 2, d.end());
+            per_rep.push_back(d[G / 2]);
+        }
+        if (e != hipSuccess) break;
+        std::nth_element(per_rep.begin(), per_rep.begin() + per_rep.size() / 2, per_rep.end());
+        res[k] = per_rep[per_rep.size() / 2];
+    }
+    if (rows) hipFree(rows);
+    if (sink) hipFree(sink);
+    if (t) hipFree(t);
+    if (e != hipSuccess) return hip_fail(e, "probe_row_load", err, err_len);
+    out->workgroups = (uint32_t)G;
+    out->values = kRowProbeValues;
+    for (int i = 0; i < 2; i++) {
+        out->slot_us[i] = res[3 * i];
+        out->coalesced_us[i] = res[3 * i + 1];
+        out->lds_us[i] = res[3 * i + 2];
+    }
     return ZIGGY_HIP_OK;
 }
 

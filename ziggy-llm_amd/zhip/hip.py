@@ -69,6 +69,11 @@ class SyncProbe(ctypes.Structure):
                 ("barrier_flags_us", ctypes.c_double), ("barrier_counter_us", ctypes.c_double)]
 
 
+class RowLoadProbe(ctypes.Structure):
+    _fields_ = [("workgroups", ctypes.c_uint32), ("values", ctypes.c_uint32),
+                ("slot_us", ctypes.c_double * 2), ("coalesced_us", ctypes.c_double * 2), ("lds_us", ctypes.c_double * 2)]
+
+
 class GenerateStats(ctypes.Structure):
     _fields_ = [("steps", ctypes.c_uint64), ("gpu_elapsed_ns", ctypes.c_uint64), ("wall_ns", ctypes.c_uint64),
                 ("next_token", ctypes.c_uint32), ("reserved", ctypes.c_uint32), ("prompt_ns", ctypes.c_uint64)]
@@ -146,6 +151,7 @@ def lib() -> ctypes.CDLL:
         "ziggy_hip_time_matvec": [vp, u32, vp, u32, sz, vp, vp, u32, u32, u32, ctypes.POINTER(ctypes.c_uint64)] + E,
         "ziggy_hip_probe_chain": [vp, vp, u32, u32, ctypes.POINTER(ChainProbe)] + E,
         "ziggy_hip_probe_sync": [vp, u32, ctypes.POINTER(SyncProbe)] + E,
+        "ziggy_hip_probe_row_load": [vp, u32, ctypes.POINTER(RowLoadProbe)] + E,
         "ziggy_hip_indexed_matvec": [vp, u32, vp, vp, vp, u32, u32, vp, u32, u32, i] + E,
         "ziggy_hip_run_gemm": [vp, u32, vp, vp, vp, u32, u32, u32, i] + E,
         "ziggy_hip_dual_indexed_matvec": [vp, u32, vp, vp, vp, vp, vp, u32, u32, vp, u32, u32] + E,
@@ -308,6 +314,13 @@ class Context:
         """In-launch hand-off and grid-barrier latencies (ziggy_hip_probe_sync)."""
         out = SyncProbe()
         _call("ziggy_hip_probe_sync", self.h, rounds, ctypes.byref(out))
+        return out
+
+    def probe_row_load(self, reps: int = 50) -> RowLoadProbe:
+        """Per-workgroup time to bring a freshly written row into every lane, three load patterns
+        (ziggy_hip_probe_row_load)."""
+        out = RowLoadProbe()
+        _call("ziggy_hip_probe_row_load", self.h, reps, ctypes.byref(out))
         return out
 
     def copy(self, src: Buffer, src_off: int, dst: Buffer, dst_off: int, nbytes: int):

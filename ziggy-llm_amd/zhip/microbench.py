@@ -135,10 +135,40 @@ def sync(args) -> dict:
     return out
 
 
+def row_load(args) -> dict:
+    ctx = hip.Context(0)
+    r = ctx.probe_row_load(args.reps)
+    ctx.close()
+    out = {"probe": "row_load", "workgroups": r.workgroups, "values": r.values, "reps": args.reps,
+           "slot_us": [round(v, 3) for v in r.slot_us], "coalesced_us": [round(v, 3) for v in r.coalesced_us],
+           "lds_us": [round(v, 3) for v in r.lds_us]}
+    print(json.dumps(out), flush=True)
+    if args.out:
+        kb = r.values * 4 // 1024
+        lines = ["# Input-row load patterns, one MI355X", "", "Command (from ziggy-llm_amd/):", "",
+                 f"    python3 -m zhip.microbench --row-load --reps {args.reps} --out <file>", "",
+                 f"{r.workgroups} workgroups of 256 lanes (two per CU); each brings a {r.values}-float row "
+                 f"({kb} KiB), written by the launch before, into every lane's registers (each wavefront holds "
+                 "the whole row, 64 floats a lane), optionally with a second row of the same size (RMSNorm "
+                 "weights). Median over workgroups of the time from the first load to every lane holding its "
+                 f"values (s_memrealtime, 100 MHz); median of {args.reps} launches.", "",
+                 "| load pattern | row alone, us | row + second row, us |", "|---|---|---|",
+                 f"| every lane loads its own 256-byte slot (16-byte loads 256 bytes apart) | "
+                 f"{out['slot_us'][0]} | {out['slot_us'][1]} |",
+                 f"| coalesced 16-byte loads, same bytes per wavefront | {out['coalesced_us'][0]} | "
+                 f"{out['coalesced_us'][1]} |",
+                 f"| once per workgroup, coalesced, through LDS; slots read there | {out['lds_us'][0]} | "
+                 f"{out['lds_us'][1]} |"]
+        with open(args.out, "w") as fh:
+            fh.write("\n".join(lines) + "\n")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--chain", action="store_true", help="the decode step's launch-structure probe")
     ap.add_argument("--sync", action="store_true", help="in-launch dependency latencies")
+    ap.add_argument("--row-load", action="store_true", help="input-row load patterns")
     ap.add_argument("--position", type=int, default=4096)
     ap.add_argument("--reps", type=int, default=5)
     ap.add_argument("--rounds", type=int, default=2000)
@@ -148,11 +178,13 @@ def main():
                     help="comma-separated ROWSxCOLS list")
     ap.add_argument("--out", help="also write the results as a markdown table")
     args = ap.parse_args()
-    if args.chain or args.sync:
+    if args.chain or args.sync or args.row_load:
         if args.chain:
             chain(args)
         if args.sync:
             sync(args)
+        if args.row_load:
+            row_load(args)
         return
     shapes = [tuple(int(v) for v in s.split("x")) for s in args.shapes.split(",")]
     ctx = hip.Context(0)
